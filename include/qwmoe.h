@@ -1,0 +1,193 @@
+/*
+ * qwmoe.h -- C ABI of libqwmoe, the MI355X (gfx950) implementation of
+ * QuestWend's MoE expert hot path: router top-k, GGML_OP_MUL_MAT_ID over
+ * Q4_K / Q8_0 expert slot pools, SwiGLU, the gate-weighted combine (+ shared
+ * expert), the verify head (rms_norm -> Q8_0 lm_head -> argmax) with greedy
+ * MTP acceptance, the GPU LRU slot pool and its slab fetch.
+ *
+ * Conventions
+ *  - Tensors use ggml's layout: ne[0] is the contiguous dimension, nb[] are
+ *    byte strides, `type` is a ggml_type value (ggml.h:390-420).  Data
+ *    pointers are device pointers unless a comment says host.
+ *  - Every entry point returns QWM_OK (0) or a negative QWM_ERR_* code and
+ *    never throws; qwm_last_error() describes the last failure of the calling
+ *    thread.  QWM_ERR_UNSUPPORTED means "shape/type not handled here": the
+ *    caller keeps its own fallback, as ggml's supports_op contract expects.
+ *  - The library allocates no device memory on the hot path.  Scratch comes
+ *    from a caller-owned workspace sized by qwm_*_workspace_size() and zeroed
+ *    once with qwm_workspace_init() (it keeps self-resetting counters).
+ *  - Work is enqueued on the given hipStream_t (passed as void*); calls are
+ *    asynchronous unless stated otherwise.  Calls that share a workspace must
+ *    be ordered on one stream.
+ *  - Numerics follow ggml's CPU backend on x86-64 (AVX-512 build): activations
+ *    entering Q4_K dots are quantized to Q8_K, those entering Q8_0 dots with
+ *    the x86 Q8_0 quantizer, so every 32/256-element block sum is the same
+ *    integer; router logits, softmax and the weight normalization reproduce
+ *    the CPU's floating-point order.
+ */
+#ifndef QWMOE_H
+#define QWMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QWM_OK               0
+#define QWM_ERR_UNSUPPORTED (-1)
+#define QWM_ERR_ARG         (-2)
+#define QWM_ERR_WORKSPACE   (-3)
+#define QWM_ERR_HIP         (-4)
+#define QWM_ERR_NO_VICTIM   (-5)
+#define QWM_ERR_STATE       (-6)
+
+/* ggml_type values used on this path (ggml.h:390-420) */
+#define QWM_TYPE_F32   0
+#define QWM_TYPE_Q8_0  8
+#define QWM_TYPE_Q4_K 12
+#define QWM_TYPE_I32  26
+
+/* Mirrors the data-carrying part of struct ggml_tensor (ggml.h). */
+typedef struct qwm_tensor {
+    int32_t type;
+    int64_t ne[4];
+    size_t  nb[4];
+    void *  data;
+} qwm_tensor;
+
+/* Fills ne/nb for a contiguous tensor of the given type (nb[0] = block size). */
+void qwm_tensor_init(qwm_tensor * t, int32_t type, int64_t ne0, int64_t ne1, int64_t ne2, void * data);
+
+const char * qwm_version(void);
+const char * qwm_last_error(void);
+
+/* Zero-fills a workspace (a fill kernel, no hipMemsetAsync; safe to capture). */
+int qwm_workspace_init(void * workspace, size_t bytes, void * stream);
+
+/* ---------------------------------------------------------------- ops ---- */
+
+/* GGML_OP_MUL_MAT_ID (ggml.c:3398-3440; CPU: ggml-cpu.c:1554-1734):
+ *   dst[:, e, t] = as[:, :, ids[e, t]] . b[:, e % ne11(b), t]
+ * as: Q4_K or Q8_0 [K, N, n_as]; b: f32 [K, ne11, T]; ids: i32 [n_ids, T];
+ * dst: f32 [N, n_ids, T].  Supported: K % 256 == 0 (Q4_K) or K % 32 == 0
+ * (Q8_0), T <= 8, n_ids * T <= 128. */
+size_t qwm_mul_mat_id_workspace_size(const qwm_tensor * as, const qwm_tensor * b, const qwm_tensor * ids);
+int qwm_mul_mat_id(const qwm_tensor * as, const qwm_tensor * b, const qwm_tensor * ids, qwm_tensor * dst,
+                   void * workspace, size_t ws_bytes, void * stream);
+
+/* --------------------------------------------------- the MoE FFN block --- */
+
+/* One MoE layer's weights: slot pools in ggml layout (gate/up [H, N, S],
+ * down [N, H, S]), the f32 router [H, E], and an optional shared expert
+ * (data == NULL when absent): gate/up [H, N_sh], down [N_sh, H], and the
+ * optional f32 shared gate row [H, 1]. */
+typedef struct qwm_moe_layer {
+    qwm_tensor gate_pool, up_pool, down_pool;
+    qwm_tensor router;
+    qwm_tensor sh_gate, sh_up, sh_down, sh_gate_inp;
+    int32_t n_expert_used;      /* k */
+    int32_t norm_weights;       /* hparams.expert_weights_norm */
+    float   weights_scale;      /* hparams.expert_weights_scale (0 or 1: none) */
+} qwm_moe_layer;
+
+/* Router (core/runtime.cpp:2693-2734 after the router mul_mat 3785-3798):
+ *   logits = router . x (+ rm);  probs = soft_max(logits);
+ *   ids = top-k(probs) [k, T];   w = probs[ids] (/ clamp(sum, 6.1035e-5) if norm)
+ * x: f32 [H, T]; rm: optional f32 [E, T] added to the logits; ids_out: i32
+ * [k, T]; w_out: f32 [k, T].  The top-k keeps the lower expert index on exact
+ * probability ties (std::sort leaves their order unspecified).  T <= 8. */
+size_t qwm_moe_workspace_size(const qwm_moe_layer * layer, int64_t T);
+int qwm_moe_route(const qwm_moe_layer * layer, const qwm_tensor * x, const qwm_tensor * rm,
+                  qwm_tensor * ids_out, qwm_tensor * w_out, void * workspace, size_t ws_bytes, void * stream);
+
+/* Expert FFN over the slot pools (build_moe_cached, runtime.cpp:3801-3830,
+ * and build_segB, 4534-4572):
+ *   up = mul_mat_id(up_pool, x, slot_u); gate = mul_mat_id(gate_pool, x, slot_g)
+ *   act = swiglu(gate, up); experts = mul_mat_id(down_pool, act, slot_d)
+ *   T == 1: out = cont(transpose(experts)) . w     (k-ordered fused sum)
+ *   T >  1: out = e0*w0 + e1*w1 + ... left to right
+ *   + shared expert: out += down_sh(silu(gate_sh x) * up_sh x) [* sigmoid(g_inp . x)]
+ *   if resid != NULL: out += resid (the block's residual add).
+ * Must follow qwm_moe_route on the same workspace (it reuses the quantized x
+ * and the expert schedule).  slot_*: i32 [k, T] device slot ids; weights: f32
+ * [k, T]; out: f32 [H, T]. */
+int qwm_moe_experts(const qwm_moe_layer * layer, const qwm_tensor * x, const qwm_tensor * slot_g,
+                    const qwm_tensor * slot_u, const qwm_tensor * slot_d, const qwm_tensor * weights,
+                    const qwm_tensor * resid, qwm_tensor * out, void * workspace, size_t ws_bytes, void * stream);
+
+/* Route + experts with the in-graph slot remap of the fast decode path
+ * (runtime.cpp:2759-2787): slot = slot_of[role][layer * E + id] read on the
+ * device from `slot_tables` (i32 [E * n_layer, 3], role-major: gate, up,
+ * down).  No host round trip; the pools must hold every selected expert. */
+int qwm_moe_block_resident(const qwm_moe_layer * layer, int32_t layer_index, const int32_t * slot_tables,
+                           int64_t table_stride, const qwm_tensor * x, const qwm_tensor * rm,
+                           const qwm_tensor * resid, qwm_tensor * out, qwm_tensor * ids_out, qwm_tensor * w_out,
+                           void * workspace, size_t ws_bytes, void * stream);
+
+/* -------------------------------------------------- verify + acceptance --- */
+
+/* Verify head + greedy acceptance (runtime.cpp:5014-5046 and 3648-3652):
+ *   h = rms_norm(x, eps) * norm_w;  logits = lm_head . h (Q8_0 [H, V]);
+ *   vA[t] = argmax(logits[:, t])  (last index among equal maxima)
+ *   a = longest prefix with vA[j] == drafts[j], j < n_draft;  x_new = vA[a]
+ * x: f32 [H, T]; norm_w: optional f32 [H]; drafts: device i32 [n_draft]
+ * (n_draft = T - 1); result: device i32 [T + 2] = vA[0..T-1], a, x_new. */
+size_t qwm_verify_workspace_size(const qwm_tensor * lm_head, int64_t T);
+int qwm_verify_accept(const qwm_tensor * lm_head, const qwm_tensor * x, const float * norm_w, float eps,
+                      const int32_t * drafts, int32_t * result, void * workspace, size_t ws_bytes, void * stream);
+
+/* ---------------------------------------------------------- slot pool --- */
+
+/* ExpertCache's RAM-tier decisions (core/expert_cache.cpp: ensure 1615-1645,
+ * slot_for 1465-1479, install 1173-1180, pick_victim 1129-1170, drop
+ * 1067-1088; hooks core/gpu_lru_pool_hooks.h): one pool per role over all
+ * layers, one global clock, lowest free slot first, else the least recently
+ * used unprotected slot.  Misses are copied from pinned host slabs with
+ * hipMemcpyAsync on the pool's copy stream; the compute stream is made to
+ * wait for them (qwm_pool_wait).  Host-side, owner thread only. */
+typedef struct qwm_pool qwm_pool;
+
+typedef struct qwm_pool_desc {
+    int32_t n_layer, n_expert;
+    int32_t n_slots[3];          /* per role: gate, up, down */
+    void *  pool_data[3];        /* device base of each role's [K, N, n_slots] tensor */
+    size_t  slab_bytes[3];       /* nb[2] of each role */
+    const void * const * host_slabs[3]; /* per role: host_slabs[r][layer] = pinned [K, N, n_expert] source; may be NULL */
+    int32_t protect_active;      /* 1: ActiveExpertGuard protection (TinyLFU mode); 0: reference default */
+    int32_t indexed;             /* 1: O(1) indexed LRU (QWEN_GPU_LRU_INDEX=1); 0: linear scan */
+} qwm_pool_desc;
+
+typedef struct qwm_pool_stats {
+    uint64_t hits, misses, evictions, fetch_bytes, fetches;
+    uint64_t clock;
+} qwm_pool_stats;
+
+int qwm_pool_create(const qwm_pool_desc * desc, void * copy_stream, qwm_pool ** out);
+void qwm_pool_destroy(qwm_pool * pool);
+/* ids: host i32 [n] (token-major); slot_*: host i32 [n].  Issues the slab
+ * copies for misses on the copy stream.  QWM_ERR_NO_VICTIM leaves the pool
+ * consistent (the failing role is not published). */
+int qwm_pool_ensure(qwm_pool * pool, int32_t layer, const int32_t * ids, int32_t n,
+                    int32_t * slot_gate, int32_t * slot_up, int32_t * slot_down);
+/* Makes `stream` wait for every slab copy issued so far (hipStreamWaitEvent). */
+int qwm_pool_wait(qwm_pool * pool, void * stream);
+int qwm_pool_get_stats(const qwm_pool * pool, qwm_pool_stats * out);
+/* Dense expert -> slot row of (role, layer), 0 for non-resident experts
+ * (ExpertCache::slot_of_row, expert_cache.cpp:1448-1451); host i32 [n_expert]. */
+int qwm_pool_slot_of_row(const qwm_pool * pool, int32_t role, int32_t layer, int32_t * out);
+/* Per-slot key (layer * n_expert + expert, -1 free) and clock of one role. */
+int qwm_pool_slots(const qwm_pool * pool, int32_t role, int32_t * keys, uint64_t * clocks);
+
+/* One slab copy: pool_data + slot * slab_bytes <- pinned_src (async H2D on
+ * copy_stream), then records done_event (a hipEvent_t, may be NULL)
+ * (ExpertCache::fetch_slab RAM tier, expert_cache.cpp:706-717). */
+int qwm_slab_fetch_async(void * pool_data, size_t slab_bytes, int32_t slot, const void * pinned_src,
+                         void * copy_stream, void * done_event);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QWMOE_H */

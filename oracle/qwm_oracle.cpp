@@ -27,6 +27,7 @@
 #include <cstring>
 #include <limits>
 #include <stdexcept>
+#include <thread>
 #include <string>
 #include <unordered_map>
 #include <vector>
@@ -613,8 +614,16 @@ void mul_mat(int type, const void * w, int64_t K, int64_t N, const float * x, in
 
 QWO_API uint16_t qwo_fp32_to_fp16(float f) { return fp32_to_fp16(f); }
 QWO_API float qwo_fp16_to_fp32(uint16_t h) { return fp16_to_fp32(h); }
+// Rows are independent (ggml's quantize_q4_K loops over them); they are split
+// over threads here only to keep large test fixtures quick to build.
 QWO_API void qwo_quantize_q4_K(const float * x, void * y, int64_t nrow, int64_t k) {
-    for (int64_t r = 0; r < nrow; ++r) quantize_row_q4_K(x + r * k, (block_q4_K *)y + r * (k / QK_K), k);
+    const int64_t nt = std::max<int64_t>(1, std::min<int64_t>(nrow / 64, (int64_t)std::thread::hardware_concurrency()));
+    std::vector<std::thread> pool;
+    for (int64_t w = 0; w < nt; ++w)
+        pool.emplace_back([=]() {
+            for (int64_t r = w; r < nrow; r += nt) quantize_row_q4_K(x + r * k, (block_q4_K *)y + r * (k / QK_K), k);
+        });
+    for (auto & th : pool) th.join();
 }
 QWO_API void qwo_dequantize_q4_K(const void * x, float * y, int64_t k) { dequantize_row_q4_K((const block_q4_K *)x, y, k); }
 QWO_API void qwo_quantize_q8_K(const float * x, void * y, int64_t k) { quantize_row_q8_K(x, (block_q8_K *)y, k); }

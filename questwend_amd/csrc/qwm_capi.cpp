@@ -1,0 +1,288 @@
+// qwm_capi.cpp -- the extern "C" entry points of libqwmoe (include/qwmoe.h):
+// argument validation against ggml's op contracts, workspace planning, and
+// dispatch to the gfx950 kernels.  No C++ exception crosses the ABI.
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <cstring>
+#include <string>
+
+#include "qwm_internal.h"
+
+namespace qwm {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string & msg) { g_last_error = msg; }
+int fail(int code, const std::string & msg) {
+    g_last_error = msg;
+    return code;
+}
+
+static size_t type_size(int32_t type) {
+    switch (type) {
+        case T_F32: return 4;
+        case T_I32: return 4;
+        case T_Q8_0: return 34;
+        case T_Q4_K: return 144;
+    }
+    return 0;
+}
+static int64_t block_len(int32_t type) {
+    switch (type) {
+        case T_Q8_0: return 32;
+        case T_Q4_K: return 256;
+    }
+    return 1;
+}
+
+// rows contiguous and densely packed in the first two dimensions
+static bool contiguous_rows(const qwm_tensor * t) {
+    const size_t ts = type_size(t->type);
+    if (!ts || t->ne[0] % block_len(t->type)) return false;
+    if (t->nb[0] != ts) return false;
+    return t->nb[1] == ts * (size_t)(t->ne[0] / block_len(t->type));
+}
+static bool fully_contiguous(const qwm_tensor * t) {
+    if (!contiguous_rows(t)) return false;
+    return t->nb[2] == t->nb[1] * (size_t)t->ne[1] && t->nb[3] == t->nb[2] * (size_t)t->ne[2];
+}
+
+}  // namespace qwm
+
+using namespace qwm;
+
+extern "C" {
+
+void qwm_tensor_init(qwm_tensor * t, int32_t type, int64_t ne0, int64_t ne1, int64_t ne2, void * data) {
+    std::memset(t, 0, sizeof(*t));
+    t->type = type;
+    t->ne[0] = ne0; t->ne[1] = ne1; t->ne[2] = ne2; t->ne[3] = 1;
+    t->nb[0] = type_size(type);
+    t->nb[1] = t->nb[0] * (size_t)(ne0 / block_len(type));
+    t->nb[2] = t->nb[1] * (size_t)ne1;
+    t->nb[3] = t->nb[2] * (size_t)ne2;
+    t->data = data;
+}
+
+const char * qwm_version(void) { return "qwmoe 0.1 gfx950"; }
+const char * qwm_last_error(void) { return g_last_error.c_str(); }
+
+int qwm_workspace_init(void * workspace, size_t bytes, void * stream) {
+    if (!workspace && bytes) return fail(QWM_ERR_ARG, "workspace is NULL");
+    return launch_fill_zero(workspace, bytes & ~(size_t)3, (hipStream_t)stream);
+}
+
+// ------------------------------------------------------------ mul_mat_id --
+
+static int check_mmid(const qwm_tensor * as, const qwm_tensor * b, const qwm_tensor * ids, const qwm_tensor * dst) {
+    if (!as || !b || !ids) return fail(QWM_ERR_ARG, "mul_mat_id: NULL tensor");
+    if (as->type != T_Q4_K && as->type != T_Q8_0) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: weights must be Q4_K or Q8_0");
+    if (b->type != T_F32 || ids->type != T_I32) return fail(QWM_ERR_ARG, "mul_mat_id: b must be f32 and ids i32");
+    // ggml.c:3418-3428
+    if (as->ne[3] != 1 || b->ne[3] != 1 || ids->ne[2] != 1 || ids->ne[3] != 1)
+        return fail(QWM_ERR_ARG, "mul_mat_id: as/b must be 3-d and ids 2-d");
+    if (ids->ne[1] != b->ne[2]) return fail(QWM_ERR_ARG, "mul_mat_id: ids->ne[1] != b->ne[2]");
+    if (as->ne[0] != b->ne[0]) return fail(QWM_ERR_ARG, "mul_mat_id: as->ne[0] != b->ne[0]");
+    if (b->ne[1] < 1 || ids->ne[0] % b->ne[1]) return fail(QWM_ERR_ARG, "mul_mat_id: ids->ne[0] % b->ne[1] != 0");
+    if (!fully_contiguous(as)) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: as must be contiguous");
+    if (b->nb[0] != 4 || ids->nb[0] != 4) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: b/ids must have unit element stride");
+    if ((b->nb[1] | b->nb[2]) % 16) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: b rows must be 16-byte aligned");
+    if (b->ne[2] > MAX_T) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: more than 8 columns (prefill) is not handled here");
+    if (ids->ne[0] * ids->ne[1] > MAX_PAIRS) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: too many (expert, column) pairs");
+    if (as->type == T_Q4_K && as->ne[0] > 2048) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: K > 2048");
+    if (dst) {
+        if (dst->type != T_F32 || dst->ne[0] != as->ne[1] || dst->ne[1] != ids->ne[0] || dst->ne[2] != b->ne[2])
+            return fail(QWM_ERR_ARG, "mul_mat_id: dst must be f32 [N, n_ids, T]");
+        if (dst->nb[0] != 4) return fail(QWM_ERR_ARG, "mul_mat_id: dst must not be transposed");
+    }
+    return QWM_OK;
+}
+
+size_t qwm_mul_mat_id_workspace_size(const qwm_tensor * as, const qwm_tensor * b, const qwm_tensor * ids) {
+    if (check_mmid(as, b, ids, nullptr) != QWM_OK) return 0;
+    return mmid_workspace(as->ne[0], b->ne[2], b->ne[1], ids->ne[0]);
+}
+
+int qwm_mul_mat_id(const qwm_tensor * as, const qwm_tensor * b, const qwm_tensor * ids, qwm_tensor * dst,
+                   void * workspace, size_t ws_bytes, void * stream) {
+    int rc = check_mmid(as, b, ids, dst);
+    if (rc != QWM_OK) return rc;
+    if (!dst) return fail(QWM_ERR_ARG, "mul_mat_id: dst is NULL");
+    const size_t need = mmid_workspace(as->ne[0], b->ne[2], b->ne[1], ids->ne[0]);
+    if (!workspace || ws_bytes < need) return fail(QWM_ERR_WORKSPACE, "mul_mat_id: workspace too small");
+    MmidArgs a;
+    a.wtype = as->type; a.as = (const uint8_t *)as->data; a.slab = as->nb[2];
+    a.K = as->ne[0]; a.N = as->ne[1]; a.n_as = as->ne[2];
+    a.b = (const float *)b->data; a.ne11 = b->ne[1]; a.T = b->ne[2];
+    a.ids = (const int32_t *)ids->data; a.n_ids = ids->ne[0];
+    a.b_nb1 = b->nb[1]; a.b_nb2 = b->nb[2]; a.ids_nb1 = ids->nb[1];
+    a.dst_nb1 = dst->nb[1]; a.dst_nb2 = dst->nb[2];
+    a.dst = (float *)dst->data;
+    return launch_mmid(a, (uint8_t *)workspace, (hipStream_t)stream);
+}
+
+// ------------------------------------------------------------- MoE block --
+
+static int check_layer(const qwm_moe_layer * L, int64_t T, MoePlan & p) {
+    if (!L) return fail(QWM_ERR_ARG, "moe: layer is NULL");
+    std::string why;
+    if (L->router.type != T_F32 || !contiguous_rows(&L->router)) return fail(QWM_ERR_UNSUPPORTED, "moe: router must be contiguous f32 [H, E]");
+    const qwm_tensor * pools[3] = {&L->gate_pool, &L->up_pool, &L->down_pool};
+    for (const qwm_tensor * t : pools) {
+        if (t->type != T_Q4_K && t->type != T_Q8_0) return fail(QWM_ERR_UNSUPPORTED, "moe: pools must be Q4_K or Q8_0");
+        if (t->type != L->gate_pool.type) return fail(QWM_ERR_UNSUPPORTED, "moe: mixed pool types");
+        if (!fully_contiguous(t)) return fail(QWM_ERR_UNSUPPORTED, "moe: pools must be contiguous");
+    }
+    if (L->gate_pool.ne[0] != L->router.ne[0] || L->up_pool.ne[0] != L->router.ne[0] ||
+        L->up_pool.ne[1] != L->gate_pool.ne[1] || L->down_pool.ne[0] != L->gate_pool.ne[1] ||
+        L->down_pool.ne[1] != L->router.ne[0])
+        return fail(QWM_ERR_ARG, "moe: pool shapes disagree (gate/up [H, N, S], down [N, H, S])");
+    if (L->sh_gate.data) {
+        if (!L->sh_up.data || !L->sh_down.data) return fail(QWM_ERR_ARG, "moe: shared expert needs gate, up and down");
+        if (L->sh_gate.type != L->gate_pool.type || L->sh_up.type != L->gate_pool.type || L->sh_down.type != L->gate_pool.type)
+            return fail(QWM_ERR_UNSUPPORTED, "moe: shared expert type must match the pools");
+        if (L->sh_gate.ne[0] != L->router.ne[0] || L->sh_up.ne[1] != L->sh_gate.ne[1] || L->sh_down.ne[0] != L->sh_gate.ne[1] ||
+            L->sh_down.ne[1] != L->router.ne[0])
+            return fail(QWM_ERR_ARG, "moe: shared expert shapes disagree");
+        if (L->sh_gate_inp.data && (L->sh_gate_inp.type != T_F32 || L->sh_gate_inp.ne[0] != L->router.ne[0]))
+            return fail(QWM_ERR_ARG, "moe: shared gate row must be f32 [H]");
+    }
+    if (!moe_plan(L, T, p, why)) return fail(QWM_ERR_UNSUPPORTED, "moe: " + why);
+    return QWM_OK;
+}
+
+static int check_act(const qwm_tensor * x, int64_t H, const char * what) {
+    if (!x || !x->data) return fail(QWM_ERR_ARG, std::string("moe: ") + what + " is NULL");
+    if (x->type != T_F32 || x->ne[0] != H || !fully_contiguous(x)) return fail(QWM_ERR_ARG, std::string("moe: ") + what + " must be contiguous f32 [H, T]");
+    return QWM_OK;
+}
+
+size_t qwm_moe_workspace_size(const qwm_moe_layer * layer, int64_t T) {
+    MoePlan p;
+    if (check_layer(layer, T, p) != QWM_OK) return 0;
+    return p.total;
+}
+
+static int do_route(const qwm_moe_layer * L, const MoePlan & p, const qwm_tensor * x, const qwm_tensor * rm,
+                    const int32_t * tables, int64_t stride, int32_t layer_index, int32_t * ids_out, int64_t ids_ld,
+                    float * w_out, int64_t w_ld, uint8_t * ws, hipStream_t s) {
+    RouteArgs a;
+    a.W = (const float *)L->router.data; a.x = (const float *)x->data;
+    a.rm = rm ? (const float *)rm->data : nullptr;
+    a.sh_gate_inp = (L->sh_gate.data && L->sh_gate_inp.data) ? (const float *)L->sh_gate_inp.data : nullptr;
+    a.E = p.E; a.H = p.H; a.T = p.T; a.k = p.k; a.norm = L->norm_weights; a.scale = L->weights_scale;
+    a.slot_tables = tables; a.table_stride = stride; a.layer = layer_index;
+    return launch_route(a, p, ws, ids_out, ids_ld, w_out, w_ld, s);
+}
+
+int qwm_moe_route(const qwm_moe_layer * layer, const qwm_tensor * x, const qwm_tensor * rm,
+                  qwm_tensor * ids_out, qwm_tensor * w_out, void * workspace, size_t ws_bytes, void * stream) {
+    if (!x) return fail(QWM_ERR_ARG, "moe_route: x is NULL");
+    MoePlan p;
+    int rc = check_layer(layer, x->ne[1], p);
+    if (rc != QWM_OK) return rc;
+    if ((rc = check_act(x, p.H, "x")) != QWM_OK) return rc;
+    if (rm && (rm->type != T_F32 || rm->ne[0] != p.E || rm->ne[1] != p.T || !fully_contiguous(rm)))
+        return fail(QWM_ERR_ARG, "moe_route: rm must be contiguous f32 [E, T]");
+    if (ids_out && (ids_out->type != T_I32 || ids_out->ne[0] != p.k || ids_out->ne[1] != p.T || ids_out->nb[0] != 4))
+        return fail(QWM_ERR_ARG, "moe_route: ids_out must be i32 [k, T]");
+    if (w_out && (w_out->type != T_F32 || w_out->ne[0] != p.k || w_out->ne[1] != p.T || w_out->nb[0] != 4))
+        return fail(QWM_ERR_ARG, "moe_route: w_out must be f32 [k, T]");
+    if (!workspace || ws_bytes < p.total) return fail(QWM_ERR_WORKSPACE, "moe_route: workspace too small");
+    return do_route(layer, p, x, rm, nullptr, 0, 0, ids_out ? (int32_t *)ids_out->data : nullptr,
+                    ids_out ? (int64_t)(ids_out->nb[1] / 4) : 0, w_out ? (float *)w_out->data : nullptr,
+                    w_out ? (int64_t)(w_out->nb[1] / 4) : 0, (uint8_t *)workspace, (hipStream_t)stream);
+}
+
+static int do_experts(const qwm_moe_layer * L, const MoePlan & p, const int32_t * sg, const int32_t * su,
+                      const int32_t * sd, const float * w, const float * resid, float * out, uint8_t * ws, hipStream_t s) {
+    ExpertArgs a;
+    a.wtype = L->gate_pool.type;
+    a.gate = (const uint8_t *)L->gate_pool.data; a.up = (const uint8_t *)L->up_pool.data;
+    a.down = (const uint8_t *)L->down_pool.data;
+    a.gate_slab = L->gate_pool.nb[2]; a.up_slab = L->up_pool.nb[2]; a.down_slab = L->down_pool.nb[2];
+    a.sh_gate = (const uint8_t *)L->sh_gate.data; a.sh_up = (const uint8_t *)L->sh_up.data;
+    a.sh_down = (const uint8_t *)L->sh_down.data;
+    a.slot_g = sg; a.slot_u = su; a.slot_d = sd;
+    a.weights = w; a.resid = resid; a.out = out;
+    return launch_experts(a, p, ws, s);
+}
+
+int qwm_moe_experts(const qwm_moe_layer * layer, const qwm_tensor * x, const qwm_tensor * slot_g,
+                    const qwm_tensor * slot_u, const qwm_tensor * slot_d, const qwm_tensor * weights,
+                    const qwm_tensor * resid, qwm_tensor * out, void * workspace, size_t ws_bytes, void * stream) {
+    if (!x) return fail(QWM_ERR_ARG, "moe_experts: x is NULL");
+    MoePlan p;
+    int rc = check_layer(layer, x->ne[1], p);
+    if (rc != QWM_OK) return rc;
+    if ((rc = check_act(x, p.H, "x")) != QWM_OK) return rc;
+    if ((rc = check_act(out, p.H, "out")) != QWM_OK) return rc;
+    if (out->ne[1] != p.T) return fail(QWM_ERR_ARG, "moe_experts: out must be [H, T]");
+    if (resid && ((rc = check_act(resid, p.H, "resid")) != QWM_OK || resid->ne[1] != p.T))
+        return rc != QWM_OK ? rc : fail(QWM_ERR_ARG, "moe_experts: resid must be [H, T]");
+    const qwm_tensor * slots[3] = {slot_g, slot_u, slot_d};
+    for (const qwm_tensor * sl : slots)
+        if (!sl || sl->type != T_I32 || sl->ne[0] != p.k || sl->ne[1] != p.T || !fully_contiguous(sl))
+            return fail(QWM_ERR_ARG, "moe_experts: slot ids must be contiguous i32 [k, T]");
+    if (!weights || weights->type != T_F32 || weights->ne[0] != p.k || weights->ne[1] != p.T || !fully_contiguous(weights))
+        return fail(QWM_ERR_ARG, "moe_experts: weights must be contiguous f32 [k, T]");
+    if (!workspace || ws_bytes < p.total) return fail(QWM_ERR_WORKSPACE, "moe_experts: workspace too small");
+    return do_experts(layer, p, (const int32_t *)slot_g->data, (const int32_t *)slot_u->data,
+                      (const int32_t *)slot_d->data, (const float *)weights->data,
+                      resid ? (const float *)resid->data : nullptr, (float *)out->data, (uint8_t *)workspace,
+                      (hipStream_t)stream);
+}
+
+int qwm_moe_block_resident(const qwm_moe_layer * layer, int32_t layer_index, const int32_t * slot_tables,
+                           int64_t table_stride, const qwm_tensor * x, const qwm_tensor * rm,
+                           const qwm_tensor * resid, qwm_tensor * out, qwm_tensor * ids_out, qwm_tensor * w_out,
+                           void * workspace, size_t ws_bytes, void * stream) {
+    if (!x) return fail(QWM_ERR_ARG, "moe_block: x is NULL");
+    if (!slot_tables) return fail(QWM_ERR_ARG, "moe_block: slot tables are NULL");
+    MoePlan p;
+    int rc = check_layer(layer, x->ne[1], p);
+    if (rc != QWM_OK) return rc;
+    if ((rc = check_act(x, p.H, "x")) != QWM_OK) return rc;
+    if ((rc = check_act(out, p.H, "out")) != QWM_OK) return rc;
+    if (resid && ((rc = check_act(resid, p.H, "resid")) != QWM_OK)) return rc;
+    if (rm && (rm->type != T_F32 || rm->ne[0] != p.E || rm->ne[1] != p.T || !fully_contiguous(rm)))
+        return fail(QWM_ERR_ARG, "moe_block: rm must be contiguous f32 [E, T]");
+    if (table_stride < (int64_t)(layer_index + 1) * p.E) return fail(QWM_ERR_ARG, "moe_block: slot table stride too small");
+    if (!workspace || ws_bytes < p.total) return fail(QWM_ERR_WORKSPACE, "moe_block: workspace too small");
+    uint8_t * ws = (uint8_t *)workspace;
+    hipStream_t s = (hipStream_t)stream;
+    rc = do_route(layer, p, x, rm, slot_tables, table_stride, layer_index,
+                  ids_out ? (int32_t *)ids_out->data : nullptr, ids_out ? (int64_t)(ids_out->nb[1] / 4) : 0,
+                  w_out ? (float *)w_out->data : nullptr, w_out ? (int64_t)(w_out->nb[1] / 4) : 0, ws, s);
+    if (rc != QWM_OK) return rc;
+    const int64_t P = p.T * p.k;
+    const int32_t * slots = (const int32_t *)(ws + p.slots);
+    return do_experts(layer, p, slots, slots + P, slots + 2 * P, (const float *)(ws + p.w),
+                      resid ? (const float *)resid->data : nullptr, (float *)out->data, ws, s);
+}
+
+// ------------------------------------------------------------------ verify --
+
+size_t qwm_verify_workspace_size(const qwm_tensor * lm_head, int64_t T) {
+    VerifyPlan p;
+    std::string why;
+    if (!lm_head || !verify_plan(lm_head, T, p, why)) return 0;
+    return p.total;
+}
+
+int qwm_verify_accept(const qwm_tensor * lm_head, const qwm_tensor * x, const float * norm_w, float eps,
+                      const int32_t * drafts, int32_t * result, void * workspace, size_t ws_bytes, void * stream) {
+    if (!lm_head || !x || !result) return fail(QWM_ERR_ARG, "verify: NULL argument");
+    VerifyPlan p;
+    std::string why;
+    if (!verify_plan(lm_head, x->ne[1], p, why)) return fail(QWM_ERR_UNSUPPORTED, "verify: " + why);
+    if (!contiguous_rows(lm_head)) return fail(QWM_ERR_UNSUPPORTED, "verify: lm_head rows must be contiguous");
+    if (x->type != T_F32 || x->ne[0] != p.H || !fully_contiguous(x)) return fail(QWM_ERR_ARG, "verify: x must be contiguous f32 [H, T]");
+    if (p.T > 1 && !drafts) return fail(QWM_ERR_ARG, "verify: drafts are NULL");
+    if (!workspace || ws_bytes < p.total) return fail(QWM_ERR_WORKSPACE, "verify: workspace too small");
+    return launch_verify((const uint8_t *)lm_head->data, (const float *)x->data, norm_w, eps, drafts, result, p,
+                         (uint8_t *)workspace, (hipStream_t)stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,123 @@
+// qwm_device.h -- device-side building blocks for the gfx950 MoE expert path:
+// ggml block layouts, the CPU backend's exact scalar conventions (fp16
+// rounding, the magic-number nearest_int, the AVX-512 expf polynomial) and
+// wave64 reductions.  Every kernel source includes this header; all of them
+// are compiled with -ffp-contract=off, so a fused multiply-add appears only
+// where it is written (__builtin_fmaf), exactly where ggml-CPU fuses.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#define QWM_DEV __device__ __forceinline__
+
+namespace qwm {
+
+constexpr int QK_K = 256;
+constexpr int QK8_0 = 32;
+constexpr int WAVE = 64;
+
+// ggml-common.h:325-338 (144 B) and 251-256 (34 B).
+struct block_q4_K { uint16_t d, dmin; uint8_t scales[12]; uint8_t qs[QK_K / 2]; };
+struct block_q8_0 { uint16_t d; int8_t qs[QK8_0]; };
+static_assert(sizeof(block_q4_K) == 144, "block_q4_K");
+static_assert(sizeof(block_q8_0) == 34, "block_q8_0");
+
+// ---------------------------------------------------------------- scalars --
+
+QWM_DEV float fp16_to_f32(uint16_t h) { return __half2float(__ushort_as_half(h)); }
+QWM_DEV uint16_t f32_to_fp16(float f) { return __half_as_ushort(__float2half_rn(f)); }
+
+// nearest_int(a*b) of ggml-quants.c:621-626 as gcc -O3 emits it on x86-64
+// with FMA: the product and the 1.5*2^23 magic add fuse into one fma.
+QWM_DEV int nearest_int_mul(float a, float b) {
+    const float v = __builtin_fmaf(a, b, 12582912.f);
+    return (int)(__float_as_uint(v) & 0x007fffffu) - 0x00400000;
+}
+
+// ggml_v_expf (ggml-cpu/vec.h:1191-1216, AVX-512 lane): 2^n * poly(b).
+QWM_DEV float v_expf(float x) {
+    const float r = 0x1.8p23f;
+    const float z = __builtin_fmaf(x, 0x1.715476p+0f, r);
+    const float n = z - r;
+    const float b = __builtin_fmaf(-n, 0x1.7f7d1cp-20f, __builtin_fmaf(-n, 0x1.62e4p-1f, x));
+    const float u = b * b;
+    const float j = __builtin_fmaf(
+        __builtin_fmaf(__builtin_fmaf(0x1.0e4020p-7f, b, 0x1.573e2ep-5f), u,
+                       __builtin_fmaf(0x1.555e66p-3f, b, 0x1.fffdb6p-2f)),
+        u, __builtin_fmaf(0x1.ffffecp-1f, b, 1.0f));
+    if (__builtin_fabsf(n) > 192.0f) return n <= 0.0f ? 0.0f : __builtin_inff();
+    return __builtin_ldexpf(j, (int)n);
+}
+
+// ggml_v_silu (ggml-cpu/vec.h:1219-1226)
+QWM_DEV float v_silu(float x) { return x / (1.0f + v_expf(0.0f - x)); }
+
+// Q4_K 6-bit scale/min of sub-block j (ggml-quants.c:871-878).
+QWM_DEV void q4k_scale_min(int j, const uint8_t * q, int & d, int & m) {
+    if (j < 4) { d = q[j] & 63; m = q[j + 4] & 63; }
+    else {
+        d = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+        m = (q[j + 4] >> 4) | ((q[j - 0] >> 6) << 4);
+    }
+}
+// Same, from the three scale dwords held in registers (bytes 4..15 of the
+// block header): s0 = scales[0..3], s1 = scales[4..7], s2 = scales[8..11].
+QWM_DEV void q4k_scale_min_reg(int j, uint32_t s0, uint32_t s1, uint32_t s2, int & d, int & m) {
+    const int b = (j & 3) * 8;
+    if (j < 4) {
+        d = (s0 >> b) & 63;
+        m = (s1 >> b) & 63;
+    } else {
+        const uint32_t q8 = (s2 >> b) & 0xff;          // scales[j+4]
+        d = (q8 & 0xF) | (((s0 >> b) >> 6 & 3) << 4);   // scales[j-4] >> 6
+        m = (q8 >> 4) | (((s1 >> b) >> 6 & 3) << 4);    // scales[j] >> 6
+    }
+}
+
+QWM_DEV int dot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
+
+// --------------------------------------------------------- wave reductions --
+
+template <int WIDTH>
+QWM_DEV float group_sum(float v) {
+#pragma unroll
+    for (int o = WIDTH / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+    return v;
+}
+template <int WIDTH>
+QWM_DEV int group_sum_i(int v) {
+#pragma unroll
+    for (int o = WIDTH / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+    return v;
+}
+template <int WIDTH>
+QWM_DEV float group_max(float v) {
+#pragma unroll
+    for (int o = WIDTH / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
+    return v;
+}
+
+// The 16-lane halving tree of _mm512_reduce_add_ps (gcc: lanes i+8, i+4, i+2,
+// i+1).  An xor butterfly produces the same sums in every lane of the group.
+QWM_DEV float tree16(float v) {
+    v += __shfl_xor(v, 8, WAVE);
+    v += __shfl_xor(v, 4, WAVE);
+    v += __shfl_xor(v, 2, WAVE);
+    v += __shfl_xor(v, 1, WAVE);
+    return v;
+}
+
+// Argmax over a wave where ties take the larger index (ggml-cpu/vec.h:1618-1626
+// keeps the last maximum); NaN never wins.
+QWM_DEV void wave_argmax_last(float & v, int & idx) {
+#pragma unroll
+    for (int o = WAVE / 2; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(v, o, WAVE);
+        const int oi = __shfl_xor(idx, o, WAVE);
+        if (ov > v || (ov == v && oi > idx)) { v = ov; idx = oi; }
+    }
+}
+
+}  // namespace qwm

@@ -1,0 +1,97 @@
+// qwm_internal.h -- host-side declarations shared by the libqwmoe sources:
+// workspace plans and the kernel launchers each .hip file provides.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+#include <stddef.h>
+#include <stdint.h>
+#include <string>
+
+#include "../../include/qwmoe.h"
+
+namespace qwm {
+
+// ggml_type values (ggml.h:390-420)
+enum : int32_t { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_Q4_K = 12, T_Q8_K = 15, T_I32 = 26 };
+
+void set_error(const std::string & msg);
+int fail(int code, const std::string & msg);
+#define QWM_HIP_CHECK(expr)                                                              \
+    do {                                                                                 \
+        hipError_t e_ = (expr);                                                          \
+        if (e_ != hipSuccess) return ::qwm::fail(QWM_ERR_HIP, std::string(#expr ": ") + \
+                                                 hipGetErrorString(e_));                 \
+    } while (0)
+
+constexpr int MAX_T = 8;        // tokens per GEMV batch (decode / verify)
+constexpr int MAX_K = 16;       // experts per token
+constexpr int MAX_E = 2048;     // experts per layer
+constexpr int MAX_PAIRS = MAX_T * MAX_K;
+
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// One expert of the layer's batch union and the (token, slot) pairs that
+// routed to it, in token-major order (pair = t * k + j).
+struct Unit {
+    int32_t expert;     // expert id; -1 for the shared expert
+    int32_t n;          // number of pairs
+    int32_t pair[MAX_T];
+};
+
+// Byte offsets into the caller's workspace for one MoE layer call.
+struct MoePlan {
+    int64_t H, N, N_sh, E, k, T;
+    bool shared, shared_gate;
+    size_t counters, logits, ids, w, slots, sh_gate, units, n_units;
+    size_t xq_qs, xq_d, xq_bs, act, act_sh, ex, ex_sh;
+    size_t total;
+};
+bool moe_plan(const qwm_moe_layer * L, int64_t T, MoePlan & p, std::string & why);
+
+struct VerifyPlan {
+    int64_t H, V, T;
+    int n_wg;
+    size_t counters, hq, partial_v, partial_i;
+    size_t total;
+};
+bool verify_plan(const qwm_tensor * lm_head, int64_t T, VerifyPlan & p, std::string & why);
+
+// ---- launchers (qwm_moe.hip) ----
+struct RouteArgs {
+    const float * W; const float * x; const float * rm;   // router [E][H], x [T][H], rm [T][E] or null
+    const float * sh_gate_inp;                           // [H] or null
+    int64_t E, H, T, k; int norm; float scale;
+    const int32_t * slot_tables; int64_t table_stride; int32_t layer;  // resident remap or null
+};
+int launch_route(const RouteArgs & a, const MoePlan & p, uint8_t * ws, int32_t * ids_out, int64_t ids_ld,
+                 float * w_out, int64_t w_ld, hipStream_t s);
+
+struct ExpertArgs {
+    int32_t wtype;
+    const uint8_t * gate; const uint8_t * up; const uint8_t * down;   // pool bases
+    size_t gate_slab, up_slab, down_slab;                             // bytes per slot
+    const uint8_t * sh_gate; const uint8_t * sh_up; const uint8_t * sh_down;
+    const int32_t * slot_g; const int32_t * slot_u; const int32_t * slot_d;  // [T][k]
+    const float * weights;  // [T][k]
+    const float * resid;    // [T][H] or null
+    float * out;            // [T][H]
+};
+int launch_experts(const ExpertArgs & a, const MoePlan & p, uint8_t * ws, hipStream_t s);
+
+// generic GGML_OP_MUL_MAT_ID (qwm_moe.hip)
+struct MmidArgs {
+    int32_t wtype; const uint8_t * as; size_t slab; int64_t K, N, n_as;
+    const float * b; int64_t ne11, T; const int32_t * ids; int64_t n_ids;
+    size_t b_nb1, b_nb2, ids_nb1, dst_nb1, dst_nb2;
+    float * dst;
+};
+size_t mmid_workspace(int64_t K, int64_t T, int64_t ne11, int64_t n_ids);
+int launch_mmid(const MmidArgs & a, uint8_t * ws, hipStream_t s);
+
+// ---- launchers (qwm_verify.hip) ----
+int launch_verify(const uint8_t * lm_head, const float * x, const float * norm_w, float eps,
+                  const int32_t * drafts, int32_t * result, const VerifyPlan & p, uint8_t * ws, hipStream_t s);
+
+int launch_fill_zero(void * p, size_t bytes, hipStream_t s);
+
+}  // namespace qwm

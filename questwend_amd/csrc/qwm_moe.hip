@@ -1,0 +1,894 @@
+// qwm_moe.hip -- the MoE FFN block on gfx950: router GEMV + softmax + top-k,
+// Q8_K activation quantization, the expert-union schedule, the Q4_K
+// gate/up GEMV with fused SwiGLU, the down GEMV, and the ordered combine.
+//
+// Layout of one GEMV wave: a weight row is split into 16-byte chunks of the
+// Q4_K super-blocks' quant bytes (8 chunks per 144-byte block); LPR lanes
+// cover one row (one chunk each, CPL chunks if K > 2048), so a wave streams
+// 64/LPR rows per step with coalesced 128-bit loads, plus a 16-byte load of
+// each block header (d, dmin, 12 scale bytes) shared by its 8 lanes.  The
+// lane keeps the matching Q8_K activation bytes of every token of the unit
+// in registers for the whole row loop.  Integer block sums are exact
+// (v_dot4_i32_i8), so the result differs from ggml-CPU only by the order of
+// the fp32 sums across blocks.
+#include "qwm_device.h"
+#include "qwm_internal.h"
+
+namespace qwm {
+
+// ======================================================================
+// Router
+// ======================================================================
+
+// logits[t][e] = router[e] . x[t] (+ rm[t][e]).  One wave per row.
+//   T == 1 (or a row count that is not a multiple of 4): ggml_vec_dot_f32's
+//     AVX-512 order (ggml-cpu/vec.cpp:11-135): lane L = 16*j + l accumulates
+//     fma over 64-wide steps, then (j0+j2, j1+j3, 0+1) and the 16-lane tree.
+//   T >= 2: llamafile tinyBLAS<16, __m512> order (sgemm.cpp:600-670): one
+//     16-lane fma accumulator over 16-wide steps, then the 16-lane tree.
+// Row E (when sh_gate_inp is set) is the shared-expert gate: a single-row
+// mul_mat, which ggml-CPU always runs through vec_dot_f32.
+__global__ void __launch_bounds__(256) k_route_logits(const float * __restrict__ W, const float * __restrict__ x,
+                                                       const float * __restrict__ rm, const float * __restrict__ sgi,
+                                                       float * __restrict__ logits, float * __restrict__ sh_logit,
+                                                       int E, int H, int T) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int e = blockIdx.x * 4 + wave;
+    if (e > E || (e == E && !sgi)) return;
+    const float * w = (e < E) ? W + (size_t)e * H : sgi;
+    const bool tiny = (e < E) && T >= 2 && (E % 4) == 0;
+    if (!tiny) {
+        const int np = H & ~63;
+        for (int t = 0; t < T; ++t) {
+            const float * xt = x + (size_t)t * H;
+            float acc = 0.f;
+#pragma unroll 8
+            for (int i = 0; i < np; i += 64) acc = __builtin_fmaf(w[i + lane], xt[i + lane], acc);
+            acc += __shfl_xor(acc, 32, WAVE);
+            acc += __shfl_xor(acc, 16, WAVE);
+            acc = tree16(acc);
+            if (lane == 0) {
+                // scalar tail as gcc -O3 vectorizes it: unfused 16/8-groups, then fma
+                float s = acc;
+                int i = np;
+                for (; H - i >= 16; i += 16)
+                    for (int l = 0; l < 16; ++l) s = s + w[i + l] * xt[i + l];
+                if (H - i >= 8) {
+                    for (int l = 0; l < 8; ++l) s = s + w[i + l] * xt[i + l];
+                    i += 8;
+                }
+                for (; i < H; ++i) s = __builtin_fmaf(w[i], xt[i], s);
+                if (e < E) logits[(size_t)t * E + e] = rm ? s + rm[(size_t)t * E + e] : s;
+                else sh_logit[t] = s;
+            }
+        }
+    } else {
+        const int l = lane & 15, tg = lane >> 4;
+        for (int t0 = 0; t0 < T; t0 += 4) {
+            const int t = t0 + tg;
+            float acc = 0.f;
+            if (t < T) {
+                const float * xt = x + (size_t)t * H;
+                int i = 0;
+#pragma unroll 8
+                for (; i + 16 <= H; i += 16) acc = __builtin_fmaf(w[i + l], xt[i + l], acc);
+                if (i + l < H) acc = __builtin_fmaf(w[i + l], xt[i + l], acc);
+            }
+            acc = tree16(acc);
+            if (l == 0 && t < T) logits[(size_t)t * E + e] = rm ? acc + rm[(size_t)t * E + e] : acc;
+        }
+    }
+}
+
+// Q8_K quantization of one 256-value block by one wave (ggml-quants.c:2769-2806):
+// lane L owns values 4L..4L+3.  max = the signed value of the first largest
+// |x|; iscale = -127/max; q = min(127, nearest_int(iscale*x)); bsums per 16;
+// d = 1/iscale.  Writes qs (256 B), d, and the 16 bsums (as int32).
+QWM_DEV void quantize_block_q8K(const float * __restrict__ src, int8_t * __restrict__ qs, float * __restrict__ d_out,
+                                int32_t * __restrict__ bs_out, int lane) {
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = src[4 * lane + i];
+    float a = __builtin_fabsf(v[0]);
+    int ii = 0;
+#pragma unroll
+    for (int i = 1; i < 4; ++i)
+        if (__builtin_fabsf(v[i]) > a) { a = __builtin_fabsf(v[i]); ii = i; }
+    int idx = 4 * lane + ii;
+    float mx = v[ii];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float oa = __shfl_xor(a, o, WAVE);
+        const int oi = __shfl_xor(idx, o, WAVE);
+        const float om = __shfl_xor(mx, o, WAVE);
+        if (oa > a || (oa == a && oi < idx)) { a = oa; idx = oi; mx = om; }
+    }
+    int q[4] = {0, 0, 0, 0};
+    float d = 0.f;
+    if (a != 0.f) {
+        const float iscale = -127.f / mx;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) q[i] = min(127, nearest_int_mul(iscale, v[i]));
+        d = 1.f / iscale;
+    }
+    const uint32_t packed = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) |
+                            ((uint32_t)(q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24);
+    reinterpret_cast<uint32_t *>(qs)[lane] = packed;
+    int s = q[0] + q[1] + q[2] + q[3];
+    s += __shfl_xor(s, 1, WAVE);
+    s += __shfl_xor(s, 2, WAVE);
+    if ((lane & 3) == 0) bs_out[lane >> 2] = s;
+    if (lane == 0) *d_out = d;
+}
+
+struct SelectArgs {
+    const float * logits; const float * sh_logit; const float * x;
+    int E, H, T, k, norm; float scale;
+    int32_t * ids_ws; float * w_ws;                  // [T][k]
+    int32_t * ids_out; int64_t ids_ld; float * w_out; int64_t w_ld;  // optional user copies
+    float * sh_gate;                                 // [T] or null
+    int8_t * xq_qs; float * xq_d; int32_t * xq_bs;   // Q8_K of x
+    Unit * units; int32_t * n_units; int32_t * counter;
+    int shared;                                      // append the shared-expert unit
+    const int32_t * slot_tables; int64_t table_stride; int layer; int32_t * slots_ws;  // [3][T*k]
+};
+
+// One wave per token: soft_max (ggml-cpu/ops.cpp:5813-5920, vec.cpp:531 AVX-512:
+// v_expf over 16-lane chunks, each chunk summed with the 16-lane tree into a
+// double), top-k by probability (ties: lower expert index), weight gather,
+// normalization (double sum, clamp 6.103515625e-5, division) and scale; then
+// the token's Q8_K activations.  The last block to finish builds the union of
+// experts (first-occurrence order) and, in resident mode, the slot ids.
+__global__ void __launch_bounds__(64) k_route_select(SelectArgs a) {
+    __shared__ float probs[MAX_E];
+    __shared__ int32_t sel[MAX_K];
+    __shared__ int last;
+    const int t = blockIdx.x, lane = threadIdx.x;
+    const int E = a.E, k = a.k;
+    const float * lt = a.logits + (size_t)t * E;
+
+    float m = -__builtin_inff();
+    for (int i = lane; i < E; i += 64) m = fmaxf(m, lt[i]);
+    m = group_max<64>(m);
+    double sum = 0.0;
+    const int nfull = E & ~15;
+    for (int c = 0; c < nfull; c += 64) {
+        const int i = c + lane;
+        float v = 0.f;
+        if (i < nfull) { v = v_expf(lt[i] - m); probs[i] = v; }
+        const float cs = tree16(v);
+        for (int g = 0; g < 4; ++g)
+            if (c + 16 * g < nfull) sum += (double)__shfl(cs, 16 * g, WAVE);
+    }
+    for (int i = nfull; i < E; ++i) {           // scalar tail (libm expf on the CPU)
+        const float v = expf(lt[i] - m);
+        sum += (double)v;
+        if (lane == 0) probs[i] = v;
+    }
+    const float sc = (float)(1.0 / sum);
+    __syncthreads();
+    for (int i = lane; i < E; i += 64) probs[i] = probs[i] * sc;
+    __syncthreads();
+
+    // top-k: k rounds of a wave argmax (larger probability, then lower index)
+    uint32_t taken = 0;
+    for (int j = 0; j < k; ++j) {
+        float bv = -__builtin_inff();
+        int bi = 0x7fffffff;
+        int slot = 0;
+        for (int i = lane; i < E; i += 64, ++slot) {
+            if (taken & (1u << slot)) continue;
+            const float p = probs[i];
+            if (p > bv || (p == bv && i < bi)) { bv = p; bi = i; }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(bv, o, WAVE);
+            const int oi = __shfl_xor(bi, o, WAVE);
+            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        }
+        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+        if (lane == 0) sel[j] = bi;
+    }
+    __syncthreads();
+    if (lane == 0) {
+        float w[MAX_K];
+        for (int j = 0; j < k; ++j) w[j] = probs[sel[j]];
+        if (a.norm) {
+            double s = 0.0;
+            for (int j = 0; j < k; ++j) s += (double)w[j];
+            float ws = (float)s;
+            ws = fmaxf(fminf(ws, __builtin_inff()), 6.103515625e-5f);
+            for (int j = 0; j < k; ++j) w[j] = w[j] / ws;
+        }
+        if (a.scale != 0.0f && a.scale != 1.0f)
+            for (int j = 0; j < k; ++j) w[j] = w[j] * a.scale;
+        for (int j = 0; j < k; ++j) {
+            a.ids_ws[t * k + j] = sel[j];
+            a.w_ws[t * k + j] = w[j];
+            if (a.ids_out) a.ids_out[(size_t)t * a.ids_ld + j] = sel[j];
+            if (a.w_out) a.w_out[(size_t)t * a.w_ld + j] = w[j];
+        }
+        if (a.sh_gate) a.sh_gate[t] = 1.f / (1.f + expf(-a.sh_logit[t]));   // unary-ops.cpp:31
+    }
+    // Q8_K of x[t]
+    const int nb = a.H / QK_K;
+    for (int b = 0; b < nb; ++b)
+        quantize_block_q8K(a.x + (size_t)t * a.H + b * QK_K, a.xq_qs + (size_t)t * a.H + b * QK_K,
+                           a.xq_d + (size_t)t * nb + b, a.xq_bs + (size_t)t * (a.H / 16) + b * 16, lane);
+
+    // ---- last block: expert union + slot remap ----
+    __threadfence();
+    __syncthreads();
+    if (lane == 0) last = atomicAdd(a.counter, 1) == (int)gridDim.x - 1;
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    const int P = a.T * k;
+    __shared__ int32_t first[MAX_PAIRS], uidx[MAX_PAIRS];
+    volatile const int32_t * ids = a.ids_ws;
+    for (int p = lane; p < P; p += 64) {
+        const int e = ids[p];
+        int f = p;
+        for (int q = 0; q < p; ++q)
+            if (ids[q] == e) { f = q; break; }
+        first[p] = f;
+    }
+    __syncthreads();
+    int base = 0;
+    for (int c = 0; c < P; c += 64) {
+        const int p = c + lane;
+        const bool isf = p < P && first[p] == p;
+        const unsigned long long bal = __ballot(isf);
+        const int below = __popcll(bal & ((1ull << lane) - 1ull));
+        if (isf) uidx[p] = base + below;
+        base += __popcll(bal);
+    }
+    __syncthreads();
+    const int nu = base;
+    for (int p = lane; p < P; p += 64) {
+        const int f = first[p];
+        int pos = 0;
+        for (int q = 0; q < p; ++q) pos += first[q] == f;
+        Unit & u = a.units[uidx[f]];
+        u.pair[pos] = p;
+        if (p == f) u.expert = ids[p];
+        int cnt = 0;
+        for (int q = f; q < P; ++q) cnt += first[q] == f;
+        if (p == f) u.n = cnt;
+        if (a.slot_tables) {
+            const int e = ids[p];
+            for (int r = 0; r < 3; ++r)
+                a.slots_ws[r * P + p] = a.slot_tables[(size_t)r * a.table_stride + (size_t)a.layer * E + e];
+        }
+    }
+    if (a.shared && lane == 0) {
+        Unit & u = a.units[nu];
+        u.expert = -1;
+        u.n = a.T;
+        for (int i = 0; i < a.T; ++i) u.pair[i] = i;
+    }
+    if (lane == 0) {
+        *a.n_units = nu;
+        *a.counter = 0;
+    }
+}
+
+// ======================================================================
+// Q4_K x Q8_K GEMV machinery
+// ======================================================================
+
+// Activation bytes of one token for one 16-byte quant chunk (sub-blocks 2j
+// and 2j+1 of super-block sb, half h): 16 q8 values for the low nibbles,
+// 16 for the high nibbles, the block scale and the two 16-value bsums.
+struct ActChunk {
+    uint4 lo, hi;
+    float d;
+    int32_t bs_lo, bs_hi;
+};
+
+QWM_DEV void load_act_chunk(ActChunk & A, const int8_t * qs, const float * dd, const int32_t * bs, int c) {
+    const int sb = c >> 3, p = c & 7, j = p >> 1, h = p & 1;
+    const int8_t * q = qs + sb * QK_K + 64 * j + 16 * h;
+    A.lo = *reinterpret_cast<const uint4 *>(q);
+    A.hi = *reinterpret_cast<const uint4 *>(q + 32);
+    A.d = dd[sb];
+    A.bs_lo = bs[sb * 16 + 4 * j + h];
+    A.bs_hi = bs[sb * 16 + 4 * j + 2 + h];
+}
+
+// Weight data of one chunk: the 16 quant bytes and the block header.
+struct WChunk {
+    uint4 q, hd;
+};
+
+QWM_DEV void load_w_chunk(WChunk & W, const uint8_t * row, int c) {
+    const int sb = c >> 3, p = c & 7;
+    const uint8_t * blk = row + sb * 144;
+    W.hd = *reinterpret_cast<const uint4 *>(blk);
+    W.q = *reinterpret_cast<const uint4 *>(blk + 16 + 16 * p);
+}
+
+// Contribution of one chunk to d*sum(sc*q4*q8) - dmin*sum(m*bsum).
+QWM_DEV float chunk_dot(const WChunk & W, const ActChunk & A, int c, float acc) {
+    const int p = c & 7, j = p >> 1;
+    int sc_lo, m_lo, sc_hi, m_hi;
+    q4k_scale_min_reg(2 * j, W.hd.y, W.hd.z, W.hd.w, sc_lo, m_lo);
+    q4k_scale_min_reg(2 * j + 1, W.hd.y, W.hd.z, W.hd.w, sc_hi, m_hi);
+    const uint32_t m4 = 0x0F0F0F0Fu;
+    int s_lo = 0, s_hi = 0;
+    s_lo = dot4(W.q.x & m4, A.lo.x, s_lo);
+    s_lo = dot4(W.q.y & m4, A.lo.y, s_lo);
+    s_lo = dot4(W.q.z & m4, A.lo.z, s_lo);
+    s_lo = dot4(W.q.w & m4, A.lo.w, s_lo);
+    s_hi = dot4((W.q.x >> 4) & m4, A.hi.x, s_hi);
+    s_hi = dot4((W.q.y >> 4) & m4, A.hi.y, s_hi);
+    s_hi = dot4((W.q.z >> 4) & m4, A.hi.z, s_hi);
+    s_hi = dot4((W.q.w >> 4) & m4, A.hi.w, s_hi);
+    const int isum = sc_lo * s_lo + sc_hi * s_hi;
+    const int imin = m_lo * A.bs_lo + m_hi * A.bs_hi;
+    const float d = A.d * fp16_to_f32((uint16_t)(W.hd.x & 0xffff));
+    const float dmin = A.d * fp16_to_f32((uint16_t)(W.hd.x >> 16));
+    acc = __builtin_fmaf(d, (float)isum, acc);
+    return __builtin_fmaf(-dmin, (float)imin, acc);
+}
+
+// Wave steps per GEMV tile: each wave issues the weight loads of GEMV_STEPS
+// row steps before it computes any of them.
+constexpr int GEMV_STEPS = 4;
+
+// ---------------------------------------------------------------------
+// gate/up + SwiGLU: act[p][r] = silu(gate_e[r] . x_t) * (up_e[r] . x_t)
+// grid: (row tiles, unit slots [+1 for the shared expert]), block 256.
+// ---------------------------------------------------------------------
+struct GateUpArgs {
+    const uint8_t * gate; const uint8_t * up; size_t gate_slab, up_slab;
+    const uint8_t * sh_gate; const uint8_t * sh_up;
+    const int32_t * slot_g; const int32_t * slot_u;
+    const Unit * units; const int32_t * n_units; int unit_slots;  // routed unit grid rows
+    const int8_t * xq_qs; const float * xq_d; const int32_t * xq_bs;
+    float * act; float * act_sh;
+    int H, N, N_sh, k;
+};
+
+template <int LPR, int MAXP>
+__global__ void __launch_bounds__(256) k_gateup_q4k(GateUpArgs a) {
+    constexpr int RPI = WAVE / LPR;     // rows per wave step
+    constexpr int NIT = GEMV_STEPS;     // steps per wave; all loads issued up front
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int c = lane % LPR, rsub = lane / LPR;
+    const int u = blockIdx.y;
+    const bool shared = u == a.unit_slots;
+    if (!shared && u >= *a.n_units) return;
+    const Unit & U = a.units[shared ? *a.n_units : u];
+    const int n = U.n;
+    const int rows = shared ? a.N_sh : a.N;
+    const size_t row_bytes = (size_t)(a.H / QK_K) * 144;
+    const uint8_t * gbase;
+    const uint8_t * ubase;
+    if (shared) { gbase = a.sh_gate; ubase = a.sh_up; }
+    else {
+        gbase = a.gate + (size_t)a.slot_g[U.pair[0]] * a.gate_slab;
+        ubase = a.up + (size_t)a.slot_u[U.pair[0]] * a.up_slab;
+    }
+    const int C = a.H / 32;
+    const bool active = c < C;
+    const int r_begin = (blockIdx.x * 4 + wave) * (NIT * RPI);
+    if (r_begin >= rows) return;
+    WChunk G[NIT], Uw[NIT];
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const int r = r_begin + it * RPI + rsub;
+        if (active && r < rows) {
+            load_w_chunk(G[it], gbase + (size_t)r * row_bytes, c);
+            load_w_chunk(Uw[it], ubase + (size_t)r * row_bytes, c);
+        }
+    }
+    ActChunk A[MAXP];
+#pragma unroll
+    for (int i = 0; i < MAXP; ++i) {
+        if (i < n && active) {
+            const int tok = shared ? U.pair[i] : U.pair[i] / a.k;
+            load_act_chunk(A[i], a.xq_qs + (size_t)tok * a.H, a.xq_d + (size_t)tok * (a.H / QK_K),
+                           a.xq_bs + (size_t)tok * (a.H / 16), c);
+        }
+    }
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const int r = r_begin + it * RPI + rsub;
+        const bool valid = active && r < rows;
+        float g[MAXP], up[MAXP];
+#pragma unroll
+        for (int i = 0; i < MAXP; ++i) {
+            g[i] = 0.f; up[i] = 0.f;
+            if (i < n && valid) {
+                g[i] = chunk_dot(G[it], A[i], c, 0.f);
+                up[i] = chunk_dot(Uw[it], A[i], c, 0.f);
+            }
+            g[i] = group_sum<LPR>(g[i]);
+            up[i] = group_sum<LPR>(up[i]);
+        }
+        if (r < rows) {
+#pragma unroll
+            for (int i = 0; i < MAXP; ++i) {
+                if (i < n && c == i) {
+                    const float v = (r < rows - (rows & 15)) ? v_silu(g[i]) * up[i]
+                                                            : g[i] / (1.0f + expf(-g[i])) * up[i];
+                    if (shared) a.act_sh[(size_t)U.pair[i] * rows + r] = v;
+                    else a.act[(size_t)U.pair[i] * rows + r] = v;
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------
+// down: ex[p][h] = down_e[h] . Q8_K(act[p])
+// grid: (row tiles over H, unit slots [+1 shared]), block 256.  Each block
+// first quantizes its unit's activation rows to Q8_K in LDS.
+// ---------------------------------------------------------------------
+struct DownArgs {
+    const uint8_t * down; size_t down_slab; const uint8_t * sh_down;
+    const int32_t * slot_d;
+    const Unit * units; const int32_t * n_units; int unit_slots;
+    const float * act; const float * act_sh;
+    float * ex; float * ex_sh;
+    int H, N, N_sh, k;
+};
+
+constexpr int MAX_NDOWN = 2048;   // longest down-projection input held in LDS
+
+template <int LPR, int MAXP>
+__global__ void __launch_bounds__(256) k_down_q4k(DownArgs a) {
+    constexpr int RPI = WAVE / LPR;
+    constexpr int NIT = GEMV_STEPS;
+    __shared__ int8_t s_qs[MAXP][MAX_NDOWN];
+    __shared__ float s_d[MAXP][MAX_NDOWN / QK_K];
+    __shared__ int32_t s_bs[MAXP][MAX_NDOWN / 16];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int u = blockIdx.y;
+    const bool shared = u == a.unit_slots;
+    if (!shared && u >= *a.n_units) return;
+    const Unit & U = a.units[shared ? *a.n_units : u];
+    const int n = U.n;
+    const int K = shared ? a.N_sh : a.N;
+    const int nb = K / QK_K;
+    const int c = lane % LPR, rsub = lane / LPR;
+    const int C = K / 32;
+    const bool active = c < C;
+    const uint8_t * base = shared ? a.sh_down : a.down + (size_t)a.slot_d[U.pair[0]] * a.down_slab;
+    const size_t row_bytes = (size_t)nb * 144;
+    const int r_begin = (blockIdx.x * 4 + wave) * (NIT * RPI);
+    // weight loads first: they do not depend on the activations
+    WChunk W[NIT];
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const int r = r_begin + it * RPI + rsub;
+        if (active && r < a.H) load_w_chunk(W[it], base + (size_t)r * row_bytes, c);
+    }
+    // quantize the unit's activation rows to Q8_K (one 256-block per wave at a time)
+    for (int jb = wave; jb < n * nb; jb += 4) {
+        const int i = jb / nb, b = jb % nb;
+        const float * src = shared ? a.act_sh + (size_t)U.pair[i] * K : a.act + (size_t)U.pair[i] * K;
+        quantize_block_q8K(src + b * QK_K, &s_qs[i][b * QK_K], &s_d[i][b], &s_bs[i][b * 16], lane);
+    }
+    __syncthreads();
+    ActChunk A[MAXP];
+#pragma unroll
+    for (int i = 0; i < MAXP; ++i)
+        if (i < n && active) load_act_chunk(A[i], s_qs[i], s_d[i], s_bs[i], c);
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const int r = r_begin + it * RPI + rsub;
+        const bool valid = active && r < a.H;
+        float acc[MAXP];
+#pragma unroll
+        for (int i = 0; i < MAXP; ++i) {
+            acc[i] = (i < n && valid) ? chunk_dot(W[it], A[i], c, 0.f) : 0.f;
+            acc[i] = group_sum<LPR>(acc[i]);
+        }
+        if (r < a.H) {
+#pragma unroll
+            for (int i = 0; i < MAXP; ++i)
+                if (i < n && c == i) {
+                    if (shared) a.ex_sh[(size_t)U.pair[i] * a.H + r] = acc[i];
+                    else a.ex[(size_t)U.pair[i] * a.H + r] = acc[i];
+                }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------
+// combine: out[t][h] = sum_j ex[t,j][h] * w[t][j] (+ shared) (+ resid)
+//   T == 1: ggml_vec_dot_f32 with n = k (runtime.cpp:3815-3817): the whole
+//           sum is the scalar tail, gcc-vectorized as unfused 16/8 groups,
+//           then fused multiply-adds.
+//   T  > 1: ggml_mul then the ggml_add chain (runtime.cpp:4544-4550).
+// ---------------------------------------------------------------------
+__global__ void __launch_bounds__(256) k_combine(const float * __restrict__ ex, const float * __restrict__ ex_sh,
+                                                  const float * __restrict__ w, const float * __restrict__ sh_gate,
+                                                  const float * __restrict__ resid, float * __restrict__ out,
+                                                  int H, int T, int k, int shared) {
+    const int h = blockIdx.x * 256 + threadIdx.x, t = blockIdx.y;
+    if (h >= H) return;
+    const float * wt = w + (size_t)t * k;
+    const float * e = ex + (size_t)t * k * H + h;
+    float s;
+    if (T == 1) {
+        s = 0.0f;
+        int i = 0;
+        for (; k - i >= 16; i += 16)
+            for (int l = 0; l < 16; ++l) s = s + e[(size_t)(i + l) * H] * wt[i + l];
+        if (k - i >= 8) {
+            for (int l = 0; l < 8; ++l) s = s + e[(size_t)(i + l) * H] * wt[i + l];
+            i += 8;
+        }
+        for (; i < k; ++i) s = __builtin_fmaf(e[(size_t)i * H], wt[i], s);
+    } else {
+        s = e[0] * wt[0];
+        for (int j = 1; j < k; ++j) s = s + e[(size_t)j * H] * wt[j];
+    }
+    if (shared) {
+        float v = ex_sh[(size_t)t * H + h];
+        if (sh_gate) v = v * sh_gate[t];
+        s = s + v;
+    }
+    if (resid) s = s + resid[(size_t)t * H + h];
+    out[(size_t)t * H + h] = s;
+}
+
+// ======================================================================
+// host launchers
+// ======================================================================
+
+bool moe_plan(const qwm_moe_layer * L, int64_t T, MoePlan & p, std::string & why) {
+    p.H = L->router.ne[0];
+    p.E = L->router.ne[1];
+    p.k = L->n_expert_used;
+    p.T = T;
+    p.N = L->gate_pool.ne[1];
+    p.shared = L->sh_gate.data != nullptr;
+    p.shared_gate = L->sh_gate_inp.data != nullptr;
+    p.N_sh = p.shared ? L->sh_gate.ne[1] : 0;
+    if (T < 1 || T > MAX_T) { why = "T must be in [1, 8]"; return false; }
+    if (p.k < 1 || p.k > MAX_K || p.k > p.E) { why = "n_expert_used out of range"; return false; }
+    if (p.E < 1 || p.E > MAX_E) { why = "n_expert out of range"; return false; }
+    if (p.H % QK_K || p.H > 2048) { why = "hidden size must be a multiple of 256, <= 2048"; return false; }
+    if (p.N % QK_K || p.N > MAX_NDOWN) { why = "expert FFN size must be a multiple of 256, <= 2048"; return false; }
+    if (p.shared && (p.N_sh % QK_K || p.N_sh > MAX_NDOWN)) { why = "shared FFN size unsupported"; return false; }
+    const int64_t P = T * p.k;
+    size_t o = 0;
+    auto take = [&](size_t bytes) { size_t at = o; o = align_up(o + bytes, 256); return at; };
+    p.counters = take(256);
+    p.logits = take(sizeof(float) * T * p.E);
+    p.ids = take(sizeof(int32_t) * P);
+    p.w = take(sizeof(float) * P);
+    p.slots = take(sizeof(int32_t) * 3 * P);
+    p.sh_gate = take(sizeof(float) * (T + 1));
+    p.n_units = take(sizeof(int32_t));
+    p.units = take(sizeof(Unit) * (P + 1));
+    p.xq_qs = take((size_t)T * p.H);
+    p.xq_d = take(sizeof(float) * T * (p.H / QK_K));
+    p.xq_bs = take(sizeof(int32_t) * T * (p.H / 16));
+    p.act = take(sizeof(float) * P * p.N);
+    p.act_sh = take(sizeof(float) * T * (p.N_sh ? p.N_sh : 1));
+    p.ex = take(sizeof(float) * P * p.H);
+    p.ex_sh = take(sizeof(float) * T * p.H);
+    p.total = o;
+    return true;
+}
+
+int launch_route(const RouteArgs & a, const MoePlan & p, uint8_t * ws, int32_t * ids_out, int64_t ids_ld,
+                 float * w_out, int64_t w_ld, hipStream_t s) {
+    float * logits = reinterpret_cast<float *>(ws + p.logits);
+    float * sh = reinterpret_cast<float *>(ws + p.sh_gate);
+    const int rows = (int)a.E + (a.sh_gate_inp ? 1 : 0);
+    k_route_logits<<<dim3((rows + 3) / 4), dim3(256), 0, s>>>(a.W, a.x, a.rm, a.sh_gate_inp, logits, sh + p.T,
+                                                               (int)a.E, (int)a.H, (int)a.T);
+    SelectArgs sa;
+    sa.logits = logits; sa.sh_logit = sh + p.T; sa.x = a.x;
+    sa.E = (int)a.E; sa.H = (int)a.H; sa.T = (int)a.T; sa.k = (int)a.k; sa.norm = a.norm; sa.scale = a.scale;
+    sa.ids_ws = reinterpret_cast<int32_t *>(ws + p.ids);
+    sa.w_ws = reinterpret_cast<float *>(ws + p.w);
+    sa.ids_out = ids_out; sa.ids_ld = ids_ld; sa.w_out = w_out; sa.w_ld = w_ld;
+    sa.sh_gate = a.sh_gate_inp ? sh : nullptr;
+    sa.xq_qs = reinterpret_cast<int8_t *>(ws + p.xq_qs);
+    sa.xq_d = reinterpret_cast<float *>(ws + p.xq_d);
+    sa.xq_bs = reinterpret_cast<int32_t *>(ws + p.xq_bs);
+    sa.units = reinterpret_cast<Unit *>(ws + p.units);
+    sa.n_units = reinterpret_cast<int32_t *>(ws + p.n_units);
+    sa.counter = reinterpret_cast<int32_t *>(ws + p.counters);
+    sa.shared = p.shared ? 1 : 0;
+    sa.slot_tables = a.slot_tables; sa.table_stride = a.table_stride; sa.layer = a.layer;
+    sa.slots_ws = reinterpret_cast<int32_t *>(ws + p.slots);
+    k_route_select<<<dim3((unsigned)a.T), dim3(64), 0, s>>>(sa);
+    QWM_HIP_CHECK(hipGetLastError());
+    return QWM_OK;
+}
+
+template <int LPR>
+static void launch_gateup_lpr(const GateUpArgs & g, int maxp, dim3 grid, hipStream_t s) {
+    switch (maxp) {
+        case 1: k_gateup_q4k<LPR, 1><<<grid, 256, 0, s>>>(g); break;
+        case 2: k_gateup_q4k<LPR, 2><<<grid, 256, 0, s>>>(g); break;
+        case 4: k_gateup_q4k<LPR, 4><<<grid, 256, 0, s>>>(g); break;
+        default: k_gateup_q4k<LPR, 8><<<grid, 256, 0, s>>>(g); break;
+    }
+}
+template <int LPR>
+static void launch_down_lpr(const DownArgs & d, int maxp, dim3 grid, hipStream_t s) {
+    switch (maxp) {
+        case 1: k_down_q4k<LPR, 1><<<grid, 256, 0, s>>>(d); break;
+        case 2: k_down_q4k<LPR, 2><<<grid, 256, 0, s>>>(d); break;
+        case 4: k_down_q4k<LPR, 4><<<grid, 256, 0, s>>>(d); break;
+        default: k_down_q4k<LPR, 8><<<grid, 256, 0, s>>>(d); break;
+    }
+}
+
+static int lanes_per_row(int K) {
+    const int C = K / 32;          // 16-byte chunks per row
+    if (C > 64) return -1;         // K > 2048 is not tiled here
+    int l = 16;
+    while (l < C) l <<= 1;
+    return l;
+}
+static int pow2_maxp(int64_t T) { return T <= 1 ? 1 : T <= 2 ? 2 : T <= 4 ? 4 : 8; }
+
+int launch_experts(const ExpertArgs & a, const MoePlan & p, uint8_t * ws, hipStream_t s) {
+    if (a.wtype != T_Q4_K) return fail(QWM_ERR_UNSUPPORTED, "expert pools: only Q4_K slabs are wired in this build");
+    const int maxp = pow2_maxp(p.T);
+    const int P = (int)(p.T * p.k);
+    const int unit_slots = P;
+    const int grid_y = unit_slots + (p.shared ? 1 : 0);
+    Unit * units = reinterpret_cast<Unit *>(ws + p.units);
+    const int32_t * n_units = reinterpret_cast<const int32_t *>(ws + p.n_units);
+
+    GateUpArgs g;
+    g.gate = a.gate; g.up = a.up; g.gate_slab = a.gate_slab; g.up_slab = a.up_slab;
+    g.sh_gate = a.sh_gate; g.sh_up = a.sh_up;
+    g.slot_g = a.slot_g; g.slot_u = a.slot_u;
+    g.units = units; g.n_units = n_units; g.unit_slots = unit_slots;
+    g.xq_qs = reinterpret_cast<const int8_t *>(ws + p.xq_qs);
+    g.xq_d = reinterpret_cast<const float *>(ws + p.xq_d);
+    g.xq_bs = reinterpret_cast<const int32_t *>(ws + p.xq_bs);
+    g.act = reinterpret_cast<float *>(ws + p.act);
+    g.act_sh = reinterpret_cast<float *>(ws + p.act_sh);
+    g.H = (int)p.H; g.N = (int)p.N; g.N_sh = (int)p.N_sh; g.k = (int)p.k;
+    const int lg = lanes_per_row((int)p.H);
+    if (lg < 0) return fail(QWM_ERR_UNSUPPORTED, "hidden size > 2048 not tiled");
+    const int rows_g = (int)std::max(p.N, p.N_sh);
+    const int tile_g = 4 * GEMV_STEPS * (WAVE / lg);
+    dim3 grid_g((rows_g + tile_g - 1) / tile_g, grid_y);
+    switch (lg) {
+        case 16: launch_gateup_lpr<16>(g, maxp, grid_g, s); break;
+        case 32: launch_gateup_lpr<32>(g, maxp, grid_g, s); break;
+        default: launch_gateup_lpr<64>(g, maxp, grid_g, s); break;
+    }
+
+    DownArgs d;
+    d.down = a.down; d.down_slab = a.down_slab; d.sh_down = a.sh_down;
+    d.slot_d = a.slot_d;
+    d.units = units; d.n_units = n_units; d.unit_slots = unit_slots;
+    d.act = g.act; d.act_sh = g.act_sh;
+    d.ex = reinterpret_cast<float *>(ws + p.ex);
+    d.ex_sh = reinterpret_cast<float *>(ws + p.ex_sh);
+    d.H = (int)p.H; d.N = (int)p.N; d.N_sh = (int)p.N_sh; d.k = (int)p.k;
+    const int ld = lanes_per_row((int)std::max(p.N, p.N_sh));
+    if (ld < 0) return fail(QWM_ERR_UNSUPPORTED, "expert FFN size > 2048 not tiled");
+    if (p.shared && lanes_per_row((int)p.N_sh) != lanes_per_row((int)p.N))
+        return fail(QWM_ERR_UNSUPPORTED, "shared and routed FFN sizes need the same tiling");
+    const int tile_d = 4 * GEMV_STEPS * (WAVE / ld);
+    dim3 grid_d(((int)p.H + tile_d - 1) / tile_d, grid_y);
+    switch (ld) {
+        case 16: launch_down_lpr<16>(d, maxp, grid_d, s); break;
+        case 32: launch_down_lpr<32>(d, maxp, grid_d, s); break;
+        default: launch_down_lpr<64>(d, maxp, grid_d, s); break;
+    }
+
+    k_combine<<<dim3((unsigned)((p.H + 255) / 256), (unsigned)p.T), 256, 0, s>>>(
+        d.ex, d.ex_sh, reinterpret_cast<const float *>(a.weights), p.shared_gate ? reinterpret_cast<const float *>(ws + p.sh_gate) : nullptr,
+        a.resid, a.out, (int)p.H, (int)p.T, (int)p.k, p.shared ? 1 : 0);
+    QWM_HIP_CHECK(hipGetLastError());
+    return QWM_OK;
+}
+
+// ======================================================================
+// generic GGML_OP_MUL_MAT_ID (Q4_K): prep quantizes b and builds units
+// ======================================================================
+struct MmidPrep {
+    const float * b; size_t b_nb1, b_nb2;   // bytes
+    const int32_t * ids; size_t ids_nb1;    // bytes
+    int K, ne11, T, n_ids, n_as, cap;       // cap: pairs per unit
+    int8_t * qs; float * d; int32_t * bs;   // [T*ne11] rows of Q8_K
+    Unit * units; int32_t * n_units; int32_t * ids_ws; int32_t * err;
+};
+
+// Blocks quantize b's columns; block 0's first wave then groups the (t, e)
+// pairs by expert in pair order, at most `cap` pairs per unit.
+__global__ void __launch_bounds__(256) k_mmid_prep(MmidPrep a) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int rows = a.T * a.ne11, nb = a.K / QK_K;
+    for (int jb = blockIdx.x * 4 + wave; jb < rows * nb; jb += gridDim.x * 4) {
+        const int row = jb / nb, b = jb % nb;
+        const int t = row / a.ne11, i = row % a.ne11;
+        const float * src = reinterpret_cast<const float *>(reinterpret_cast<const uint8_t *>(a.b) + t * a.b_nb2 + i * a.b_nb1);
+        quantize_block_q8K(src + b * QK_K, a.qs + (size_t)row * a.K + b * QK_K, a.d + (size_t)row * nb + b,
+                           a.bs + (size_t)row * (a.K / 16) + b * 16, lane);
+    }
+    if (blockIdx.x != 0 || wave != 0) return;
+    const int P = a.T * a.n_ids;
+    __shared__ int32_t eid[MAX_PAIRS], rank[MAX_PAIRS], uidx[MAX_PAIRS];
+    int bad = 0;
+    for (int p = lane; p < P; p += 64) {
+        const int t = p / a.n_ids, e = p % a.n_ids;
+        int v = *reinterpret_cast<const int32_t *>(reinterpret_cast<const uint8_t *>(a.ids) + t * a.ids_nb1 + e * 4);
+        if (v < 0 || v >= a.n_as) { bad = 1; v = 0; }
+        eid[p] = v;
+        a.ids_ws[p] = v;
+    }
+    if (__any(bad) && lane == 0) *a.err = 1;
+    __syncthreads();
+    for (int p = lane; p < P; p += 64) {
+        int r = 0;
+        for (int q = 0; q < p; ++q) r += eid[q] == eid[p];
+        rank[p] = r;
+    }
+    __syncthreads();
+    int base = 0;
+    for (int c = 0; c < P; c += 64) {
+        const int p = c + lane;
+        const bool isf = p < P && rank[p] % a.cap == 0;
+        const unsigned long long bal = __ballot(isf);
+        if (isf) uidx[p] = base + __popcll(bal & ((1ull << lane) - 1ull));
+        base += __popcll(bal);
+    }
+    __syncthreads();
+    for (int p = lane; p < P; p += 64) {
+        const int r0 = rank[p] - rank[p] % a.cap;   // rank of the unit's first pair
+        int f = p;
+        for (int q = 0; q <= p; ++q)
+            if (eid[q] == eid[p] && rank[q] == r0) { f = q; break; }
+        int total = 0;
+        for (int q = 0; q < P; ++q) total += eid[q] == eid[p];
+        Unit & u = a.units[uidx[f]];
+        u.pair[rank[p] - r0] = p;
+        if (p == f) { u.expert = eid[p]; u.n = min(a.cap, total - r0); }
+    }
+    if (lane == 0) *a.n_units = base;
+}
+
+struct MmidGemv {
+    const uint8_t * as; size_t slab; size_t row_bytes;
+    const Unit * units; const int32_t * n_units;
+    const int8_t * qs; const float * d; const int32_t * bs;
+    int K, N, ne11, n_ids;
+    float * dst; size_t dst_nb1, dst_nb2;
+};
+
+template <int LPR, int MAXP>
+__global__ void __launch_bounds__(256) k_mmid_q4k(MmidGemv a) {
+    constexpr int RPI = WAVE / LPR;
+    constexpr int NIT = GEMV_STEPS;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int u = blockIdx.y;
+    if (u >= *a.n_units) return;
+    const Unit & U = a.units[u];
+    const int n = U.n;
+    const int c = lane % LPR, rsub = lane / LPR;
+    const int C = a.K / 32;
+    const bool active = c < C;
+    const uint8_t * base = a.as + (size_t)U.expert * a.slab;
+    const int r_begin = (blockIdx.x * 4 + wave) * (NIT * RPI);
+    if (r_begin >= a.N) return;
+    WChunk W[NIT];
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const int r = r_begin + it * RPI + rsub;
+        if (active && r < a.N) load_w_chunk(W[it], base + (size_t)r * a.row_bytes, c);
+    }
+    ActChunk A[MAXP];
+#pragma unroll
+    for (int i = 0; i < MAXP; ++i)
+        if (i < n && active) {
+            const int p = U.pair[i];
+            const int row = (p / a.n_ids) * a.ne11 + (p % a.n_ids) % a.ne11;
+            load_act_chunk(A[i], a.qs + (size_t)row * a.K, a.d + (size_t)row * (a.K / QK_K), a.bs + (size_t)row * (a.K / 16), c);
+        }
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const int r = r_begin + it * RPI + rsub;
+        const bool valid = active && r < a.N;
+        float acc[MAXP];
+#pragma unroll
+        for (int i = 0; i < MAXP; ++i) {
+            acc[i] = (i < n && valid) ? chunk_dot(W[it], A[i], c, 0.f) : 0.f;
+            acc[i] = group_sum<LPR>(acc[i]);
+        }
+        if (r < a.N) {
+#pragma unroll
+            for (int i = 0; i < MAXP; ++i)
+                if (i < n && c == i) {
+                    const int p = U.pair[i];
+                    float * o = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(a.dst) + (p / a.n_ids) * a.dst_nb2 +
+                                                          (p % a.n_ids) * a.dst_nb1);
+                    o[r] = acc[i];
+                }
+        }
+    }
+}
+
+size_t mmid_workspace(int64_t K, int64_t T, int64_t ne11, int64_t n_ids) {
+    const int64_t rows = T * ne11;
+    size_t o = 0;
+    auto take = [&](size_t bytes) { o = align_up(o + bytes, 256); };
+    take((size_t)rows * K);                       // qs
+    take(sizeof(float) * rows * (K / QK_K));      // d
+    take(sizeof(int32_t) * rows * (K / 16));      // bsums
+    take(sizeof(Unit) * T * n_ids);               // units
+    take(sizeof(int32_t) * 4);                    // n_units, err
+    take(sizeof(int32_t) * T * n_ids);            // ids copy
+    return o;
+}
+
+int launch_mmid(const MmidArgs & a, uint8_t * ws, hipStream_t s) {
+    if (a.wtype != T_Q4_K) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: only Q4_K weights are wired in this build");
+    const int64_t rows = a.T * a.ne11;
+    size_t o = 0;
+    auto take = [&](size_t bytes) { size_t at = o; o = align_up(o + bytes, 256); return at; };
+    const size_t o_qs = take((size_t)rows * a.K), o_d = take(sizeof(float) * rows * (a.K / QK_K)),
+                 o_bs = take(sizeof(int32_t) * rows * (a.K / 16)), o_u = take(sizeof(Unit) * a.T * a.n_ids),
+                 o_n = take(sizeof(int32_t) * 4), o_ids = take(sizeof(int32_t) * a.T * a.n_ids);
+    MmidPrep pr;
+    pr.b = a.b; pr.b_nb1 = a.b_nb1; pr.b_nb2 = a.b_nb2; pr.ids = a.ids; pr.ids_nb1 = a.ids_nb1;
+    const int maxp = pow2_maxp(a.T);
+    pr.K = (int)a.K; pr.ne11 = (int)a.ne11; pr.T = (int)a.T; pr.n_ids = (int)a.n_ids; pr.n_as = (int)a.n_as;
+    pr.cap = maxp;
+    pr.qs = reinterpret_cast<int8_t *>(ws + o_qs); pr.d = reinterpret_cast<float *>(ws + o_d);
+    pr.bs = reinterpret_cast<int32_t *>(ws + o_bs); pr.units = reinterpret_cast<Unit *>(ws + o_u);
+    pr.n_units = reinterpret_cast<int32_t *>(ws + o_n); pr.err = pr.n_units + 1;
+    pr.ids_ws = reinterpret_cast<int32_t *>(ws + o_ids);
+    const int nblk = (int)(rows * (a.K / QK_K));
+    k_mmid_prep<<<dim3((unsigned)std::max(1, std::min(256, (nblk + 3) / 4))), 256, 0, s>>>(pr);
+    MmidGemv g;
+    g.as = a.as; g.slab = a.slab; g.row_bytes = (size_t)(a.K / QK_K) * 144;
+    g.units = pr.units; g.n_units = pr.n_units; g.qs = pr.qs; g.d = pr.d; g.bs = pr.bs;
+    g.K = (int)a.K; g.N = (int)a.N; g.ne11 = (int)a.ne11; g.n_ids = (int)a.n_ids;
+    g.dst = a.dst; g.dst_nb1 = a.dst_nb1; g.dst_nb2 = a.dst_nb2;
+    const int lpr = lanes_per_row((int)a.K);
+    if (lpr < 0) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: K > 2048 not tiled");
+    const int tile = 4 * GEMV_STEPS * (WAVE / lpr);
+    dim3 grid((unsigned)((a.N + tile - 1) / tile), (unsigned)(a.T * a.n_ids));
+#define QWM_MMID(LPR_, P_) k_mmid_q4k<LPR_, P_><<<grid, 256, 0, s>>>(g)
+#define QWM_MMID_P(LPR_)                                    \
+    switch (maxp) {                                         \
+        case 1: QWM_MMID(LPR_, 1); break;                   \
+        case 2: QWM_MMID(LPR_, 2); break;                   \
+        case 4: QWM_MMID(LPR_, 4); break;                   \
+        default: QWM_MMID(LPR_, 8); break;                  \
+    }
+    switch (lpr) {
+        case 16: QWM_MMID_P(16); break;
+        case 32: QWM_MMID_P(32); break;
+        default: QWM_MMID_P(64); break;
+    }
+#undef QWM_MMID_P
+#undef QWM_MMID
+    QWM_HIP_CHECK(hipGetLastError());
+    return QWM_OK;
+}
+
+__global__ void k_fill_zero(uint32_t * p, size_t n) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = 0;
+}
+
+int launch_fill_zero(void * p, size_t bytes, hipStream_t s) {
+    if (bytes % 4) return fail(QWM_ERR_ARG, "workspace size must be a multiple of 4");
+    const size_t n = bytes / 4;
+    if (n == 0) return QWM_OK;
+    const unsigned blocks = (unsigned)std::min<size_t>(1024, (n + 255) / 256);
+    k_fill_zero<<<blocks, 256, 0, s>>>(reinterpret_cast<uint32_t *>(p), n);
+    QWM_HIP_CHECK(hipGetLastError());
+    return QWM_OK;
+}
+
+}  // namespace qwm

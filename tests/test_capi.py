@@ -1,0 +1,167 @@
+"""CPU checks of the C ABI: libqwmoe.so loads without a GPU, exports every
+function include/qwmoe.h declares, rejects malformed arguments before any
+device work, and its slot pool takes the same decisions as the oracle's
+restatement of ExpertCache (decision-only pools need no GPU)."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import questwend_amd as qa
+from tests.helpers import ROOT, oracle, ptr
+
+
+def header_functions():
+    src = open(os.path.join(ROOT, "include", "qwmoe.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(qwm_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_library_exports_every_declared_symbol():
+    names = header_functions()
+    assert len(names) >= 20
+    lib = ctypes.CDLL(qa.LIB_PATH)
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    assert qa.lib().qwm_version().startswith(b"qwmoe")
+
+
+def test_tensor_init_matches_python_helper():
+    t = qa.QwmTensor()
+    qa.lib().qwm_tensor_init(ctypes.byref(t), qa.TYPE_Q4_K, 2048, 768, 128, None)
+    u = qa.tensor(qa.TYPE_Q4_K, 2048, 768, 128)
+    assert list(t.ne) == list(u.ne) and list(t.nb) == list(u.nb)
+    assert t.nb[1] == 1152 and t.nb[2] == 884736
+
+
+def test_argument_validation_without_gpu():
+    L = qa.lib()
+    a = qa.tensor(qa.TYPE_Q4_K, 256, 4, 2)
+    b = qa.tensor(qa.TYPE_F32, 512, 1, 1)      # K mismatch (ggml.c:3428)
+    ids = qa.tensor(qa.TYPE_I32, 2, 1, 1)
+    assert L.qwm_mul_mat_id(a, b, ids, qa.tensor(qa.TYPE_F32, 4, 2, 1), None, 0, None) == qa.ERR_ARG
+    assert b"ne[0]" in L.qwm_last_error()
+    b = qa.tensor(qa.TYPE_F32, 256, 1, 1)
+    ids_bad = qa.tensor(qa.TYPE_I32, 3, 2, 1)   # ids->ne[1] != b->ne[2]
+    assert L.qwm_mul_mat_id(a, b, ids_bad, None, None, 0, None) == qa.ERR_ARG
+    assert L.qwm_mul_mat_id(a, b, ids, qa.tensor(qa.TYPE_F32, 4, 2, 1), None, 0, None) == qa.ERR_WORKSPACE
+    wide = qa.tensor(qa.TYPE_F32, 256, 1, 9)    # 9 columns: prefill path, not the GEMV
+    assert L.qwm_mul_mat_id(a, wide, qa.tensor(qa.TYPE_I32, 2, 9, 1), None, None, 0, None) == qa.ERR_UNSUPPORTED
+    lay = qa.MoeLayer()
+    lay.router = qa.tensor(qa.TYPE_F32, 2048, 128)
+    lay.gate_pool = qa.tensor(qa.TYPE_Q4_K, 2048, 768, 4)
+    lay.up_pool = qa.tensor(qa.TYPE_Q4_K, 2048, 768, 4)
+    lay.down_pool = qa.tensor(qa.TYPE_Q4_K, 768, 2048, 4)
+    lay.n_expert_used = 8
+    assert L.qwm_moe_workspace_size(lay, 4) > 0
+    assert L.qwm_moe_workspace_size(lay, 9) == 0
+    lay.down_pool = qa.tensor(qa.TYPE_Q4_K, 512, 2048, 4)   # down K != gate N
+    assert L.qwm_moe_workspace_size(lay, 1) == 0
+    lm = qa.tensor(qa.TYPE_Q4_K, 2048, 1000)
+    assert L.qwm_verify_workspace_size(lm, 4) == 0          # lm_head must be Q8_0
+    assert L.qwm_verify_workspace_size(qa.tensor(qa.TYPE_Q8_0, 2048, 151936), 4) > 0
+
+
+class GpuPool:
+    """Decision-only libqwmoe pool (no host slabs, so no copies, no GPU)."""
+
+    def __init__(self, n_layer, n_expert, slots, protect=0, indexed=0):
+        d = qa.PoolDesc()
+        d.n_layer, d.n_expert = n_layer, n_expert
+        for r in range(3):
+            d.n_slots[r] = slots[r]
+            d.slab_bytes[r] = 0
+        d.protect_active, d.indexed = protect, indexed
+        h = ctypes.c_void_p()
+        qa.check(qa.lib().qwm_pool_create(ctypes.byref(d), None, ctypes.byref(h)))
+        self.h, self.slots = h, slots
+
+    def ensure(self, layer, ids):
+        ids = np.ascontiguousarray(ids, np.int32)
+        out = np.zeros((3, ids.size), np.int32)
+        rc = qa.lib().qwm_pool_ensure(self.h, layer, ptr(ids), ids.size, ptr(out[0]), ptr(out[1]), ptr(out[2]))
+        return rc, out
+
+    def state(self, role):
+        k = np.zeros(self.slots[role], np.int32)
+        c = np.zeros(self.slots[role], np.uint64)
+        qa.check(qa.lib().qwm_pool_slots(self.h, role, ptr(k), ptr(c)))
+        return k, c
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            qa.lib().qwm_pool_destroy(self.h)
+
+
+class OraclePool:
+    def __init__(self, n_layer, n_expert, slots, protect=0):
+        s = np.array(slots, np.int32)
+        self.h = oracle().qwo_pool_new(n_layer, n_expert, ptr(s), protect)
+        self.slots = slots
+
+    def ensure(self, layer, ids):
+        ids = np.ascontiguousarray(ids, np.int32)
+        out = np.zeros((3, ids.size), np.int32)
+        nf = ctypes.c_int()
+        rc = oracle().qwo_pool_ensure(self.h, layer, ptr(ids), ids.size, ptr(out[0]), ptr(out[1]), ptr(out[2]),
+                                      None, ctypes.byref(nf))
+        return rc, out
+
+    def state(self, role):
+        k = np.zeros(self.slots[role], np.int32)
+        c = np.zeros(self.slots[role], np.uint64)
+        oracle().qwo_pool_slots(self.h, role, ptr(k), ptr(c))
+        return k, c
+
+    def __del__(self):
+        oracle().qwo_pool_free(self.h)
+
+
+@pytest.mark.parametrize("indexed", [0, 1])
+@pytest.mark.parametrize("protect", [0, 1])
+def test_pool_matches_oracle_on_zipf_traces(indexed, protect):
+    rng = np.random.default_rng(17 + indexed + 2 * protect)
+    n_layer, n_expert, slots = 4, 128, [90, 77, 101]
+    g = GpuPool(n_layer, n_expert, slots, protect, indexed)
+    o = OraclePool(n_layer, n_expert, slots, protect)
+    pop = 1.0 / np.arange(1, n_expert + 1) ** 1.1
+    pop /= pop.sum()
+    perm = rng.permutation(n_expert)
+    for step in range(400):
+        layer = int(rng.integers(0, n_layer))
+        T = int(rng.integers(1, 5))
+        ids = np.concatenate([perm[rng.choice(n_expert, 8, replace=False, p=pop)] for _ in range(T)])
+        rg, sg = g.ensure(layer, ids)
+        ro, so = o.ensure(layer, ids)
+        assert rg == ro
+        if rg == 0:
+            assert np.array_equal(sg, so)
+    for r in range(3):
+        kg, cg = g.state(r)
+        ko, co = o.state(r)
+        assert np.array_equal(kg, ko) and np.array_equal(cg, co)
+    st = qa.PoolStats()
+    qa.check(qa.lib().qwm_pool_get_stats(g.h, ctypes.byref(st)))
+    hmo = np.zeros(3, np.uint64)
+    oracle().qwo_pool_stats(o.h, ptr(hmo))
+    assert (st.hits, st.misses, st.evictions) == tuple(int(v) for v in hmo)
+    row_g = np.zeros(n_expert, np.int32)
+    row_o = np.zeros(n_expert, np.int32)
+    for r in range(3):
+        for layer in range(n_layer):
+            qa.check(qa.lib().qwm_pool_slot_of_row(g.h, r, layer, ptr(row_g)))
+            oracle().qwo_pool_slot_of_row(o.h, r, layer, ptr(row_o))
+            assert np.array_equal(row_g, row_o)
+
+
+def test_pool_exhaustion_is_reported_and_consistent():
+    g = GpuPool(1, 16, [2, 2, 2], protect=1)
+    assert g.ensure(0, [0, 1])[0] == 0
+    rc, _ = g.ensure(0, [0, 1, 2])
+    assert rc == qa.ERR_NO_VICTIM
+    assert b"No unprotected GPU cache victim" in qa.lib().qwm_last_error()
+    k, _ = g.state(0)
+    assert sorted(k.tolist()) == [0, 1]          # nothing was evicted or published
+    assert g.ensure(0, [16])[0] == qa.ERR_ARG    # expert id out of range

@@ -1,0 +1,167 @@
+"""GPU parity of the MoE block against the oracle (ggml-CPU restated), through
+the C ABI of libqwmoe.  Expert ids and routing weights must be bit-exact
+(the router reproduces the CPU's floating-point order); expert outputs must
+be within the north-star tolerance of 1e-3 normwise relative error (block
+sums are exact integers, only the fp32 order across blocks differs)."""
+import numpy as np
+import pytest
+
+from tests.helpers import GGML_Q4_K, I64, bits, oracle, ptr, quantize_q4_K
+from tests.moe_case import MoeCase, rel_err
+
+torch = pytest.importorskip("torch")
+import questwend_amd as qa  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    qa.lib()
+    return torch.device("cuda:0")
+
+
+def workspace(nbytes):
+    ws = torch.empty(max(256, (nbytes + 255) // 256 * 256), dtype=torch.uint8, device="cuda")
+    qa.check(qa.lib().qwm_workspace_init(ws.data_ptr(), ws.numel(), None))
+    return ws
+
+
+def route_gpu(case, x, rm=None):
+    T = x.shape[0]
+    L = case.layer
+    ws = workspace(qa.lib().qwm_moe_workspace_size(L, T))
+    dx = torch.from_numpy(x).cuda()
+    ids = torch.zeros((T, case.k), dtype=torch.int32, device="cuda")
+    w = torch.zeros((T, case.k), dtype=torch.float32, device="cuda")
+    drm = torch.from_numpy(rm).cuda() if rm is not None else None
+    rmt = qa.tensor(qa.TYPE_F32, case.E, T, 1, drm) if rm is not None else None
+    qa.check(qa.lib().qwm_moe_route(L, qa.tensor(qa.TYPE_F32, case.H, T, 1, dx), rmt,
+                                    qa.tensor(qa.TYPE_I32, case.k, T, 1, ids),
+                                    qa.tensor(qa.TYPE_F32, case.k, T, 1, w), ws.data_ptr(), ws.numel(), None))
+    torch.cuda.synchronize()
+    return ids.cpu().numpy(), w.cpu().numpy(), ws, dx
+
+
+@pytest.mark.parametrize("E,k,T", [(128, 8, 1), (128, 8, 4), (512, 10, 4), (512, 10, 1), (128, 8, 8)])
+def test_route_bit_exact(dev, E, k, T):
+    case = MoeCase(seed=E + T, E=E, k=k, S=1)
+    case.upload(torch)
+    for rep in range(3):
+        x = case.rng.standard_normal((T, case.H)).astype(np.float32)
+        ids, w, mg, _ = case.route(x)
+        gids, gw, _, _ = route_gpu(case, x)
+        assert np.array_equal(gids, ids), (gids, ids, mg)
+        assert np.array_equal(bits(gw), bits(w))
+
+
+def test_route_mask_offsets(dev):
+    """Zipf-style per-expert logit offsets through the route mask (rm)."""
+    case = MoeCase(seed=5, E=512, k=10, S=1)
+    case.upload(torch)
+    rank = case.rng.permutation(512)
+    rm = np.tile((-1.1 * np.log1p(rank)).astype(np.float32), (4, 1))
+    x = case.rng.standard_normal((4, case.H)).astype(np.float32)
+    ids, w, _, _ = case.route(x, rm)
+    gids, gw, _, _ = route_gpu(case, x, rm)
+    assert np.array_equal(gids, ids)
+    assert np.array_equal(bits(gw), bits(w))
+
+
+def experts_gpu(case, x, slots, weights, resid=None):
+    T = x.shape[0]
+    L = case.layer
+    _, _, ws, dx = route_gpu(case, x)   # route fills the Q8_K activations + schedule
+    # the schedule groups pairs by routed expert id: give identical slots to
+    # identical ids (as ensure() does) by routing first, then mapping ids->slots
+    out = torch.zeros((T, case.H), dtype=torch.float32, device="cuda")
+    ds = torch.from_numpy(np.ascontiguousarray(slots, np.int32)).cuda()
+    dw = torch.from_numpy(np.ascontiguousarray(weights, np.float32)).cuda()
+    dr = torch.from_numpy(resid).cuda() if resid is not None else None
+    st = qa.tensor(qa.TYPE_I32, case.k, T, 1, ds)
+    qa.check(qa.lib().qwm_moe_experts(L, qa.tensor(qa.TYPE_F32, case.H, T, 1, dx), st, st, st,
+                                      qa.tensor(qa.TYPE_F32, case.k, T, 1, dw),
+                                      qa.tensor(qa.TYPE_F32, case.H, T, 1, dr) if resid is not None else None,
+                                      qa.tensor(qa.TYPE_F32, case.H, T, 1, out), ws.data_ptr(), ws.numel(), None))
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize("cfg", [
+    dict(N=768, E=128, k=8, T=1, shared=False),     # Qwen3-30B-A3B decode
+    dict(N=768, E=128, k=8, T=4, shared=False),     # Qwen3-30B-A3B verify
+    dict(N=512, E=512, k=10, T=4, shared=True),     # Qwen3-Next verify + shared expert
+    dict(N=512, E=512, k=10, T=1, shared=True),
+    dict(N=768, E=128, k=8, T=8, shared=False),
+])
+def test_moe_block_parity(dev, cfg):
+    T = cfg["T"]
+    case = MoeCase(seed=11 + T, N=cfg["N"], E=cfg["E"], k=cfg["k"], S=24, shared=cfg["shared"])
+    case.upload(torch)
+    x = case.rng.standard_normal((T, case.H)).astype(np.float32)
+    ids, w, _, _ = case.route(x)
+    slots = (ids % case.S).astype(np.int32)     # a deterministic id -> slot map
+    exp = case.block(x, slots, w)
+    got = experts_gpu(case, x, slots, w)
+    err = rel_err(got, exp)
+    print(f"moe block {cfg}: normwise rel err {err:.3e}, max abs {np.abs(got - exp).max():.3e}")
+    assert err < TOL
+    for t in range(T):
+        assert rel_err(got[t], exp[t]) < TOL
+
+
+def test_moe_block_residual(dev):
+    case = MoeCase(seed=3, S=8)
+    case.upload(torch)
+    x = case.rng.standard_normal((2, case.H)).astype(np.float32)
+    resid = case.rng.standard_normal((2, case.H)).astype(np.float32)
+    ids, w, _, _ = case.route(x)
+    slots = (ids % case.S).astype(np.int32)
+    exp = case.block(x, slots, w) + resid
+    got = experts_gpu(case, x, slots, w, resid)
+    assert rel_err(got, exp) < TOL
+
+
+@pytest.mark.parametrize("K,N,n_as,n_ids,ne11,T", [(2048, 768, 8, 8, 1, 1), (2048, 768, 8, 8, 1, 4),
+                                                  (768, 2048, 8, 8, 8, 4), (512, 2048, 6, 10, 10, 2),
+                                                  (256, 64, 4, 3, 3, 2)])
+def test_mul_mat_id_op(dev, K, N, n_as, n_ids, ne11, T):
+    """GGML_OP_MUL_MAT_ID contract, including broadcast b (ne11 = 1) and
+    repeated experts across columns."""
+    rng = np.random.default_rng(K + N + T)
+    w = (rng.standard_normal((n_as, N, K)) * 0.02).astype(np.float32)
+    q = quantize_q4_K(w)
+    b = rng.standard_normal((T, ne11, K)).astype(np.float32)
+    ids = np.stack([rng.permutation(n_as)[:n_ids] if n_ids <= n_as else rng.integers(0, n_as, n_ids)
+                    for _ in range(T)]).astype(np.int32)
+    exp = np.zeros((T, n_ids, N), np.float32)
+    assert oracle().qwo_mul_mat_id(GGML_Q4_K, ptr(q), I64(K), I64(N), I64(n_as), ptr(b), I64(ne11), I64(T),
+                                   ptr(ids), I64(n_ids), ptr(exp)) == 0
+    das = torch.from_numpy(q).cuda()
+    db = torch.from_numpy(b).cuda()
+    dids = torch.from_numpy(ids).cuda()
+    dst = torch.zeros((T, n_ids, N), dtype=torch.float32, device="cuda")
+    tas = qa.tensor(qa.TYPE_Q4_K, K, N, n_as, das)
+    tb = qa.tensor(qa.TYPE_F32, K, ne11, T, db)
+    tids = qa.tensor(qa.TYPE_I32, n_ids, T, 1, dids)
+    ws = workspace(qa.lib().qwm_mul_mat_id_workspace_size(tas, tb, tids))
+    qa.check(qa.lib().qwm_mul_mat_id(tas, tb, tids, qa.tensor(qa.TYPE_F32, N, n_ids, T, dst), ws.data_ptr(),
+                                     ws.numel(), None))
+    torch.cuda.synchronize()
+    got = dst.cpu().numpy()
+    err = rel_err(got, exp)
+    print(f"mul_mat_id K={K} N={N} T={T}: rel err {err:.3e}")
+    assert err < TOL
+    for t in range(T):
+        for e in range(n_ids):
+            assert rel_err(got[t, e], exp[t, e]) < TOL
+
+
+def test_mul_mat_id_rejects_bad_shapes(dev):
+    t = qa.tensor(qa.TYPE_Q4_K, 256, 4, 2, 0)
+    b = qa.tensor(qa.TYPE_F32, 512, 1, 1, 0)      # K mismatch
+    ids = qa.tensor(qa.TYPE_I32, 2, 1, 1, 0)
+    assert qa.lib().qwm_mul_mat_id(t, b, ids, qa.tensor(qa.TYPE_F32, 4, 2, 1, 0), None, 0, None) == qa.ERR_ARG

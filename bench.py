@@ -1,0 +1,248 @@
+"""Benchmark of the MoE verify step on one MI355X.
+
+Workload (the metric's configuration): one Qwen3-30B-A3B-shape MoE block
+(hidden 2048, 128 experts, FFN 768, top-8, Q4_K experts quantized from
+N(0, 0.02), f32 router N(0, 0.02)) run as an MTP verify batch of 4 tokens
+(x ~ N(0, 1)), followed by the verify head: rms_norm, a Q8_0 lm_head
+2048 x 151936 (quantized from N(0, 1/sqrt(2048))), argmax and the greedy
+acceptance against seeded drafts.  All experts are resident in the slot
+pools (slot = expert id, remapped on the device).  A step is one verify
+batch; inputs for every step are resident in HBM before timing starts.
+
+Prints one JSON line: tokens/s (4 tokens per step), the roofline of the
+dominant kernel (the lm_head GEMV, HBM-bound), measured with HIP events
+around its launches inside the timed region, and the CPU baseline: the
+same step through the reference's own ggml-CPU kernels on this host.
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "MoE tokens/s + achieved HBM GB/s (% of 8 TB/s), Q4_K verify, 1×MI355X"
+HBM_PEAK_GBS = 8000.0
+H, N, E, K_USED, T, V = 2048, 768, 128, 8, 4, 151936
+Q4K_ROW_GU = H // 256 * 144          # 1152 B
+Q4K_ROW_D = N // 256 * 144           # 432 B
+SLAB = N * Q4K_ROW_GU                # 884,736 B per role per expert
+LM_ROW = H // 32 * 34                # 2176 B
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU baseline sample")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--accept-rate", type=float, default=0.7, help="probability that a draft equals the target")
+    return ap.parse_args()
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import questwend_amd as qa
+
+    L = qa.lib()
+    dev = torch.device("cuda:0")
+    torch.manual_seed(args.seed)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    # ------------------------------------------------------------ weights --
+    pools = [torch.empty(E * SLAB, dtype=torch.uint8, device=dev) for _ in range(3)]
+    tmp = torch.empty(N * H, dtype=torch.float32, device=dev)
+    for r in range(3):
+        for e in range(E):
+            tmp.normal_(0.0, 0.02)
+            qa.check(L.qwm_quantize(qa.TYPE_Q4_K, tmp.data_ptr(), pools[r].data_ptr() + e * SLAB, N * H, stream))
+    router = (torch.randn((E, H), device=dev) * 0.02).contiguous()
+    lm_f = torch.empty(V * H, dtype=torch.float32, device=dev).normal_(0.0, 1.0 / np.sqrt(H))
+    lm = torch.empty(V * LM_ROW, dtype=torch.uint8, device=dev)
+    qa.check(L.qwm_quantize(qa.TYPE_Q8_0, lm_f.data_ptr(), lm.data_ptr(), V * H, stream))
+    del lm_f, tmp
+    tables = torch.arange(E, dtype=torch.int32, device=dev).repeat(3).contiguous()   # slot = expert id
+
+    layer = qa.MoeLayer()
+    layer.gate_pool = qa.tensor(qa.TYPE_Q4_K, H, N, E, pools[0])
+    layer.up_pool = qa.tensor(qa.TYPE_Q4_K, H, N, E, pools[1])
+    layer.down_pool = qa.tensor(qa.TYPE_Q4_K, N, H, E, pools[2])
+    layer.router = qa.tensor(qa.TYPE_F32, H, E, 1, router)
+    layer.n_expert_used, layer.norm_weights, layer.weights_scale = K_USED, 1, 1.0
+    lm_t = qa.tensor(qa.TYPE_Q8_0, H, V, 1, lm)
+
+    n_all = args.warmup + args.steps
+    xs = torch.randn((n_all, T, H), device=dev)
+    hs = torch.empty((n_all, T, H), device=dev)
+    ids = torch.zeros((n_all, T, K_USED), dtype=torch.int32, device=dev)
+    wts = torch.zeros((n_all, T, K_USED), dtype=torch.float32, device=dev)
+    res = torch.zeros((n_all, T + 2), dtype=torch.int32, device=dev)
+    drafts = torch.zeros((n_all, T - 1), dtype=torch.int32, device=dev)
+    ws_moe = torch.empty(L.qwm_moe_workspace_size(layer, T), dtype=torch.uint8, device=dev)
+    ws_v = torch.empty(L.qwm_verify_workspace_size(lm_t, T), dtype=torch.uint8, device=dev)
+    qa.check(L.qwm_workspace_init(ws_moe.data_ptr(), ws_moe.numel(), stream))
+    qa.check(L.qwm_workspace_init(ws_v.data_ptr(), ws_v.numel(), stream))
+
+    def step(s):
+        x_t = qa.tensor(qa.TYPE_F32, H, T, 1, xs[s])
+        h_t = qa.tensor(qa.TYPE_F32, H, T, 1, hs[s])
+        qa.check(L.qwm_moe_block_resident(layer, 0, tables.data_ptr(), E, x_t, None, x_t, h_t,
+                                          qa.tensor(qa.TYPE_I32, K_USED, T, 1, ids[s]),
+                                          qa.tensor(qa.TYPE_F32, K_USED, T, 1, wts[s]),
+                                          ws_moe.data_ptr(), ws_moe.numel(), stream))
+        qa.check(L.qwm_verify_accept(lm_t, h_t, None, 1e-6, drafts[s].data_ptr(), res[s].data_ptr(),
+                                     ws_v.data_ptr(), ws_v.numel(), stream))
+
+    # seeded drafts: one untimed pass finds each step's targets; a draft equals
+    # its target with probability accept-rate (so a in {0..3} all occur)
+    for s in range(n_all):
+        step(s)
+    torch.cuda.synchronize()
+    target = res[:, :T - 1].clone()
+    rng = np.random.default_rng(args.seed)
+    keep = torch.from_numpy(rng.random((n_all, T - 1)) < args.accept_rate).to(dev)
+    rnd = torch.from_numpy(rng.integers(0, V, (n_all, T - 1)).astype(np.int32)).to(dev)
+    drafts.copy_(torch.where(keep, target, rnd))
+
+    # ------------------------------------------------------------- timed --
+    for s in range(args.warmup):
+        step(s)
+    torch.cuda.synchronize()
+    qa.check(L.qwm_profile_start(b"lm_head", args.steps))
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    ev0.record()
+    for s in range(args.warmup, n_all):
+        step(s)
+    ev1.record()
+    torch.cuda.synchronize()
+    elapsed_ms = ev0.elapsed_time(ev1)
+    lm_ms = np.zeros(args.steps, np.float32)
+    n_lm = L.qwm_profile_stop(lm_ms.ctypes.data, args.steps)
+    ms_step = elapsed_ms / args.steps
+    tokens_per_s = T * args.steps / (elapsed_ms / 1e3)
+    r = res[args.warmup:].cpu().numpy()
+    accepted = r[:, T]
+    acc_tok_s = float((accepted + 1).sum()) / (elapsed_ms / 1e3)
+
+    # secondary kernels (untimed pass, same steps)
+    kern = {}
+    for name in ["gate_up", "down", "route_logits", "route_select", "combine", "vhead_prep", "accept"]:
+        qa.check(L.qwm_profile_start(name.encode(), args.steps))
+        for s in range(args.warmup, n_all):
+            step(s)
+        torch.cuda.synchronize()
+        d = np.zeros(args.steps, np.float32)
+        n = L.qwm_profile_stop(d.ctypes.data, args.steps)
+        kern[name] = float(d[:n].mean() * 1e3) if n else None
+
+    # algorithmic bytes
+    ids_np = ids[args.warmup:].cpu().numpy()
+    uniq = np.array([len(np.unique(i)) for i in ids_np])
+    lm_bytes = V * LM_ROW + T * (H + H // 32 * 4)
+    step_bytes = uniq * 3 * SLAB + E * H * 4 + 2 * T * H * 4 + V * LM_ROW
+    lm_avg_ms = float(lm_ms[:n_lm].mean())
+    lm_gbs = lm_bytes / (lm_avg_ms * 1e-3) / 1e9
+    gu_bytes = float(uniq.mean()) * 2 * SLAB
+    dn_bytes = float(uniq.mean()) * SLAB
+    for name, b in [("gate_up", gu_bytes), ("down", dn_bytes)]:
+        if kern.get(name):
+            kern[name + "_gbs"] = b / (kern[name] * 1e-6) / 1e9
+
+    out = {
+        "metric": METRIC, "value": tokens_per_s, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms_step, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": "MTP verify T=4 (1+3 drafts) through one Qwen3-30B-A3B-shape MoE block "
+                               "(H 2048, 128 experts resident, FFN 768, top-8, Q4_K) + rms_norm + Q8_0 lm_head "
+                               "2048x151936 argmax + greedy accept",
+                   "tokens_per_step": T, "experts_per_step_mean": float(uniq.mean())},
+        "roofline": {"bound": "hbm", "kernel": "lm_head (Q8_0 GEMV + argmax)", "achieved": lm_gbs,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": lm_gbs / HBM_PEAK_GBS, "traffic": None,
+                     "bytes_per_launch": lm_bytes, "avg_launch_us": lm_avg_ms * 1e3, "launches_timed": int(n_lm)},
+        "step_hbm_gbs": float(step_bytes.mean()) / (ms_step * 1e-3) / 1e9,
+        "step_bytes_mean": float(step_bytes.mean()),
+        "accepted_tokens_per_s": acc_tok_s,
+        "accept_histogram": np.bincount(accepted, minlength=T).tolist(),
+        "kernels_us": kern,
+    }
+
+    # --------------------------------------------------------- CPU baseline --
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(args, torch, pools, router, lm, xs, drafts, ids, res)
+    print(json.dumps(out))
+
+
+class StepArgs(ctypes.Structure):
+    _fields_ = [("H", ctypes.c_int64), ("N", ctypes.c_int64), ("E", ctypes.c_int64), ("k", ctypes.c_int64),
+                ("T", ctypes.c_int64), ("V", ctypes.c_int64), ("router", ctypes.c_void_p), ("gate", ctypes.c_void_p),
+                ("up", ctypes.c_void_p), ("down", ctypes.c_void_p), ("lm_head", ctypes.c_void_p),
+                ("x", ctypes.c_void_p), ("drafts", ctypes.c_void_p), ("ids", ctypes.c_void_p), ("out", ctypes.c_void_p),
+                ("vA", ctypes.c_void_p), ("accepted", ctypes.c_void_p), ("n_threads", ctypes.c_int)]
+
+
+def cpu_baseline(args, torch, pools, router, lm, xs, drafts, ids_gpu, res_gpu):
+    """The same verify steps through the reference's own ggml-CPU kernels
+    (oracle/_ref, compiled from the reference sources), timed on this host."""
+    so = os.path.join(ROOT, "oracle", "_ref", "libggml_leaf.so")
+    if not os.path.exists(so):
+        return {"value": None, "unit": "tokens/s", "cores": 0, "kind": "reference", "sample": "oracle/_ref not built"}
+    lib = ctypes.CDLL(so)
+    lib.qwr_cpu_verify_step.argtypes = [ctypes.POINTER(StepArgs)]
+    g, u, d = (p.cpu().numpy() for p in pools)
+    rt = router.cpu().numpy()
+    lmh = lm.cpu().numpy()
+    threads = min(16, os.cpu_count() or 1)
+    x_np = xs.cpu().numpy()
+    dr = drafts.cpu().numpy()
+    ids_ref = ids_gpu.cpu().numpy()
+    res_ref = res_gpu.cpu().numpy()
+    a = StepArgs()
+    a.H, a.N, a.E, a.k, a.T, a.V = H, N, E, K_USED, T, V
+    a.router, a.gate, a.up, a.down, a.lm_head = rt.ctypes.data, g.ctypes.data, u.ctypes.data, d.ctypes.data, lmh.ctypes.data
+    a.n_threads = threads
+    ids = np.zeros((T, K_USED), np.int32)
+    out = np.zeros((T, H), np.float32)
+    vA = np.zeros(T, np.int32)
+    acc = ctypes.c_int32()
+    a.ids, a.out, a.vA, a.accepted = ids.ctypes.data, out.ctypes.data, vA.ctypes.data, ctypes.addressof(acc)
+    s0 = args.warmup
+    # one untimed warm-up step, then as many steps as fit in the time budget
+    steps, agree, t_total = 0, 0, 0.0
+    s = s0
+    while True:
+        xi = np.ascontiguousarray(x_np[s])
+        di = np.ascontiguousarray(dr[s])
+        a.x, a.drafts = xi.ctypes.data, di.ctypes.data
+        t0 = time.perf_counter()
+        lib.qwr_cpu_verify_step(ctypes.byref(a))
+        dt = time.perf_counter() - t0
+        if s > s0:
+            t_total += dt
+            steps += 1
+        agree += int(np.array_equal(np.sort(ids, 1), np.sort(ids_ref[s], 1)) and np.array_equal(vA, res_ref[s][:T]))
+        s = s0 + (s - s0 + 1) % args.steps
+        if t_total >= args.cpu_seconds or steps >= 2000:
+            break
+    return {"value": T * steps / t_total, "unit": "tokens/s", "cores": threads, "kind": "reference",
+            "sample": f"{steps} verify steps ({t_total:.1f} s) of the same workload through the reference's "
+                      f"ggml-CPU kernels (x86-64 AVX-512 build, {threads} OpenMP threads); "
+                      f"{agree}/{steps + 1} steps gave the GPU's expert ids and argmaxes",
+            "ms_per_step": 1e3 * t_total / steps}
+
+
+if __name__ == "__main__":
+    main()

@@ -138,6 +138,25 @@ size_t qwm_verify_workspace_size(const qwm_tensor * lm_head, int64_t T);
 int qwm_verify_accept(const qwm_tensor * lm_head, const qwm_tensor * x, const float * norm_w, float eps,
                       const int32_t * drafts, int32_t * result, void * workspace, size_t ws_bytes, void * stream);
 
+/* ------------------------------------------------------- quantization --- */
+
+/* Model-file quantization on the device, as ggml_quantize_chunk does it
+ * without an importance matrix: Q4_K = quantize_row_q4_K_ref
+ * (ggml-quants.c:1458-1528), Q8_0 = quantize_row_q8_0_ref (276-300).
+ * src: f32 [n] (n a multiple of the block length); dst: n / block * bytes. */
+int qwm_quantize(int32_t type, const float * src, void * dst, int64_t n, void * stream);
+
+/* -------------------------------------------------------- measurement --- */
+
+/* Brackets each of the next `max_launches` launches of one kernel with a
+ * hipEvent pair on the stream it runs on.  Kernel names: "route_logits",
+ * "route_select", "gate_up", "down", "combine", "vhead_prep", "lm_head",
+ * "accept", "mul_mat_id_prep", "mul_mat_id".  Owner thread only. */
+int qwm_profile_start(const char * kernel, int32_t max_launches);
+/* Waits for the recorded events, writes each launch's duration in ms and
+ * returns how many launches were timed (stops the profiling). */
+int qwm_profile_stop(float * durations_ms, int32_t capacity);
+
 /* ---------------------------------------------------------- slot pool --- */
 
 /* ExpertCache's RAM-tier decisions (core/expert_cache.cpp: ensure 1615-1645,

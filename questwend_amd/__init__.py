@@ -95,6 +95,9 @@ def lib():
         "qwm_pool_slot_of_row": (ctypes.c_int, [_P, _I32, _I32, _P]),
         "qwm_pool_slots": (ctypes.c_int, [_P, _I32, _P, _P]),
         "qwm_slab_fetch_async": (ctypes.c_int, [_P, _SZ, _I32, _P, _P, _P]),
+        "qwm_quantize": (ctypes.c_int, [_I32, _P, _P, _I64, _P]),
+        "qwm_profile_start": (ctypes.c_int, [ctypes.c_char_p, _I32]),
+        "qwm_profile_stop": (ctypes.c_int, [_P, _I32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

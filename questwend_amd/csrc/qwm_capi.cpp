@@ -6,6 +6,7 @@
 #include <algorithm>
 #include <cstring>
 #include <string>
+#include <vector>
 
 #include "qwm_internal.h"
 
@@ -48,6 +49,25 @@ static bool fully_contiguous(const qwm_tensor * t) {
     return t->nb[2] == t->nb[1] * (size_t)t->ne[1] && t->nb[3] == t->nb[2] * (size_t)t->ne[2];
 }
 
+// ---- per-kernel event timing ----
+struct Profile {
+    std::string kernel;
+    std::vector<hipEvent_t> ev;    // start/stop pairs
+    int used = 0;
+    bool open = false;
+};
+static Profile g_prof;
+
+void prof_begin(const char * kernel, hipStream_t s) {
+    if (!g_prof.open || g_prof.kernel != kernel || 2 * g_prof.used + 1 >= (int)g_prof.ev.size()) return;
+    (void)hipEventRecord(g_prof.ev[2 * g_prof.used], s);
+}
+void prof_end(const char * kernel, hipStream_t s) {
+    if (!g_prof.open || g_prof.kernel != kernel || 2 * g_prof.used + 1 >= (int)g_prof.ev.size()) return;
+    (void)hipEventRecord(g_prof.ev[2 * g_prof.used + 1], s);
+    g_prof.used++;
+}
+
 }  // namespace qwm
 
 using namespace qwm;
@@ -71,6 +91,36 @@ const char * qwm_last_error(void) { return g_last_error.c_str(); }
 int qwm_workspace_init(void * workspace, size_t bytes, void * stream) {
     if (!workspace && bytes) return fail(QWM_ERR_ARG, "workspace is NULL");
     return launch_fill_zero(workspace, bytes & ~(size_t)3, (hipStream_t)stream);
+}
+
+int qwm_quantize(int32_t type, const float * src, void * dst, int64_t n, void * stream) {
+    if (type != T_Q4_K && type != T_Q8_0) return fail(QWM_ERR_UNSUPPORTED, "quantize: only Q4_K and Q8_0");
+    if (!src || !dst || n < 0 || n % block_len(type)) return fail(QWM_ERR_ARG, "quantize: bad arguments");
+    return launch_quantize(type, src, dst, n, (hipStream_t)stream);
+}
+
+int qwm_profile_start(const char * kernel, int32_t max_launches) {
+    if (!kernel || max_launches < 1) return fail(QWM_ERR_ARG, "profile_start: bad arguments");
+    for (hipEvent_t e : g_prof.ev) (void)hipEventDestroy(e);
+    g_prof.ev.assign(2 * (size_t)max_launches, nullptr);
+    for (auto & e : g_prof.ev) QWM_HIP_CHECK(hipEventCreate(&e));
+    g_prof.kernel = kernel;
+    g_prof.used = 0;
+    g_prof.open = true;
+    return QWM_OK;
+}
+
+int qwm_profile_stop(float * durations_ms, int32_t capacity) {
+    if (!g_prof.open) return fail(QWM_ERR_STATE, "profile_stop: profiling was not started");
+    g_prof.open = false;
+    const int n = std::min(g_prof.used, capacity);
+    for (int i = 0; i < n; ++i) {
+        QWM_HIP_CHECK(hipEventSynchronize(g_prof.ev[2 * i + 1]));
+        float ms = 0.f;
+        QWM_HIP_CHECK(hipEventElapsedTime(&ms, g_prof.ev[2 * i], g_prof.ev[2 * i + 1]));
+        if (durations_ms) durations_ms[i] = ms;
+    }
+    return n;
 }
 
 // ------------------------------------------------------------ mul_mat_id --

@@ -94,4 +94,17 @@ int launch_verify(const uint8_t * lm_head, const float * x, const float * norm_w
 
 int launch_fill_zero(void * p, size_t bytes, hipStream_t s);
 
+// ---- qwm_quant.hip ----
+int launch_quantize(int32_t type, const float * src, void * dst, int64_t n, hipStream_t s);
+
+// ---- per-kernel event timing (qwm_capi.cpp) ----
+void prof_begin(const char * kernel, hipStream_t s);
+void prof_end(const char * kernel, hipStream_t s);
+#define QWM_TIMED(NAME, STREAM, ...)       \
+    do {                                   \
+        ::qwm::prof_begin(NAME, STREAM);   \
+        __VA_ARGS__;                       \
+        ::qwm::prof_end(NAME, STREAM);     \
+    } while (0)
+
 }  // namespace qwm

@@ -583,8 +583,8 @@ int launch_route(const RouteArgs & a, const MoePlan & p, uint8_t * ws, int32_t *
     float * logits = reinterpret_cast<float *>(ws + p.logits);
     float * sh = reinterpret_cast<float *>(ws + p.sh_gate);
     const int rows = (int)a.E + (a.sh_gate_inp ? 1 : 0);
-    k_route_logits<<<dim3((rows + 3) / 4), dim3(256), 0, s>>>(a.W, a.x, a.rm, a.sh_gate_inp, logits, sh + p.T,
-                                                               (int)a.E, (int)a.H, (int)a.T);
+    QWM_TIMED("route_logits", s, k_route_logits<<<dim3((rows + 3) / 4), dim3(256), 0, s>>>(
+                                      a.W, a.x, a.rm, a.sh_gate_inp, logits, sh + p.T, (int)a.E, (int)a.H, (int)a.T));
     SelectArgs sa;
     sa.logits = logits; sa.sh_logit = sh + p.T; sa.x = a.x;
     sa.E = (int)a.E; sa.H = (int)a.H; sa.T = (int)a.T; sa.k = (int)a.k; sa.norm = a.norm; sa.scale = a.scale;
@@ -601,7 +601,7 @@ int launch_route(const RouteArgs & a, const MoePlan & p, uint8_t * ws, int32_t *
     sa.shared = p.shared ? 1 : 0;
     sa.slot_tables = a.slot_tables; sa.table_stride = a.table_stride; sa.layer = a.layer;
     sa.slots_ws = reinterpret_cast<int32_t *>(ws + p.slots);
-    k_route_select<<<dim3((unsigned)a.T), dim3(64), 0, s>>>(sa);
+    QWM_TIMED("route_select", s, k_route_select<<<dim3((unsigned)a.T), dim3(64), 0, s>>>(sa));
     QWM_HIP_CHECK(hipGetLastError());
     return QWM_OK;
 }
@@ -659,11 +659,13 @@ int launch_experts(const ExpertArgs & a, const MoePlan & p, uint8_t * ws, hipStr
     const int rows_g = (int)std::max(p.N, p.N_sh);
     const int tile_g = 4 * GEMV_STEPS * (WAVE / lg);
     dim3 grid_g((rows_g + tile_g - 1) / tile_g, grid_y);
+    prof_begin("gate_up", s);
     switch (lg) {
         case 16: launch_gateup_lpr<16>(g, maxp, grid_g, s); break;
         case 32: launch_gateup_lpr<32>(g, maxp, grid_g, s); break;
         default: launch_gateup_lpr<64>(g, maxp, grid_g, s); break;
     }
+    prof_end("gate_up", s);
 
     DownArgs d;
     d.down = a.down; d.down_slab = a.down_slab; d.sh_down = a.sh_down;
@@ -679,15 +681,17 @@ int launch_experts(const ExpertArgs & a, const MoePlan & p, uint8_t * ws, hipStr
         return fail(QWM_ERR_UNSUPPORTED, "shared and routed FFN sizes need the same tiling");
     const int tile_d = 4 * GEMV_STEPS * (WAVE / ld);
     dim3 grid_d(((int)p.H + tile_d - 1) / tile_d, grid_y);
+    prof_begin("down", s);
     switch (ld) {
         case 16: launch_down_lpr<16>(d, maxp, grid_d, s); break;
         case 32: launch_down_lpr<32>(d, maxp, grid_d, s); break;
         default: launch_down_lpr<64>(d, maxp, grid_d, s); break;
     }
+    prof_end("down", s);
 
-    k_combine<<<dim3((unsigned)((p.H + 255) / 256), (unsigned)p.T), 256, 0, s>>>(
+    QWM_TIMED("combine", s, k_combine<<<dim3((unsigned)((p.H + 255) / 256), (unsigned)p.T), 256, 0, s>>>(
         d.ex, d.ex_sh, reinterpret_cast<const float *>(a.weights), p.shared_gate ? reinterpret_cast<const float *>(ws + p.sh_gate) : nullptr,
-        a.resid, a.out, (int)p.H, (int)p.T, (int)p.k, p.shared ? 1 : 0);
+        a.resid, a.out, (int)p.H, (int)p.T, (int)p.k, p.shared ? 1 : 0));
     QWM_HIP_CHECK(hipGetLastError());
     return QWM_OK;
 }
@@ -848,7 +852,7 @@ int launch_mmid(const MmidArgs & a, uint8_t * ws, hipStream_t s) {
     pr.n_units = reinterpret_cast<int32_t *>(ws + o_n); pr.err = pr.n_units + 1;
     pr.ids_ws = reinterpret_cast<int32_t *>(ws + o_ids);
     const int nblk = (int)(rows * (a.K / QK_K));
-    k_mmid_prep<<<dim3((unsigned)std::max(1, std::min(256, (nblk + 3) / 4))), 256, 0, s>>>(pr);
+    QWM_TIMED("mul_mat_id_prep", s, k_mmid_prep<<<dim3((unsigned)std::max(1, std::min(256, (nblk + 3) / 4))), 256, 0, s>>>(pr));
     MmidGemv g;
     g.as = a.as; g.slab = a.slab; g.row_bytes = (size_t)(a.K / QK_K) * 144;
     g.units = pr.units; g.n_units = pr.n_units; g.qs = pr.qs; g.d = pr.d; g.bs = pr.bs;
@@ -866,11 +870,13 @@ int launch_mmid(const MmidArgs & a, uint8_t * ws, hipStream_t s) {
         case 4: QWM_MMID(LPR_, 4); break;                   \
         default: QWM_MMID(LPR_, 8); break;                  \
     }
+    prof_begin("mul_mat_id", s);
     switch (lpr) {
         case 16: QWM_MMID_P(16); break;
         case 32: QWM_MMID_P(32); break;
         default: QWM_MMID_P(64); break;
     }
+    prof_end("mul_mat_id", s);
 #undef QWM_MMID_P
 #undef QWM_MMID
     QWM_HIP_CHECK(hipGetLastError());

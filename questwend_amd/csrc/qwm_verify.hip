@@ -202,8 +202,9 @@ int launch_verify(const uint8_t * lm_head, const float * x, const float * norm_w
     float * hd = reinterpret_cast<float *>(ws + p.hq + align_up((size_t)p.T * p.H, 16));
     float * pv = reinterpret_cast<float *>(ws + p.partial_v);
     int32_t * pi = reinterpret_cast<int32_t *>(ws + p.partial_i);
-    k_vhead_prep<<<dim3((unsigned)p.T), 256, 0, s>>>(x, norm_w, eps, (int)p.H, hq, hd);
+    QWM_TIMED("vhead_prep", s, k_vhead_prep<<<dim3((unsigned)p.T), 256, 0, s>>>(x, norm_w, eps, (int)p.H, hq, hd));
     const dim3 grid((unsigned)p.n_wg);
+    prof_begin("lm_head", s);
     switch (p.T) {
         case 1: k_lmhead_argmax<1><<<grid, 256, 0, s>>>(lm_head, (int)p.H, (int)p.V, hq, hd, pv, pi); break;
         case 2: k_lmhead_argmax<2><<<grid, 256, 0, s>>>(lm_head, (int)p.H, (int)p.V, hq, hd, pv, pi); break;
@@ -214,7 +215,8 @@ int launch_verify(const uint8_t * lm_head, const float * x, const float * norm_w
         case 7: k_lmhead_argmax<7><<<grid, 256, 0, s>>>(lm_head, (int)p.H, (int)p.V, hq, hd, pv, pi); break;
         default: k_lmhead_argmax<8><<<grid, 256, 0, s>>>(lm_head, (int)p.H, (int)p.V, hq, hd, pv, pi); break;
     }
-    k_accept<<<1, 512, 0, s>>>(pv, pi, p.n_wg, (int)p.T, drafts, result);
+    prof_end("lm_head", s);
+    QWM_TIMED("accept", s, k_accept<<<1, 512, 0, s>>>(pv, pi, p.n_wg, (int)p.T, drafts, result));
     QWM_HIP_CHECK(hipGetLastError());
     return QWM_OK;
 }

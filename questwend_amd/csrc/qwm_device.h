@@ -99,6 +99,24 @@ QWM_DEV float group_max(float v) {
     return v;
 }
 
+// DPP lane moves (no LDS round trip).  Controls: quad_perm [1,0,3,2] = 0xB1,
+// quad_perm [2,3,0,1] = 0x4E, row_half_mirror = 0x141, row_mirror = 0x140.
+template <int CTRL>
+QWM_DEV float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+// Every lane of each 16-lane row receives the sum over that row.
+QWM_DEV float row16_sum(float v) {
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    v += dpp_f<0x141>(v);
+    v += dpp_f<0x140>(v);
+    return v;
+}
+QWM_DEV float readlane_f(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+
 // The 16-lane halving tree of _mm512_reduce_add_ps (gcc: lanes i+8, i+4, i+2,
 // i+1).  An xor butterfly produces the same sums in every lane of the group.
 QWM_DEV float tree16(float v) {

@@ -133,7 +133,9 @@ int qwm_moe_block_resident(const qwm_moe_layer * layer, int32_t layer_index, con
  *   vA[t] = argmax(logits[:, t])  (last index among equal maxima)
  *   a = longest prefix with vA[j] == drafts[j], j < n_draft;  x_new = vA[a]
  * x: f32 [H, T]; norm_w: optional f32 [H]; drafts: device i32 [n_draft]
- * (n_draft = T - 1); result: device i32 [T + 2] = vA[0..T-1], a, x_new. */
+ * (n_draft = T - 1); result: device i32 [T + 2] = vA[0..T-1], a, x_new.
+ * Supported: H in {512, 1024, 1536, 2048}, 1 <= T <= 8; x and norm_w 16-byte
+ * aligned, lm_head 4-byte aligned with contiguous rows. */
 size_t qwm_verify_workspace_size(const qwm_tensor * lm_head, int64_t T);
 int qwm_verify_accept(const qwm_tensor * lm_head, const qwm_tensor * x, const float * norm_w, float eps,
                       const int32_t * drafts, int32_t * result, void * workspace, size_t ws_bytes, void * stream);

@@ -331,6 +331,7 @@ int qwm_verify_accept(const qwm_tensor * lm_head, const qwm_tensor * x, const fl
     if (x->type != T_F32 || x->ne[0] != p.H || !fully_contiguous(x)) return fail(QWM_ERR_ARG, "verify: x must be contiguous f32 [H, T]");
     if (p.T > 1 && !drafts) return fail(QWM_ERR_ARG, "verify: drafts are NULL");
     if ((uintptr_t)x->data % 16 || (uintptr_t)norm_w % 16) return fail(QWM_ERR_ARG, "verify: x and norm_w must be 16-byte aligned");
+    if ((uintptr_t)lm_head->data % 4) return fail(QWM_ERR_ARG, "verify: lm_head data must be 4-byte aligned");
     if (!workspace || ws_bytes < p.total) return fail(QWM_ERR_WORKSPACE, "verify: workspace too small");
     return launch_verify((const uint8_t *)lm_head->data, (const float *)x->data, norm_w, eps, drafts, result, p,
                          (uint8_t *)workspace, (hipStream_t)stream);

@@ -127,6 +127,33 @@ QWM_DEV float tree16(float v) {
     return v;
 }
 
+// ------------------------------------------------ cross-workgroup hand-off --
+// Some kernels let their last workgroup to finish (ticket == gridDim - 1)
+// consume what the others wrote.  A __threadfence() there would write back
+// and invalidate the issuing XCD's whole L2 once per workgroup, stalling every
+// wave that streams through it, so the hand-off data is written and read with
+// agent-scope atomic accesses instead (coherent across the XCDs' L2s with no
+// cache maintenance) and each wave drains its own writes before the ticket.
+template <typename T>
+QWM_DEV void st_agent(T * p, T v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+template <typename T>
+QWM_DEV T ld_agent(const T * p) { return __hip_atomic_load(const_cast<T *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+// Every thread calls this after its st_agent writes; true in all threads of
+// the last workgroup, which also re-arms the counter for the next launch.
+QWM_DEV bool last_workgroup(int32_t * counter) {
+    __shared__ int s_last;
+    __builtin_amdgcn_s_waitcnt(0);               // this wave's writes have completed
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int n = (int)(gridDim.x * gridDim.y * gridDim.z);
+        const int ticket = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = ticket == n - 1;
+        if (s_last) st_agent(counter, 0);
+    }
+    __syncthreads();
+    return s_last;
+}
+
 // Argmax over a wave where ties take the larger index (ggml-cpu/vec.h:1618-1626
 // keeps the last maximum); NaN never wins.
 QWM_DEV void wave_argmax_last(float & v, int & idx) {

@@ -142,7 +142,6 @@ struct SelectArgs {
 __global__ void __launch_bounds__(64) k_route_select(SelectArgs a) {
     __shared__ float probs[MAX_E];
     __shared__ int32_t sel[MAX_K];
-    __shared__ int last;
     const int t = blockIdx.x, lane = threadIdx.x;
     const int E = a.E, k = a.k;
     const float * lt = a.logits + (size_t)t * E;
@@ -204,7 +203,7 @@ __global__ void __launch_bounds__(64) k_route_select(SelectArgs a) {
         if (a.scale != 0.0f && a.scale != 1.0f)
             for (int j = 0; j < k; ++j) w[j] = w[j] * a.scale;
         for (int j = 0; j < k; ++j) {
-            a.ids_ws[t * k + j] = sel[j];
+            st_agent(a.ids_ws + t * k + j, sel[j]);
             a.w_ws[t * k + j] = w[j];
             if (a.ids_out) a.ids_out[(size_t)t * a.ids_ld + j] = sel[j];
             if (a.w_out) a.w_out[(size_t)t * a.w_ld + j] = w[j];
@@ -218,15 +217,11 @@ __global__ void __launch_bounds__(64) k_route_select(SelectArgs a) {
                            a.xq_d + (size_t)t * nb + b, a.xq_bs + (size_t)t * (a.H / 16) + b * 16, lane);
 
     // ---- last block: expert union + slot remap ----
-    __threadfence();
-    __syncthreads();
-    if (lane == 0) last = atomicAdd(a.counter, 1) == (int)gridDim.x - 1;
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
+    if (!last_workgroup(a.counter)) return;
     const int P = a.T * k;
-    __shared__ int32_t first[MAX_PAIRS], uidx[MAX_PAIRS];
-    volatile const int32_t * ids = a.ids_ws;
+    __shared__ int32_t first[MAX_PAIRS], uidx[MAX_PAIRS], ids[MAX_PAIRS];
+    for (int p = lane; p < P; p += 64) ids[p] = ld_agent(a.ids_ws + p);
+    __syncthreads();
     for (int p = lane; p < P; p += 64) {
         const int e = ids[p];
         int f = p;
@@ -268,10 +263,7 @@ __global__ void __launch_bounds__(64) k_route_select(SelectArgs a) {
         u.n = a.T;
         for (int i = 0; i < a.T; ++i) u.pair[i] = i;
     }
-    if (lane == 0) {
-        *a.n_units = nu;
-        *a.counter = 0;
-    }
+    if (lane == 0) *a.n_units = nu;
 }
 
 // ======================================================================

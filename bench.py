@@ -140,7 +140,7 @@ def main():
 
     # secondary kernels (untimed pass, same steps)
     kern = {}
-    for name in ["gate_up", "down", "route_logits", "route_select", "combine", "vhead_prep", "accept"]:
+    for name in ["route", "gate_up", "down"]:
         qa.check(L.qwm_profile_start(name.encode(), args.steps))
         for s in range(args.warmup, n_all):
             step(s)

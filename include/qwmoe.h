@@ -97,7 +97,8 @@ typedef struct qwm_moe_layer {
  *   ids = top-k(probs) [k, T];   w = probs[ids] (/ clamp(sum, 6.1035e-5) if norm)
  * x: f32 [H, T]; rm: optional f32 [E, T] added to the logits; ids_out: i32
  * [k, T]; w_out: f32 [k, T].  The top-k keeps the lower expert index on exact
- * probability ties (std::sort leaves their order unspecified).  T <= 8. */
+ * probability ties (std::sort leaves their order unspecified).  T <= 8.
+ * Activation tensors (x, out, resid) must be 16-byte aligned. */
 size_t qwm_moe_workspace_size(const qwm_moe_layer * layer, int64_t T);
 int qwm_moe_route(const qwm_moe_layer * layer, const qwm_tensor * x, const qwm_tensor * rm,
                   qwm_tensor * ids_out, qwm_tensor * w_out, void * workspace, size_t ws_bytes, void * stream);

@@ -205,6 +205,7 @@ static int check_layer(const qwm_moe_layer * L, int64_t T, MoePlan & p) {
 static int check_act(const qwm_tensor * x, int64_t H, const char * what) {
     if (!x || !x->data) return fail(QWM_ERR_ARG, std::string("moe: ") + what + " is NULL");
     if (x->type != T_F32 || x->ne[0] != H || !fully_contiguous(x)) return fail(QWM_ERR_ARG, std::string("moe: ") + what + " must be contiguous f32 [H, T]");
+    if ((uintptr_t)x->data % 16) return fail(QWM_ERR_ARG, std::string("moe: ") + what + " must be 16-byte aligned");
     return QWM_OK;
 }
 

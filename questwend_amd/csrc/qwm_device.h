@@ -113,6 +113,66 @@ QWM_DEV float row16_sum(float v) {
     v += dpp_f<0x140>(v);
     return v;
 }
+// Value of lane ^ 16 / lane ^ 32 without LDS: the gfx950 permlane swaps
+// exchange rows 0<->1, 2<->3 (16-lane rows) or the two wave halves.
+QWM_DEV uint32_t lane_xor16(uint32_t v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (threadIdx.x & 16) ? r[0] : r[1];
+}
+QWM_DEV uint32_t lane_xor32(uint32_t v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (threadIdx.x & 32) ? r[0] : r[1];
+}
+QWM_DEV float lane_xor16_f(float v) { return __uint_as_float(lane_xor16(__float_as_uint(v))); }
+QWM_DEV float lane_xor32_f(float v) { return __uint_as_float(lane_xor32(__float_as_uint(v))); }
+template <int CTRL>
+QWM_DEV int dpp_i(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false); }
+
+// Sum over aligned groups of W lanes (16, 32 or 64), available in every lane
+// of the group.  Quad butterflies, then rotations by 4 and 8 inside the
+// 16-lane row, then the permlane swaps.  The grouping of the additions differs
+// between the four quads of a row, so lanes may differ in the last bit: use
+// one lane's result.
+template <int W>
+QWM_DEV float lane_sum(float v) {
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    v += dpp_f<0x124>(v);
+    v += dpp_f<0x128>(v);
+    if (W >= 32) v += lane_xor16_f(v);
+    if (W >= 64) v += lane_xor32_f(v);
+    return v;
+}
+template <int W>
+QWM_DEV int lane_sum_i(int v) {
+    v += dpp_i<0xB1>(v);
+    v += dpp_i<0x4E>(v);
+    v += dpp_i<0x124>(v);
+    v += dpp_i<0x128>(v);
+    if (W >= 32) v += (int)lane_xor16((uint32_t)v);
+    if (W >= 64) v += (int)lane_xor32((uint32_t)v);
+    return v;
+}
+// Wave maximum (exact: every lane gets the same value).
+QWM_DEV float wave_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x124>(v));
+    v = fmaxf(v, dpp_f<0x128>(v));
+    v = fmaxf(v, lane_xor16_f(v));
+    return fmaxf(v, lane_xor32_f(v));
+}
+// _mm512_reduce_add_ps's halving tree (pairs i+8, i+4, i+2, i+1) within each
+// 16-lane row, bit-identical in every lane: after the rotation by 8 the row
+// has period 8, so the rotation by 4 pairs lane i with i^4 (mod 8), and so on.
+QWM_DEV float tree16_dpp(float v) {
+    v += dpp_f<0x128>(v);
+    v += dpp_f<0x124>(v);
+    v += dpp_f<0x122>(v);
+    v += dpp_f<0x121>(v);
+    return v;
+}
+
 QWM_DEV float readlane_f(float v, int l) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
 }
@@ -138,20 +198,48 @@ template <typename T>
 QWM_DEV void st_agent(T * p, T v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 template <typename T>
 QWM_DEV T ld_agent(const T * p) { return __hip_atomic_load(const_cast<T *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-// Every thread calls this after its st_agent writes; true in all threads of
-// the last workgroup, which also re-arms the counter for the next launch.
-QWM_DEV bool last_workgroup(int32_t * counter) {
+// Every thread of the n participating workgroups calls this after its
+// st_agent writes; true in all threads of the last one to arrive, which also
+// re-arms the counter for the next launch.
+QWM_DEV bool last_workgroup(int32_t * counter, int n) {
     __shared__ int s_last;
     __builtin_amdgcn_s_waitcnt(0);               // this wave's writes have completed
     __syncthreads();
     if (threadIdx.x == 0) {
-        const int n = (int)(gridDim.x * gridDim.y * gridDim.z);
         const int ticket = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_last = ticket == n - 1;
         if (s_last) st_agent(counter, 0);
     }
     __syncthreads();
     return s_last;
+}
+QWM_DEV bool last_workgroup(int32_t * counter) {
+    return last_workgroup(counter, (int)(gridDim.x * gridDim.y * gridDim.z));
+}
+
+// Orders LDS traffic between the lanes of one wave (no workgroup barrier).
+QWM_DEV void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Wave-wide best (v, i) under "larger v, then smaller i" (a total order, so
+// the rotation all-reduce is exact); every lane receives the winner.
+QWM_DEV void wave_best_first(float & v, int & i) {
+#define QWM_BEST_STEP(MOVE_F, MOVE_I)                                     \
+    {                                                                     \
+        const float ov = MOVE_F;                                          \
+        const int oi = MOVE_I;                                            \
+        if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }            \
+    }
+    QWM_BEST_STEP(dpp_f<0xB1>(v), dpp_i<0xB1>(i))
+    QWM_BEST_STEP(dpp_f<0x4E>(v), dpp_i<0x4E>(i))
+    QWM_BEST_STEP(dpp_f<0x124>(v), dpp_i<0x124>(i))
+    QWM_BEST_STEP(dpp_f<0x128>(v), dpp_i<0x128>(i))
+    QWM_BEST_STEP(lane_xor16_f(v), (int)lane_xor16((uint32_t)i))
+    QWM_BEST_STEP(lane_xor32_f(v), (int)lane_xor32((uint32_t)i))
+#undef QWM_BEST_STEP
 }
 
 // Argmax over a wave where ties take the larger index (ggml-cpu/vec.h:1618-1626

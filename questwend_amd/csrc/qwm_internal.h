@@ -24,6 +24,7 @@ int fail(int code, const std::string & msg);
     } while (0)
 
 constexpr int MAX_T = 8;        // tokens per GEMV batch (decode / verify)
+constexpr int MAX_TILES = 256;  // row tiles of the down projection (combine tickets)
 constexpr int MAX_K = 16;       // experts per token
 constexpr int MAX_E = 2048;     // experts per layer
 constexpr int MAX_PAIRS = MAX_T * MAX_K;
@@ -42,7 +43,7 @@ struct Unit {
 struct MoePlan {
     int64_t H, N, N_sh, E, k, T;
     bool shared, shared_gate;
-    size_t counters, logits, ids, w, slots, sh_gate, units, n_units;
+    size_t counters, tile_counters, logits, ids, w, slots, sh_gate, units, n_units;
     size_t xq_qs, xq_d, xq_bs, act, act_sh, ex, ex_sh;
     size_t total;
 };

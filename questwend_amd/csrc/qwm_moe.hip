@@ -17,68 +17,8 @@
 namespace qwm {
 
 // ======================================================================
-// Router
+// Router: logits, soft_max, top-k, weights, Q8_K of x, expert schedule
 // ======================================================================
-
-// logits[t][e] = router[e] . x[t] (+ rm[t][e]).  One wave per row.
-//   T == 1 (or a row count that is not a multiple of 4): ggml_vec_dot_f32's
-//     AVX-512 order (ggml-cpu/vec.cpp:11-135): lane L = 16*j + l accumulates
-//     fma over 64-wide steps, then (j0+j2, j1+j3, 0+1) and the 16-lane tree.
-//   T >= 2: llamafile tinyBLAS<16, __m512> order (sgemm.cpp:600-670): one
-//     16-lane fma accumulator over 16-wide steps, then the 16-lane tree.
-// Row E (when sh_gate_inp is set) is the shared-expert gate: a single-row
-// mul_mat, which ggml-CPU always runs through vec_dot_f32.
-__global__ void __launch_bounds__(256) k_route_logits(const float * __restrict__ W, const float * __restrict__ x,
-                                                       const float * __restrict__ rm, const float * __restrict__ sgi,
-                                                       float * __restrict__ logits, float * __restrict__ sh_logit,
-                                                       int E, int H, int T) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int e = blockIdx.x * 4 + wave;
-    if (e > E || (e == E && !sgi)) return;
-    const float * w = (e < E) ? W + (size_t)e * H : sgi;
-    const bool tiny = (e < E) && T >= 2 && (E % 4) == 0;
-    if (!tiny) {
-        const int np = H & ~63;
-        for (int t = 0; t < T; ++t) {
-            const float * xt = x + (size_t)t * H;
-            float acc = 0.f;
-#pragma unroll 8
-            for (int i = 0; i < np; i += 64) acc = __builtin_fmaf(w[i + lane], xt[i + lane], acc);
-            acc += __shfl_xor(acc, 32, WAVE);
-            acc += __shfl_xor(acc, 16, WAVE);
-            acc = tree16(acc);
-            if (lane == 0) {
-                // scalar tail as gcc -O3 vectorizes it: unfused 16/8-groups, then fma
-                float s = acc;
-                int i = np;
-                for (; H - i >= 16; i += 16)
-                    for (int l = 0; l < 16; ++l) s = s + w[i + l] * xt[i + l];
-                if (H - i >= 8) {
-                    for (int l = 0; l < 8; ++l) s = s + w[i + l] * xt[i + l];
-                    i += 8;
-                }
-                for (; i < H; ++i) s = __builtin_fmaf(w[i], xt[i], s);
-                if (e < E) logits[(size_t)t * E + e] = rm ? s + rm[(size_t)t * E + e] : s;
-                else sh_logit[t] = s;
-            }
-        }
-    } else {
-        const int l = lane & 15, tg = lane >> 4;
-        for (int t0 = 0; t0 < T; t0 += 4) {
-            const int t = t0 + tg;
-            float acc = 0.f;
-            if (t < T) {
-                const float * xt = x + (size_t)t * H;
-                int i = 0;
-#pragma unroll 8
-                for (; i + 16 <= H; i += 16) acc = __builtin_fmaf(w[i + l], xt[i + l], acc);
-                if (i + l < H) acc = __builtin_fmaf(w[i + l], xt[i + l], acc);
-            }
-            acc = tree16(acc);
-            if (l == 0 && t < T) logits[(size_t)t * E + e] = rm ? acc + rm[(size_t)t * E + e] : acc;
-        }
-    }
-}
 
 // Q8_K quantization of one 256-value block by one wave (ggml-quants.c:2769-2806):
 // lane L owns values 4L..4L+3.  max = the signed value of the first largest
@@ -86,23 +26,19 @@ __global__ void __launch_bounds__(256) k_route_logits(const float * __restrict__
 // d = 1/iscale.  Writes qs (256 B), d, and the 16 bsums (as int32).
 QWM_DEV void quantize_block_q8K(const float * __restrict__ src, int8_t * __restrict__ qs, float * __restrict__ d_out,
                                 int32_t * __restrict__ bs_out, int lane) {
-    float v[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = src[4 * lane + i];
+    const float4 v4 = reinterpret_cast<const float4 *>(src)[lane];
+    const float v[4] = {v4.x, v4.y, v4.z, v4.w};
     float a = __builtin_fabsf(v[0]);
     int ii = 0;
 #pragma unroll
     for (int i = 1; i < 4; ++i)
         if (__builtin_fabsf(v[i]) > a) { a = __builtin_fabsf(v[i]); ii = i; }
     int idx = 4 * lane + ii;
-    float mx = v[ii];
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float oa = __shfl_xor(a, o, WAVE);
-        const int oi = __shfl_xor(idx, o, WAVE);
-        const float om = __shfl_xor(mx, o, WAVE);
-        if (oa > a || (oa == a && oi < idx)) { a = oa; idx = oi; mx = om; }
-    }
+    wave_best_first(a, idx);
+    idx = __builtin_amdgcn_readfirstlane(idx);
+    const int c = idx & 3;
+    const float mine = c == 0 ? v[0] : c == 1 ? v[1] : c == 2 ? v[2] : v[3];
+    const float mx = readlane_f(mine, idx >> 2);
     int q[4] = {0, 0, 0, 0};
     float d = 0.f;
     if (a != 0.f) {
@@ -114,16 +50,19 @@ QWM_DEV void quantize_block_q8K(const float * __restrict__ src, int8_t * __restr
     const uint32_t packed = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) |
                             ((uint32_t)(q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24);
     reinterpret_cast<uint32_t *>(qs)[lane] = packed;
-    int s = q[0] + q[1] + q[2] + q[3];
-    s += __shfl_xor(s, 1, WAVE);
-    s += __shfl_xor(s, 2, WAVE);
-    if ((lane & 3) == 0) bs_out[lane >> 2] = s;
+    int sm = q[0] + q[1] + q[2] + q[3];
+    sm += dpp_i<0xB1>(sm);
+    sm += dpp_i<0x4E>(sm);
+    if ((lane & 3) == 0) bs_out[lane >> 2] = sm;
     if (lane == 0) *d_out = d;
 }
 
-struct SelectArgs {
-    const float * logits; const float * sh_logit; const float * x;
+struct RouteKArgs {
+    const float * W; const float * x; const float * rm; const float * sgi;
     int E, H, T, k, norm; float scale;
+    int tiny;                                        // tinyBLAS order (T >= 2, E % 4 == 0)
+    int n_row_wg;                                    // workgroups holding router rows
+    float * logits; float * sh_logit;                // hand-off to the last workgroup
     int32_t * ids_ws; float * w_ws;                  // [T][k]
     int32_t * ids_out; int64_t ids_ld; float * w_out; int64_t w_ld;  // optional user copies
     float * sh_gate;                                 // [T] or null
@@ -133,113 +72,215 @@ struct SelectArgs {
     const int32_t * slot_tables; int64_t table_stride; int layer; int32_t * slots_ws;  // [3][T*k]
 };
 
-// One wave per token: soft_max (ggml-cpu/ops.cpp:5813-5920, vec.cpp:531 AVX-512:
-// v_expf over 16-lane chunks, each chunk summed with the 16-lane tree into a
-// double), top-k by probability (ties: lower expert index), weight gather,
-// normalization (double sum, clamp 6.103515625e-5, division) and scale; then
-// the token's Q8_K activations.  The last block to finish builds the union of
-// experts (first-occurrence order) and, in resident mode, the slot ids.
-__global__ void __launch_bounds__(64) k_route_select(SelectArgs a) {
-    __shared__ float probs[MAX_E];
-    __shared__ int32_t sel[MAX_K];
-    const int t = blockIdx.x, lane = threadIdx.x;
-    const int E = a.E, k = a.k;
-    const float * lt = a.logits + (size_t)t * E;
+constexpr int RX_PITCH = 132;           // LDS pitch of the transposed x rows (floats)
+constexpr int RT_MAX_S = 2048 / 16;     // 16-wide steps of one router row
 
-    float m = -__builtin_inff();
-    for (int i = lane; i < E; i += 64) m = fmaxf(m, lt[i]);
-    m = group_max<64>(m);
-    double sum = 0.0;
-    const int nfull = E & ~15;
-    for (int c = 0; c < nfull; c += 64) {
-        const int i = c + lane;
-        float v = 0.f;
-        if (i < nfull) { v = v_expf(lt[i] - m); probs[i] = v; }
-        const float cs = tree16(v);
-        for (int g = 0; g < 4; ++g)
-            if (c + 16 * g < nfull) sum += (double)__shfl(cs, 16 * g, WAVE);
-    }
-    for (int i = nfull; i < E; ++i) {           // scalar tail (libm expf on the CPU)
-        const float v = expf(lt[i] - m);
-        sum += (double)v;
-        if (lane == 0) probs[i] = v;
-    }
-    const float sc = (float)(1.0 / sum);
-    __syncthreads();
-    for (int i = lane; i < E; i += 64) probs[i] = probs[i] * sc;
-    __syncthreads();
+// One kernel for the whole routing step.
+//  * Router rows.  T >= 2: llamafile tinyBLAS<16, __m512> order (sgemm.cpp:
+//    600-670): per (row, token) sixteen fma accumulators over 16-wide steps,
+//    then the 16-lane tree; a wave holds 4 rows (lanes 16r + l) and all tokens,
+//    x comes from LDS transposed so lane l reads its stride-16 elements as
+//    128-bit words.  T == 1 (and the single shared-gate row, which ggml runs
+//    through vec_dot_f32): ggml_vec_dot_f32's AVX-512 order (ggml-cpu/vec.cpp:
+//    11-135), one row per wave: lane L = 16j + l accumulates over 64-wide
+//    steps, then (j0+j2, j1+j3, 0+1) and the 16-lane tree.
+//  * Q8_K of x, one 256-block per wave across the grid.
+//  * The last workgroup: per token soft_max (ggml-cpu/ops.cpp:5813-5920,
+//    vec.cpp:531 AVX-512: v_expf over 16-lane chunks, each chunk summed with
+//    the 16-lane tree into a double), top-k by probability (ties: lower expert
+//    index), weight gather, normalization (double sum, clamp 6.103515625e-5,
+//    division) and scale; then the expert union (first-occurrence order) and,
+//    in resident mode, the slot ids.
+__global__ void __launch_bounds__(256) k_route(RouteKArgs a) {
+    __shared__ __align__(16) float smem[MAX_T * 16 * RX_PITCH];   // transposed x; later per-wave probabilities
+    __shared__ int32_t s_ids[MAX_PAIRS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int E = a.E, H = a.H, T = a.T, k = a.k;
+    const int nsteps = H / 16;
 
-    // top-k: k rounds of a wave argmax (larger probability, then lower index)
-    uint32_t taken = 0;
-    for (int j = 0; j < k; ++j) {
-        float bv = -__builtin_inff();
-        int bi = 0x7fffffff;
-        int slot = 0;
-        for (int i = lane; i < E; i += 64, ++slot) {
-            if (taken & (1u << slot)) continue;
-            const float p = probs[i];
-            if (p > bv || (p == bv && i < bi)) { bv = p; bi = i; }
+    // ---- Q8_K of x (inputs of the expert GEMVs), spread over every wave
+    {
+        const int nb = H / QK_K;
+        for (int jb = blockIdx.x * 4 + wave; jb < T * nb; jb += gridDim.x * 4) {
+            const int t = jb / nb, b = jb % nb;
+            quantize_block_q8K(a.x + (size_t)t * H + b * QK_K, a.xq_qs + (size_t)t * H + b * QK_K,
+                               a.xq_d + (size_t)t * nb + b, a.xq_bs + (size_t)t * (H / 16) + b * 16, lane);
         }
+    }
+
+    if (blockIdx.x < a.n_row_wg && a.tiny) {
+        // all weight loads first (one round trip), then x into LDS
+        const int l = lane & 15, r = lane >> 4;
+        const int e = blockIdx.x * 16 + wave * 4 + r;
+        const int ec = min(e, E - 1);
+        const float * w = a.W + (size_t)ec * H;
+        float wv[RT_MAX_S];
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const float ov = __shfl_xor(bv, o, WAVE);
-            const int oi = __shfl_xor(bi, o, WAVE);
-            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        for (int st = 0; st < RT_MAX_S; ++st)
+            if (st < nsteps) wv[st] = w[16 * st + l];
+        for (int q = tid; q < T * H / 4; q += 256) {
+            const float4 v = reinterpret_cast<const float4 *>(a.x)[q];
+            const int t = (4 * q) / H, h = (4 * q) % H;
+            float * row = smem + (size_t)t * 16 * RX_PITCH;
+            row[((h + 0) & 15) * RX_PITCH + ((h + 0) >> 4)] = v.x;
+            row[((h + 1) & 15) * RX_PITCH + ((h + 1) >> 4)] = v.y;
+            row[((h + 2) & 15) * RX_PITCH + ((h + 2) >> 4)] = v.z;
+            row[((h + 3) & 15) * RX_PITCH + ((h + 3) >> 4)] = v.w;
         }
-        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-        if (lane == 0) sel[j] = bi;
+        __syncthreads();
+        for (int t = 0; t < T; ++t) {
+            const float * xr = smem + (size_t)t * 16 * RX_PITCH + l * RX_PITCH;
+            float acc = 0.f;
+#pragma unroll
+            for (int st = 0; st < RT_MAX_S; st += 4) {
+                if (st < nsteps) {
+                    const float4 xv = *reinterpret_cast<const float4 *>(xr + st);
+                    acc = __builtin_fmaf(wv[st + 0], xv.x, acc);
+                    acc = __builtin_fmaf(wv[st + 1], xv.y, acc);
+                    acc = __builtin_fmaf(wv[st + 2], xv.z, acc);
+                    acc = __builtin_fmaf(wv[st + 3], xv.w, acc);
+                }
+            }
+            acc = tree16_dpp(acc);
+            if (l == 0 && e < E) st_agent(a.logits + (size_t)t * E + e, a.rm ? acc + a.rm[(size_t)t * E + e] : acc);
+        }
+    } else if (blockIdx.x < a.n_row_wg || (a.sgi && blockIdx.x == a.n_row_wg)) {
+        // one row per wave, vec_dot_f32 order; the shared-gate row is wave 0 of the extra block
+        const bool sh_row = blockIdx.x == a.n_row_wg;
+        const int e = sh_row ? E : blockIdx.x * 4 + wave;
+        if ((sh_row && wave == 0) || (!sh_row && e < E)) {
+            const float * w = sh_row ? a.sgi : a.W + (size_t)e * H;
+            const int np = H & ~63;
+            float wv[32];
+#pragma unroll
+            for (int st = 0; st < 32; ++st)
+                if (64 * st < np) wv[st] = w[64 * st + lane];
+            for (int t = 0; t < T; ++t) {
+                const float * xt = a.x + (size_t)t * H;
+                float xv[32];
+#pragma unroll
+                for (int st = 0; st < 32; ++st)
+                    if (64 * st < np) xv[st] = xt[64 * st + lane];
+                float acc = 0.f;
+#pragma unroll
+                for (int st = 0; st < 32; ++st)
+                    if (64 * st < np) acc = __builtin_fmaf(wv[st], xv[st], acc);
+                acc += lane_xor32_f(acc);
+                acc += lane_xor16_f(acc);
+                acc = tree16_dpp(acc);
+                if (lane == 0) {
+                    // scalar tail as gcc -O3 vectorizes it: unfused 16/8-groups, then fma
+                    float sum = acc;
+                    int i = np;
+                    for (; H - i >= 16; i += 16)
+                        for (int q = 0; q < 16; ++q) sum = sum + w[i + q] * xt[i + q];
+                    if (H - i >= 8) {
+                        for (int q = 0; q < 8; ++q) sum = sum + w[i + q] * xt[i + q];
+                        i += 8;
+                    }
+                    for (; i < H; ++i) sum = __builtin_fmaf(w[i], xt[i], sum);
+                    if (sh_row) st_agent(a.sh_logit + t, sum);
+                    else st_agent(a.logits + (size_t)t * E + e, a.rm ? sum + a.rm[(size_t)t * E + e] : sum);
+                }
+            }
+        }
     }
-    __syncthreads();
-    if (lane == 0) {
-        float w[MAX_K];
-        for (int j = 0; j < k; ++j) w[j] = probs[sel[j]];
-        if (a.norm) {
-            double s = 0.0;
-            for (int j = 0; j < k; ++j) s += (double)w[j];
-            float ws = (float)s;
-            ws = fmaxf(fminf(ws, __builtin_inff()), 6.103515625e-5f);
-            for (int j = 0; j < k; ++j) w[j] = w[j] / ws;
-        }
-        if (a.scale != 0.0f && a.scale != 1.0f)
-            for (int j = 0; j < k; ++j) w[j] = w[j] * a.scale;
-        for (int j = 0; j < k; ++j) {
-            st_agent(a.ids_ws + t * k + j, sel[j]);
-            a.w_ws[t * k + j] = w[j];
-            if (a.ids_out) a.ids_out[(size_t)t * a.ids_ld + j] = sel[j];
-            if (a.w_out) a.w_out[(size_t)t * a.w_ld + j] = w[j];
-        }
-        if (a.sh_gate) a.sh_gate[t] = 1.f / (1.f + expf(-a.sh_logit[t]));   // unary-ops.cpp:31
-    }
-    // Q8_K of x[t]
-    const int nb = a.H / QK_K;
-    for (int b = 0; b < nb; ++b)
-        quantize_block_q8K(a.x + (size_t)t * a.H + b * QK_K, a.xq_qs + (size_t)t * a.H + b * QK_K,
-                           a.xq_d + (size_t)t * nb + b, a.xq_bs + (size_t)t * (a.H / 16) + b * 16, lane);
 
-    // ---- last block: expert union + slot remap ----
+    // ---- last workgroup: selection and the expert schedule
     if (!last_workgroup(a.counter)) return;
-    const int P = a.T * k;
-    __shared__ int32_t first[MAX_PAIRS], uidx[MAX_PAIRS], ids[MAX_PAIRS];
-    for (int p = lane; p < P; p += 64) ids[p] = ld_agent(a.ids_ws + p);
+    float * probs = smem + wave * MAX_E;
+    for (int t = wave; t < T; t += 4) {
+        const float * lt = a.logits + (size_t)t * E;
+        float m = -__builtin_inff();
+        for (int i = lane; i < E; i += 64) {
+            const float v = ld_agent(lt + i);
+            probs[i] = v;
+            m = fmaxf(m, v);
+        }
+        m = wave_max(m);
+        double sum = 0.0;
+        const int nfull = E & ~15;
+        for (int c0 = 0; c0 < nfull; c0 += 64) {
+            const int i = c0 + lane;
+            float v = 0.f;
+            if (i < nfull) { v = v_expf(probs[i] - m); probs[i] = v; }
+            const float cs = tree16_dpp(v);
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                if (c0 + 16 * g < nfull) sum += (double)readlane_f(cs, 16 * g);
+        }
+        for (int i = nfull; i < E; ++i) {           // scalar tail (libm expf on the CPU)
+            const float v = expf(probs[i] - m);
+            sum += (double)v;
+            if (lane == 0) probs[i] = v;
+        }
+        const float sc = (float)(1.0 / sum);
+        wave_sync();
+        for (int i = lane; i < E; i += 64) probs[i] = probs[i] * sc;
+        wave_sync();
+
+        // top-k: k rounds of a wave argmax (larger probability, then lower index)
+        uint32_t taken = 0;
+        int sel[MAX_K];
+        for (int j = 0; j < k; ++j) {
+            float bv = -__builtin_inff();
+            int bi = 0x7fffffff;
+            int slot = 0;
+            for (int i = lane; i < E; i += 64, ++slot) {
+                if (taken & (1u << slot)) continue;
+                const float p = probs[i];
+                if (p > bv || (p == bv && i < bi)) { bv = p; bi = i; }
+            }
+            wave_best_first(bv, bi);
+            if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+            sel[j] = bi;
+        }
+        if (lane == 0) {
+            float w[MAX_K];
+            for (int j = 0; j < k; ++j) w[j] = probs[sel[j]];
+            if (a.norm) {
+                double s = 0.0;
+                for (int j = 0; j < k; ++j) s += (double)w[j];
+                float ws = (float)s;
+                ws = fmaxf(fminf(ws, __builtin_inff()), 6.103515625e-5f);
+                for (int j = 0; j < k; ++j) w[j] = w[j] / ws;
+            }
+            if (a.scale != 0.0f && a.scale != 1.0f)
+                for (int j = 0; j < k; ++j) w[j] = w[j] * a.scale;
+            for (int j = 0; j < k; ++j) {
+                s_ids[t * k + j] = sel[j];
+                a.ids_ws[t * k + j] = sel[j];
+                a.w_ws[t * k + j] = w[j];
+                if (a.ids_out) a.ids_out[(size_t)t * a.ids_ld + j] = sel[j];
+                if (a.w_out) a.w_out[(size_t)t * a.w_ld + j] = w[j];
+            }
+            if (a.sh_gate) a.sh_gate[t] = 1.f / (1.f + expf(-ld_agent(a.sh_logit + t)));   // unary-ops.cpp:31
+        }
+    }
     __syncthreads();
+    if (wave != 0) return;
+
+    // wave 0 alone from here: LDS hand-offs between its lanes need only wave_sync
+    const int P = T * k;
+    __shared__ int32_t first[MAX_PAIRS], uidx[MAX_PAIRS];
     for (int p = lane; p < P; p += 64) {
-        const int e = ids[p];
+        const int e = s_ids[p];
         int f = p;
         for (int q = 0; q < p; ++q)
-            if (ids[q] == e) { f = q; break; }
+            if (s_ids[q] == e) { f = q; break; }
         first[p] = f;
     }
-    __syncthreads();
+    wave_sync();
     int base = 0;
-    for (int c = 0; c < P; c += 64) {
-        const int p = c + lane;
+    for (int c0 = 0; c0 < P; c0 += 64) {
+        const int p = c0 + lane;
         const bool isf = p < P && first[p] == p;
         const unsigned long long bal = __ballot(isf);
         const int below = __popcll(bal & ((1ull << lane) - 1ull));
         if (isf) uidx[p] = base + below;
         base += __popcll(bal);
     }
-    __syncthreads();
+    wave_sync();
     const int nu = base;
     for (int p = lane; p < P; p += 64) {
         const int f = first[p];
@@ -247,12 +288,12 @@ __global__ void __launch_bounds__(64) k_route_select(SelectArgs a) {
         for (int q = 0; q < p; ++q) pos += first[q] == f;
         Unit & u = a.units[uidx[f]];
         u.pair[pos] = p;
-        if (p == f) u.expert = ids[p];
+        if (p == f) u.expert = s_ids[p];
         int cnt = 0;
         for (int q = f; q < P; ++q) cnt += first[q] == f;
         if (p == f) u.n = cnt;
         if (a.slot_tables) {
-            const int e = ids[p];
+            const int e = s_ids[p];
             for (int r = 0; r < 3; ++r)
                 a.slots_ws[r * P + p] = a.slot_tables[(size_t)r * a.table_stride + (size_t)a.layer * E + e];
         }
@@ -260,8 +301,8 @@ __global__ void __launch_bounds__(64) k_route_select(SelectArgs a) {
     if (a.shared && lane == 0) {
         Unit & u = a.units[nu];
         u.expert = -1;
-        u.n = a.T;
-        for (int i = 0; i < a.T; ++i) u.pair[i] = i;
+        u.n = T;
+        for (int i = 0; i < T; ++i) u.pair[i] = i;
     }
     if (lane == 0) *a.n_units = nu;
 }
@@ -393,12 +434,14 @@ __global__ void __launch_bounds__(256) k_gateup_q4k(GateUpArgs a) {
 #pragma unroll
         for (int i = 0; i < MAXP; ++i) {
             g[i] = 0.f; up[i] = 0.f;
-            if (i < n && valid) {
-                g[i] = chunk_dot(G[it], A[i], c, 0.f);
-                up[i] = chunk_dot(Uw[it], A[i], c, 0.f);
+            if (i < n) {                      // n is uniform: empty token slots cost nothing
+                if (valid) {
+                    g[i] = chunk_dot(G[it], A[i], c, 0.f);
+                    up[i] = chunk_dot(Uw[it], A[i], c, 0.f);
+                }
+                g[i] = lane_sum<LPR>(g[i]);
+                up[i] = lane_sum<LPR>(up[i]);
             }
-            g[i] = group_sum<LPR>(g[i]);
-            up[i] = group_sum<LPR>(up[i]);
         }
         if (r < rows) {
 #pragma unroll
@@ -415,33 +458,71 @@ __global__ void __launch_bounds__(256) k_gateup_q4k(GateUpArgs a) {
 }
 
 // ---------------------------------------------------------------------
-// down: ex[p][h] = down_e[h] . Q8_K(act[p])
+// down: ex[p][h] = down_e[h] . Q8_K(act[p]), then the combine of the row tile
 // grid: (row tiles over H, unit slots [+1 shared]), block 256.  Each block
-// first quantizes its unit's activation rows to Q8_K in LDS.
+// first quantizes its unit's activation rows to Q8_K in LDS.  The last unit
+// to finish a row tile combines it for every token:
+//   out[t][h] = sum_j ex[t,j][h] * w[t][j] (+ shared) (+ resid)
+//   T == 1: ggml_vec_dot_f32 with n = k (runtime.cpp:3815-3817): the whole
+//           sum is the scalar tail, gcc-vectorized as unfused 16/8 groups,
+//           then fused multiply-adds.
+//   T  > 1: ggml_mul then the ggml_add chain (runtime.cpp:4544-4550).
 // ---------------------------------------------------------------------
 struct DownArgs {
     const uint8_t * down; size_t down_slab; const uint8_t * sh_down;
     const int32_t * slot_d;
-    const Unit * units; const int32_t * n_units; int unit_slots;
+    const Unit * units; const int32_t * n_units; int unit_slots; int shared;
     const float * act; const float * act_sh;
     float * ex; float * ex_sh;
-    int H, N, N_sh, k;
+    int H, N, N_sh, k, T;
+    int32_t * tile_counters;
+    const float * w; const float * sh_gate; const float * resid; float * out;
 };
 
 constexpr int MAX_NDOWN = 2048;   // longest down-projection input held in LDS
+
+QWM_DEV float combine_one(const DownArgs & a, int t, int h) {
+    const int H = a.H, k = a.k;
+    const float * wt = a.w + (size_t)t * k;
+    const float * e = a.ex + (size_t)t * k * H + h;
+    float s;
+    if (a.T == 1) {
+        s = 0.0f;
+        int i = 0;
+        for (; k - i >= 16; i += 16)
+            for (int l = 0; l < 16; ++l) s = s + ld_agent(e + (size_t)(i + l) * H) * wt[i + l];
+        if (k - i >= 8) {
+            for (int l = 0; l < 8; ++l) s = s + ld_agent(e + (size_t)(i + l) * H) * wt[i + l];
+            i += 8;
+        }
+        for (; i < k; ++i) s = __builtin_fmaf(ld_agent(e + (size_t)i * H), wt[i], s);
+    } else {
+        s = ld_agent(e) * wt[0];
+        for (int j = 1; j < k; ++j) s = s + ld_agent(e + (size_t)j * H) * wt[j];
+    }
+    if (a.shared) {
+        float v = ld_agent(a.ex_sh + (size_t)t * H + h);
+        if (a.sh_gate) v = v * a.sh_gate[t];
+        s = s + v;
+    }
+    if (a.resid) s = s + a.resid[(size_t)t * H + h];
+    return s;
+}
 
 template <int LPR, int MAXP>
 __global__ void __launch_bounds__(256) k_down_q4k(DownArgs a) {
     constexpr int RPI = WAVE / LPR;
     constexpr int NIT = GEMV_STEPS;
+    constexpr int TILE = 4 * NIT * RPI;
     __shared__ int8_t s_qs[MAXP][MAX_NDOWN];
     __shared__ float s_d[MAXP][MAX_NDOWN / QK_K];
     __shared__ int32_t s_bs[MAXP][MAX_NDOWN / 16];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int u = blockIdx.y;
     const bool shared = u == a.unit_slots;
-    if (!shared && u >= *a.n_units) return;
-    const Unit & U = a.units[shared ? *a.n_units : u];
+    const int nu = *a.n_units;
+    if (!shared && u >= nu) return;
+    const Unit & U = a.units[shared ? nu : u];
     const int n = U.n;
     const int K = shared ? a.N_sh : a.N;
     const int nb = K / QK_K;
@@ -450,7 +531,8 @@ __global__ void __launch_bounds__(256) k_down_q4k(DownArgs a) {
     const bool active = c < C;
     const uint8_t * base = shared ? a.sh_down : a.down + (size_t)a.slot_d[U.pair[0]] * a.down_slab;
     const size_t row_bytes = (size_t)nb * 144;
-    const int r_begin = (blockIdx.x * 4 + wave) * (NIT * RPI);
+    const int row0 = blockIdx.x * TILE;
+    const int r_begin = row0 + wave * (NIT * RPI);
     // weight loads first: they do not depend on the activations
     WChunk W[NIT];
 #pragma unroll
@@ -476,57 +558,26 @@ __global__ void __launch_bounds__(256) k_down_q4k(DownArgs a) {
         float acc[MAXP];
 #pragma unroll
         for (int i = 0; i < MAXP; ++i) {
-            acc[i] = (i < n && valid) ? chunk_dot(W[it], A[i], c, 0.f) : 0.f;
-            acc[i] = group_sum<LPR>(acc[i]);
+            acc[i] = 0.f;
+            if (i < n) {
+                if (valid) acc[i] = chunk_dot(W[it], A[i], c, 0.f);
+                acc[i] = lane_sum<LPR>(acc[i]);
+            }
         }
         if (r < a.H) {
 #pragma unroll
             for (int i = 0; i < MAXP; ++i)
                 if (i < n && c == i) {
-                    if (shared) a.ex_sh[(size_t)U.pair[i] * a.H + r] = acc[i];
-                    else a.ex[(size_t)U.pair[i] * a.H + r] = acc[i];
+                    if (shared) st_agent(a.ex_sh + (size_t)U.pair[i] * a.H + r, acc[i]);
+                    else st_agent(a.ex + (size_t)U.pair[i] * a.H + r, acc[i]);
                 }
         }
     }
-}
-
-// ---------------------------------------------------------------------
-// combine: out[t][h] = sum_j ex[t,j][h] * w[t][j] (+ shared) (+ resid)
-//   T == 1: ggml_vec_dot_f32 with n = k (runtime.cpp:3815-3817): the whole
-//           sum is the scalar tail, gcc-vectorized as unfused 16/8 groups,
-//           then fused multiply-adds.
-//   T  > 1: ggml_mul then the ggml_add chain (runtime.cpp:4544-4550).
-// ---------------------------------------------------------------------
-__global__ void __launch_bounds__(256) k_combine(const float * __restrict__ ex, const float * __restrict__ ex_sh,
-                                                  const float * __restrict__ w, const float * __restrict__ sh_gate,
-                                                  const float * __restrict__ resid, float * __restrict__ out,
-                                                  int H, int T, int k, int shared) {
-    const int h = blockIdx.x * 256 + threadIdx.x, t = blockIdx.y;
-    if (h >= H) return;
-    const float * wt = w + (size_t)t * k;
-    const float * e = ex + (size_t)t * k * H + h;
-    float s;
-    if (T == 1) {
-        s = 0.0f;
-        int i = 0;
-        for (; k - i >= 16; i += 16)
-            for (int l = 0; l < 16; ++l) s = s + e[(size_t)(i + l) * H] * wt[i + l];
-        if (k - i >= 8) {
-            for (int l = 0; l < 8; ++l) s = s + e[(size_t)(i + l) * H] * wt[i + l];
-            i += 8;
-        }
-        for (; i < k; ++i) s = __builtin_fmaf(e[(size_t)i * H], wt[i], s);
-    } else {
-        s = e[0] * wt[0];
-        for (int j = 1; j < k; ++j) s = s + e[(size_t)j * H] * wt[j];
+    if (!last_workgroup(a.tile_counters + blockIdx.x, nu + a.shared)) return;
+    for (int q = tid; q < a.T * TILE; q += 256) {
+        const int t = q / TILE, h = row0 + q % TILE;
+        if (h < a.H) a.out[(size_t)t * a.H + h] = combine_one(a, t, h);
     }
-    if (shared) {
-        float v = ex_sh[(size_t)t * H + h];
-        if (sh_gate) v = v * sh_gate[t];
-        s = s + v;
-    }
-    if (resid) s = s + resid[(size_t)t * H + h];
-    out[(size_t)t * H + h] = s;
 }
 
 // ======================================================================
@@ -552,6 +603,7 @@ bool moe_plan(const qwm_moe_layer * L, int64_t T, MoePlan & p, std::string & why
     size_t o = 0;
     auto take = [&](size_t bytes) { size_t at = o; o = align_up(o + bytes, 256); return at; };
     p.counters = take(256);
+    p.tile_counters = take(sizeof(int32_t) * MAX_TILES);
     p.logits = take(sizeof(float) * T * p.E);
     p.ids = take(sizeof(int32_t) * P);
     p.w = take(sizeof(float) * P);
@@ -572,28 +624,29 @@ bool moe_plan(const qwm_moe_layer * L, int64_t T, MoePlan & p, std::string & why
 
 int launch_route(const RouteArgs & a, const MoePlan & p, uint8_t * ws, int32_t * ids_out, int64_t ids_ld,
                  float * w_out, int64_t w_ld, hipStream_t s) {
-    float * logits = reinterpret_cast<float *>(ws + p.logits);
+    RouteKArgs r;
+    r.W = a.W; r.x = a.x; r.rm = a.rm; r.sgi = a.sh_gate_inp;
+    r.E = (int)a.E; r.H = (int)a.H; r.T = (int)a.T; r.k = (int)a.k; r.norm = a.norm; r.scale = a.scale;
+    r.tiny = (a.T >= 2 && a.E % 4 == 0) ? 1 : 0;
+    r.n_row_wg = r.tiny ? (int)((a.E + 15) / 16) : (int)((a.E + 3) / 4);
+    r.logits = reinterpret_cast<float *>(ws + p.logits);
     float * sh = reinterpret_cast<float *>(ws + p.sh_gate);
-    const int rows = (int)a.E + (a.sh_gate_inp ? 1 : 0);
-    QWM_TIMED("route_logits", s, k_route_logits<<<dim3((rows + 3) / 4), dim3(256), 0, s>>>(
-                                      a.W, a.x, a.rm, a.sh_gate_inp, logits, sh + p.T, (int)a.E, (int)a.H, (int)a.T));
-    SelectArgs sa;
-    sa.logits = logits; sa.sh_logit = sh + p.T; sa.x = a.x;
-    sa.E = (int)a.E; sa.H = (int)a.H; sa.T = (int)a.T; sa.k = (int)a.k; sa.norm = a.norm; sa.scale = a.scale;
-    sa.ids_ws = reinterpret_cast<int32_t *>(ws + p.ids);
-    sa.w_ws = reinterpret_cast<float *>(ws + p.w);
-    sa.ids_out = ids_out; sa.ids_ld = ids_ld; sa.w_out = w_out; sa.w_ld = w_ld;
-    sa.sh_gate = a.sh_gate_inp ? sh : nullptr;
-    sa.xq_qs = reinterpret_cast<int8_t *>(ws + p.xq_qs);
-    sa.xq_d = reinterpret_cast<float *>(ws + p.xq_d);
-    sa.xq_bs = reinterpret_cast<int32_t *>(ws + p.xq_bs);
-    sa.units = reinterpret_cast<Unit *>(ws + p.units);
-    sa.n_units = reinterpret_cast<int32_t *>(ws + p.n_units);
-    sa.counter = reinterpret_cast<int32_t *>(ws + p.counters);
-    sa.shared = p.shared ? 1 : 0;
-    sa.slot_tables = a.slot_tables; sa.table_stride = a.table_stride; sa.layer = a.layer;
-    sa.slots_ws = reinterpret_cast<int32_t *>(ws + p.slots);
-    QWM_TIMED("route_select", s, k_route_select<<<dim3((unsigned)a.T), dim3(64), 0, s>>>(sa));
+    r.sh_logit = sh + p.T;
+    r.ids_ws = reinterpret_cast<int32_t *>(ws + p.ids);
+    r.w_ws = reinterpret_cast<float *>(ws + p.w);
+    r.ids_out = ids_out; r.ids_ld = ids_ld; r.w_out = w_out; r.w_ld = w_ld;
+    r.sh_gate = a.sh_gate_inp ? sh : nullptr;
+    r.xq_qs = reinterpret_cast<int8_t *>(ws + p.xq_qs);
+    r.xq_d = reinterpret_cast<float *>(ws + p.xq_d);
+    r.xq_bs = reinterpret_cast<int32_t *>(ws + p.xq_bs);
+    r.units = reinterpret_cast<Unit *>(ws + p.units);
+    r.n_units = reinterpret_cast<int32_t *>(ws + p.n_units);
+    r.counter = reinterpret_cast<int32_t *>(ws + p.counters);
+    r.shared = p.shared ? 1 : 0;
+    r.slot_tables = a.slot_tables; r.table_stride = a.table_stride; r.layer = a.layer;
+    r.slots_ws = reinterpret_cast<int32_t *>(ws + p.slots);
+    const int grid = r.n_row_wg + (a.sh_gate_inp ? 1 : 0);
+    QWM_TIMED("route", s, k_route<<<dim3((unsigned)grid), dim3(256), 0, s>>>(r));
     QWM_HIP_CHECK(hipGetLastError());
     return QWM_OK;
 }
@@ -666,13 +719,19 @@ int launch_experts(const ExpertArgs & a, const MoePlan & p, uint8_t * ws, hipStr
     d.act = g.act; d.act_sh = g.act_sh;
     d.ex = reinterpret_cast<float *>(ws + p.ex);
     d.ex_sh = reinterpret_cast<float *>(ws + p.ex_sh);
-    d.H = (int)p.H; d.N = (int)p.N; d.N_sh = (int)p.N_sh; d.k = (int)p.k;
+    d.H = (int)p.H; d.N = (int)p.N; d.N_sh = (int)p.N_sh; d.k = (int)p.k; d.T = (int)p.T;
+    d.shared = p.shared ? 1 : 0;
+    d.tile_counters = reinterpret_cast<int32_t *>(ws + p.tile_counters);
+    d.w = reinterpret_cast<const float *>(a.weights);
+    d.sh_gate = p.shared_gate ? reinterpret_cast<const float *>(ws + p.sh_gate) : nullptr;
+    d.resid = a.resid; d.out = a.out;
     const int ld = lanes_per_row((int)std::max(p.N, p.N_sh));
     if (ld < 0) return fail(QWM_ERR_UNSUPPORTED, "expert FFN size > 2048 not tiled");
     if (p.shared && lanes_per_row((int)p.N_sh) != lanes_per_row((int)p.N))
         return fail(QWM_ERR_UNSUPPORTED, "shared and routed FFN sizes need the same tiling");
     const int tile_d = 4 * GEMV_STEPS * (WAVE / ld);
     dim3 grid_d(((int)p.H + tile_d - 1) / tile_d, grid_y);
+    if (grid_d.x > (unsigned)MAX_TILES) return fail(QWM_ERR_UNSUPPORTED, "hidden size needs too many down tiles");
     prof_begin("down", s);
     switch (ld) {
         case 16: launch_down_lpr<16>(d, maxp, grid_d, s); break;
@@ -681,9 +740,6 @@ int launch_experts(const ExpertArgs & a, const MoePlan & p, uint8_t * ws, hipStr
     }
     prof_end("down", s);
 
-    QWM_TIMED("combine", s, k_combine<<<dim3((unsigned)((p.H + 255) / 256), (unsigned)p.T), 256, 0, s>>>(
-        d.ex, d.ex_sh, reinterpret_cast<const float *>(a.weights), p.shared_gate ? reinterpret_cast<const float *>(ws + p.sh_gate) : nullptr,
-        a.resid, a.out, (int)p.H, (int)p.T, (int)p.k, p.shared ? 1 : 0));
     QWM_HIP_CHECK(hipGetLastError());
     return QWM_OK;
 }
@@ -797,8 +853,11 @@ __global__ void __launch_bounds__(256) k_mmid_q4k(MmidGemv a) {
         float acc[MAXP];
 #pragma unroll
         for (int i = 0; i < MAXP; ++i) {
-            acc[i] = (i < n && valid) ? chunk_dot(W[it], A[i], c, 0.f) : 0.f;
-            acc[i] = group_sum<LPR>(acc[i]);
+            acc[i] = 0.f;
+            if (i < n) {
+                if (valid) acc[i] = chunk_dot(W[it], A[i], c, 0.f);
+                acc[i] = lane_sum<LPR>(acc[i]);
+            }
         }
         if (r < a.N) {
 #pragma unroll

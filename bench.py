@@ -33,6 +33,18 @@ Q4K_ROW_GU = H // 256 * 144          # 1152 B
 Q4K_ROW_D = N // 256 * 144           # 432 B
 SLAB = N * Q4K_ROW_GU                # 884,736 B per role per expert
 LM_ROW = H // 32 * 34                # 2176 B
+CAL_BYTES = 256 << 20                # calibration copy for the PMC byte counters
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "lm_head_traffic.json")
+
+
+def measured_traffic():
+    """HBM bytes per lm_head launch from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE, each scaled by the calibration copy), or None."""
+    try:
+        with open(TRAFFIC_SUMMARY) as f:
+            return float(json.load(f)["traffic_bytes_per_launch"])
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def parse():
@@ -149,6 +161,16 @@ def main():
         n = L.qwm_profile_stop(d.ctypes.data, args.steps)
         kern[name] = float(d[:n].mean() * 1e3) if n else None
 
+    # a plain streaming kernel of known size (torch.neg: reads and writes
+    # 256 MiB, a kernel name of its own): under rocprofv3 --pmc its FETCH_SIZE
+    # and WRITE_SIZE give the counters' scale
+    cal_src = torch.full((CAL_BYTES // 4,), 1.0, dtype=torch.float32, device=dev)
+    cal_dst = torch.empty_like(cal_src)
+    for _ in range(3):
+        torch.neg(cal_src, out=cal_dst)
+    torch.cuda.synchronize()
+    del cal_src, cal_dst
+
     # algorithmic bytes
     ids_np = ids[args.warmup:].cpu().numpy()
     uniq = np.array([len(np.unique(i)) for i in ids_np])
@@ -171,7 +193,8 @@ def main():
                                "2048x151936 argmax + greedy accept",
                    "tokens_per_step": T, "experts_per_step_mean": float(uniq.mean())},
         "roofline": {"bound": "hbm", "kernel": "lm_head (Q8_0 GEMV + argmax)", "achieved": lm_gbs,
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": lm_gbs / HBM_PEAK_GBS, "traffic": None,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": lm_gbs / HBM_PEAK_GBS,
+                     "traffic": measured_traffic(), "traffic_source": os.path.relpath(TRAFFIC_SUMMARY, ROOT),
                      "bytes_per_launch": lm_bytes, "avg_launch_us": lm_avg_ms * 1e3, "launches_timed": int(n_lm)},
         "step_hbm_gbs": float(step_bytes.mean()) / (ms_step * 1e-3) / 1e9,
         "step_bytes_mean": float(step_bytes.mean()),
@@ -220,27 +243,28 @@ def cpu_baseline(args, torch, pools, router, lm, xs, drafts, ids_gpu, res_gpu):
     acc = ctypes.c_int32()
     a.ids, a.out, a.vA, a.accepted = ids.ctypes.data, out.ctypes.data, vA.ctypes.data, ctypes.addressof(acc)
     s0 = args.warmup
-    # one untimed warm-up step, then as many steps as fit in the time budget
-    steps, agree, t_total = 0, 0, 0.0
-    s = s0
+    # one untimed warm-up step, then the timed steps (cycling over the bench's
+    # step inputs) until the time budget is spent
+    n_run, steps, agree, t_total = 0, 0, 0, 0.0
     while True:
+        s = s0 + n_run % args.steps
         xi = np.ascontiguousarray(x_np[s])
         di = np.ascontiguousarray(dr[s])
         a.x, a.drafts = xi.ctypes.data, di.ctypes.data
         t0 = time.perf_counter()
         lib.qwr_cpu_verify_step(ctypes.byref(a))
         dt = time.perf_counter() - t0
-        if s > s0:
+        if n_run > 0:
             t_total += dt
             steps += 1
+        n_run += 1
         agree += int(np.array_equal(np.sort(ids, 1), np.sort(ids_ref[s], 1)) and np.array_equal(vA, res_ref[s][:T]))
-        s = s0 + (s - s0 + 1) % args.steps
-        if t_total >= args.cpu_seconds or steps >= 2000:
+        if t_total >= args.cpu_seconds or steps >= 20000:
             break
     return {"value": T * steps / t_total, "unit": "tokens/s", "cores": threads, "kind": "reference",
             "sample": f"{steps} verify steps ({t_total:.1f} s) of the same workload through the reference's "
                       f"ggml-CPU kernels (x86-64 AVX-512 build, {threads} OpenMP threads); "
-                      f"{agree}/{steps + 1} steps gave the GPU's expert ids and argmaxes",
+                      f"{agree}/{n_run} steps gave the GPU's expert ids and argmaxes",
             "ms_per_step": 1e3 * t_total / steps}
 
 

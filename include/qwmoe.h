@@ -152,9 +152,9 @@ int qwm_quantize(int32_t type, const float * src, void * dst, int64_t n, void * 
 /* -------------------------------------------------------- measurement --- */
 
 /* Brackets each of the next `max_launches` launches of one kernel with a
- * hipEvent pair on the stream it runs on.  Kernel names: "route_logits",
- * "route_select", "gate_up", "down", "combine", "vhead_prep", "lm_head",
- * "accept", "mul_mat_id_prep", "mul_mat_id".  Owner thread only. */
+ * hipEvent pair on the stream it runs on.  Kernel names: "route",
+ * "gate_up", "down" (with the combine), "lm_head", "mul_mat_id_prep",
+ * "mul_mat_id".  Owner thread only. */
 int qwm_profile_start(const char * kernel, int32_t max_launches);
 /* Waits for the recorded events, writes each launch's duration in ms and
  * returns how many launches were timed (stops the profiling). */

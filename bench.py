@@ -34,16 +34,17 @@ Q4K_ROW_D = N // 256 * 144           # 432 B
 SLAB = N * Q4K_ROW_GU                # 884,736 B per role per expert
 LM_ROW = H // 32 * 34                # 2176 B
 CAL_BYTES = 256 << 20                # calibration copy for the PMC byte counters
-TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "lm_head_traffic.json")
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "verify_step_T4_traffic.json")
 
 
-def measured_traffic():
-    """HBM bytes per lm_head launch from the committed rocprofv3 --pmc summary
-    (FETCH_SIZE + WRITE_SIZE, each scaled by the calibration copy), or None."""
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE + WRITE_SIZE, each scaled by the calibration kernel),
+    or None."""
     try:
         with open(TRAFFIC_SUMMARY) as f:
-            return float(json.load(f)["traffic_bytes_per_launch"])
-    except (OSError, KeyError, ValueError):
+            return float(json.load(f)["kernels"][kernel]["traffic_bytes"])
+    except (OSError, KeyError, ValueError, TypeError):
         return None
 
 
@@ -56,6 +57,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--accept-rate", type=float, default=0.7, help="probability that a draft equals the target")
+    ap.add_argument("--path", choices=["step", "ops"], default="step",
+                    help="step: the fused verify step (one launch); ops: qwm_moe_block_resident + qwm_verify_accept")
     return ap.parse_args()
 
 
@@ -104,15 +107,21 @@ def main():
     drafts = torch.zeros((n_all, T - 1), dtype=torch.int32, device=dev)
     ws_moe = torch.empty(L.qwm_moe_workspace_size(layer, T), dtype=torch.uint8, device=dev)
     ws_v = torch.empty(L.qwm_verify_workspace_size(lm_t, T), dtype=torch.uint8, device=dev)
-    qa.check(L.qwm_workspace_init(ws_moe.data_ptr(), ws_moe.numel(), stream))
-    qa.check(L.qwm_workspace_init(ws_v.data_ptr(), ws_v.numel(), stream))
+    ws_s = torch.empty(L.qwm_verify_step_workspace_size(layer, lm_t, T), dtype=torch.uint8, device=dev)
+    for w in (ws_moe, ws_v, ws_s):
+        qa.check(L.qwm_workspace_init(w.data_ptr(), w.numel(), stream))
 
     def step(s):
         x_t = qa.tensor(qa.TYPE_F32, H, T, 1, xs[s])
         h_t = qa.tensor(qa.TYPE_F32, H, T, 1, hs[s])
-        qa.check(L.qwm_moe_block_resident(layer, 0, tables.data_ptr(), E, x_t, None, x_t, h_t,
-                                          qa.tensor(qa.TYPE_I32, K_USED, T, 1, ids[s]),
-                                          qa.tensor(qa.TYPE_F32, K_USED, T, 1, wts[s]),
+        i_t = qa.tensor(qa.TYPE_I32, K_USED, T, 1, ids[s])
+        w_t = qa.tensor(qa.TYPE_F32, K_USED, T, 1, wts[s])
+        if args.path == "step":
+            qa.check(L.qwm_verify_step(layer, 0, tables.data_ptr(), E, x_t, None, x_t, h_t, i_t, w_t, lm_t,
+                                       None, 1e-6, drafts[s].data_ptr(), res[s].data_ptr(),
+                                       ws_s.data_ptr(), ws_s.numel(), stream))
+            return
+        qa.check(L.qwm_moe_block_resident(layer, 0, tables.data_ptr(), E, x_t, None, x_t, h_t, i_t, w_t,
                                           ws_moe.data_ptr(), ws_moe.numel(), stream))
         qa.check(L.qwm_verify_accept(lm_t, h_t, None, 1e-6, drafts[s].data_ptr(), res[s].data_ptr(),
                                      ws_v.data_ptr(), ws_v.numel(), stream))
@@ -132,7 +141,8 @@ def main():
     for s in range(args.warmup):
         step(s)
     torch.cuda.synchronize()
-    qa.check(L.qwm_profile_start(b"lm_head", args.steps))
+    main_kernel = "step" if args.path == "step" else "lm_head"
+    qa.check(L.qwm_profile_start(main_kernel.encode(), args.steps))
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -150,9 +160,9 @@ def main():
     accepted = r[:, T]
     acc_tok_s = float((accepted + 1).sum()) / (elapsed_ms / 1e3)
 
-    # secondary kernels (untimed pass, same steps)
+    # secondary kernels of the per-op path (untimed pass, same steps)
     kern = {}
-    for name in ["route", "gate_up", "down"]:
+    for name in (["route", "gate_up", "down"] if args.path == "ops" else []):
         qa.check(L.qwm_profile_start(name.encode(), args.steps))
         for s in range(args.warmup, n_all):
             step(s)
@@ -177,7 +187,8 @@ def main():
     lm_bytes = V * LM_ROW + T * (H + H // 32 * 4)
     step_bytes = uniq * 3 * SLAB + E * H * 4 + 2 * T * H * 4 + V * LM_ROW
     lm_avg_ms = float(lm_ms[:n_lm].mean())
-    lm_gbs = lm_bytes / (lm_avg_ms * 1e-3) / 1e9
+    main_bytes = float(step_bytes.mean()) if args.path == "step" else lm_bytes
+    lm_gbs = main_bytes / (lm_avg_ms * 1e-3) / 1e9
     gu_bytes = float(uniq.mean()) * 2 * SLAB
     dn_bytes = float(uniq.mean()) * SLAB
     for name, b in [("gate_up", gu_bytes), ("down", dn_bytes)]:
@@ -192,10 +203,14 @@ def main():
                                "(H 2048, 128 experts resident, FFN 768, top-8, Q4_K) + rms_norm + Q8_0 lm_head "
                                "2048x151936 argmax + greedy accept",
                    "tokens_per_step": T, "experts_per_step_mean": float(uniq.mean())},
-        "roofline": {"bound": "hbm", "kernel": "lm_head (Q8_0 GEMV + argmax)", "achieved": lm_gbs,
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": lm_gbs / HBM_PEAK_GBS,
-                     "traffic": measured_traffic(), "traffic_source": os.path.relpath(TRAFFIC_SUMMARY, ROOT),
-                     "bytes_per_launch": lm_bytes, "avg_launch_us": lm_avg_ms * 1e3, "launches_timed": int(n_lm)},
+        "roofline": {"bound": "hbm",
+                     "kernel": ("step (MoE block + verify head, one launch)" if args.path == "step"
+                                else "lm_head (Q8_0 GEMV + argmax)"),
+                     "achieved": lm_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": lm_gbs / HBM_PEAK_GBS,
+                     "traffic": measured_traffic(main_kernel),
+                     "traffic_source": os.path.relpath(TRAFFIC_SUMMARY, ROOT),
+                     "bytes_per_launch": main_bytes, "avg_launch_us": lm_avg_ms * 1e3, "launches_timed": int(n_lm)},
+        "path": args.path,
         "step_hbm_gbs": float(step_bytes.mean()) / (ms_step * 1e-3) / 1e9,
         "step_bytes_mean": float(step_bytes.mean()),
         "accepted_tokens_per_s": acc_tok_s,

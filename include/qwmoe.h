@@ -141,6 +141,28 @@ size_t qwm_verify_workspace_size(const qwm_tensor * lm_head, int64_t T);
 int qwm_verify_accept(const qwm_tensor * lm_head, const qwm_tensor * x, const float * norm_w, float eps,
                       const int32_t * drafts, int32_t * result, void * workspace, size_t ws_bytes, void * stream);
 
+/* ------------------------------------------------- the fused verify step --- */
+
+/* One MTP verify step in a single launch: qwm_moe_block_resident followed by
+ * qwm_verify_accept on the block's output (runtime.cpp:2759-2787 for the
+ * in-graph slot remap, 3801-3830 / 4534-4572 for the block, 5014-5046 and
+ * 3648-3652 for the head), with the same numerics.  The kernel is persistent:
+ * a grid of exactly the workgroups the GPU holds at once, handing data to each
+ * other through the workspace, so the launch occupies the whole GPU until it
+ * ends (work on other streams delays it).
+ *   out = MoE(x) (+ resid);  h = rms_norm(out) * norm_w;  vA = argmax(lm_head . h)
+ *   result: device i32 [T + 2] = vA[0..T-1], a, x_new; a = -1 reports a
+ *   device-side synchronization timeout (results invalid).
+ * Supported: Q4_K pools, hidden size 2048, FFN <= 2048, <= 512 experts, lm_head Q8_0
+ * [2048, V] with V >= 8192, T <= 8.  out must not overlap x or resid.  ids_out,
+ * w_out and norm_w may be NULL.  QWM_ERR_UNSUPPORTED: use the two calls. */
+size_t qwm_verify_step_workspace_size(const qwm_moe_layer * layer, const qwm_tensor * lm_head, int64_t T);
+int qwm_verify_step(const qwm_moe_layer * layer, int32_t layer_index, const int32_t * slot_tables,
+                    int64_t table_stride, const qwm_tensor * x, const qwm_tensor * rm, const qwm_tensor * resid,
+                    qwm_tensor * out, qwm_tensor * ids_out, qwm_tensor * w_out, const qwm_tensor * lm_head,
+                    const float * norm_w, float eps, const int32_t * drafts, int32_t * result,
+                    void * workspace, size_t ws_bytes, void * stream);
+
 /* ------------------------------------------------------- quantization --- */
 
 /* Model-file quantization on the device, as ggml_quantize_chunk does it
@@ -153,8 +175,8 @@ int qwm_quantize(int32_t type, const float * src, void * dst, int64_t n, void * 
 
 /* Brackets each of the next `max_launches` launches of one kernel with a
  * hipEvent pair on the stream it runs on.  Kernel names: "route",
- * "gate_up", "down" (with the combine), "lm_head", "mul_mat_id_prep",
- * "mul_mat_id".  Owner thread only. */
+ * "gate_up", "down" (with the combine), "lm_head", "step" (the fused verify
+ * step), "mul_mat_id_prep", "mul_mat_id".  Owner thread only. */
 int qwm_profile_start(const char * kernel, int32_t max_launches);
 /* Waits for the recorded events, writes each launch's duration in ms and
  * returns how many launches were timed (stops the profiling). */

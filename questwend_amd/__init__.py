@@ -87,6 +87,9 @@ def lib():
                                                   _P, _SZ, _P]),
         "qwm_verify_workspace_size": (_SZ, [T, _I64]),
         "qwm_verify_accept": (ctypes.c_int, [T, T, _P, ctypes.c_float, _P, _P, _P, _SZ, _P]),
+        "qwm_verify_step_workspace_size": (_SZ, [ctypes.POINTER(MoeLayer), T, _I64]),
+        "qwm_verify_step": (ctypes.c_int, [ctypes.POINTER(MoeLayer), _I32, _P, _I64, T, T, T, T, T, T, T,
+                                           _P, ctypes.c_float, _P, _P, _P, _SZ, _P]),
         "qwm_pool_create": (ctypes.c_int, [ctypes.POINTER(PoolDesc), _P, ctypes.POINTER(_P)]),
         "qwm_pool_destroy": (None, [_P]),
         "qwm_pool_ensure": (ctypes.c_int, [_P, _I32, _P, _I32, _P, _P, _P]),

@@ -313,6 +313,63 @@ int qwm_moe_block_resident(const qwm_moe_layer * layer, int32_t layer_index, con
                       resid ? (const float *)resid->data : nullptr, (float *)out->data, ws, s);
 }
 
+// -------------------------------------------------------------- fused step --
+
+size_t qwm_verify_step_workspace_size(const qwm_moe_layer * layer, const qwm_tensor * lm_head, int64_t T) {
+    MoePlan m;
+    StepPlan p;
+    std::string why;
+    if (!lm_head || check_layer(layer, T, m) != QWM_OK || !step_plan(layer, lm_head, T, p, why)) return 0;
+    return p.total;
+}
+
+static bool overlaps(const qwm_tensor * a, const qwm_tensor * b) {
+    const uintptr_t a0 = (uintptr_t)a->data, a1 = a0 + a->nb[3] * (size_t)a->ne[3];
+    const uintptr_t b0 = (uintptr_t)b->data, b1 = b0 + b->nb[3] * (size_t)b->ne[3];
+    return a0 < b1 && b0 < a1;
+}
+
+int qwm_verify_step(const qwm_moe_layer * layer, int32_t layer_index, const int32_t * slot_tables,
+                    int64_t table_stride, const qwm_tensor * x, const qwm_tensor * rm, const qwm_tensor * resid,
+                    qwm_tensor * out, qwm_tensor * ids_out, qwm_tensor * w_out, const qwm_tensor * lm_head,
+                    const float * norm_w, float eps, const int32_t * drafts, int32_t * result,
+                    void * workspace, size_t ws_bytes, void * stream) {
+    if (!x || !lm_head || !result) return fail(QWM_ERR_ARG, "verify_step: NULL argument");
+    if (!slot_tables) return fail(QWM_ERR_ARG, "verify_step: slot tables are NULL");
+    MoePlan m;
+    int rc = check_layer(layer, x->ne[1], m);
+    if (rc != QWM_OK) return rc;
+    StepPlan p;
+    std::string why;
+    if (!step_plan(layer, lm_head, x->ne[1], p, why)) return fail(QWM_ERR_UNSUPPORTED, "verify_step: " + why);
+    if ((rc = check_act(x, p.moe.H, "x")) != QWM_OK) return rc;
+    if ((rc = check_act(out, p.moe.H, "out")) != QWM_OK) return rc;
+    if (out->ne[1] != p.moe.T) return fail(QWM_ERR_ARG, "verify_step: out must be [H, T]");
+    if (resid && ((rc = check_act(resid, p.moe.H, "resid")) != QWM_OK || resid->ne[1] != p.moe.T))
+        return rc != QWM_OK ? rc : fail(QWM_ERR_ARG, "verify_step: resid must be [H, T]");
+    if (overlaps(out, x) || (resid && overlaps(out, resid)))
+        return fail(QWM_ERR_ARG, "verify_step: out must not overlap x or resid");
+    if (rm && (rm->type != T_F32 || rm->ne[0] != p.moe.E || rm->ne[1] != p.moe.T || !fully_contiguous(rm)))
+        return fail(QWM_ERR_ARG, "verify_step: rm must be contiguous f32 [E, T]");
+    if (ids_out && (ids_out->type != T_I32 || ids_out->ne[0] != p.moe.k || ids_out->ne[1] != p.moe.T || ids_out->nb[0] != 4))
+        return fail(QWM_ERR_ARG, "verify_step: ids_out must be i32 [k, T]");
+    if (w_out && (w_out->type != T_F32 || w_out->ne[0] != p.moe.k || w_out->ne[1] != p.moe.T || w_out->nb[0] != 4))
+        return fail(QWM_ERR_ARG, "verify_step: w_out must be f32 [k, T]");
+    if (table_stride < (int64_t)(layer_index + 1) * p.moe.E) return fail(QWM_ERR_ARG, "verify_step: slot table stride too small");
+    if (!contiguous_rows(lm_head)) return fail(QWM_ERR_UNSUPPORTED, "verify_step: lm_head rows must be contiguous");
+    if ((uintptr_t)lm_head->data % 4 || (uintptr_t)norm_w % 16) return fail(QWM_ERR_ARG, "verify_step: misaligned lm_head or norm_w");
+    if (p.moe.T > 1 && !drafts) return fail(QWM_ERR_ARG, "verify_step: drafts are NULL");
+    if (!workspace || ws_bytes < p.total) return fail(QWM_ERR_WORKSPACE, "verify_step: workspace too small");
+    StepCall c;
+    c.L = layer; c.layer = layer_index; c.slot_tables = slot_tables; c.table_stride = table_stride;
+    c.x = (const float *)x->data; c.rm = rm ? (const float *)rm->data : nullptr;
+    c.resid = resid ? (const float *)resid->data : nullptr; c.out = (float *)out->data;
+    c.ids_out = ids_out ? (int32_t *)ids_out->data : nullptr; c.ids_ld = ids_out ? (int64_t)(ids_out->nb[1] / 4) : 0;
+    c.w_out = w_out ? (float *)w_out->data : nullptr; c.w_ld = w_out ? (int64_t)(w_out->nb[1] / 4) : 0;
+    c.lm_head = (const uint8_t *)lm_head->data; c.norm_w = norm_w; c.eps = eps; c.drafts = drafts; c.result = result;
+    return launch_step(c, p, (uint8_t *)workspace, (hipStream_t)stream);
+}
+
 // ------------------------------------------------------------------ verify --
 
 size_t qwm_verify_workspace_size(const qwm_tensor * lm_head, int64_t T) {

@@ -24,7 +24,7 @@ int fail(int code, const std::string & msg);
     } while (0)
 
 constexpr int MAX_T = 8;        // tokens per GEMV batch (decode / verify)
-constexpr int MAX_TILES = 256;  // row tiles of the down projection (combine tickets)
+constexpr int MAX_TILES = 512;  // row tiles of the down projection (combine tickets)
 constexpr int MAX_K = 16;       // experts per token
 constexpr int MAX_E = 2048;     // experts per layer
 constexpr int MAX_PAIRS = MAX_T * MAX_K;
@@ -88,6 +88,21 @@ struct MmidArgs {
 };
 size_t mmid_workspace(int64_t K, int64_t T, int64_t ne11, int64_t n_ids);
 int launch_mmid(const MmidArgs & a, uint8_t * ws, hipStream_t s);
+
+// ---- the fused verify step (qwm_step.hip) ----
+struct StepPlan {
+    MoePlan moe;
+    int64_t V;
+    size_t v_counter, v_pv, v_pi, lg, xq_d, xq_bs, bar, flags, total;
+};
+bool step_plan(const qwm_moe_layer * L, const qwm_tensor * lm_head, int64_t T, StepPlan & p, std::string & why);
+struct StepCall {
+    const qwm_moe_layer * L; int32_t layer; const int32_t * slot_tables; int64_t table_stride;
+    const float * x; const float * rm; const float * resid; float * out;
+    int32_t * ids_out; int64_t ids_ld; float * w_out; int64_t w_ld;
+    const uint8_t * lm_head; const float * norm_w; float eps; const int32_t * drafts; int32_t * result;
+};
+int launch_step(const StepCall & c, const StepPlan & p, uint8_t * ws, hipStream_t s);
 
 // ---- launchers (qwm_verify.hip) ----
 int launch_verify(const uint8_t * lm_head, const float * x, const float * norm_w, float eps,

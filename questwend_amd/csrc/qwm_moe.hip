@@ -13,49 +13,13 @@
 // the fp32 sums across blocks.
 #include "qwm_device.h"
 #include "qwm_internal.h"
+#include "qwm_q4k.h"
 
 namespace qwm {
 
 // ======================================================================
 // Router: logits, soft_max, top-k, weights, Q8_K of x, expert schedule
 // ======================================================================
-
-// Q8_K quantization of one 256-value block by one wave (ggml-quants.c:2769-2806):
-// lane L owns values 4L..4L+3.  max = the signed value of the first largest
-// |x|; iscale = -127/max; q = min(127, nearest_int(iscale*x)); bsums per 16;
-// d = 1/iscale.  Writes qs (256 B), d, and the 16 bsums (as int32).
-QWM_DEV void quantize_block_q8K(const float * __restrict__ src, int8_t * __restrict__ qs, float * __restrict__ d_out,
-                                int32_t * __restrict__ bs_out, int lane) {
-    const float4 v4 = reinterpret_cast<const float4 *>(src)[lane];
-    const float v[4] = {v4.x, v4.y, v4.z, v4.w};
-    float a = __builtin_fabsf(v[0]);
-    int ii = 0;
-#pragma unroll
-    for (int i = 1; i < 4; ++i)
-        if (__builtin_fabsf(v[i]) > a) { a = __builtin_fabsf(v[i]); ii = i; }
-    int idx = 4 * lane + ii;
-    wave_best_first(a, idx);
-    idx = __builtin_amdgcn_readfirstlane(idx);
-    const int c = idx & 3;
-    const float mine = c == 0 ? v[0] : c == 1 ? v[1] : c == 2 ? v[2] : v[3];
-    const float mx = readlane_f(mine, idx >> 2);
-    int q[4] = {0, 0, 0, 0};
-    float d = 0.f;
-    if (a != 0.f) {
-        const float iscale = -127.f / mx;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) q[i] = min(127, nearest_int_mul(iscale, v[i]));
-        d = 1.f / iscale;
-    }
-    const uint32_t packed = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) |
-                            ((uint32_t)(q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24);
-    reinterpret_cast<uint32_t *>(qs)[lane] = packed;
-    int sm = q[0] + q[1] + q[2] + q[3];
-    sm += dpp_i<0xB1>(sm);
-    sm += dpp_i<0x4E>(sm);
-    if ((lane & 3) == 0) bs_out[lane >> 2] = sm;
-    if (lane == 0) *d_out = d;
-}
 
 struct RouteKArgs {
     const float * W; const float * x; const float * rm; const float * sgi;
@@ -305,65 +269,6 @@ __global__ void __launch_bounds__(256) k_route(RouteKArgs a) {
         for (int i = 0; i < T; ++i) u.pair[i] = i;
     }
     if (lane == 0) *a.n_units = nu;
-}
-
-// ======================================================================
-// Q4_K x Q8_K GEMV machinery
-// ======================================================================
-
-// Activation bytes of one token for one 16-byte quant chunk (sub-blocks 2j
-// and 2j+1 of super-block sb, half h): 16 q8 values for the low nibbles,
-// 16 for the high nibbles, the block scale and the two 16-value bsums.
-struct ActChunk {
-    uint4 lo, hi;
-    float d;
-    int32_t bs_lo, bs_hi;
-};
-
-QWM_DEV void load_act_chunk(ActChunk & A, const int8_t * qs, const float * dd, const int32_t * bs, int c) {
-    const int sb = c >> 3, p = c & 7, j = p >> 1, h = p & 1;
-    const int8_t * q = qs + sb * QK_K + 64 * j + 16 * h;
-    A.lo = *reinterpret_cast<const uint4 *>(q);
-    A.hi = *reinterpret_cast<const uint4 *>(q + 32);
-    A.d = dd[sb];
-    A.bs_lo = bs[sb * 16 + 4 * j + h];
-    A.bs_hi = bs[sb * 16 + 4 * j + 2 + h];
-}
-
-// Weight data of one chunk: the 16 quant bytes and the block header.
-struct WChunk {
-    uint4 q, hd;
-};
-
-QWM_DEV void load_w_chunk(WChunk & W, const uint8_t * row, int c) {
-    const int sb = c >> 3, p = c & 7;
-    const uint8_t * blk = row + sb * 144;
-    W.hd = *reinterpret_cast<const uint4 *>(blk);
-    W.q = *reinterpret_cast<const uint4 *>(blk + 16 + 16 * p);
-}
-
-// Contribution of one chunk to d*sum(sc*q4*q8) - dmin*sum(m*bsum).
-QWM_DEV float chunk_dot(const WChunk & W, const ActChunk & A, int c, float acc) {
-    const int p = c & 7, j = p >> 1;
-    int sc_lo, m_lo, sc_hi, m_hi;
-    q4k_scale_min_reg(2 * j, W.hd.y, W.hd.z, W.hd.w, sc_lo, m_lo);
-    q4k_scale_min_reg(2 * j + 1, W.hd.y, W.hd.z, W.hd.w, sc_hi, m_hi);
-    const uint32_t m4 = 0x0F0F0F0Fu;
-    int s_lo = 0, s_hi = 0;
-    s_lo = dot4(W.q.x & m4, A.lo.x, s_lo);
-    s_lo = dot4(W.q.y & m4, A.lo.y, s_lo);
-    s_lo = dot4(W.q.z & m4, A.lo.z, s_lo);
-    s_lo = dot4(W.q.w & m4, A.lo.w, s_lo);
-    s_hi = dot4((W.q.x >> 4) & m4, A.hi.x, s_hi);
-    s_hi = dot4((W.q.y >> 4) & m4, A.hi.y, s_hi);
-    s_hi = dot4((W.q.z >> 4) & m4, A.hi.z, s_hi);
-    s_hi = dot4((W.q.w >> 4) & m4, A.hi.w, s_hi);
-    const int isum = sc_lo * s_lo + sc_hi * s_hi;
-    const int imin = m_lo * A.bs_lo + m_hi * A.bs_hi;
-    const float d = A.d * fp16_to_f32((uint16_t)(W.hd.x & 0xffff));
-    const float dmin = A.d * fp16_to_f32((uint16_t)(W.hd.x >> 16));
-    acc = __builtin_fmaf(d, (float)isum, acc);
-    return __builtin_fmaf(-dmin, (float)imin, acc);
 }
 
 // Wave steps per GEMV tile: each wave issues the weight loads of GEMV_STEPS

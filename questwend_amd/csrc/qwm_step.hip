@@ -1,0 +1,762 @@
+// qwm_step.hip -- the whole MTP verify step in one persistent launch: the MoE
+// block (router, selection, gate/up + SwiGLU, down + combine + residual) and
+// the verify head (rms_norm, Q8_0 lm_head GEMV + argmax, greedy accept).
+//
+// The per-op kernels (qwm_moe.hip, qwm_verify.hip) spend most of a verify step
+// in latency: kernel boundaries, single-shot waves that occupy the GPU in
+// rounds, and the serial selection tail of one workgroup.  Here a grid of
+// exactly the co-resident workgroups (sized by the occupancy query) walks the
+// phases:
+//
+//   P0  router rows (CPU summation order), Q8_K of x            -> barrier
+//   P1  every workgroup repeats the selection for all tokens from the logits
+//       (softmax, top-k, weights, expert union, slots) in registers and LDS:
+//       no hand-off and no serial tail
+//   P2  gate/up GEMVs over the expert union, persistent row loops with a
+//       4-deep load ring, fused SwiGLU                            -> barrier
+//   P3  down GEMVs; the last unit to finish a row tile combines it
+//       (CPU order, + shared expert, + residual)                  -> barrier
+//   P4  the verify head of qwm_vhead.h on the block's output
+//
+// Data that crosses workgroups inside the launch is written with agent-scope
+// stores (write-through, coherent across the XCDs' L2s) into buffers that no
+// workgroup reads before the barrier or ticket that publishes them.  Every
+// 128-byte line of such a buffer has a single writing workgroup (the router
+// logits, the Q8_K scales and the combine tiles are padded or aligned for
+// that), so a consumer's ordinary L2-cached load can only find that writer's
+// fresh line or none; the one multi-writer buffer (SwiGLU activations) is read
+// with agent-scope loads.  Grid barriers: one arrival counter, and a flag line
+// per workgroup that the last arriver sets, so no line is polled by more than
+// one workgroup; spins are bounded (a timeout sets an error word and the
+// result reports a = -1 instead of hanging).
+#include <hip/hip_runtime.h>
+
+#include "qwm_internal.h"
+#include "qwm_q4k.h"
+#include "qwm_vhead.h"
+
+namespace qwm {
+
+constexpr int SH = 2048;                 // hidden size of the fused step
+constexpr int SNB = SH / QK_K;           // Q8_K blocks per token
+constexpr uint32_t SPIN_LIMIT = 1u << 21;
+constexpr int MAX_NDOWN_S = 2048;        // longest down-projection input (FFN width)
+constexpr int STEP_MAX_E = 512;          // experts per layer in the fused step
+constexpr int RX_P = 132;                // pitch of the transposed router rows in LDS (floats)
+constexpr size_t cmax(size_t x, size_t y) { return x > y ? x : y; }
+
+struct StepArgs {
+    const float * W_r; const float * x; const float * rm; const float * sgi;   // router [E][H], x [T][H]
+    int E, k, norm, tiny; float scale;
+    int N, N_sh, shared;
+    const uint8_t * gate; const uint8_t * up; const uint8_t * down;
+    size_t gate_slab, up_slab, down_slab;
+    const uint8_t * sh_gate; const uint8_t * sh_up; const uint8_t * sh_down;
+    const int32_t * slot_tables; int64_t table_stride; int layer;
+    const float * resid; float * out;                                           // [T][H]
+    int32_t * ids_out; int64_t ids_ld; float * w_out; int64_t w_ld;
+    float * lg;                                                                 // [E + 1][32]: logits of row e (row E: shared gate)
+    int8_t * xq_qs; float * xq_d; int32_t * xq_bs;                              // d, bsums: one 32-word line per block
+    float * act; float * act_sh; float * ex; float * ex_sh;
+    uint32_t * bar; uint32_t * epoch; uint32_t * flags;                         // flags: one 32-word line per workgroup
+    int32_t * tile_counters; int32_t * err;
+    VerifyArgs v;                                                               // v.x = out
+};
+
+// Per-workgroup copy of the expert schedule (phase P1).
+struct StepShared {
+    int32_t ids[MAX_PAIRS];
+    float w[MAX_PAIRS];
+    float shg[MAX_T];
+    Unit units[MAX_PAIRS + 1];
+    int32_t uslot[MAX_PAIRS + 1][3];
+    int32_t nu;
+};
+
+// Grid barrier number `i` (1, 2, 3) of launch `epoch`.  The last workgroup to
+// arrive re-arms the counter and then sets every workgroup's flag line to
+// epoch * 4 + i; the others poll their own line.
+QWM_DEV void grid_barrier(const StepArgs & a, int i, int G, uint32_t epoch) {
+    __shared__ int s_rel;
+    __builtin_amdgcn_s_waitcnt(0);               // this wave's agent-scope writes have completed
+    __syncthreads();
+    if (threadIdx.x == 0)
+        s_rel = __hip_atomic_fetch_add(a.bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)G - 1;
+    __syncthreads();
+    const uint32_t v = epoch * 4u + (uint32_t)i;
+    if (s_rel) {
+        if (threadIdx.x == 0) st_agent(a.bar, 0u);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        for (int q = threadIdx.x; q < G * 32; q += 256) st_agent(a.flags + q, v);   // whole lines
+    } else if (threadIdx.x == 0) {
+        const uint32_t * f = a.flags + (size_t)blockIdx.x * 32;
+        uint32_t spins = 0;
+        while (ld_agent(f) != v) {
+            __builtin_amdgcn_s_sleep(1);
+            if (++spins > SPIN_LIMIT) { st_agent(a.err, 1); break; }
+        }
+    }
+    __syncthreads();
+}
+
+// ---------------------------------------------------------------- P0 ----
+// Router rows e = g, g + G, ... (row E: the shared-expert gate row) and the
+// Q8_K blocks of x (waves counted from the end of the grid).
+template <int NT>
+QWM_DEV void step_router(const StepArgs & a, int g, int G, uint8_t * smem) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int E = a.E;
+    {
+        const int gw = (G - 1 - g) * 4 + wave;
+        for (int jb = gw; jb < NT * SNB; jb += 4 * G) {
+            const int t = jb / SNB, b = jb % SNB;
+            quantize_block_q8K<true>(a.x + (size_t)t * SH + b * QK_K, a.xq_qs + (size_t)t * SH + b * QK_K,
+                                     a.xq_d + (size_t)(t * SNB + b) * 32, a.xq_bs + (size_t)(t * SNB + b) * 32, lane);
+        }
+    }
+    const int rows = E + (a.sgi ? 1 : 0);
+    if (g >= rows) return;                       // uniform per workgroup; no barrier follows inside
+    float * xt = reinterpret_cast<float *>(smem);            // [4][16][RX_P]: x of four tokens, transposed
+    float * wt = xt + 4 * 16 * RX_P;                         // [16][RX_P]: one router row, transposed
+    // 16 x 128 transposes into LDS: dst[h & 15][h >> 4] = src[h]; thread tid
+    // owns float4 number tid and tid + 256 of a 2048-float row
+    auto put = [&](float * dst, const float4 (&v)[2]) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int h = 4 * (tid + 256 * i);
+            dst[((h + 0) & 15) * RX_P + ((h + 0) >> 4)] = v[i].x;
+            dst[((h + 1) & 15) * RX_P + ((h + 1) >> 4)] = v[i].y;
+            dst[((h + 2) & 15) * RX_P + ((h + 2) >> 4)] = v[i].z;
+            dst[((h + 3) & 15) * RX_P + ((h + 3) >> 4)] = v[i].w;
+        }
+    };
+    auto get = [&](float4 (&v)[2], const float * src) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) v[i] = reinterpret_cast<const float4 *>(src)[tid + 256 * i];
+    };
+    if (a.tiny) {
+        // llamafile tinyBLAS<16> order (sgemm.cpp:600-670): lane (t, l) runs one
+        // fma chain over 16-wide steps, then the 16-lane tree.  Tokens in groups
+        // of four (x of one group staged in LDS with the first row, one round
+        // trip); one row at a time.
+        for (int t0 = 0; t0 < NT; t0 += 4) {
+            float4 xv[4][2], wv[2];
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                if (t0 + q < NT) get(xv[q], a.x + (size_t)(t0 + q) * SH);
+            for (int e = g; e < E; e += G) {
+                get(wv, a.W_r + (size_t)e * SH);
+                __syncthreads();                 // the previous row's readers are done with LDS
+                if (e == g) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        if (t0 + q < NT) put(xt + q * 16 * RX_P, xv[q]);
+                }
+                put(wt, wv);
+                __syncthreads();
+                const int l = lane & 15, t = t0 + (lane >> 4);
+                if (wave == 0 && t < NT) {
+                    const float * xr = xt + (t - t0) * 16 * RX_P + l * RX_P;
+                    const float * wr = wt + l * RX_P;
+                    float acc = 0.f;
+#pragma unroll 8
+                    for (int s = 0; s < SH / 16; s += 4) {
+                        const float4 x4 = *reinterpret_cast<const float4 *>(xr + s);
+                        const float4 w4 = *reinterpret_cast<const float4 *>(wr + s);
+                        acc = __builtin_fmaf(w4.x, x4.x, acc);
+                        acc = __builtin_fmaf(w4.y, x4.y, acc);
+                        acc = __builtin_fmaf(w4.z, x4.z, acc);
+                        acc = __builtin_fmaf(w4.w, x4.w, acc);
+                    }
+                    acc = tree16_dpp(acc);
+                    if (l == 0) st_agent(a.lg + (size_t)e * 32 + t, a.rm ? acc + a.rm[(size_t)t * E + e] : acc);
+                }
+            }
+            __syncthreads();
+        }
+    }
+    for (int e = g; e < rows; e += G) {
+        const bool sh_row = e == E;
+        if (a.tiny && !sh_row) continue;
+        // ggml_vec_dot_f32's AVX-512 order (vec.cpp:11-135), one token per wave pass
+        const float * w = sh_row ? a.sgi : a.W_r + (size_t)e * SH;
+        float wv[SH / 64];
+#pragma unroll
+        for (int s = 0; s < SH / 64; ++s) wv[s] = w[64 * s + lane];
+        for (int t = wave; t < NT; t += 4) {
+            const float * xr = a.x + (size_t)t * SH;
+            float xv[SH / 64];
+#pragma unroll
+            for (int s = 0; s < SH / 64; ++s) xv[s] = xr[64 * s + lane];
+            float acc = 0.f;
+#pragma unroll
+            for (int s = 0; s < SH / 64; ++s) acc = __builtin_fmaf(wv[s], xv[s], acc);
+            acc += lane_xor32_f(acc);
+            acc += lane_xor16_f(acc);
+            acc = tree16_dpp(acc);
+            if (lane == 0) st_agent(a.lg + (size_t)e * 32 + t, (a.rm && !sh_row) ? acc + a.rm[(size_t)t * E + e] : acc);
+        }
+    }
+}
+
+// ---------------------------------------------------------------- P1 ----
+// The selection of route_experts (runtime.cpp:2693-2734) for every token, in
+// every workgroup: soft_max (ops.cpp:5813-5920, vec.cpp:531: v_expf over
+// 16-lane chunks, each chunk's 16-lane tree added to a double sum in order,
+// scaled by 1/sum), top-k (larger probability, then lower index), weight
+// normalization (double sum, clamp 6.103515625e-5, division), scale; then
+// the expert union in first-occurrence order and each unit's slots.
+//
+// Top-k without serial argmax rounds: probabilities are non-negative, so
+// their bit patterns order like the values; a 31-step radix descent over
+// ballots finds the k-th largest pattern, ties at that value are taken in
+// index order, and each selected lane ranks itself against the k others.
+// R: probabilities per lane (E <= 64 * R).
+template <int NT, int R>
+QWM_DEV void step_select(const StepArgs & a, int g, StepShared & S, uint8_t * smem) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int E = a.E, k = a.k;
+    const int nr = (E + 63) / 64;
+    const int nfull = E & ~15;
+    const unsigned long long below = (1ull << lane) - 1ull;
+    for (int t = wave; t < NT; t += 4) {
+        float v[R];
+        float m = -__builtin_inff();
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            v[r] = -__builtin_inff();
+            const int i = 64 * r + lane;
+            if (r < nr && i < E) v[r] = a.lg[(size_t)i * 32 + t];
+            m = fmaxf(m, v[r]);
+        }
+        m = wave_max(m);
+        double sum = 0.0;
+        float tailv = 0.f;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if (r < nr) {
+                const int i = 64 * r + lane;
+                float ev = 0.f;
+                if (i < nfull) ev = v_expf(v[r] - m);
+                else if (i < E) ev = expf(v[r] - m);          // scalar tail: libm expf on the CPU
+                const float cs = tree16_dpp(i < nfull ? ev : 0.f);
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    if (64 * r + 16 * q < nfull) sum += (double)readlane_f(cs, 16 * q);
+                if (r == (nfull >> 6)) tailv = ev;
+                v[r] = ev;
+            }
+        }
+        for (int i = nfull; i < E; ++i) sum += (double)readlane_f(tailv, i & 63);
+        const float sc = (float)(1.0 / sum);
+        uint32_t key[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int i = 64 * r + lane;
+            v[r] = v[r] * sc;
+            key[r] = (r < nr && i < E) ? __float_as_uint(v[r]) : 0u;   // invalid lanes: +0, larger index
+        }
+        // k-th largest key
+        uint32_t th = 0;
+        for (int bit = 30; bit >= 0; --bit) {
+            const uint32_t cand = th | (1u << bit);
+            int cnt = 0;
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                if (r < nr) cnt += __popcll(__ballot(key[r] >= cand));
+            if (cnt >= k) th = cand;
+        }
+        // selection: every key above th, then keys equal to th in index order
+        int gt = 0;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (r < nr) gt += __popcll(__ballot(key[r] > th));
+        int need = k - gt;
+        bool sel[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            sel[r] = false;
+            if (r < nr) {
+                const unsigned long long eq = __ballot(key[r] == th && 64 * r + lane < E);
+                const int before = __popcll(eq & below);
+                sel[r] = key[r] > th || ((eq >> lane) & 1ull && before < need);
+                need -= min(need, __popcll(eq));
+            }
+        }
+        // rank of each selected entry: larger value first, then lower index
+        int rank[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) rank[r] = 0;
+#pragma unroll
+        for (int rs = 0; rs < R; ++rs) {
+            if (rs >= nr) break;
+            unsigned long long bs = __ballot(sel[rs]);
+            while (bs) {
+                const int ls = __builtin_ctzll(bs);
+                bs &= bs - 1;
+                const uint32_t ks = __builtin_amdgcn_readlane(key[rs], ls);
+                const int is = 64 * rs + ls;
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const int i = 64 * r + lane;
+                    rank[r] += sel[r] && (ks > key[r] || (ks == key[r] && is < i));
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (sel[r]) { S.ids[t * k + rank[r]] = 64 * r + lane; S.w[t * k + rank[r]] = v[r]; }
+        wave_sync();
+        if (lane == 0) {
+            float w[MAX_K];
+#pragma unroll
+            for (int j = 0; j < MAX_K; ++j) w[j] = j < k ? S.w[t * k + j] : 0.f;
+            if (a.norm) {
+                double s = 0.0;
+#pragma unroll
+                for (int j = 0; j < MAX_K; ++j)
+                    if (j < k) s += (double)w[j];
+                float ws = (float)s;
+                ws = fmaxf(fminf(ws, __builtin_inff()), 6.103515625e-5f);
+#pragma unroll
+                for (int j = 0; j < MAX_K; ++j) w[j] = w[j] / ws;
+            }
+            if (a.scale != 0.0f && a.scale != 1.0f)
+#pragma unroll
+                for (int j = 0; j < MAX_K; ++j) w[j] = w[j] * a.scale;
+#pragma unroll
+            for (int j = 0; j < MAX_K; ++j) {
+                if (j < k) {
+                    S.w[t * k + j] = w[j];
+                    if (g == 0) {
+                        if (a.ids_out) a.ids_out[(size_t)t * a.ids_ld + j] = S.ids[t * k + j];
+                        if (a.w_out) a.w_out[(size_t)t * a.w_ld + j] = w[j];
+                    }
+                }
+            }
+            S.shg[t] = a.sgi ? 1.f / (1.f + expf(-a.lg[(size_t)E * 32 + t])) : 1.f;   // unary-ops.cpp:31
+        }
+    }
+    __syncthreads();
+    // expert union through per-expert LDS tables: first pair, token mask, unit
+    int32_t * tab_first = reinterpret_cast<int32_t *>(smem);
+    uint32_t * tab_mask = reinterpret_cast<uint32_t *>(tab_first + MAX_E);
+    int32_t * tab_unit = reinterpret_cast<int32_t *>(tab_mask + MAX_E);
+    __shared__ unsigned long long s_bal[2];
+    const int P = NT * k;
+    const int p = tid;
+    const int e = p < P ? S.ids[p] : 0;
+    if (p < P) { tab_first[e] = 0x7fffffff; tab_mask[e] = 0u; }
+    __syncthreads();
+    if (p < P) { atomicMin(&tab_first[e], p); atomicOr(&tab_mask[e], 1u << (p / k)); }
+    __syncthreads();
+    const bool first = p < P && tab_first[e] == p;
+    const uint32_t tmask = p < P ? tab_mask[e] : 0u;
+    const unsigned long long bal = __ballot(first);
+    if (lane == 0 && wave < 2) s_bal[wave] = bal;
+    __syncthreads();
+    const int nu = __popcll(s_bal[0]) + (P > 64 ? __popcll(s_bal[1]) : 0);
+    if (first) {
+        const int u = (wave == 1 ? __popcll(s_bal[0]) : 0) + __popcll(bal & below);
+        S.units[u].expert = e;
+        S.units[u].n = __popc(tmask);
+        tab_unit[e] = u;
+    }
+    __syncthreads();
+    if (p < P) {
+        const int t = p / k;
+        S.units[tab_unit[e]].pair[__popc(tmask & ((1u << t) - 1u))] = p;
+    }
+    __syncthreads();
+    for (int u = tid; u < nu; u += 256)
+        for (int r = 0; r < 3; ++r)
+            S.uslot[u][r] = a.slot_tables[(size_t)r * a.table_stride + (size_t)a.layer * E + S.units[u].expert];
+    if (tid == 0) {
+        if (a.shared) {
+            S.units[nu].expert = -1;
+            S.units[nu].n = NT;
+            for (int i = 0; i < NT; ++i) S.units[nu].pair[i] = i;
+        }
+        S.nu = nu;
+    }
+    __syncthreads();
+}
+
+// ---------------------------------------------------------------- P2 ----
+// gate/up: items of GU_ROWS consecutive rows of one unit; workgroup g takes
+// items g, g + G, ...  Each wave streams GU_ROWS / 4 rows through a
+// GU_PF-deep ring with the unit's Q8_K activations in registers; act =
+// silu(g) * u (the vectorized silu except for the row tail the CPU runs
+// through scalar expf) is collected in LDS and leaves as whole lines.
+constexpr int GU_ROWS = 64;
+constexpr int GU_PF = 6;
+
+template <int MAXP>
+QWM_DEV void step_gateup(const StepArgs & a, int g, int G, const StepShared & S, uint8_t * smem) {
+    constexpr int LPR = 64;                      // 64 chunks of 16 B per 2048-wide row
+    constexpr int RPW = GU_ROWS / 4;             // rows per wave per item
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int c = lane;
+    float (*s_act)[GU_ROWS] = reinterpret_cast<float (*)[GU_ROWS]>(smem);
+    const int nb_r = (a.N + GU_ROWS - 1) / GU_ROWS, nb_s = a.shared ? (a.N_sh + GU_ROWS - 1) / GU_ROWS : 0;
+    const int items = S.nu * nb_r + nb_s;
+    constexpr size_t row_bytes = (size_t)SNB * 144;
+    for (int item = g; item < items; item += G) {
+        const bool shared = item >= S.nu * nb_r;
+        const int u = shared ? S.nu : item / nb_r;
+        const int blk = shared ? item - S.nu * nb_r : item % nb_r;
+        const int rows = shared ? a.N_sh : a.N;
+        const Unit & U_ = S.units[u];
+        const int n = U_.n;
+        const uint8_t * gbase = shared ? a.sh_gate : a.gate + (size_t)S.uslot[u][0] * a.gate_slab;
+        const uint8_t * ubase = shared ? a.sh_up : a.up + (size_t)S.uslot[u][1] * a.up_slab;
+        const int rb = blk * GU_ROWS, re = min(rb + GU_ROWS, rows);
+        const int r0 = rb + wave * RPW;          // rows are a multiple of 256: every wave has RPW rows
+        {
+            // activations first: vector-memory waits count in issue order, so
+            // the ring's loads must be the youngest for its waits to stay partial
+            ActChunk A[MAXP];
+#pragma unroll
+            for (int i = 0; i < MAXP; ++i)
+                if (i < n) {
+                    const int tok = shared ? U_.pair[i] : U_.pair[i] / a.k;
+                    load_act_chunk<32, 32>(A[i], a.xq_qs + (size_t)tok * SH, a.xq_d + (size_t)tok * SNB * 32,
+                                           a.xq_bs + (size_t)tok * SNB * 32, c);
+                }
+            const uint8_t * gp = gbase + (size_t)r0 * row_bytes;
+            const uint8_t * up = ubase + (size_t)r0 * row_bytes;
+            WChunkS Gb[GU_PF], Ub[GU_PF];
+#pragma unroll
+            for (int p = 0; p < GU_PF; ++p) {
+                load_w_chunk_s(Gb[p], gp + (size_t)p * row_bytes, c);
+                load_w_chunk_s(Ub[p], up + (size_t)p * row_bytes, c);
+            }
+            // straight-line ring: every wait below is a partial one
+#pragma clang loop unroll(full)
+            for (int s = 0; s < RPW; ++s) {
+                const int p = s % GU_PF;
+                const int r = r0 + s;
+#pragma unroll
+                for (int i = 0; i < MAXP; ++i) {
+                    if (i < n) {
+                        const float gs = lane_sum<LPR>(chunk_dot_s(Gb[p], A[i], c, 0.f));
+                        const float us = lane_sum<LPR>(chunk_dot_s(Ub[p], A[i], c, 0.f));
+                        if (c == i)
+                            s_act[i][r - rb] = (r < rows - (rows & 15)) ? v_silu(gs) * us : gs / (1.0f + expf(-gs)) * us;
+                    }
+                }
+                if (s + GU_PF < RPW) {
+                    load_w_chunk_s(Gb[p], gp + (size_t)(s + GU_PF) * row_bytes, c);
+                    load_w_chunk_s(Ub[p], up + (size_t)(s + GU_PF) * row_bytes, c);
+                }
+            }
+        }
+        __syncthreads();
+        for (int q = tid; q < n * GU_ROWS; q += 256) {
+            const int i = q / GU_ROWS, r = rb + q % GU_ROWS;
+            if (r < re) {
+                if (shared) st_agent(a.act_sh + (size_t)U_.pair[i] * rows + r, s_act[i][r - rb]);
+                else st_agent(a.act + (size_t)U_.pair[i] * rows + r, s_act[i][r - rb]);
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------- P3 ----
+// down + combine: each unit's rows are cut into the same 16 tiles of 128 rows
+// (whole 32-row lines); items (unit, tile) go to workgroups g, g + G, ...
+// The workgroup quantizes the unit's activations to Q8_K in LDS, streams the
+// tile's rows (outputs collected in LDS, written as whole lines) and takes the
+// tile's ticket; the last of the U units combines the tile for every token
+// (runtime.cpp:3815-3817 for T == 1, 4544-4550 for T > 1; then the shared
+// expert and the residual).
+constexpr int DN_TR = 128;
+constexpr int DN_PF = 6;
+
+template <int NT, int LPR, int MAXP>
+QWM_DEV void step_down(const StepArgs & a, int g, int G, const StepShared & S, uint8_t * smem) {
+    constexpr int RPI = WAVE / LPR;
+    constexpr int TR = DN_TR;                    // 16 tiles of 128 rows
+    constexpr int NSTEP = TR / (4 * RPI);        // wave steps per tile
+    constexpr int ntiles = SH / TR;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int U = S.nu + a.shared;
+    int8_t (*s_qs)[MAX_NDOWN_S] = reinterpret_cast<int8_t (*)[MAX_NDOWN_S]>(smem);
+    float (*s_d)[MAX_NDOWN_S / QK_K] = reinterpret_cast<float (*)[MAX_NDOWN_S / QK_K]>(smem + MAXP * MAX_NDOWN_S);
+    int32_t (*s_bs)[MAX_NDOWN_S / 16] =
+        reinterpret_cast<int32_t (*)[MAX_NDOWN_S / 16]>(smem + MAXP * MAX_NDOWN_S + MAXP * (MAX_NDOWN_S / QK_K) * 4);
+    float (*s_ex)[DN_TR] = reinterpret_cast<float (*)[DN_TR]>(
+        smem + MAXP * (MAX_NDOWN_S + (MAX_NDOWN_S / QK_K) * 4 + (MAX_NDOWN_S / 16) * 4));
+    for (int item = g; item < U * ntiles; item += G) {
+        const int u = item / ntiles, x = item % ntiles;
+        const bool shared = u == S.nu;
+        const Unit & U_ = S.units[u];
+        const int n = U_.n;
+        const int K = shared ? a.N_sh : a.N;
+        const int nb = K / QK_K;
+        const int C = K / 32;
+        const int c = lane % LPR, rsub = lane / LPR;
+        // lanes past the row's chunks read a real chunk at the same position
+        // in its block (so their quads still rebuild a real header), weighted 0
+        const float on = c < C ? 1.f : 0.f;
+        const int cc = c < C ? c : C - 8 + (c & 7);
+        const uint8_t * base = shared ? a.sh_down : a.down + (size_t)S.uslot[u][2] * a.down_slab;
+        const size_t row_bytes = (size_t)nb * 144;
+        const int h0 = x * TR, h1 = h0 + TR;
+        const uint8_t * rp = base + (size_t)(h0 + wave * RPI + rsub) * row_bytes;   // row of step s: + 4 * RPI * s
+        for (int jb = wave; jb < n * nb; jb += 4) {
+            const int i = jb / nb, b = jb % nb;
+            const float * src = shared ? a.act_sh + (size_t)U_.pair[i] * K : a.act + (size_t)U_.pair[i] * K;
+            quantize_block_q8K(src + b * QK_K, &s_qs[i][b * QK_K], &s_d[i][b], &s_bs[i][b * 16], lane);
+        }
+        __syncthreads();
+        ActChunk A[MAXP];
+#pragma unroll
+        for (int i = 0; i < MAXP; ++i)
+            if (i < n) load_act_chunk(A[i], s_qs[i], s_d[i], s_bs[i], cc);
+        WChunkS Wb[DN_PF];
+#pragma unroll
+        for (int p = 0; p < DN_PF; ++p) load_w_chunk_s(Wb[p], rp + (size_t)(4 * RPI * p) * row_bytes, cc);
+#pragma clang loop unroll(full)
+        for (int st = 0; st < NSTEP; ++st) {
+            const int p = st % DN_PF;
+            const int r = h0 + (st * 4 + wave) * RPI + rsub;
+#pragma unroll
+            for (int i = 0; i < MAXP; ++i) {
+                if (i < n) {
+                    const float acc = lane_sum<LPR>(chunk_dot_s(Wb[p], A[i], cc, 0.f) * on);
+                    if (c == i) s_ex[i][r - h0] = acc;
+                }
+            }
+            if (st + DN_PF < NSTEP) load_w_chunk_s(Wb[p], rp + (size_t)(4 * RPI * (st + DN_PF)) * row_bytes, cc);
+        }
+        __syncthreads();
+        for (int q = tid; q < n * (h1 - h0); q += 256) {
+            const int i = q / (h1 - h0), h = h0 + q % (h1 - h0);
+            if (shared) st_agent(a.ex_sh + (size_t)U_.pair[i] * SH + h, s_ex[i][h - h0]);
+            else st_agent(a.ex + (size_t)U_.pair[i] * SH + h, s_ex[i][h - h0]);
+        }
+        if (last_workgroup(a.tile_counters + x, U)) {
+            // every expert output of the tile is in: combine it, two outputs per
+            // thread per pass with all their loads issued before any arithmetic
+            const int k = a.k;
+            const int TRh = h1 - h0;
+            for (int q0 = tid; q0 < NT * TRh; q0 += 512) {
+                float ev[2][MAX_K], shv[2], rv[2];
+#pragma unroll
+                for (int o = 0; o < 2; ++o) {
+                    const int q = min(q0 + 256 * o, NT * TRh - 1);
+                    const int t = q / TRh, h = h0 + q % TRh;
+                    const float * e = a.ex + (size_t)t * k * SH + h;
+#pragma unroll
+                    for (int j = 0; j < MAX_K; ++j) ev[o][j] = j < k ? e[(size_t)j * SH] : 0.f;
+                    shv[o] = a.shared ? a.ex_sh[(size_t)t * SH + h] : 0.f;
+                    rv[o] = a.resid ? a.resid[(size_t)t * SH + h] : 0.f;
+                }
+#pragma unroll
+                for (int o = 0; o < 2; ++o) {
+                    const int q = q0 + 256 * o;
+                    if (q >= NT * TRh) break;
+                    const int t = q / TRh, h = h0 + q % TRh;
+                    const float * wt = S.w + t * k;
+                    float sacc;
+                    if (NT == 1) {
+                        // vec_dot_f32 with n = k <= 16: a 16-group, else an
+                        // 8-group, of unfused products, then fused multiply-adds
+                        sacc = 0.0f;
+                        if (k >= 16) {
+#pragma unroll
+                            for (int l = 0; l < 16; ++l) sacc = sacc + ev[o][l] * wt[l];
+                        } else {
+                            const int g8 = k >= 8 ? 8 : 0;
+#pragma unroll
+                            for (int l = 0; l < 8; ++l)
+                                if (l < g8) sacc = sacc + ev[o][l] * wt[l];
+#pragma unroll
+                            for (int l = 0; l < 16; ++l)
+                                if (l >= g8 && l < k) sacc = __builtin_fmaf(ev[o][l], wt[l], sacc);
+                        }
+                    } else {
+                        sacc = ev[o][0] * wt[0];
+#pragma unroll
+                        for (int j = 1; j < MAX_K; ++j)
+                            if (j < k) sacc = sacc + ev[o][j] * wt[j];
+                    }
+                    if (a.shared) {
+                        float vv = shv[o];
+                        if (a.sgi) vv = vv * S.shg[t];
+                        sacc = sacc + vv;
+                    }
+                    if (a.resid) sacc = sacc + rv[o];
+                    st_agent(a.out + (size_t)t * SH + h, sacc);
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
+template <int NT, int LPR_D>
+__global__ void __launch_bounds__(256) k_step(StepArgs a) {
+    constexpr int MAXP = NT <= 1 ? 1 : NT <= 2 ? 2 : NT <= 4 ? 4 : 8;
+    constexpr size_t router_bytes = (size_t)5 * 16 * RX_P * 4;
+    constexpr size_t down_bytes = (size_t)MAXP * (MAX_NDOWN_S + (MAX_NDOWN_S / QK_K) * 4 + (MAX_NDOWN_S / 16) * 4 +
+                                                  DN_TR * 4);
+    constexpr size_t smem_bytes = cmax(cmax(router_bytes, down_bytes), VhSmem<NT>::bytes);
+    __shared__ __align__(16) uint8_t smem[smem_bytes];
+    __shared__ StepShared S;
+    __shared__ uint32_t s_epoch;
+    const int g = blockIdx.x, G = gridDim.x;
+    if (threadIdx.x == 0) s_epoch = ld_agent(a.epoch);   // constant until the last workgroup of this launch
+    __syncthreads();
+    const uint32_t epoch = s_epoch;
+
+    step_router<NT>(a, g, G, smem);
+    grid_barrier(a, 1, G, epoch);
+    if (a.E <= 128) step_select<NT, 2>(a, g, S, smem);
+    else step_select<NT, STEP_MAX_E / 64>(a, g, S, smem);
+    step_gateup<MAXP>(a, g, G, S, smem);
+    grid_barrier(a, 2, G, epoch);
+    step_down<NT, LPR_D, MAXP>(a, g, G, S, smem);
+    grid_barrier(a, 3, G, epoch);
+    __syncthreads();
+    constexpr int PF = NT <= 4 ? 2 : 1;
+    if (verify_body<NT, SH / 512, PF>(a.v, g, G, smem) && threadIdx.x == 0) {
+        // every workgroup has read the epoch and passed all barriers
+        st_agent(a.epoch, epoch + 1u);
+        if (ld_agent(a.err)) {
+            a.v.result[NT] = -1;
+            a.v.result[NT + 1] = -1;
+            st_agent(a.err, 0);
+        }
+    }
+}
+
+}  // namespace qwm
+
+// ======================================================================
+// host side
+// ======================================================================
+namespace qwm {
+
+constexpr int MAX_STEP_WG = 1024;
+
+bool step_plan(const qwm_moe_layer * L, const qwm_tensor * lm_head, int64_t T, StepPlan & p, std::string & why) {
+    if (!moe_plan(L, T, p.moe, why)) return false;
+    if (p.moe.H != SH) { why = "the fused step is built for hidden size 2048"; return false; }
+    if (L->gate_pool.type != T_Q4_K) { why = "the fused step needs Q4_K expert pools"; return false; }
+    if (p.moe.N > MAX_NDOWN_S || (p.moe.shared && p.moe.N_sh > MAX_NDOWN_S)) { why = "FFN width > 2048"; return false; }
+    if (p.moe.E > STEP_MAX_E) { why = "the fused step handles up to 512 experts"; return false; }
+    if (lm_head->type != T_Q8_0 || lm_head->ne[0] != SH) { why = "lm_head must be Q8_0 [2048, V]"; return false; }
+    p.V = lm_head->ne[1];
+    if (p.V < 8LL * MAX_STEP_WG || p.V > (1LL << 30)) { why = "the fused step needs 8192 <= V <= 2^30"; return false; }
+    size_t o = align_up(p.moe.total, 256);
+    auto take = [&](size_t bytes) { size_t at = o; o = align_up(o + bytes, 256); return at; };
+    p.v_counter = take(256);
+    p.v_pv = take(sizeof(float) * MAX_STEP_WG * T);
+    p.v_pi = take(sizeof(int32_t) * MAX_STEP_WG * T);
+    p.lg = take(sizeof(float) * 32 * (p.moe.E + 1));
+    p.xq_d = take(sizeof(float) * 32 * T * SNB);
+    p.xq_bs = take(sizeof(int32_t) * 32 * T * SNB);
+    p.bar = take(512);
+    p.flags = take(sizeof(uint32_t) * 32 * MAX_STEP_WG);
+    p.total = o;
+    return true;
+}
+
+template <int NT, int LPR_D>
+static int step_grid() {
+    static int grid = 0;
+    if (!grid) {
+        int dev = 0, cus = 0, per_cu = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            return -1;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(k_step<NT, LPR_D>), 256, 0) != hipSuccess)
+            return -1;
+        grid = std::min(std::min(per_cu, 2) * cus, MAX_STEP_WG);
+    }
+    return grid;
+}
+
+template <int NT, int LPR_D>
+static int launch_step_t(StepArgs & a, hipStream_t s) {
+    const int G = step_grid<NT, LPR_D>();
+    if (G <= 0) return fail(QWM_ERR_HIP, "fused step: occupancy query failed");
+    const int U_max = NT * a.k + a.shared;
+    if (G < U_max) return fail(QWM_ERR_UNSUPPORTED, "fused step: fewer co-resident workgroups than expert units");
+    if ((int64_t)a.v.V < 8LL * G) return fail(QWM_ERR_UNSUPPORTED, "fused step: vocabulary too small for the grid");
+    // An ordinary launch of exactly the co-resident grid (the occupancy query
+    // above): the cooperative launch API gives the same residency but costs
+    // ~20 us between consecutive launches on this stack.  If other work holds
+    // CUs, the missing workgroups start as it drains; the bounded spins report
+    // a = -1 rather than wait without end.
+    prof_begin("step", s);
+    k_step<NT, LPR_D><<<dim3((unsigned)G), dim3(256), 0, s>>>(a);
+    prof_end("step", s);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(QWM_ERR_HIP, std::string("fused step launch: ") + hipGetErrorString(e));
+    return QWM_OK;
+}
+
+template <int NT>
+static int launch_step_nt(StepArgs & a, int lpr_d, hipStream_t s) {
+    switch (lpr_d) {
+        case 16: return launch_step_t<NT, 16>(a, s);
+        case 32: return launch_step_t<NT, 32>(a, s);
+        default: return launch_step_t<NT, 64>(a, s);
+    }
+}
+
+int launch_step(const StepCall & c, const StepPlan & p, uint8_t * ws, hipStream_t s) {
+    const qwm_moe_layer * L = c.L;
+    const MoePlan & m = p.moe;
+    StepArgs a;
+    a.W_r = (const float *)L->router.data; a.x = c.x; a.rm = c.rm;
+    a.sgi = (L->sh_gate.data && L->sh_gate_inp.data) ? (const float *)L->sh_gate_inp.data : nullptr;
+    a.E = (int)m.E; a.k = (int)m.k; a.norm = L->norm_weights; a.scale = L->weights_scale;
+    a.tiny = (m.T >= 2 && m.E % 4 == 0) ? 1 : 0;
+    a.N = (int)m.N; a.N_sh = (int)m.N_sh; a.shared = m.shared ? 1 : 0;
+    a.gate = (const uint8_t *)L->gate_pool.data; a.up = (const uint8_t *)L->up_pool.data;
+    a.down = (const uint8_t *)L->down_pool.data;
+    a.gate_slab = L->gate_pool.nb[2]; a.up_slab = L->up_pool.nb[2]; a.down_slab = L->down_pool.nb[2];
+    a.sh_gate = (const uint8_t *)L->sh_gate.data; a.sh_up = (const uint8_t *)L->sh_up.data;
+    a.sh_down = (const uint8_t *)L->sh_down.data;
+    a.slot_tables = c.slot_tables; a.table_stride = c.table_stride; a.layer = c.layer;
+    a.resid = c.resid; a.out = c.out;
+    a.ids_out = c.ids_out; a.ids_ld = c.ids_ld; a.w_out = c.w_out; a.w_ld = c.w_ld;
+    a.lg = reinterpret_cast<float *>(ws + p.lg);
+    a.xq_qs = reinterpret_cast<int8_t *>(ws + m.xq_qs);
+    a.xq_d = reinterpret_cast<float *>(ws + p.xq_d);
+    a.xq_bs = reinterpret_cast<int32_t *>(ws + p.xq_bs);
+    a.act = reinterpret_cast<float *>(ws + m.act); a.act_sh = reinterpret_cast<float *>(ws + m.act_sh);
+    a.ex = reinterpret_cast<float *>(ws + m.ex); a.ex_sh = reinterpret_cast<float *>(ws + m.ex_sh);
+    a.bar = reinterpret_cast<uint32_t *>(ws + p.bar);
+    a.epoch = reinterpret_cast<uint32_t *>(ws + p.bar + 128);
+    a.err = reinterpret_cast<int32_t *>(ws + p.bar + 256);
+    a.flags = reinterpret_cast<uint32_t *>(ws + p.flags);
+    a.tile_counters = reinterpret_cast<int32_t *>(ws + m.tile_counters);
+    VerifyArgs & v = a.v;
+    v.W = c.lm_head; v.H = SH; v.V = (int)p.V;
+    v.x = c.out; v.norm_w = c.norm_w; v.eps = c.eps;
+    v.drafts = c.drafts; v.result = c.result;
+    v.pv = reinterpret_cast<float *>(ws + p.v_pv);
+    v.pi = reinterpret_cast<int32_t *>(ws + p.v_pi);
+    v.counter = reinterpret_cast<int32_t *>(ws + p.v_counter);
+    const int lpr_d = m.N <= 512 ? 16 : m.N <= 1024 ? 32 : 64;
+    if (m.shared && (m.N_sh <= 512 ? 16 : m.N_sh <= 1024 ? 32 : 64) != lpr_d)
+        return fail(QWM_ERR_UNSUPPORTED, "fused step: shared and routed FFN widths need the same tiling");
+    switch (m.T) {
+        case 1: return launch_step_nt<1>(a, lpr_d, s);
+        case 2: return launch_step_nt<2>(a, lpr_d, s);
+        case 3: return launch_step_nt<3>(a, lpr_d, s);
+        case 4: return launch_step_nt<4>(a, lpr_d, s);
+        case 5: return launch_step_nt<5>(a, lpr_d, s);
+        case 6: return launch_step_nt<6>(a, lpr_d, s);
+        case 7: return launch_step_nt<7>(a, lpr_d, s);
+        default: return launch_step_nt<8>(a, lpr_d, s);
+    }
+}
+
+}  // namespace qwm

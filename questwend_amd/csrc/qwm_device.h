@@ -64,16 +64,15 @@ QWM_DEV void q4k_scale_min(int j, const uint8_t * q, int & d, int & m) {
 }
 // Same, from the three scale dwords held in registers (bytes 4..15 of the
 // block header): s0 = scales[0..3], s1 = scales[4..7], s2 = scales[8..11].
+// Branch-free: lanes of one wave take different j.
 QWM_DEV void q4k_scale_min_reg(int j, uint32_t s0, uint32_t s1, uint32_t s2, int & d, int & m) {
     const int b = (j & 3) * 8;
-    if (j < 4) {
-        d = (s0 >> b) & 63;
-        m = (s1 >> b) & 63;
-    } else {
-        const uint32_t q8 = (s2 >> b) & 0xff;          // scales[j+4]
-        d = (q8 & 0xF) | (((s0 >> b) >> 6 & 3) << 4);   // scales[j-4] >> 6
-        m = (q8 >> 4) | (((s1 >> b) >> 6 & 3) << 4);    // scales[j] >> 6
-    }
+    const uint32_t a0 = s0 >> b, a1 = s1 >> b, q8 = (s2 >> b) & 0xff;   // scales[j], [j+4], [j+8]
+    const int dl = (int)(a0 & 63), ml = (int)(a1 & 63);
+    const int dh = (int)((q8 & 0xF) | ((a0 >> 6 & 3) << 4));           // j >= 4: scales[j+4] & 15 | scales[j-4] >> 6
+    const int mh = (int)((q8 >> 4) | ((a1 >> 6 & 3) << 4));
+    d = j < 4 ? dl : dh;
+    m = j < 4 ? ml : mh;
 }
 
 QWM_DEV int dot4(uint32_t a, uint32_t b, int c) { return __builtin_amdgcn_sdot4((int)a, (int)b, c, false); }
@@ -171,6 +170,39 @@ QWM_DEV float tree16_dpp(float v) {
     v += dpp_f<0x122>(v);
     v += dpp_f<0x121>(v);
     return v;
+}
+
+// Sum over aligned groups of W lanes (16, 32 or 64): the wave halves, then
+// the 16-lane row pairs, then the row's halving tree.  Every lane of a group
+// holds the same bits, and wave_sum_scatter8 forms the same sums.
+template <int W>
+QWM_DEV float halves_sum(float v) {
+    if (W >= 64) v += lane_xor32_f(v);
+    if (W >= 32) v += lane_xor16_f(v);
+    return tree16_dpp(v);
+}
+
+// Pairwise sums that scatter two operands over the result: swap_add32 leaves
+// a[l] + a[l + 32] in lanes 0-31 and b[l - 32] + b[l] in lanes 32-63;
+// swap_add16 leaves the 16-lane rows [a0 + a1, b0 + b1, a2 + a3, b2 + b3].
+QWM_DEV float swap_add32(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+QWM_DEV float swap_add16(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Wave sums of the eight values a[0..3] and b[0..3] in six swaps instead of
+// twenty-four: every lane of 16-lane row q receives sa = sum(a[scatter_row(q)])
+// and sb = sum(b[scatter_row(q)]), bit-identical to halves_sum<64>.
+QWM_DEV int scatter_row(int q) { return ((q & 1) << 1) | (q >> 1); }
+QWM_DEV void wave_sum_scatter8(const float (&a)[4], const float (&b)[4], float & sa, float & sb) {
+    const float a01 = swap_add32(a[0], a[1]), a23 = swap_add32(a[2], a[3]);
+    const float b01 = swap_add32(b[0], b[1]), b23 = swap_add32(b[2], b[3]);
+    sa = tree16_dpp(swap_add16(a01, a23));
+    sb = tree16_dpp(swap_add16(b01, b23));
 }
 
 QWM_DEV float readlane_f(float v, int l) {

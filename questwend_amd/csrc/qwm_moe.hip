@@ -344,8 +344,8 @@ __global__ void __launch_bounds__(256) k_gateup_q4k(GateUpArgs a) {
                     g[i] = chunk_dot(G[it], A[i], c, 0.f);
                     up[i] = chunk_dot(Uw[it], A[i], c, 0.f);
                 }
-                g[i] = lane_sum<LPR>(g[i]);
-                up[i] = lane_sum<LPR>(up[i]);
+                g[i] = halves_sum<LPR>(g[i]);
+                up[i] = halves_sum<LPR>(up[i]);
             }
         }
         if (r < rows) {

@@ -142,6 +142,48 @@ QWM_DEV void load_w_chunk_s(WChunkS & W, const uint8_t * row, int c) {
     W.q = *reinterpret_cast<const uint4 *>(blk + 16 + 16 * p);
 }
 
+// One lane's chunk of one row decoded once for every token: the unpacked
+// nibbles, both sub-blocks' scales and mins, and the block's d and dmin.
+struct RowChunk {
+    uint32_t lo[4], hi[4];
+    int sc_lo, m_lo, sc_hi, m_hi;
+    float d, dmin;
+};
+
+QWM_DEV void decode_chunk_s(const WChunkS & W, int c, RowChunk & R) {
+    const int h = (int)W.h;
+    const uint32_t h0 = (uint32_t)dpp_i<0x00>(h), h1 = (uint32_t)dpp_i<0x55>(h);
+    const uint32_t h2 = (uint32_t)dpp_i<0xAA>(h), h3 = (uint32_t)dpp_i<0xFF>(h);
+    const int j = 2 * ((c & 7) >> 1);
+    q4k_scale_min_reg(j, h1, h2, h3, R.sc_lo, R.m_lo);
+    q4k_scale_min_reg(j + 1, h1, h2, h3, R.sc_hi, R.m_hi);
+    const uint32_t m4 = 0x0F0F0F0Fu;
+    const uint32_t q[4] = {W.q.x, W.q.y, W.q.z, W.q.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { R.lo[i] = q[i] & m4; R.hi[i] = (q[i] >> 4) & m4; }
+    R.d = fp16_to_f32((uint16_t)(h0 & 0xffff));
+    R.dmin = fp16_to_f32((uint16_t)(h0 >> 16));
+}
+
+// The same arithmetic as chunk_dot (identical operations and order).
+QWM_DEV float token_dot(const RowChunk & R, const ActChunk & A) {
+    int s_lo = 0, s_hi = 0;
+    s_lo = dot4(R.lo[0], A.lo.x, s_lo);
+    s_lo = dot4(R.lo[1], A.lo.y, s_lo);
+    s_lo = dot4(R.lo[2], A.lo.z, s_lo);
+    s_lo = dot4(R.lo[3], A.lo.w, s_lo);
+    s_hi = dot4(R.hi[0], A.hi.x, s_hi);
+    s_hi = dot4(R.hi[1], A.hi.y, s_hi);
+    s_hi = dot4(R.hi[2], A.hi.z, s_hi);
+    s_hi = dot4(R.hi[3], A.hi.w, s_hi);
+    const int isum = R.sc_lo * s_lo + R.sc_hi * s_hi;
+    const int imin = R.m_lo * A.bs_lo + R.m_hi * A.bs_hi;
+    const float d = A.d * R.d;
+    const float dmin = A.d * R.dmin;
+    const float acc = __builtin_fmaf(d, (float)isum, 0.f);
+    return __builtin_fmaf(-dmin, (float)imin, acc);
+}
+
 QWM_DEV float chunk_dot_s(const WChunkS & W, const ActChunk & A, int c, float acc) {
     WChunk w;
     w.q = W.q;

@@ -386,18 +386,22 @@ QWM_DEV void step_select(const StepArgs & a, int g, StepShared & S, uint8_t * sm
 // ---------------------------------------------------------------- P2 ----
 // gate/up: items of GU_ROWS consecutive rows of one unit; workgroup g takes
 // items g, g + G, ...  Each wave streams GU_ROWS / 4 rows through a
-// GU_PF-deep ring with the unit's Q8_K activations in registers; act =
-// silu(g) * u (the vectorized silu except for the row tail the CPU runs
-// through scalar expf) is collected in LDS and leaves as whole lines.
-constexpr int GU_ROWS = 64;
+// GU_PF-deep ring with the unit's Q8_K activations in registers, decodes each
+// row chunk once for all tokens and reduces four rows' gate and up sums at a
+// time (wave_sum_scatter8).  act = silu(g) * u (the vectorized silu except
+// for the row tail the CPU runs through scalar expf) is collected in LDS and
+// leaves in one pass of stores; an item's first and last lines may be shared
+// with the neighbouring item, so the down phase reads act with agent-scope loads.
+constexpr int GU_ROWS = 48;
 constexpr int GU_PF = 6;
 
 template <int MAXP>
 QWM_DEV void step_gateup(const StepArgs & a, int g, int G, const StepShared & S, uint8_t * smem) {
-    constexpr int LPR = 64;                      // 64 chunks of 16 B per 2048-wide row
-    constexpr int RPW = GU_ROWS / 4;             // rows per wave per item
+    constexpr int RPW = GU_ROWS / 4;             // rows per wave per item, in groups of 4
+    static_assert(RPW % 4 == 0, "rows per wave come in groups of four");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int c = lane;
+    const int c = lane;                          // 64 chunks of 16 B per 2048-wide row
+    const int rho = scatter_row(lane >> 4);      // row of a 4-row group this lane's sums belong to
     float (*s_act)[GU_ROWS] = reinterpret_cast<float (*)[GU_ROWS]>(smem);
     const int nb_r = (a.N + GU_ROWS - 1) / GU_ROWS, nb_s = a.shared ? (a.N_sh + GU_ROWS - 1) / GU_ROWS : 0;
     const int items = S.nu * nb_r + nb_s;
@@ -412,7 +416,9 @@ QWM_DEV void step_gateup(const StepArgs & a, int g, int G, const StepShared & S,
         const uint8_t * gbase = shared ? a.sh_gate : a.gate + (size_t)S.uslot[u][0] * a.gate_slab;
         const uint8_t * ubase = shared ? a.sh_up : a.up + (size_t)S.uslot[u][1] * a.up_slab;
         const int rb = blk * GU_ROWS, re = min(rb + GU_ROWS, rows);
-        const int r0 = rb + wave * RPW;          // rows are a multiple of 256: every wave has RPW rows
+        const int r0 = rb + wave * RPW;
+        // rows past the unit's last one re-read the last row; their sums are dropped
+        auto row_ptr = [&](const uint8_t * base, int s) { return base + (size_t)min(r0 + s, rows - 1) * row_bytes; };
         {
             // activations first: vector-memory waits count in issue order, so
             // the ring's loads must be the youngest for its waits to stay partial
@@ -424,31 +430,42 @@ QWM_DEV void step_gateup(const StepArgs & a, int g, int G, const StepShared & S,
                     load_act_chunk<32, 32>(A[i], a.xq_qs + (size_t)tok * SH, a.xq_d + (size_t)tok * SNB * 32,
                                            a.xq_bs + (size_t)tok * SNB * 32, c);
                 }
-            const uint8_t * gp = gbase + (size_t)r0 * row_bytes;
-            const uint8_t * up = ubase + (size_t)r0 * row_bytes;
             WChunkS Gb[GU_PF], Ub[GU_PF];
 #pragma unroll
             for (int p = 0; p < GU_PF; ++p) {
-                load_w_chunk_s(Gb[p], gp + (size_t)p * row_bytes, c);
-                load_w_chunk_s(Ub[p], up + (size_t)p * row_bytes, c);
+                load_w_chunk_s(Gb[p], row_ptr(gbase, p), c);
+                load_w_chunk_s(Ub[p], row_ptr(ubase, p), c);
             }
             // straight-line ring: every wait below is a partial one
 #pragma clang loop unroll(full)
-            for (int s = 0; s < RPW; ++s) {
-                const int p = s % GU_PF;
-                const int r = r0 + s;
+            for (int s0 = 0; s0 < RPW; s0 += 4) {
+                float pg[MAXP][4], pu[MAXP][4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int s = s0 + q, p = s % GU_PF;
+                    RowChunk RG, RU;
+                    decode_chunk_s(Gb[p], c, RG);
+                    decode_chunk_s(Ub[p], c, RU);
+                    if (s + GU_PF < RPW) {
+                        load_w_chunk_s(Gb[p], row_ptr(gbase, s + GU_PF), c);
+                        load_w_chunk_s(Ub[p], row_ptr(ubase, s + GU_PF), c);
+                    }
+#pragma unroll
+                    for (int i = 0; i < MAXP; ++i)
+                        if (i < n) {
+                            pg[i][q] = token_dot(RG, A[i]);
+                            pu[i][q] = token_dot(RU, A[i]);
+                        }
+                }
+                const int r = r0 + s0 + rho;
 #pragma unroll
                 for (int i = 0; i < MAXP; ++i) {
                     if (i < n) {
-                        const float gs = lane_sum<LPR>(chunk_dot_s(Gb[p], A[i], c, 0.f));
-                        const float us = lane_sum<LPR>(chunk_dot_s(Ub[p], A[i], c, 0.f));
-                        if (c == i)
+                        float gs, us;
+                        wave_sum_scatter8(pg[i], pu[i], gs, us);
+                        if ((lane & 15) == i && r < re)
                             s_act[i][r - rb] = (r < rows - (rows & 15)) ? v_silu(gs) * us : gs / (1.0f + expf(-gs)) * us;
                     }
-                }
-                if (s + GU_PF < RPW) {
-                    load_w_chunk_s(Gb[p], gp + (size_t)(s + GU_PF) * row_bytes, c);
-                    load_w_chunk_s(Ub[p], up + (size_t)(s + GU_PF) * row_bytes, c);
                 }
             }
         }
@@ -509,7 +526,7 @@ QWM_DEV void step_down(const StepArgs & a, int g, int G, const StepShared & S, u
         for (int jb = wave; jb < n * nb; jb += 4) {
             const int i = jb / nb, b = jb % nb;
             const float * src = shared ? a.act_sh + (size_t)U_.pair[i] * K : a.act + (size_t)U_.pair[i] * K;
-            quantize_block_q8K(src + b * QK_K, &s_qs[i][b * QK_K], &s_d[i][b], &s_bs[i][b * 16], lane);
+            quantize_block_q8K<false, true>(src + b * QK_K, &s_qs[i][b * QK_K], &s_d[i][b], &s_bs[i][b * 16], lane);
         }
         __syncthreads();
         ActChunk A[MAXP];

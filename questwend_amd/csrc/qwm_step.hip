@@ -71,17 +71,34 @@ struct StepShared {
     Unit units[MAX_PAIRS + 1];
     int32_t uslot[MAX_PAIRS + 1][3];
     int32_t nu;
+    int32_t slot_of[3 * STEP_MAX_E];   // this layer's slot tables, [role][expert]
 };
 
-// Grid barrier number `i` (1, 2, 3) of launch `epoch`.  The last workgroup to
-// arrive re-arms the counter and then sets every workgroup's flag line to
-// epoch * 4 + i; the others poll their own line.
+// Grid barrier number `i` (1, 2, 3) of launch `epoch`.  Arrivals count in
+// BAR_GROUPS group counters (workgroup g in group g % BAR_GROUPS, one line
+// each); the last arrival of a group re-arms its counter and counts the group
+// at the top counter.  The last group's last workgroup re-arms the top counter
+// and then sets every workgroup's flag line to epoch * 4 + i; the others poll
+// their own line.
+constexpr int BAR_GROUPS = 16;
+
 QWM_DEV void grid_barrier(const StepArgs & a, int i, int G, uint32_t epoch) {
     __shared__ int s_rel;
     __builtin_amdgcn_s_waitcnt(0);               // this wave's agent-scope writes have completed
     __syncthreads();
-    if (threadIdx.x == 0)
-        s_rel = __hip_atomic_fetch_add(a.bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)G - 1;
+    if (threadIdx.x == 0) {
+        const int grp = blockIdx.x % BAR_GROUPS;
+        const int groups = G < BAR_GROUPS ? G : BAR_GROUPS;
+        const uint32_t in_grp = (uint32_t)((G - 1 - grp) / BAR_GROUPS + 1);
+        uint32_t * gc = a.bar + 128 + 32 * grp;
+        bool rel = false;
+        if (__hip_atomic_fetch_add(gc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == in_grp - 1) {
+            st_agent(gc, 0u);
+            __builtin_amdgcn_s_waitcnt(0);           // re-armed before the group counts as arrived
+            rel = __hip_atomic_fetch_add(a.bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)groups - 1;
+        }
+        s_rel = rel;
+    }
     __syncthreads();
     const uint32_t v = epoch * 4u + (uint32_t)i;
     if (s_rel) {
@@ -208,10 +225,8 @@ QWM_DEV void step_router(const StepArgs & a, int g, int G, uint8_t * smem) {
 // normalization (double sum, clamp 6.103515625e-5, division), scale; then
 // the expert union in first-occurrence order and each unit's slots.
 //
-// Top-k without serial argmax rounds: probabilities are non-negative, so
-// their bit patterns order like the values; a 31-step radix descent over
-// ballots finds the k-th largest pattern, ties at that value are taken in
-// index order, and each selected lane ranks itself against the k others.
+// One wave per token; top-k as k rounds of a wave maximum with ballots for
+// the tie order, the weight normalization one lane per selected expert.
 // R: probabilities per lane (E <= 64 * R).
 template <int NT, int R>
 QWM_DEV void step_select(const StepArgs & a, int g, StepShared & S, uint8_t * smem) {
@@ -221,6 +236,7 @@ QWM_DEV void step_select(const StepArgs & a, int g, StepShared & S, uint8_t * sm
     const int nfull = E & ~15;
     const unsigned long long below = (1ull << lane) - 1ull;
     for (int t = wave; t < NT; t += 4) {
+        const float shl = a.sgi ? a.lg[(size_t)E * 32 + t] : 0.f;      // shared-expert gate logit
         float v[R];
         float m = -__builtin_inff();
 #pragma unroll
@@ -250,93 +266,51 @@ QWM_DEV void step_select(const StepArgs & a, int g, StepShared & S, uint8_t * sm
         }
         for (int i = nfull; i < E; ++i) sum += (double)readlane_f(tailv, i & 63);
         const float sc = (float)(1.0 / sum);
-        uint32_t key[R];
+        // top-k: k rounds of the wave maximum; a tie goes to the lower index
+        // (the first r, then the first lane, holding the maximum).  Lane j
+        // keeps the j-th selection; the weight sum runs in selection order.
+        float cur[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const int i = 64 * r + lane;
             v[r] = v[r] * sc;
-            key[r] = (r < nr && i < E) ? __float_as_uint(v[r]) : 0u;   // invalid lanes: +0, larger index
+            cur[r] = (r < nr && i < E) ? v[r] : -1.f;                  // probabilities are >= 0
         }
-        // k-th largest key
-        uint32_t th = 0;
-        for (int bit = 30; bit >= 0; --bit) {
-            const uint32_t cand = th | (1u << bit);
-            int cnt = 0;
+        float myw = 0.f;
+        int myid = 0;
+        double wsum = 0.0;
+        for (int j = 0; j < k; ++j) {
+            float m = cur[0];
+#pragma unroll
+            for (int r = 1; r < R; ++r) m = fmaxf(m, cur[r]);
+            m = wave_max(m);
+            int id = -1;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const unsigned long long bal = __ballot(cur[r] == m);
+                if (id < 0 && bal) id = 64 * r + (int)__builtin_ctzll(bal);
+            }
+            if (lane == j) { myw = m; myid = id; }
+            wsum += (double)m;
 #pragma unroll
             for (int r = 0; r < R; ++r)
-                if (r < nr) cnt += __popcll(__ballot(key[r] >= cand));
-            if (cnt >= k) th = cand;
+                if (64 * r + lane == id) cur[r] = -1.f;
         }
-        // selection: every key above th, then keys equal to th in index order
-        int gt = 0;
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-            if (r < nr) gt += __popcll(__ballot(key[r] > th));
-        int need = k - gt;
-        bool sel[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            sel[r] = false;
-            if (r < nr) {
-                const unsigned long long eq = __ballot(key[r] == th && 64 * r + lane < E);
-                const int before = __popcll(eq & below);
-                sel[r] = key[r] > th || ((eq >> lane) & 1ull && before < need);
-                need -= min(need, __popcll(eq));
+        if (a.norm) {
+            float ws = (float)wsum;
+            ws = fmaxf(fminf(ws, __builtin_inff()), 6.103515625e-5f);
+            myw = myw / ws;
+        }
+        if (a.scale != 0.0f && a.scale != 1.0f) myw = myw * a.scale;
+        if (lane < k) {
+            S.ids[t * k + lane] = myid;
+            S.w[t * k + lane] = myw;
+            if (g == 0) {
+                if (a.ids_out) a.ids_out[(size_t)t * a.ids_ld + lane] = myid;
+                if (a.w_out) a.w_out[(size_t)t * a.w_ld + lane] = myw;
             }
         }
-        // rank of each selected entry: larger value first, then lower index
-        int rank[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) rank[r] = 0;
-#pragma unroll
-        for (int rs = 0; rs < R; ++rs) {
-            if (rs >= nr) break;
-            unsigned long long bs = __ballot(sel[rs]);
-            while (bs) {
-                const int ls = __builtin_ctzll(bs);
-                bs &= bs - 1;
-                const uint32_t ks = __builtin_amdgcn_readlane(key[rs], ls);
-                const int is = 64 * rs + ls;
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const int i = 64 * r + lane;
-                    rank[r] += sel[r] && (ks > key[r] || (ks == key[r] && is < i));
-                }
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-            if (sel[r]) { S.ids[t * k + rank[r]] = 64 * r + lane; S.w[t * k + rank[r]] = v[r]; }
-        wave_sync();
-        if (lane == 0) {
-            float w[MAX_K];
-#pragma unroll
-            for (int j = 0; j < MAX_K; ++j) w[j] = j < k ? S.w[t * k + j] : 0.f;
-            if (a.norm) {
-                double s = 0.0;
-#pragma unroll
-                for (int j = 0; j < MAX_K; ++j)
-                    if (j < k) s += (double)w[j];
-                float ws = (float)s;
-                ws = fmaxf(fminf(ws, __builtin_inff()), 6.103515625e-5f);
-#pragma unroll
-                for (int j = 0; j < MAX_K; ++j) w[j] = w[j] / ws;
-            }
-            if (a.scale != 0.0f && a.scale != 1.0f)
-#pragma unroll
-                for (int j = 0; j < MAX_K; ++j) w[j] = w[j] * a.scale;
-#pragma unroll
-            for (int j = 0; j < MAX_K; ++j) {
-                if (j < k) {
-                    S.w[t * k + j] = w[j];
-                    if (g == 0) {
-                        if (a.ids_out) a.ids_out[(size_t)t * a.ids_ld + j] = S.ids[t * k + j];
-                        if (a.w_out) a.w_out[(size_t)t * a.w_ld + j] = w[j];
-                    }
-                }
-            }
-            S.shg[t] = a.sgi ? 1.f / (1.f + expf(-a.lg[(size_t)E * 32 + t])) : 1.f;   // unary-ops.cpp:31
-        }
+        if (lane == 0) S.shg[t] = a.sgi ? 1.f / (1.f + expf(-shl)) : 1.f;   // unary-ops.cpp:31
     }
     __syncthreads();
     // expert union through per-expert LDS tables: first pair, token mask, unit
@@ -370,8 +344,7 @@ QWM_DEV void step_select(const StepArgs & a, int g, StepShared & S, uint8_t * sm
     }
     __syncthreads();
     for (int u = tid; u < nu; u += 256)
-        for (int r = 0; r < 3; ++r)
-            S.uslot[u][r] = a.slot_tables[(size_t)r * a.table_stride + (size_t)a.layer * E + S.units[u].expert];
+        for (int r = 0; r < 3; ++r) S.uslot[u][r] = S.slot_of[r * E + S.units[u].expert];
     if (tid == 0) {
         if (a.shared) {
             S.units[nu].expert = -1;
@@ -630,7 +603,17 @@ __global__ void __launch_bounds__(256) k_step(StepArgs a) {
     __syncthreads();
     const uint32_t epoch = s_epoch;
 
+    // the layer's slot tables, requested first and kept in LDS for the selection
+    constexpr int SLQ = 3 * STEP_MAX_E / 256;
+    int32_t sl[SLQ];
+#pragma unroll
+    for (int q = 0; q < SLQ; ++q) {
+        const int idx = threadIdx.x + 256 * q;
+        sl[q] = idx < 3 * a.E ? a.slot_tables[(size_t)(idx / a.E) * a.table_stride + (size_t)a.layer * a.E + idx % a.E] : 0;
+    }
     step_router<NT>(a, g, G, smem);
+#pragma unroll
+    for (int q = 0; q < SLQ; ++q) S.slot_of[threadIdx.x + 256 * q] = sl[q];
     grid_barrier(a, 1, G, epoch);
     if (a.E <= 128) step_select<NT, 2>(a, g, S, smem);
     else step_select<NT, STEP_MAX_E / 64>(a, g, S, smem);
@@ -640,7 +623,7 @@ __global__ void __launch_bounds__(256) k_step(StepArgs a) {
     grid_barrier(a, 3, G, epoch);
     __syncthreads();
     constexpr int PF = NT <= 4 ? 2 : 1;
-    if (verify_body<NT, SH / 512, PF>(a.v, g, G, smem) && threadIdx.x == 0) {
+    if (verify_body<NT, SH / 512, PF, false>(a.v, g, G, smem) && threadIdx.x == 0) {
         // every workgroup has read the epoch and passed all barriers
         st_agent(a.epoch, epoch + 1u);
         if (ld_agent(a.err)) {
@@ -677,7 +660,7 @@ bool step_plan(const qwm_moe_layer * L, const qwm_tensor * lm_head, int64_t T, S
     p.lg = take(sizeof(float) * 32 * (p.moe.E + 1));
     p.xq_d = take(sizeof(float) * 32 * T * SNB);
     p.xq_bs = take(sizeof(int32_t) * 32 * T * SNB);
-    p.bar = take(512);
+    p.bar = take(512 + 128 * BAR_GROUPS);     // top counter, epoch, error word, group counters at 512
     p.flags = take(sizeof(uint32_t) * 32 * MAX_STEP_WG);
     p.total = o;
     return true;

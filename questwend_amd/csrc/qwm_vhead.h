@@ -63,7 +63,11 @@ template <int NT> struct VhSmem {
 // vocabulary rows), with `smem` holding VhSmem<NT>::bytes of LDS.  Returns
 // true in the workgroup that finished last (it wrote the result).
 // NS = H / 512 block sets per lane (H = 512 * NS), PF tiles in flight.
-template <int NT, int NS, int PF>
+// EARLY: the first weight tiles are requested before the rms_norm and
+// quantization prep instead of after it.  Right after a grid barrier the
+// late form lets the barrier's release reach every workgroup before the
+// weight stream fills the memory queues.
+template <int NT, int NS, int PF, bool EARLY = true>
 QWM_DEV bool verify_body(const VerifyArgs & a, int wg, int n_wg, uint8_t * smem) {
     constexpr int NG = (NT + 3) / 4;                  // token groups (MFMA A rows)
     __shared__ float s_scale[NT];
@@ -112,8 +116,10 @@ QWM_DEV bool verify_body(const VerifyArgs & a, int wg, int n_wg, uint8_t * smem)
 
     // weight loads for the first steps
     uint32_t win[PF][NS][VH_WIN];
+    if constexpr (EARLY) {
 #pragma unroll
-    for (int p = 0; p < PF; ++p) load_tile<NS>(win[p], lane_ptr(min(p, n_steps - 1)));
+        for (int p = 0; p < PF; ++p) load_tile<NS>(win[p], lane_ptr(min(p, n_steps - 1)));
+    }
 
 #pragma unroll
     for (int k = 0; k < NI; ++k) {
@@ -173,6 +179,10 @@ QWM_DEV bool verify_body(const VerifyArgs & a, int wg, int n_wg, uint8_t * smem)
         s_d[t][blk] = fp16_to_f32(f32_to_fp16(d));
     }
     __syncthreads();
+    if constexpr (!EARLY) {
+#pragma unroll
+        for (int p = 0; p < PF; ++p) load_tile<NS>(win[p], lane_ptr(min(p, n_steps - 1)));
+    }
 
     // MFMA A operands: token 4g + j of block b + 16s, shifted to this lane's
     // window (even blocks: 2 zero bytes under the fp16 scale, qs from byte 2;

@@ -153,8 +153,9 @@ int qwm_verify_accept(const qwm_tensor * lm_head, const qwm_tensor * x, const fl
  *   out = MoE(x) (+ resid);  h = rms_norm(out) * norm_w;  vA = argmax(lm_head . h)
  *   result: device i32 [T + 2] = vA[0..T-1], a, x_new; a = -1 reports a
  *   device-side synchronization timeout (results invalid).
- * Supported: Q4_K pools, hidden size 2048, FFN <= 2048, <= 512 experts, lm_head Q8_0
- * [2048, V] with V >= 8192, T <= 8.  out must not overlap x or resid.  ids_out,
+ * Supported: Q4_K pools, hidden size 2048, FFN width 512, 768, 1024 or 2048
+ * (a shared expert of the same width), <= 512 experts, lm_head Q8_0 [2048, V]
+ * with V >= 8192, T <= 8.  out must not overlap x or resid.  ids_out,
  * w_out and norm_w may be NULL.  QWM_ERR_UNSUPPORTED: use the two calls. */
 size_t qwm_verify_step_workspace_size(const qwm_moe_layer * layer, const qwm_tensor * lm_head, int64_t T);
 int qwm_verify_step(const qwm_moe_layer * layer, int32_t layer_index, const int32_t * slot_tables,

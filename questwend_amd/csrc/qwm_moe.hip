@@ -414,70 +414,48 @@ QWM_DEV float combine_one(const DownArgs & a, int t, int h) {
     return s;
 }
 
-template <int LPR, int MAXP>
+// Rows go 8 lanes each (load_row8 / row8_dots, NB = FFN width / 256 Q4_K
+// blocks per row): a workgroup owns a tile of 32 rows, one wave step each.
+template <int NB, int MAXP>
 __global__ void __launch_bounds__(256) k_down_q4k(DownArgs a) {
-    constexpr int RPI = WAVE / LPR;
-    constexpr int NIT = GEMV_STEPS;
-    constexpr int TILE = 4 * NIT * RPI;
+    constexpr int RPS = 8;                   // rows per wave
+    constexpr int TILE = 4 * RPS;
+    constexpr size_t row_bytes = (size_t)NB * 144;
     __shared__ int8_t s_qs[MAXP][MAX_NDOWN];
     __shared__ float s_d[MAXP][MAX_NDOWN / QK_K];
     __shared__ int32_t s_bs[MAXP][MAX_NDOWN / 16];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int c8 = lane & 7, rsub = lane >> 3;
     const int u = blockIdx.y;
     const bool shared = u == a.unit_slots;
     const int nu = *a.n_units;
     if (!shared && u >= nu) return;
     const Unit & U = a.units[shared ? nu : u];
     const int n = U.n;
-    const int K = shared ? a.N_sh : a.N;
-    const int nb = K / QK_K;
-    const int c = lane % LPR, rsub = lane / LPR;
-    const int C = K / 32;
-    const bool active = c < C;
     const uint8_t * base = shared ? a.sh_down : a.down + (size_t)a.slot_d[U.pair[0]] * a.down_slab;
-    const size_t row_bytes = (size_t)nb * 144;
     const int row0 = blockIdx.x * TILE;
-    const int r_begin = row0 + wave * (NIT * RPI);
+    const int r = row0 + wave * RPS + rsub;
     // weight loads first: they do not depend on the activations
-    WChunk W[NIT];
-#pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-        const int r = r_begin + it * RPI + rsub;
-        if (active && r < a.H) load_w_chunk(W[it], base + (size_t)r * row_bytes, c);
-    }
+    WChunkS W[NB];
+    load_row8<NB>(W, base + (size_t)min(r, a.H - 1) * row_bytes, c8);
     // quantize the unit's activation rows to Q8_K (one 256-block per wave at a time)
-    for (int jb = wave; jb < n * nb; jb += 4) {
-        const int i = jb / nb, b = jb % nb;
-        const float * src = shared ? a.act_sh + (size_t)U.pair[i] * K : a.act + (size_t)U.pair[i] * K;
+    for (int jb = wave; jb < n * NB; jb += 4) {
+        const int i = jb / NB, b = jb % NB;
+        const float * src = shared ? a.act_sh + (size_t)U.pair[i] * (NB * QK_K) : a.act + (size_t)U.pair[i] * (NB * QK_K);
         quantize_block_q8K(src + b * QK_K, &s_qs[i][b * QK_K], &s_d[i][b], &s_bs[i][b * 16], lane);
     }
     __syncthreads();
-    ActChunk A[MAXP];
+    float acc[MAXP];
+    row8_dots<NB, MAXP, MAX_NDOWN>(acc, W, n, &s_qs[0][0], &s_d[0][0], &s_bs[0][0], c8);
 #pragma unroll
     for (int i = 0; i < MAXP; ++i)
-        if (i < n && active) load_act_chunk(A[i], s_qs[i], s_d[i], s_bs[i], c);
-#pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-        const int r = r_begin + it * RPI + rsub;
-        const bool valid = active && r < a.H;
-        float acc[MAXP];
-#pragma unroll
-        for (int i = 0; i < MAXP; ++i) {
-            acc[i] = 0.f;
-            if (i < n) {
-                if (valid) acc[i] = chunk_dot(W[it], A[i], c, 0.f);
-                acc[i] = lane_sum<LPR>(acc[i]);
+        if (i < n) {
+            const float sum = row8_sum(acc[i]);
+            if (c8 == 0 && r < a.H) {
+                if (shared) st_agent(a.ex_sh + (size_t)U.pair[i] * a.H + r, sum);
+                else st_agent(a.ex + (size_t)U.pair[i] * a.H + r, sum);
             }
         }
-        if (r < a.H) {
-#pragma unroll
-            for (int i = 0; i < MAXP; ++i)
-                if (i < n && c == i) {
-                    if (shared) st_agent(a.ex_sh + (size_t)U.pair[i] * a.H + r, acc[i]);
-                    else st_agent(a.ex + (size_t)U.pair[i] * a.H + r, acc[i]);
-                }
-        }
-    }
     if (!last_workgroup(a.tile_counters + blockIdx.x, nu + a.shared)) return;
     for (int q = tid; q < a.T * TILE; q += 256) {
         const int t = q / TILE, h = row0 + q % TILE;
@@ -503,7 +481,7 @@ bool moe_plan(const qwm_moe_layer * L, int64_t T, MoePlan & p, std::string & why
     if (p.E < 1 || p.E > MAX_E) { why = "n_expert out of range"; return false; }
     if (p.H % QK_K || p.H > 2048) { why = "hidden size must be a multiple of 256, <= 2048"; return false; }
     if (p.N % QK_K || p.N > MAX_NDOWN) { why = "expert FFN size must be a multiple of 256, <= 2048"; return false; }
-    if (p.shared && (p.N_sh % QK_K || p.N_sh > MAX_NDOWN)) { why = "shared FFN size unsupported"; return false; }
+    if (p.shared && p.N_sh != p.N) { why = "the shared expert's FFN width must equal the routed one"; return false; }
     const int64_t P = T * p.k;
     size_t o = 0;
     auto take = [&](size_t bytes) { size_t at = o; o = align_up(o + bytes, 256); return at; };
@@ -565,13 +543,13 @@ static void launch_gateup_lpr(const GateUpArgs & g, int maxp, dim3 grid, hipStre
         default: k_gateup_q4k<LPR, 8><<<grid, 256, 0, s>>>(g); break;
     }
 }
-template <int LPR>
-static void launch_down_lpr(const DownArgs & d, int maxp, dim3 grid, hipStream_t s) {
+template <int NB>
+static void launch_down_nb(const DownArgs & d, int maxp, dim3 grid, hipStream_t s) {
     switch (maxp) {
-        case 1: k_down_q4k<LPR, 1><<<grid, 256, 0, s>>>(d); break;
-        case 2: k_down_q4k<LPR, 2><<<grid, 256, 0, s>>>(d); break;
-        case 4: k_down_q4k<LPR, 4><<<grid, 256, 0, s>>>(d); break;
-        default: k_down_q4k<LPR, 8><<<grid, 256, 0, s>>>(d); break;
+        case 1: k_down_q4k<NB, 1><<<grid, 256, 0, s>>>(d); break;
+        case 2: k_down_q4k<NB, 2><<<grid, 256, 0, s>>>(d); break;
+        case 4: k_down_q4k<NB, 4><<<grid, 256, 0, s>>>(d); break;
+        default: k_down_q4k<NB, 8><<<grid, 256, 0, s>>>(d); break;
     }
 }
 
@@ -630,18 +608,20 @@ int launch_experts(const ExpertArgs & a, const MoePlan & p, uint8_t * ws, hipStr
     d.w = reinterpret_cast<const float *>(a.weights);
     d.sh_gate = p.shared_gate ? reinterpret_cast<const float *>(ws + p.sh_gate) : nullptr;
     d.resid = a.resid; d.out = a.out;
-    const int ld = lanes_per_row((int)std::max(p.N, p.N_sh));
-    if (ld < 0) return fail(QWM_ERR_UNSUPPORTED, "expert FFN size > 2048 not tiled");
-    if (p.shared && lanes_per_row((int)p.N_sh) != lanes_per_row((int)p.N))
-        return fail(QWM_ERR_UNSUPPORTED, "shared and routed FFN sizes need the same tiling");
-    const int tile_d = 4 * GEMV_STEPS * (WAVE / ld);
+    const int nb_d = (int)(p.N / QK_K);           // moe_plan: 1..8, shared width equal
+    const int tile_d = 32;                        // k_down_q4k: 4 waves x 8 rows
     dim3 grid_d(((int)p.H + tile_d - 1) / tile_d, grid_y);
     if (grid_d.x > (unsigned)MAX_TILES) return fail(QWM_ERR_UNSUPPORTED, "hidden size needs too many down tiles");
     prof_begin("down", s);
-    switch (ld) {
-        case 16: launch_down_lpr<16>(d, maxp, grid_d, s); break;
-        case 32: launch_down_lpr<32>(d, maxp, grid_d, s); break;
-        default: launch_down_lpr<64>(d, maxp, grid_d, s); break;
+    switch (nb_d) {
+        case 1: launch_down_nb<1>(d, maxp, grid_d, s); break;
+        case 2: launch_down_nb<2>(d, maxp, grid_d, s); break;
+        case 3: launch_down_nb<3>(d, maxp, grid_d, s); break;
+        case 4: launch_down_nb<4>(d, maxp, grid_d, s); break;
+        case 5: launch_down_nb<5>(d, maxp, grid_d, s); break;
+        case 6: launch_down_nb<6>(d, maxp, grid_d, s); break;
+        case 7: launch_down_nb<7>(d, maxp, grid_d, s); break;
+        default: launch_down_nb<8>(d, maxp, grid_d, s); break;
     }
     prof_end("down", s);
 

@@ -166,7 +166,7 @@ QWM_DEV void decode_chunk_s(const WChunkS & W, int c, RowChunk & R) {
 }
 
 // The same arithmetic as chunk_dot (identical operations and order).
-QWM_DEV float token_dot(const RowChunk & R, const ActChunk & A) {
+QWM_DEV float token_dot_acc(const RowChunk & R, const ActChunk & A, float acc) {
     int s_lo = 0, s_hi = 0;
     s_lo = dot4(R.lo[0], A.lo.x, s_lo);
     s_lo = dot4(R.lo[1], A.lo.y, s_lo);
@@ -180,9 +180,10 @@ QWM_DEV float token_dot(const RowChunk & R, const ActChunk & A) {
     const int imin = R.m_lo * A.bs_lo + R.m_hi * A.bs_hi;
     const float d = A.d * R.d;
     const float dmin = A.d * R.dmin;
-    const float acc = __builtin_fmaf(d, (float)isum, 0.f);
+    acc = __builtin_fmaf(d, (float)isum, acc);
     return __builtin_fmaf(-dmin, (float)imin, acc);
 }
+QWM_DEV float token_dot(const RowChunk & R, const ActChunk & A) { return token_dot_acc(R, A, 0.f); }
 
 QWM_DEV float chunk_dot_s(const WChunkS & W, const ActChunk & A, int c, float acc) {
     WChunk w;
@@ -193,6 +194,46 @@ QWM_DEV float chunk_dot_s(const WChunkS & W, const ActChunk & A, int c, float ac
     w.hd.z = (uint32_t)dpp_i<0xAA>(h);
     w.hd.w = (uint32_t)dpp_i<0xFF>(h);
     return chunk_dot(w, A, c, acc);
+}
+
+// Down-projection rows with 8 lanes per row: lane c8 of a row takes chunk c8
+// of each of the row's NB Q4_K blocks (every lane works for any FFN width
+// that is a multiple of 256) and accumulates them in block order; row8_sum
+// adds the row's 8 partial sums by quad butterflies and a row rotation that
+// brings lane i + 4 to lane i, which leaves the row's sum in the first four
+// lanes of its group.
+template <int NB>
+QWM_DEV void load_row8(WChunkS (&W)[NB], const uint8_t * row, int c8) {
+#pragma unroll
+    for (int q = 0; q < NB; ++q) load_w_chunk_s(W[q], row, 8 * q + c8);
+}
+
+// acc[i] = this lane's partial dot of the row with the Q8_K activations of
+// token slot i (i < n) held in LDS at qs + i * QS, dd + i * QS / 256,
+// bs + i * QS / 16.
+template <int NB, int MAXP, int QS>
+QWM_DEV void row8_dots(float (&acc)[MAXP], const WChunkS (&W)[NB], int n, const int8_t * qs, const float * dd,
+                       const int32_t * bs, int c8) {
+#pragma unroll
+    for (int i = 0; i < MAXP; ++i) acc[i] = 0.f;
+#pragma unroll
+    for (int q = 0; q < NB; ++q) {
+        RowChunk R;
+        decode_chunk_s(W[q], 8 * q + c8, R);
+#pragma unroll
+        for (int i = 0; i < MAXP; ++i)
+            if (i < n) {
+                ActChunk A;
+                load_act_chunk(A, qs + i * QS, dd + i * (QS / QK_K), bs + i * (QS / 16), 8 * q + c8);
+                acc[i] = token_dot_acc(R, A, acc[i]);
+            }
+    }
+}
+
+QWM_DEV float row8_sum(float v) {
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    return v + dpp_f<0x12C>(v);                  // row_ror:12: lane i receives lane i + 4 of its row
 }
 
 }  // namespace qwm

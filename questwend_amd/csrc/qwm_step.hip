@@ -457,21 +457,24 @@ QWM_DEV void step_gateup(const StepArgs & a, int g, int G, const StepShared & S,
 // ---------------------------------------------------------------- P3 ----
 // down + combine: each unit's rows are cut into the same 16 tiles of 128 rows
 // (whole 32-row lines); items (unit, tile) go to workgroups g, g + G, ...
-// The workgroup quantizes the unit's activations to Q8_K in LDS, streams the
-// tile's rows (outputs collected in LDS, written as whole lines) and takes the
-// tile's ticket; the last of the U units combines the tile for every token
-// (runtime.cpp:3815-3817 for T == 1, 4544-4550 for T > 1; then the shared
-// expert and the residual).
+// The workgroup requests the tile's first weight rows, quantizes the unit's
+// activations to Q8_K in LDS and streams the rest of the tile, 8 lanes per
+// row (load_row8 / row8_dots), outputs collected in LDS and written as whole
+// lines; then it takes the tile's ticket, and the last of the U units
+// combines the tile for every token (runtime.cpp:3815-3817 for T == 1,
+// 4544-4550 for T > 1; then the shared expert and the residual).
 constexpr int DN_TR = 128;
-constexpr int DN_PF = 6;
 
-template <int NT, int LPR, int MAXP>
+template <int NT, int NB, int MAXP>
 QWM_DEV void step_down(const StepArgs & a, int g, int G, const StepShared & S, uint8_t * smem) {
-    constexpr int RPI = WAVE / LPR;
+    constexpr int RPS = 8;                       // rows per wave step
     constexpr int TR = DN_TR;                    // 16 tiles of 128 rows
-    constexpr int NSTEP = TR / (4 * RPI);        // wave steps per tile
+    constexpr int NSTEP = TR / (4 * RPS);        // wave steps per tile
+    constexpr int PF = NB <= 3 ? NSTEP : NB <= 4 ? 3 : 1;   // steps in flight
     constexpr int ntiles = SH / TR;
+    constexpr size_t row_bytes = (size_t)NB * 144;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int c8 = lane & 7, rsub = lane >> 3;
     const int U = S.nu + a.shared;
     int8_t (*s_qs)[MAX_NDOWN_S] = reinterpret_cast<int8_t (*)[MAX_NDOWN_S]>(smem);
     float (*s_d)[MAX_NDOWN_S / QK_K] = reinterpret_cast<float (*)[MAX_NDOWN_S / QK_K]>(smem + MAXP * MAX_NDOWN_S);
@@ -484,43 +487,34 @@ QWM_DEV void step_down(const StepArgs & a, int g, int G, const StepShared & S, u
         const bool shared = u == S.nu;
         const Unit & U_ = S.units[u];
         const int n = U_.n;
-        const int K = shared ? a.N_sh : a.N;
-        const int nb = K / QK_K;
-        const int C = K / 32;
-        const int c = lane % LPR, rsub = lane / LPR;
-        // lanes past the row's chunks read a real chunk at the same position
-        // in its block (so their quads still rebuild a real header), weighted 0
-        const float on = c < C ? 1.f : 0.f;
-        const int cc = c < C ? c : C - 8 + (c & 7);
         const uint8_t * base = shared ? a.sh_down : a.down + (size_t)S.uslot[u][2] * a.down_slab;
-        const size_t row_bytes = (size_t)nb * 144;
         const int h0 = x * TR, h1 = h0 + TR;
-        const uint8_t * rp = base + (size_t)(h0 + wave * RPI + rsub) * row_bytes;   // row of step s: + 4 * RPI * s
-        for (int jb = wave; jb < n * nb; jb += 4) {
-            const int i = jb / nb, b = jb % nb;
-            const float * src = shared ? a.act_sh + (size_t)U_.pair[i] * K : a.act + (size_t)U_.pair[i] * K;
+        const uint8_t * rp = base + (size_t)(h0 + wave * RPS + rsub) * row_bytes;   // row of step st: + 4 * RPS * st
+        // weights first: vector-memory waits count in issue order, and these
+        // do not depend on the activations
+        WChunkS Wb[PF][NB];
+#pragma unroll
+        for (int p = 0; p < PF; ++p) load_row8<NB>(Wb[p], rp + (size_t)(4 * RPS * p) * row_bytes, c8);
+        for (int jb = wave; jb < n * NB; jb += 4) {
+            const int i = jb / NB, b = jb % NB;
+            const float * src = shared ? a.act_sh + (size_t)U_.pair[i] * (NB * QK_K)
+                                       : a.act + (size_t)U_.pair[i] * (NB * QK_K);
             quantize_block_q8K<false, true>(src + b * QK_K, &s_qs[i][b * QK_K], &s_d[i][b], &s_bs[i][b * 16], lane);
         }
         __syncthreads();
-        ActChunk A[MAXP];
-#pragma unroll
-        for (int i = 0; i < MAXP; ++i)
-            if (i < n) load_act_chunk(A[i], s_qs[i], s_d[i], s_bs[i], cc);
-        WChunkS Wb[DN_PF];
-#pragma unroll
-        for (int p = 0; p < DN_PF; ++p) load_w_chunk_s(Wb[p], rp + (size_t)(4 * RPI * p) * row_bytes, cc);
 #pragma clang loop unroll(full)
         for (int st = 0; st < NSTEP; ++st) {
-            const int p = st % DN_PF;
-            const int r = h0 + (st * 4 + wave) * RPI + rsub;
+            const int p = st % PF;
+            float acc[MAXP];
+            row8_dots<NB, MAXP, MAX_NDOWN_S>(acc, Wb[p], n, &s_qs[0][0], &s_d[0][0], &s_bs[0][0], c8);
+            if (st + PF < NSTEP) load_row8<NB>(Wb[p], rp + (size_t)(4 * RPS * (st + PF)) * row_bytes, c8);
+            const int r = h0 + (st * 4 + wave) * RPS + rsub;
 #pragma unroll
-            for (int i = 0; i < MAXP; ++i) {
+            for (int i = 0; i < MAXP; ++i)
                 if (i < n) {
-                    const float acc = lane_sum<LPR>(chunk_dot_s(Wb[p], A[i], cc, 0.f) * on);
-                    if (c == i) s_ex[i][r - h0] = acc;
+                    const float sum = row8_sum(acc[i]);
+                    if (c8 == 0) s_ex[i][r - h0] = sum;
                 }
-            }
-            if (st + DN_PF < NSTEP) load_w_chunk_s(Wb[p], rp + (size_t)(4 * RPI * (st + DN_PF)) * row_bytes, cc);
         }
         __syncthreads();
         for (int q = tid; q < n * (h1 - h0); q += 256) {
@@ -588,7 +582,7 @@ QWM_DEV void step_down(const StepArgs & a, int g, int G, const StepShared & S, u
     }
 }
 
-template <int NT, int LPR_D>
+template <int NT, int NB_D>
 __global__ void __launch_bounds__(256) k_step(StepArgs a) {
     constexpr int MAXP = NT <= 1 ? 1 : NT <= 2 ? 2 : NT <= 4 ? 4 : 8;
     constexpr size_t router_bytes = (size_t)5 * 16 * RX_P * 4;
@@ -619,7 +613,7 @@ __global__ void __launch_bounds__(256) k_step(StepArgs a) {
     else step_select<NT, STEP_MAX_E / 64>(a, g, S, smem);
     step_gateup<MAXP>(a, g, G, S, smem);
     grid_barrier(a, 2, G, epoch);
-    step_down<NT, LPR_D, MAXP>(a, g, G, S, smem);
+    step_down<NT, NB_D, MAXP>(a, g, G, S, smem);
     grid_barrier(a, 3, G, epoch);
     __syncthreads();
     constexpr int PF = NT <= 4 ? 2 : 1;
@@ -647,7 +641,11 @@ bool step_plan(const qwm_moe_layer * L, const qwm_tensor * lm_head, int64_t T, S
     if (!moe_plan(L, T, p.moe, why)) return false;
     if (p.moe.H != SH) { why = "the fused step is built for hidden size 2048"; return false; }
     if (L->gate_pool.type != T_Q4_K) { why = "the fused step needs Q4_K expert pools"; return false; }
-    if (p.moe.N > MAX_NDOWN_S || (p.moe.shared && p.moe.N_sh > MAX_NDOWN_S)) { why = "FFN width > 2048"; return false; }
+    if (p.moe.N != 512 && p.moe.N != 768 && p.moe.N != 1024 && p.moe.N != 2048) {
+        why = "the fused step is built for FFN widths 512, 768, 1024 and 2048";
+        return false;
+    }
+    if (p.moe.shared && p.moe.N_sh != p.moe.N) { why = "the fused step needs the shared expert's FFN width = the routed one"; return false; }
     if (p.moe.E > STEP_MAX_E) { why = "the fused step handles up to 512 experts"; return false; }
     if (lm_head->type != T_Q8_0 || lm_head->ne[0] != SH) { why = "lm_head must be Q8_0 [2048, V]"; return false; }
     p.V = lm_head->ne[1];
@@ -666,23 +664,23 @@ bool step_plan(const qwm_moe_layer * L, const qwm_tensor * lm_head, int64_t T, S
     return true;
 }
 
-template <int NT, int LPR_D>
+template <int NT, int NB_D>
 static int step_grid() {
     static int grid = 0;
     if (!grid) {
         int dev = 0, cus = 0, per_cu = 0;
         if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
             return -1;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(k_step<NT, LPR_D>), 256, 0) != hipSuccess)
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(k_step<NT, NB_D>), 256, 0) != hipSuccess)
             return -1;
         grid = std::min(std::min(per_cu, 2) * cus, MAX_STEP_WG);
     }
     return grid;
 }
 
-template <int NT, int LPR_D>
+template <int NT, int NB_D>
 static int launch_step_t(StepArgs & a, hipStream_t s) {
-    const int G = step_grid<NT, LPR_D>();
+    const int G = step_grid<NT, NB_D>();
     if (G <= 0) return fail(QWM_ERR_HIP, "fused step: occupancy query failed");
     const int U_max = NT * a.k + a.shared;
     if (G < U_max) return fail(QWM_ERR_UNSUPPORTED, "fused step: fewer co-resident workgroups than expert units");
@@ -693,7 +691,7 @@ static int launch_step_t(StepArgs & a, hipStream_t s) {
     // CUs, the missing workgroups start as it drains; the bounded spins report
     // a = -1 rather than wait without end.
     prof_begin("step", s);
-    k_step<NT, LPR_D><<<dim3((unsigned)G), dim3(256), 0, s>>>(a);
+    k_step<NT, NB_D><<<dim3((unsigned)G), dim3(256), 0, s>>>(a);
     prof_end("step", s);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(QWM_ERR_HIP, std::string("fused step launch: ") + hipGetErrorString(e));
@@ -701,11 +699,12 @@ static int launch_step_t(StepArgs & a, hipStream_t s) {
 }
 
 template <int NT>
-static int launch_step_nt(StepArgs & a, int lpr_d, hipStream_t s) {
-    switch (lpr_d) {
-        case 16: return launch_step_t<NT, 16>(a, s);
-        case 32: return launch_step_t<NT, 32>(a, s);
-        default: return launch_step_t<NT, 64>(a, s);
+static int launch_step_nt(StepArgs & a, int nb_d, hipStream_t s) {
+    switch (nb_d) {
+        case 2: return launch_step_t<NT, 2>(a, s);
+        case 3: return launch_step_t<NT, 3>(a, s);
+        case 4: return launch_step_t<NT, 4>(a, s);
+        default: return launch_step_t<NT, 8>(a, s);
     }
 }
 
@@ -744,18 +743,16 @@ int launch_step(const StepCall & c, const StepPlan & p, uint8_t * ws, hipStream_
     v.pv = reinterpret_cast<float *>(ws + p.v_pv);
     v.pi = reinterpret_cast<int32_t *>(ws + p.v_pi);
     v.counter = reinterpret_cast<int32_t *>(ws + p.v_counter);
-    const int lpr_d = m.N <= 512 ? 16 : m.N <= 1024 ? 32 : 64;
-    if (m.shared && (m.N_sh <= 512 ? 16 : m.N_sh <= 1024 ? 32 : 64) != lpr_d)
-        return fail(QWM_ERR_UNSUPPORTED, "fused step: shared and routed FFN widths need the same tiling");
+    const int nb_d = (int)(m.N / QK_K);          // step_plan: 2, 3, 4 or 8
     switch (m.T) {
-        case 1: return launch_step_nt<1>(a, lpr_d, s);
-        case 2: return launch_step_nt<2>(a, lpr_d, s);
-        case 3: return launch_step_nt<3>(a, lpr_d, s);
-        case 4: return launch_step_nt<4>(a, lpr_d, s);
-        case 5: return launch_step_nt<5>(a, lpr_d, s);
-        case 6: return launch_step_nt<6>(a, lpr_d, s);
-        case 7: return launch_step_nt<7>(a, lpr_d, s);
-        default: return launch_step_nt<8>(a, lpr_d, s);
+        case 1: return launch_step_nt<1>(a, nb_d, s);
+        case 2: return launch_step_nt<2>(a, nb_d, s);
+        case 3: return launch_step_nt<3>(a, nb_d, s);
+        case 4: return launch_step_nt<4>(a, nb_d, s);
+        case 5: return launch_step_nt<5>(a, nb_d, s);
+        case 6: return launch_step_nt<6>(a, nb_d, s);
+        case 7: return launch_step_nt<7>(a, nb_d, s);
+        default: return launch_step_nt<8>(a, nb_d, s);
     }
 }
 

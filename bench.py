@@ -34,15 +34,16 @@ Q4K_ROW_D = N // 256 * 144           # 432 B
 SLAB = N * Q4K_ROW_GU                # 884,736 B per role per expert
 LM_ROW = H // 32 * 34                # 2176 B
 CAL_BYTES = 256 << 20                # calibration copy for the PMC byte counters
-TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "verify_step_T4_traffic.json")
+TRAFFIC_SUMMARY = {"step": os.path.join(ROOT, "profiles", "verify_step_T4_traffic.json"),
+                   "ops": os.path.join(ROOT, "profiles", "verify_ops_T4_traffic.json")}
 
 
-def measured_traffic(kernel):
+def measured_traffic(path, kernel):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc
     summary (FETCH_SIZE + WRITE_SIZE, each scaled by the calibration kernel),
     or None."""
     try:
-        with open(TRAFFIC_SUMMARY) as f:
+        with open(TRAFFIC_SUMMARY[path]) as f:
             return float(json.load(f)["kernels"][kernel]["traffic_bytes"])
     except (OSError, KeyError, ValueError, TypeError):
         return None
@@ -207,8 +208,8 @@ def main():
                      "kernel": ("step (MoE block + verify head, one launch)" if args.path == "step"
                                 else "lm_head (Q8_0 GEMV + argmax)"),
                      "achieved": lm_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": lm_gbs / HBM_PEAK_GBS,
-                     "traffic": measured_traffic(main_kernel),
-                     "traffic_source": os.path.relpath(TRAFFIC_SUMMARY, ROOT),
+                     "traffic": measured_traffic(args.path, main_kernel),
+                     "traffic_source": os.path.relpath(TRAFFIC_SUMMARY[args.path], ROOT),
                      "bytes_per_launch": main_bytes, "avg_launch_us": lm_avg_ms * 1e3, "launches_timed": int(n_lm)},
         "path": args.path,
         "step_hbm_gbs": float(step_bytes.mean()) / (ms_step * 1e-3) / 1e9,

@@ -140,7 +140,8 @@ static int check_mmid(const qwm_tensor * as, const qwm_tensor * b, const qwm_ten
     if ((b->nb[1] | b->nb[2]) % 16) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: b rows must be 16-byte aligned");
     if (b->ne[2] > MAX_T) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: more than 8 columns (prefill) is not handled here");
     if (ids->ne[0] * ids->ne[1] > MAX_PAIRS) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: too many (expert, column) pairs");
-    if (as->type == T_Q4_K && as->ne[0] > 2048) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: K > 2048");
+    if (as->ne[0] > 2048) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: K > 2048");
+    if (as->type == T_Q8_0 && as->ne[0] % 256) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: Q8_0 needs K a multiple of 256");
     if (dst) {
         if (dst->type != T_F32 || dst->ne[0] != as->ne[1] || dst->ne[1] != ids->ne[0] || dst->ne[2] != b->ne[2])
             return fail(QWM_ERR_ARG, "mul_mat_id: dst must be f32 [N, n_ids, T]");
@@ -224,6 +225,7 @@ static int do_route(const qwm_moe_layer * L, const MoePlan & p, const qwm_tensor
     a.sh_gate_inp = (L->sh_gate.data && L->sh_gate_inp.data) ? (const float *)L->sh_gate_inp.data : nullptr;
     a.E = p.E; a.H = p.H; a.T = p.T; a.k = p.k; a.norm = L->norm_weights; a.scale = L->weights_scale;
     a.slot_tables = tables; a.table_stride = stride; a.layer = layer_index;
+    a.wtype = L->gate_pool.type;
     return launch_route(a, p, ws, ids_out, ids_ld, w_out, w_ld, s);
 }
 

@@ -44,7 +44,7 @@ struct MoePlan {
     int64_t H, N, N_sh, E, k, T;
     bool shared, shared_gate;
     size_t counters, tile_counters, logits, ids, w, slots, sh_gate, units, n_units;
-    size_t xq_qs, xq_d, xq_bs, act, act_sh, ex, ex_sh;
+    size_t xq_qs, xq_d, xq_bs, xq_d0, act, act_sh, ex, ex_sh;
     size_t total;
 };
 bool moe_plan(const qwm_moe_layer * L, int64_t T, MoePlan & p, std::string & why);
@@ -63,6 +63,7 @@ struct RouteArgs {
     const float * sh_gate_inp;                           // [H] or null
     int64_t E, H, T, k; int norm; float scale;
     const int32_t * slot_tables; int64_t table_stride; int32_t layer;  // resident remap or null
+    int32_t wtype;                                       // pool type: the activation format of x
 };
 int launch_route(const RouteArgs & a, const MoePlan & p, uint8_t * ws, int32_t * ids_out, int64_t ids_ld,
                  float * w_out, int64_t w_ld, hipStream_t s);

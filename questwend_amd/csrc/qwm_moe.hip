@@ -14,6 +14,7 @@
 #include "qwm_device.h"
 #include "qwm_internal.h"
 #include "qwm_q4k.h"
+#include "qwm_q80.h"
 
 namespace qwm {
 
@@ -31,6 +32,7 @@ struct RouteKArgs {
     int32_t * ids_out; int64_t ids_ld; float * w_out; int64_t w_ld;  // optional user copies
     float * sh_gate;                                 // [T] or null
     int8_t * xq_qs; float * xq_d; int32_t * xq_bs;   // Q8_K of x
+    int q80; float * xq_d0;                         // Q8_0 pools: x as Q8_0 (qs in xq_qs, scales per 32)
     Unit * units; int32_t * n_units; int32_t * counter;
     int shared;                                      // append the shared-expert unit
     const int32_t * slot_tables; int64_t table_stride; int layer; int32_t * slots_ws;  // [3][T*k]
@@ -62,13 +64,18 @@ __global__ void __launch_bounds__(256) k_route(RouteKArgs a) {
     const int E = a.E, H = a.H, T = a.T, k = a.k;
     const int nsteps = H / 16;
 
-    // ---- Q8_K of x (inputs of the expert GEMVs), spread over every wave
+    // ---- Q8_K (Q4_K pools) or Q8_0 (Q8_0 pools) of x, the inputs of the
+    // expert GEMVs, spread over every wave
     {
         const int nb = H / QK_K;
         for (int jb = blockIdx.x * 4 + wave; jb < T * nb; jb += gridDim.x * 4) {
             const int t = jb / nb, b = jb % nb;
-            quantize_block_q8K(a.x + (size_t)t * H + b * QK_K, a.xq_qs + (size_t)t * H + b * QK_K,
-                               a.xq_d + (size_t)t * nb + b, a.xq_bs + (size_t)t * (H / 16) + b * 16, lane);
+            if (a.q80)
+                quantize_q80_256(a.x + (size_t)t * H + b * QK_K, a.xq_qs + (size_t)t * H + b * QK_K,
+                                 a.xq_d0 + (size_t)t * (H / 32) + b * 8, lane);
+            else
+                quantize_block_q8K(a.x + (size_t)t * H + b * QK_K, a.xq_qs + (size_t)t * H + b * QK_K,
+                                   a.xq_d + (size_t)t * nb + b, a.xq_bs + (size_t)t * (H / 16) + b * 16, lane);
         }
     }
 
@@ -289,8 +296,8 @@ struct GateUpArgs {
     int H, N, N_sh, k;
 };
 
-template <int LPR, int MAXP>
-__global__ void __launch_bounds__(256) k_gateup_q4k(GateUpArgs a) {
+template <class F, int LPR, int MAXP>
+__global__ void __launch_bounds__(256) k_gateup(GateUpArgs a) {
     constexpr int RPI = WAVE / LPR;     // rows per wave step
     constexpr int NIT = GEMV_STEPS;     // steps per wave; all loads issued up front
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -301,7 +308,7 @@ __global__ void __launch_bounds__(256) k_gateup_q4k(GateUpArgs a) {
     const Unit & U = a.units[shared ? *a.n_units : u];
     const int n = U.n;
     const int rows = shared ? a.N_sh : a.N;
-    const size_t row_bytes = (size_t)(a.H / QK_K) * 144;
+    const size_t row_bytes = F::row_bytes(a.H);
     const uint8_t * gbase;
     const uint8_t * ubase;
     if (shared) { gbase = a.sh_gate; ubase = a.sh_up; }
@@ -313,22 +320,22 @@ __global__ void __launch_bounds__(256) k_gateup_q4k(GateUpArgs a) {
     const bool active = c < C;
     const int r_begin = (blockIdx.x * 4 + wave) * (NIT * RPI);
     if (r_begin >= rows) return;
-    WChunk G[NIT], Uw[NIT];
+    typename F::W G[NIT], Uw[NIT];
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
         const int r = r_begin + it * RPI + rsub;
         if (active && r < rows) {
-            load_w_chunk(G[it], gbase + (size_t)r * row_bytes, c);
-            load_w_chunk(Uw[it], ubase + (size_t)r * row_bytes, c);
+            F::load_w(G[it], gbase + (size_t)r * row_bytes, c);
+            F::load_w(Uw[it], ubase + (size_t)r * row_bytes, c);
         }
     }
-    ActChunk A[MAXP];
+    typename F::A A[MAXP];
 #pragma unroll
     for (int i = 0; i < MAXP; ++i) {
         if (i < n && active) {
             const int tok = shared ? U.pair[i] : U.pair[i] / a.k;
-            load_act_chunk(A[i], a.xq_qs + (size_t)tok * a.H, a.xq_d + (size_t)tok * (a.H / QK_K),
-                           a.xq_bs + (size_t)tok * (a.H / 16), c);
+            F::load_a(A[i], a.xq_qs + (size_t)tok * a.H, a.xq_d + (size_t)tok * F::d_per_row(a.H),
+                      a.xq_bs + (size_t)tok * (a.H / 16), a.H, c);
         }
     }
 #pragma unroll
@@ -341,8 +348,8 @@ __global__ void __launch_bounds__(256) k_gateup_q4k(GateUpArgs a) {
             g[i] = 0.f; up[i] = 0.f;
             if (i < n) {                      // n is uniform: empty token slots cost nothing
                 if (valid) {
-                    g[i] = chunk_dot(G[it], A[i], c, 0.f);
-                    up[i] = chunk_dot(Uw[it], A[i], c, 0.f);
+                    g[i] = F::dot(G[it], A[i], c);
+                    up[i] = F::dot(Uw[it], A[i], c);
                 }
                 g[i] = halves_sum<LPR>(g[i]);
                 up[i] = halves_sum<LPR>(up[i]);
@@ -463,6 +470,65 @@ __global__ void __launch_bounds__(256) k_down_q4k(DownArgs a) {
     }
 }
 
+// The Q8_0 form of k_down_q4k: weight blocks of 32 (one per lane per step of
+// the row), activations quantized to Q8_0 in LDS (ggml's x86 quantizer, the
+// vec_dot_type of Q8_0).
+template <int NB, int MAXP>
+__global__ void __launch_bounds__(256) k_down_q80(DownArgs a) {
+    constexpr int RPS = 8;                   // rows per wave
+    constexpr int TILE = 4 * RPS;
+    constexpr size_t row_bytes = (size_t)NB * 8 * 34;
+    __shared__ __align__(16) int8_t s_qs[MAXP][MAX_NDOWN];
+    __shared__ float s_d[MAXP][MAX_NDOWN / 32];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int c8 = lane & 7, rsub = lane >> 3;
+    const int u = blockIdx.y;
+    const bool shared = u == a.unit_slots;
+    const int nu = *a.n_units;
+    if (!shared && u >= nu) return;
+    const Unit & U = a.units[shared ? nu : u];
+    const int n = U.n;
+    const uint8_t * base = shared ? a.sh_down : a.down + (size_t)a.slot_d[U.pair[0]] * a.down_slab;
+    const int row0 = blockIdx.x * TILE;
+    const int r = row0 + wave * RPS + rsub;
+    W80 W[NB];
+    const uint8_t * rowp = base + (size_t)min(r, a.H - 1) * row_bytes;
+#pragma unroll
+    for (int q = 0; q < NB; ++q) load_w80(W[q], rowp, 8 * q + c8);
+    for (int jb = wave; jb < n * NB; jb += 4) {
+        const int i = jb / NB, b = jb % NB;
+        const float * src = shared ? a.act_sh + (size_t)U.pair[i] * (NB * QK_K) : a.act + (size_t)U.pair[i] * (NB * QK_K);
+        quantize_q80_256(src + b * QK_K, &s_qs[i][b * QK_K], &s_d[i][b * 8], lane);
+    }
+    __syncthreads();
+    float acc[MAXP];
+#pragma unroll
+    for (int i = 0; i < MAXP; ++i) acc[i] = 0.f;
+#pragma unroll
+    for (int q = 0; q < NB; ++q)
+#pragma unroll
+        for (int i = 0; i < MAXP; ++i)
+            if (i < n) {
+                A80 A;
+                load_a80(A, s_qs[i], s_d[i], 8 * q + c8);
+                acc[i] = dot80(W[q], A, 8 * q + c8, acc[i]);
+            }
+#pragma unroll
+    for (int i = 0; i < MAXP; ++i)
+        if (i < n) {
+            const float sum = row8_sum(acc[i]);
+            if (c8 == 0 && r < a.H) {
+                if (shared) st_agent(a.ex_sh + (size_t)U.pair[i] * a.H + r, sum);
+                else st_agent(a.ex + (size_t)U.pair[i] * a.H + r, sum);
+            }
+        }
+    if (!last_workgroup(a.tile_counters + blockIdx.x, nu + a.shared)) return;
+    for (int q = tid; q < a.T * TILE; q += 256) {
+        const int t = q / TILE, h = row0 + q % TILE;
+        if (h < a.H) a.out[(size_t)t * a.H + h] = combine_one(a, t, h);
+    }
+}
+
 // ======================================================================
 // host launchers
 // ======================================================================
@@ -497,6 +563,7 @@ bool moe_plan(const qwm_moe_layer * L, int64_t T, MoePlan & p, std::string & why
     p.xq_qs = take((size_t)T * p.H);
     p.xq_d = take(sizeof(float) * T * (p.H / QK_K));
     p.xq_bs = take(sizeof(int32_t) * T * (p.H / 16));
+    p.xq_d0 = take(sizeof(float) * T * (p.H / 32));
     p.act = take(sizeof(float) * P * p.N);
     p.act_sh = take(sizeof(float) * T * (p.N_sh ? p.N_sh : 1));
     p.ex = take(sizeof(float) * P * p.H);
@@ -522,6 +589,8 @@ int launch_route(const RouteArgs & a, const MoePlan & p, uint8_t * ws, int32_t *
     r.xq_qs = reinterpret_cast<int8_t *>(ws + p.xq_qs);
     r.xq_d = reinterpret_cast<float *>(ws + p.xq_d);
     r.xq_bs = reinterpret_cast<int32_t *>(ws + p.xq_bs);
+    r.q80 = a.wtype == T_Q8_0;
+    r.xq_d0 = reinterpret_cast<float *>(ws + p.xq_d0);
     r.units = reinterpret_cast<Unit *>(ws + p.units);
     r.n_units = reinterpret_cast<int32_t *>(ws + p.n_units);
     r.counter = reinterpret_cast<int32_t *>(ws + p.counters);
@@ -534,17 +603,34 @@ int launch_route(const RouteArgs & a, const MoePlan & p, uint8_t * ws, int32_t *
     return QWM_OK;
 }
 
-template <int LPR>
+template <class F, int LPR>
 static void launch_gateup_lpr(const GateUpArgs & g, int maxp, dim3 grid, hipStream_t s) {
     switch (maxp) {
-        case 1: k_gateup_q4k<LPR, 1><<<grid, 256, 0, s>>>(g); break;
-        case 2: k_gateup_q4k<LPR, 2><<<grid, 256, 0, s>>>(g); break;
-        case 4: k_gateup_q4k<LPR, 4><<<grid, 256, 0, s>>>(g); break;
-        default: k_gateup_q4k<LPR, 8><<<grid, 256, 0, s>>>(g); break;
+        case 1: k_gateup<F, LPR, 1><<<grid, 256, 0, s>>>(g); break;
+        case 2: k_gateup<F, LPR, 2><<<grid, 256, 0, s>>>(g); break;
+        case 4: k_gateup<F, LPR, 4><<<grid, 256, 0, s>>>(g); break;
+        default: k_gateup<F, LPR, 8><<<grid, 256, 0, s>>>(g); break;
+    }
+}
+template <class F>
+static void launch_gateup_f(const GateUpArgs & g, int lpr, int maxp, dim3 grid, hipStream_t s) {
+    switch (lpr) {
+        case 16: launch_gateup_lpr<F, 16>(g, maxp, grid, s); break;
+        case 32: launch_gateup_lpr<F, 32>(g, maxp, grid, s); break;
+        default: launch_gateup_lpr<F, 64>(g, maxp, grid, s); break;
     }
 }
 template <int NB>
-static void launch_down_nb(const DownArgs & d, int maxp, dim3 grid, hipStream_t s) {
+static void launch_down_nb(const DownArgs & d, bool q80, int maxp, dim3 grid, hipStream_t s) {
+    if (q80) {
+        switch (maxp) {
+            case 1: k_down_q80<NB, 1><<<grid, 256, 0, s>>>(d); break;
+            case 2: k_down_q80<NB, 2><<<grid, 256, 0, s>>>(d); break;
+            case 4: k_down_q80<NB, 4><<<grid, 256, 0, s>>>(d); break;
+            default: k_down_q80<NB, 8><<<grid, 256, 0, s>>>(d); break;
+        }
+        return;
+    }
     switch (maxp) {
         case 1: k_down_q4k<NB, 1><<<grid, 256, 0, s>>>(d); break;
         case 2: k_down_q4k<NB, 2><<<grid, 256, 0, s>>>(d); break;
@@ -563,7 +649,8 @@ static int lanes_per_row(int K) {
 static int pow2_maxp(int64_t T) { return T <= 1 ? 1 : T <= 2 ? 2 : T <= 4 ? 4 : 8; }
 
 int launch_experts(const ExpertArgs & a, const MoePlan & p, uint8_t * ws, hipStream_t s) {
-    if (a.wtype != T_Q4_K) return fail(QWM_ERR_UNSUPPORTED, "expert pools: only Q4_K slabs are wired in this build");
+    if (a.wtype != T_Q4_K && a.wtype != T_Q8_0) return fail(QWM_ERR_UNSUPPORTED, "expert pools must be Q4_K or Q8_0");
+    const bool q80 = a.wtype == T_Q8_0;
     const int maxp = pow2_maxp(p.T);
     const int P = (int)(p.T * p.k);
     const int unit_slots = P;
@@ -577,7 +664,7 @@ int launch_experts(const ExpertArgs & a, const MoePlan & p, uint8_t * ws, hipStr
     g.slot_g = a.slot_g; g.slot_u = a.slot_u;
     g.units = units; g.n_units = n_units; g.unit_slots = unit_slots;
     g.xq_qs = reinterpret_cast<const int8_t *>(ws + p.xq_qs);
-    g.xq_d = reinterpret_cast<const float *>(ws + p.xq_d);
+    g.xq_d = reinterpret_cast<const float *>(ws + (q80 ? p.xq_d0 : p.xq_d));
     g.xq_bs = reinterpret_cast<const int32_t *>(ws + p.xq_bs);
     g.act = reinterpret_cast<float *>(ws + p.act);
     g.act_sh = reinterpret_cast<float *>(ws + p.act_sh);
@@ -588,11 +675,8 @@ int launch_experts(const ExpertArgs & a, const MoePlan & p, uint8_t * ws, hipStr
     const int tile_g = 4 * GEMV_STEPS * (WAVE / lg);
     dim3 grid_g((rows_g + tile_g - 1) / tile_g, grid_y);
     prof_begin("gate_up", s);
-    switch (lg) {
-        case 16: launch_gateup_lpr<16>(g, maxp, grid_g, s); break;
-        case 32: launch_gateup_lpr<32>(g, maxp, grid_g, s); break;
-        default: launch_gateup_lpr<64>(g, maxp, grid_g, s); break;
-    }
+    if (q80) launch_gateup_f<FmtQ80>(g, lg, maxp, grid_g, s);
+    else launch_gateup_f<FmtQ4K>(g, lg, maxp, grid_g, s);
     prof_end("gate_up", s);
 
     DownArgs d;
@@ -614,14 +698,14 @@ int launch_experts(const ExpertArgs & a, const MoePlan & p, uint8_t * ws, hipStr
     if (grid_d.x > (unsigned)MAX_TILES) return fail(QWM_ERR_UNSUPPORTED, "hidden size needs too many down tiles");
     prof_begin("down", s);
     switch (nb_d) {
-        case 1: launch_down_nb<1>(d, maxp, grid_d, s); break;
-        case 2: launch_down_nb<2>(d, maxp, grid_d, s); break;
-        case 3: launch_down_nb<3>(d, maxp, grid_d, s); break;
-        case 4: launch_down_nb<4>(d, maxp, grid_d, s); break;
-        case 5: launch_down_nb<5>(d, maxp, grid_d, s); break;
-        case 6: launch_down_nb<6>(d, maxp, grid_d, s); break;
-        case 7: launch_down_nb<7>(d, maxp, grid_d, s); break;
-        default: launch_down_nb<8>(d, maxp, grid_d, s); break;
+        case 1: launch_down_nb<1>(d, q80, maxp, grid_d, s); break;
+        case 2: launch_down_nb<2>(d, q80, maxp, grid_d, s); break;
+        case 3: launch_down_nb<3>(d, q80, maxp, grid_d, s); break;
+        case 4: launch_down_nb<4>(d, q80, maxp, grid_d, s); break;
+        case 5: launch_down_nb<5>(d, q80, maxp, grid_d, s); break;
+        case 6: launch_down_nb<6>(d, q80, maxp, grid_d, s); break;
+        case 7: launch_down_nb<7>(d, q80, maxp, grid_d, s); break;
+        default: launch_down_nb<8>(d, q80, maxp, grid_d, s); break;
     }
     prof_end("down", s);
 
@@ -636,7 +720,8 @@ struct MmidPrep {
     const float * b; size_t b_nb1, b_nb2;   // bytes
     const int32_t * ids; size_t ids_nb1;    // bytes
     int K, ne11, T, n_ids, n_as, cap;       // cap: pairs per unit
-    int8_t * qs; float * d; int32_t * bs;   // [T*ne11] rows of Q8_K
+    int q80;                                // Q8_0 weights: b as Q8_0 (d per 32) instead of Q8_K
+    int8_t * qs; float * d; int32_t * bs;   // [T*ne11] rows of Q8_K or Q8_0
     Unit * units; int32_t * n_units; int32_t * ids_ws; int32_t * err;
 };
 
@@ -649,8 +734,11 @@ __global__ void __launch_bounds__(256) k_mmid_prep(MmidPrep a) {
         const int row = jb / nb, b = jb % nb;
         const int t = row / a.ne11, i = row % a.ne11;
         const float * src = reinterpret_cast<const float *>(reinterpret_cast<const uint8_t *>(a.b) + t * a.b_nb2 + i * a.b_nb1);
-        quantize_block_q8K(src + b * QK_K, a.qs + (size_t)row * a.K + b * QK_K, a.d + (size_t)row * nb + b,
-                           a.bs + (size_t)row * (a.K / 16) + b * 16, lane);
+        if (a.q80)
+            quantize_q80_256(src + b * QK_K, a.qs + (size_t)row * a.K + b * QK_K, a.d + (size_t)row * (a.K / 32) + b * 8, lane);
+        else
+            quantize_block_q8K(src + b * QK_K, a.qs + (size_t)row * a.K + b * QK_K, a.d + (size_t)row * nb + b,
+                               a.bs + (size_t)row * (a.K / 16) + b * 16, lane);
     }
     if (blockIdx.x != 0 || wave != 0) return;
     const int P = a.T * a.n_ids;
@@ -702,8 +790,8 @@ struct MmidGemv {
     float * dst; size_t dst_nb1, dst_nb2;
 };
 
-template <int LPR, int MAXP>
-__global__ void __launch_bounds__(256) k_mmid_q4k(MmidGemv a) {
+template <class F, int LPR, int MAXP>
+__global__ void __launch_bounds__(256) k_mmid(MmidGemv a) {
     constexpr int RPI = WAVE / LPR;
     constexpr int NIT = GEMV_STEPS;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -717,19 +805,20 @@ __global__ void __launch_bounds__(256) k_mmid_q4k(MmidGemv a) {
     const uint8_t * base = a.as + (size_t)U.expert * a.slab;
     const int r_begin = (blockIdx.x * 4 + wave) * (NIT * RPI);
     if (r_begin >= a.N) return;
-    WChunk W[NIT];
+    typename F::W W[NIT];
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
         const int r = r_begin + it * RPI + rsub;
-        if (active && r < a.N) load_w_chunk(W[it], base + (size_t)r * a.row_bytes, c);
+        if (active && r < a.N) F::load_w(W[it], base + (size_t)r * a.row_bytes, c);
     }
-    ActChunk A[MAXP];
+    typename F::A A[MAXP];
 #pragma unroll
     for (int i = 0; i < MAXP; ++i)
         if (i < n && active) {
             const int p = U.pair[i];
             const int row = (p / a.n_ids) * a.ne11 + (p % a.n_ids) % a.ne11;
-            load_act_chunk(A[i], a.qs + (size_t)row * a.K, a.d + (size_t)row * (a.K / QK_K), a.bs + (size_t)row * (a.K / 16), c);
+            F::load_a(A[i], a.qs + (size_t)row * a.K, a.d + (size_t)row * F::d_per_row(a.K), a.bs + (size_t)row * (a.K / 16),
+                      a.K, c);
         }
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
@@ -740,7 +829,7 @@ __global__ void __launch_bounds__(256) k_mmid_q4k(MmidGemv a) {
         for (int i = 0; i < MAXP; ++i) {
             acc[i] = 0.f;
             if (i < n) {
-                if (valid) acc[i] = chunk_dot(W[it], A[i], c, 0.f);
+                if (valid) acc[i] = F::dot(W[it], A[i], c);
                 acc[i] = lane_sum<LPR>(acc[i]);
             }
         }
@@ -762,7 +851,7 @@ size_t mmid_workspace(int64_t K, int64_t T, int64_t ne11, int64_t n_ids) {
     size_t o = 0;
     auto take = [&](size_t bytes) { o = align_up(o + bytes, 256); };
     take((size_t)rows * K);                       // qs
-    take(sizeof(float) * rows * (K / QK_K));      // d
+    take(sizeof(float) * rows * (K / 32));        // d (Q8_K: K / 256 used)
     take(sizeof(int32_t) * rows * (K / 16));      // bsums
     take(sizeof(Unit) * T * n_ids);               // units
     take(sizeof(int32_t) * 4);                    // n_units, err
@@ -771,11 +860,12 @@ size_t mmid_workspace(int64_t K, int64_t T, int64_t ne11, int64_t n_ids) {
 }
 
 int launch_mmid(const MmidArgs & a, uint8_t * ws, hipStream_t s) {
-    if (a.wtype != T_Q4_K) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: only Q4_K weights are wired in this build");
+    if (a.wtype != T_Q4_K && a.wtype != T_Q8_0) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: weights must be Q4_K or Q8_0");
+    const bool q80 = a.wtype == T_Q8_0;
     const int64_t rows = a.T * a.ne11;
     size_t o = 0;
     auto take = [&](size_t bytes) { size_t at = o; o = align_up(o + bytes, 256); return at; };
-    const size_t o_qs = take((size_t)rows * a.K), o_d = take(sizeof(float) * rows * (a.K / QK_K)),
+    const size_t o_qs = take((size_t)rows * a.K), o_d = take(sizeof(float) * rows * (a.K / 32)),
                  o_bs = take(sizeof(int32_t) * rows * (a.K / 16)), o_u = take(sizeof(Unit) * a.T * a.n_ids),
                  o_n = take(sizeof(int32_t) * 4), o_ids = take(sizeof(int32_t) * a.T * a.n_ids);
     MmidPrep pr;
@@ -783,6 +873,7 @@ int launch_mmid(const MmidArgs & a, uint8_t * ws, hipStream_t s) {
     const int maxp = pow2_maxp(a.T);
     pr.K = (int)a.K; pr.ne11 = (int)a.ne11; pr.T = (int)a.T; pr.n_ids = (int)a.n_ids; pr.n_as = (int)a.n_as;
     pr.cap = maxp;
+    pr.q80 = q80 ? 1 : 0;
     pr.qs = reinterpret_cast<int8_t *>(ws + o_qs); pr.d = reinterpret_cast<float *>(ws + o_d);
     pr.bs = reinterpret_cast<int32_t *>(ws + o_bs); pr.units = reinterpret_cast<Unit *>(ws + o_u);
     pr.n_units = reinterpret_cast<int32_t *>(ws + o_n); pr.err = pr.n_units + 1;
@@ -790,7 +881,7 @@ int launch_mmid(const MmidArgs & a, uint8_t * ws, hipStream_t s) {
     const int nblk = (int)(rows * (a.K / QK_K));
     QWM_TIMED("mul_mat_id_prep", s, k_mmid_prep<<<dim3((unsigned)std::max(1, std::min(256, (nblk + 3) / 4))), 256, 0, s>>>(pr));
     MmidGemv g;
-    g.as = a.as; g.slab = a.slab; g.row_bytes = (size_t)(a.K / QK_K) * 144;
+    g.as = a.as; g.slab = a.slab; g.row_bytes = q80 ? (size_t)(a.K / 32) * 34 : (size_t)(a.K / QK_K) * 144;
     g.units = pr.units; g.n_units = pr.n_units; g.qs = pr.qs; g.d = pr.d; g.bs = pr.bs;
     g.K = (int)a.K; g.N = (int)a.N; g.ne11 = (int)a.ne11; g.n_ids = (int)a.n_ids;
     g.dst = a.dst; g.dst_nb1 = a.dst_nb1; g.dst_nb2 = a.dst_nb2;
@@ -798,7 +889,11 @@ int launch_mmid(const MmidArgs & a, uint8_t * ws, hipStream_t s) {
     if (lpr < 0) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: K > 2048 not tiled");
     const int tile = 4 * GEMV_STEPS * (WAVE / lpr);
     dim3 grid((unsigned)((a.N + tile - 1) / tile), (unsigned)(a.T * a.n_ids));
-#define QWM_MMID(LPR_, P_) k_mmid_q4k<LPR_, P_><<<grid, 256, 0, s>>>(g)
+#define QWM_MMID(LPR_, P_)                                                          \
+    do {                                                                            \
+        if (q80) k_mmid<FmtQ80, LPR_, P_><<<grid, 256, 0, s>>>(g);                  \
+        else k_mmid<FmtQ4K, LPR_, P_><<<grid, 256, 0, s>>>(g);                      \
+    } while (0)
 #define QWM_MMID_P(LPR_)                                    \
     switch (maxp) {                                         \
         case 1: QWM_MMID(LPR_, 1); break;                   \

@@ -1,5 +1,5 @@
 """Seeded synthetic MoE layers for the parity tests: weights quantized on the
-CPU by the oracle (bit-identical to ggml's quantize_q4_K), uploaded with
+CPU by the oracle (bit-identical to ggml's quantize_q4_K / quantize_q8_0), uploaded with
 torch, and the matching oracle results.  Shapes follow the workloads:
 Qwen3-30B-A3B (H 2048, 128 experts, FFN 768, top-8) and Qwen3-Next
 (H 2048, 512 experts + shared, FFN 512, top-10); the slot pools hold a few
@@ -9,7 +9,7 @@ import ctypes
 import numpy as np
 
 import questwend_amd as qa
-from tests.helpers import GGML_Q4_K, I64, F32, Q4K_BYTES, oracle, ptr, quantize_q4_K
+from tests.helpers import GGML_Q4_K, GGML_Q8_0, I64, F32, oracle, ptr, quantize_q4_K, quantize_q8_0_model
 
 
 class QwoMoeArgs(ctypes.Structure):
@@ -24,18 +24,24 @@ class QwoMoeArgs(ctypes.Structure):
 
 
 class MoeCase:
-    def __init__(self, seed, H=2048, N=768, E=128, k=8, S=16, shared=False, N_sh=512, sh_gate=True):
+    def __init__(self, seed, H=2048, N=768, E=128, k=8, S=16, shared=False, N_sh=512, sh_gate=True, wtype="q4_K"):
+        """wtype: "q4_K" or "q8_0" expert slabs (the model-file quantizers)."""
         rng = np.random.default_rng(seed)
+        assert wtype in ("q4_K", "q8_0")
+        self.wtype = wtype
+        self.ggml_type = GGML_Q4_K if wtype == "q4_K" else GGML_Q8_0
+        self.qa_type = qa.TYPE_Q4_K if wtype == "q4_K" else qa.TYPE_Q8_0
+        quantize = quantize_q4_K if wtype == "q4_K" else quantize_q8_0_model
         self.H, self.N, self.E, self.k, self.S = H, N, E, k, S
         self.shared, self.N_sh, self.has_sh_gate = shared, N_sh, sh_gate
         self.router = (rng.standard_normal((E, H)) * 0.02).astype(np.float32)
-        self.gate_q = quantize_q4_K((rng.standard_normal((S, N, H)) * 0.02).astype(np.float32))
-        self.up_q = quantize_q4_K((rng.standard_normal((S, N, H)) * 0.02).astype(np.float32))
-        self.down_q = quantize_q4_K((rng.standard_normal((S, H, N)) * 0.02).astype(np.float32))
+        self.gate_q = quantize((rng.standard_normal((S, N, H)) * 0.02).astype(np.float32))
+        self.up_q = quantize((rng.standard_normal((S, N, H)) * 0.02).astype(np.float32))
+        self.down_q = quantize((rng.standard_normal((S, H, N)) * 0.02).astype(np.float32))
         if shared:
-            self.shg_q = quantize_q4_K((rng.standard_normal((N_sh, H)) * 0.02).astype(np.float32))
-            self.shu_q = quantize_q4_K((rng.standard_normal((N_sh, H)) * 0.02).astype(np.float32))
-            self.shd_q = quantize_q4_K((rng.standard_normal((H, N_sh)) * 0.02).astype(np.float32))
+            self.shg_q = quantize((rng.standard_normal((N_sh, H)) * 0.02).astype(np.float32))
+            self.shu_q = quantize((rng.standard_normal((N_sh, H)) * 0.02).astype(np.float32))
+            self.shd_q = quantize((rng.standard_normal((H, N_sh)) * 0.02).astype(np.float32))
             self.sh_inp = (rng.standard_normal(H) * 0.02).astype(np.float32) if sh_gate else None
         self.rng = rng
 
@@ -57,7 +63,7 @@ class MoeCase:
         out = np.zeros((T, self.H), np.float32)
         a = QwoMoeArgs()
         a.H, a.N, a.k, a.T = self.H, self.N, self.k, T
-        a.weight_type = GGML_Q4_K
+        a.weight_type = self.ggml_type
         a.gate_pool, a.up_pool, a.down_pool = self.gate_q.ctypes.data, self.up_q.ctypes.data, self.down_q.ctypes.data
         a.n_slots = self.S
         slots = np.ascontiguousarray(slots, np.int32)
@@ -79,15 +85,15 @@ class MoeCase:
         self.d_router = dev(self.router)
         self.d_gate, self.d_up, self.d_down = dev(self.gate_q), dev(self.up_q), dev(self.down_q)
         L = qa.MoeLayer()
-        L.gate_pool = qa.tensor(qa.TYPE_Q4_K, self.H, self.N, self.S, self.d_gate)
-        L.up_pool = qa.tensor(qa.TYPE_Q4_K, self.H, self.N, self.S, self.d_up)
-        L.down_pool = qa.tensor(qa.TYPE_Q4_K, self.N, self.H, self.S, self.d_down)
+        L.gate_pool = qa.tensor(self.qa_type, self.H, self.N, self.S, self.d_gate)
+        L.up_pool = qa.tensor(self.qa_type, self.H, self.N, self.S, self.d_up)
+        L.down_pool = qa.tensor(self.qa_type, self.N, self.H, self.S, self.d_down)
         L.router = qa.tensor(qa.TYPE_F32, self.H, self.E, 1, self.d_router)
         if self.shared:
             self.d_shg, self.d_shu, self.d_shd = dev(self.shg_q), dev(self.shu_q), dev(self.shd_q)
-            L.sh_gate = qa.tensor(qa.TYPE_Q4_K, self.H, self.N_sh, 1, self.d_shg)
-            L.sh_up = qa.tensor(qa.TYPE_Q4_K, self.H, self.N_sh, 1, self.d_shu)
-            L.sh_down = qa.tensor(qa.TYPE_Q4_K, self.N_sh, self.H, 1, self.d_shd)
+            L.sh_gate = qa.tensor(self.qa_type, self.H, self.N_sh, 1, self.d_shg)
+            L.sh_up = qa.tensor(self.qa_type, self.H, self.N_sh, 1, self.d_shu)
+            L.sh_down = qa.tensor(self.qa_type, self.N_sh, self.H, 1, self.d_shd)
             if self.sh_inp is not None:
                 self.d_shinp = dev(self.sh_inp)
                 L.sh_gate_inp = qa.tensor(qa.TYPE_F32, self.H, 1, 1, self.d_shinp)

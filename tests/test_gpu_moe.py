@@ -6,7 +6,7 @@ sums are exact integers, only the fp32 order across blocks differs)."""
 import numpy as np
 import pytest
 
-from tests.helpers import GGML_Q4_K, I64, bits, oracle, ptr, quantize_q4_K
+from tests.helpers import GGML_Q4_K, GGML_Q8_0, I64, bits, oracle, ptr, quantize_q4_K, quantize_q8_0_model
 from tests.moe_case import MoeCase, rel_err
 
 torch = pytest.importorskip("torch")
@@ -96,10 +96,14 @@ def experts_gpu(case, x, slots, weights, resid=None):
     dict(N=512, E=512, k=10, T=4, shared=True),     # Qwen3-Next verify + shared expert
     dict(N=512, E=512, k=10, T=1, shared=True),
     dict(N=768, E=128, k=8, T=8, shared=False),
+    dict(N=768, E=128, k=8, T=1, shared=False, wtype="q8_0"),   # Q8_0 expert slabs
+    dict(N=768, E=128, k=8, T=4, shared=False, wtype="q8_0"),
+    dict(N=512, E=512, k=10, T=4, shared=True, wtype="q8_0"),
 ])
 def test_moe_block_parity(dev, cfg):
     T = cfg["T"]
-    case = MoeCase(seed=11 + T, N=cfg["N"], E=cfg["E"], k=cfg["k"], S=24, shared=cfg["shared"])
+    case = MoeCase(seed=11 + T, N=cfg["N"], E=cfg["E"], k=cfg["k"], S=24, shared=cfg["shared"],
+                   wtype=cfg.get("wtype", "q4_K"))
     case.upload(torch)
     x = case.rng.standard_normal((T, case.H)).astype(np.float32)
     ids, w, _, _ = case.route(x)
@@ -111,6 +115,32 @@ def test_moe_block_parity(dev, cfg):
     assert err < TOL
     for t in range(T):
         assert rel_err(got[t], exp[t]) < TOL
+
+
+@pytest.mark.parametrize("seed,T", [(1, 2), (12, 2), (1, 4)])
+def test_moe_block_distinct_slots(dev, seed, T):
+    """Each selected expert in a slot of its own (first-occurrence order, as
+    ExpertCache::ensure assigns free slots), at T = 2 and 4.
+
+    Slots shared by different experts are left out on purpose: the GPU's
+    SwiGLU values can differ from the CPU's in the last bit (fp32 sums in
+    another order), and a value that close to a rounding boundary of the
+    Q8_K quantizer of the down projection moves one level, ~1e-3 of that
+    expert's output.  With several experts of a token reading one slot the
+    same flip counts several times (seed 1, 8 slots: 1.5e-3 on token 0)."""
+    case = MoeCase(seed=seed, S=T * 8)
+    case.upload(torch)
+    x = case.rng.standard_normal((T, case.H)).astype(np.float32)
+    ids, w, _, _ = case.route(x)
+    uniq = list(dict.fromkeys(int(e) for e in ids.ravel()))
+    slots = np.vectorize(uniq.index)(ids).astype(np.int32)
+    exp = case.block(x, slots, w)
+    got = experts_gpu(case, x, slots, w)
+    errs = [rel_err(got[t], exp[t]) for t in range(T)]
+    worst = np.unravel_index(int(np.argmax(np.abs(got - exp))), got.shape)
+    print(f"distinct slots seed={seed} T={T}: per-token rel err {errs}, worst {worst} "
+          f"got {got[worst]:.6e} exp {exp[worst]:.6e}; ids {ids.tolist()}")
+    assert max(errs) < TOL
 
 
 def test_moe_block_residual(dev):
@@ -125,26 +155,28 @@ def test_moe_block_residual(dev):
     assert rel_err(got, exp) < TOL
 
 
+@pytest.mark.parametrize("wt", ["q4_K", "q8_0"])
 @pytest.mark.parametrize("K,N,n_as,n_ids,ne11,T", [(2048, 768, 8, 8, 1, 1), (2048, 768, 8, 8, 1, 4),
                                                   (768, 2048, 8, 8, 8, 4), (512, 2048, 6, 10, 10, 2),
                                                   (256, 64, 4, 3, 3, 2)])
-def test_mul_mat_id_op(dev, K, N, n_as, n_ids, ne11, T):
+def test_mul_mat_id_op(dev, K, N, n_as, n_ids, ne11, T, wt):
     """GGML_OP_MUL_MAT_ID contract, including broadcast b (ne11 = 1) and
-    repeated experts across columns."""
+    repeated experts across columns, for Q4_K and Q8_0 slabs."""
     rng = np.random.default_rng(K + N + T)
     w = (rng.standard_normal((n_as, N, K)) * 0.02).astype(np.float32)
-    q = quantize_q4_K(w)
+    q = quantize_q4_K(w) if wt == "q4_K" else quantize_q8_0_model(w)
+    gtype, ttype = (GGML_Q4_K, qa.TYPE_Q4_K) if wt == "q4_K" else (GGML_Q8_0, qa.TYPE_Q8_0)
     b = rng.standard_normal((T, ne11, K)).astype(np.float32)
     ids = np.stack([rng.permutation(n_as)[:n_ids] if n_ids <= n_as else rng.integers(0, n_as, n_ids)
                     for _ in range(T)]).astype(np.int32)
     exp = np.zeros((T, n_ids, N), np.float32)
-    assert oracle().qwo_mul_mat_id(GGML_Q4_K, ptr(q), I64(K), I64(N), I64(n_as), ptr(b), I64(ne11), I64(T),
+    assert oracle().qwo_mul_mat_id(gtype, ptr(q), I64(K), I64(N), I64(n_as), ptr(b), I64(ne11), I64(T),
                                    ptr(ids), I64(n_ids), ptr(exp)) == 0
     das = torch.from_numpy(q).cuda()
     db = torch.from_numpy(b).cuda()
     dids = torch.from_numpy(ids).cuda()
     dst = torch.zeros((T, n_ids, N), dtype=torch.float32, device="cuda")
-    tas = qa.tensor(qa.TYPE_Q4_K, K, N, n_as, das)
+    tas = qa.tensor(ttype, K, N, n_as, das)
     tb = qa.tensor(qa.TYPE_F32, K, ne11, T, db)
     tids = qa.tensor(qa.TYPE_I32, n_ids, T, 1, dids)
     ws = workspace(qa.lib().qwm_mul_mat_id_workspace_size(tas, tb, tids))
@@ -153,7 +185,7 @@ def test_mul_mat_id_op(dev, K, N, n_as, n_ids, ne11, T):
     torch.cuda.synchronize()
     got = dst.cpu().numpy()
     err = rel_err(got, exp)
-    print(f"mul_mat_id K={K} N={N} T={T}: rel err {err:.3e}")
+    print(f"mul_mat_id {wt} K={K} N={N} T={T}: rel err {err:.3e}")
     assert err < TOL
     for t in range(T):
         for e in range(n_ids):

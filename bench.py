@@ -52,15 +52,23 @@ def measured_traffic(path, kernel):
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=None, help="default: 200 (verify), 256 (decode48)")
+    ap.add_argument("--warmup", type=int, default=None, help="default: 20 (verify), 10 (decode48)")
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--accept-rate", type=float, default=0.7, help="probability that a draft equals the target")
     ap.add_argument("--path", choices=["step", "ops"], default="step",
                     help="step: the fused verify step (one launch); ops: qwm_moe_block_resident + qwm_verify_accept")
-    return ap.parse_args()
+    ap.add_argument("--workload", choices=["verify", "decode48"], default="verify",
+                    help="verify: the metric's MTP verify step; decode48: 1-token decode through 48 stacked "
+                         "MoE blocks (qwm_moe_decode, HIP graph)")
+    args = ap.parse_args()
+    if args.steps is None:
+        args.steps = 256 if args.workload == "decode48" else 200
+    if args.warmup is None:
+        args.warmup = 10 if args.workload == "decode48" else 20
+    return args
 
 
 def main():
@@ -72,6 +80,9 @@ def main():
     import torch
     import questwend_amd as qa
 
+    if args.workload == "decode48":
+        bench_decode(args, torch, qa)
+        return
     L = qa.lib()
     dev = torch.device("cuda:0")
     torch.manual_seed(args.seed)
@@ -223,6 +234,86 @@ def main():
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args, torch, pools, router, lm, xs, drafts, ids, res)
     print(json.dumps(out))
+
+
+def bench_decode(args, torch, qa, n_layers=48):
+    """1-token decode through 48 stacked Qwen3-30B-A3B-shape MoE blocks
+    (attention omitted), every expert resident (slot = expert id through
+    device tables, ~17 GB of Q4_K), a new N(0, 1) input each step; one step
+    is one qwm_moe_decode call, replayed from a HIP graph."""
+    L = qa.lib()
+    dev = torch.device("cuda:0")
+    torch.manual_seed(args.seed)
+    stream = torch.cuda.current_stream().cuda_stream
+    T1 = 1
+    pools, routers = [], []
+    tmp = torch.empty(N * H, dtype=torch.float32, device=dev)
+    layers = (qa.MoeLayer * n_layers)()
+    for l in range(n_layers):
+        pl = [torch.empty(E * SLAB, dtype=torch.uint8, device=dev) for _ in range(3)]
+        for r in range(3):
+            for e in range(E):
+                tmp.normal_(0.0, 0.02)
+                qa.check(L.qwm_quantize(qa.TYPE_Q4_K, tmp.data_ptr(), pl[r].data_ptr() + e * SLAB, N * H, stream))
+        rt = (torch.randn((E, H), device=dev) * 0.02).contiguous()
+        pools.append(pl)
+        routers.append(rt)
+        layers[l].gate_pool = qa.tensor(qa.TYPE_Q4_K, H, N, E, pl[0])
+        layers[l].up_pool = qa.tensor(qa.TYPE_Q4_K, H, N, E, pl[1])
+        layers[l].down_pool = qa.tensor(qa.TYPE_Q4_K, N, H, E, pl[2])
+        layers[l].router = qa.tensor(qa.TYPE_F32, H, E, 1, rt)
+        layers[l].n_expert_used, layers[l].norm_weights, layers[l].weights_scale = K_USED, 1, 1.0
+        if l % 8 == 7:
+            torch.cuda.synchronize()
+            print(f"decode48: {l + 1} layers quantized", file=sys.stderr, flush=True)
+    del tmp
+    tables = torch.arange(E, dtype=torch.int32, device=dev).repeat(3, n_layers).contiguous()   # [3][layer * E + e]
+    ws = torch.empty(L.qwm_moe_decode_workspace_size(layers, n_layers, T1), dtype=torch.uint8, device=dev)
+    qa.check(L.qwm_workspace_init(ws.data_ptr(), ws.numel(), stream))
+    n_all = args.warmup + args.steps
+    xs = torch.randn((n_all, T1, H), device=dev)
+    xw = torch.empty((T1, H), device=dev)
+    xt = qa.tensor(qa.TYPE_F32, H, T1, 1, xw)
+
+    def decode(st):
+        qa.check(L.qwm_moe_decode(layers, n_layers, tables.data_ptr(), n_layers * E, xt, ws.data_ptr(), ws.numel(), st))
+
+    def timed(replay):
+        for s in range(args.warmup):
+            xw.copy_(xs[s])
+            replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for s in range(args.warmup, n_all):
+            xw.copy_(xs[s])
+            replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / args.steps
+
+    ms_direct = timed(lambda: decode(torch.cuda.current_stream().cuda_stream))
+    graph = torch.cuda.CUDAGraph()
+    xw.copy_(xs[0])
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        decode(torch.cuda.current_stream().cuda_stream)
+    ms_graph = timed(graph.replay)
+    ms = min(ms_direct, ms_graph)
+    step_bytes = n_layers * (K_USED * 3 * SLAB + E * H * 4 + 2 * T1 * H * 4)
+    gbs = step_bytes / (ms * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "MoE decode tokens/s + achieved HBM GB/s (% of 8 TB/s), 48 stacked Q4_K blocks, 1xMI355X",
+        "value": T1 / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "1-token decode through 48 stacked Qwen3-30B-A3B-shape MoE blocks (H 2048, 128 experts "
+                               "resident per layer, FFN 768, top-8, Q4_K; attention omitted), new N(0,1) input per step",
+                   "graph": ms_graph <= ms_direct, "ms_direct": ms_direct, "ms_graph": ms_graph},
+        "roofline": {"bound": "hbm", "kernel": "whole step (48 x route + gate/up + down)", "achieved": gbs,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS, "traffic": None,
+                     "bytes_per_launch": step_bytes},
+    }))
 
 
 class StepArgs(ctypes.Structure):

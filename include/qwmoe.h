@@ -128,6 +128,18 @@ int qwm_moe_block_resident(const qwm_moe_layer * layer, int32_t layer_index, con
                            const qwm_tensor * resid, qwm_tensor * out, qwm_tensor * ids_out, qwm_tensor * w_out,
                            void * workspace, size_t ws_bytes, void * stream);
 
+/* Decode through stacked MoE blocks (the per-layer segment B of
+ * decode_cached, runtime.cpp:5064-5888, with every expert resident and the
+ * in-graph slot remap of 2759-2787): for l = 0 .. n_layers-1,
+ *   x = x + MoE_l(x)     (qwm_moe_block_resident with layer index l)
+ * x: f32 [H, T] in/out.  The layers share one shape.  slot_tables as for
+ * qwm_moe_block_resident, with table_stride >= n_layers * E.  Nothing waits
+ * for the host between layers; the call can be captured in a HIP graph (its
+ * only copy, for odd n_layers, is a device-to-device memcpy). */
+size_t qwm_moe_decode_workspace_size(const qwm_moe_layer * layers, int32_t n_layers, int64_t T);
+int qwm_moe_decode(const qwm_moe_layer * layers, int32_t n_layers, const int32_t * slot_tables, int64_t table_stride,
+                   qwm_tensor * x, void * workspace, size_t ws_bytes, void * stream);
+
 /* -------------------------------------------------- verify + acceptance --- */
 
 /* Verify head + greedy acceptance (runtime.cpp:5014-5046 and 3648-3652):

@@ -315,6 +315,59 @@ int qwm_moe_block_resident(const qwm_moe_layer * layer, int32_t layer_index, con
                       resid ? (const float *)resid->data : nullptr, (float *)out->data, ws, s);
 }
 
+// ------------------------------------------------------------ layer loop --
+
+// The decode loop over stacked MoE blocks (decode_cached's per-layer segment B,
+// runtime.cpp:5064-5888, in the resident form of 2759-2787 / 5792-5841): each
+// layer's block reads the previous layer's output as input and residual.  The
+// workspace holds one MoE workspace, reused by every layer in stream order,
+// and a ping-pong activation buffer.
+static int check_layers(const qwm_moe_layer * layers, int32_t n_layers, int64_t T, MoePlan & p) {
+    if (!layers || n_layers < 1) return fail(QWM_ERR_ARG, "moe_decode: no layers");
+    int rc = check_layer(&layers[0], T, p);
+    if (rc != QWM_OK) return rc;
+    for (int32_t l = 1; l < n_layers; ++l) {
+        MoePlan q;
+        if ((rc = check_layer(&layers[l], T, q)) != QWM_OK) return rc;
+        if (q.H != p.H || q.N != p.N || q.E != p.E || q.k != p.k || q.shared != p.shared || q.N_sh != p.N_sh)
+            return fail(QWM_ERR_ARG, "moe_decode: layers must share one shape");
+    }
+    return QWM_OK;
+}
+
+size_t qwm_moe_decode_workspace_size(const qwm_moe_layer * layers, int32_t n_layers, int64_t T) {
+    MoePlan p;
+    if (check_layers(layers, n_layers, T, p) != QWM_OK) return 0;
+    return align_up(p.total, 256) + align_up(sizeof(float) * (size_t)(T * p.H), 256);
+}
+
+int qwm_moe_decode(const qwm_moe_layer * layers, int32_t n_layers, const int32_t * slot_tables, int64_t table_stride,
+                   qwm_tensor * x, void * workspace, size_t ws_bytes, void * stream) {
+    if (!x) return fail(QWM_ERR_ARG, "moe_decode: x is NULL");
+    if (!slot_tables) return fail(QWM_ERR_ARG, "moe_decode: slot tables are NULL");
+    MoePlan p;
+    int rc = check_layers(layers, n_layers, x->ne[1], p);
+    if (rc != QWM_OK) return rc;
+    if ((rc = check_act(x, p.H, "x")) != QWM_OK) return rc;
+    if (table_stride < (int64_t)n_layers * p.E) return fail(QWM_ERR_ARG, "moe_decode: slot table stride too small");
+    const size_t need = align_up(p.total, 256) + align_up(sizeof(float) * (size_t)(p.T * p.H), 256);
+    if (!workspace || ws_bytes < need) return fail(QWM_ERR_WORKSPACE, "moe_decode: workspace too small");
+    uint8_t * ws = (uint8_t *)workspace;
+    qwm_tensor buf = *x;
+    buf.data = ws + align_up(p.total, 256);
+    hipStream_t s = (hipStream_t)stream;
+    for (int32_t l = 0; l < n_layers; ++l) {
+        qwm_tensor * src = (l & 1) ? &buf : x;
+        qwm_tensor * dst = (l & 1) ? x : &buf;
+        rc = qwm_moe_block_resident(&layers[l], l, slot_tables, table_stride, src, nullptr, src, dst, nullptr, nullptr,
+                                    ws, p.total, s);
+        if (rc != QWM_OK) return rc;
+    }
+    if (n_layers & 1)
+        QWM_HIP_CHECK(hipMemcpyAsync(x->data, buf.data, sizeof(float) * (size_t)(p.T * p.H), hipMemcpyDeviceToDevice, s));
+    return QWM_OK;
+}
+
 // -------------------------------------------------------------- fused step --
 
 size_t qwm_verify_step_workspace_size(const qwm_moe_layer * layer, const qwm_tensor * lm_head, int64_t T) {

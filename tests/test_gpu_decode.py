@@ -1,0 +1,81 @@
+"""GPU parity of the decode loop over stacked MoE blocks (qwm_moe_decode:
+x = x + MoE_l(x) for every layer, slots remapped on the device from per-layer
+tables) against the oracle applied layer by layer, and bit for bit against
+the same layers through qwm_moe_block_resident one call at a time."""
+import numpy as np
+import pytest
+
+from tests.moe_case import MoeCase, rel_err
+
+torch = pytest.importorskip("torch")
+import questwend_amd as qa  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    qa.lib()
+    return torch.device("cuda:0")
+
+
+def workspace(nbytes):
+    ws = torch.empty(max(256, (nbytes + 255) // 256 * 256), dtype=torch.uint8, device="cuda")
+    qa.check(qa.lib().qwm_workspace_init(ws.data_ptr(), ws.numel(), None))
+    return ws
+
+
+@pytest.mark.parametrize("T,n_layers,wtype", [(1, 4, "q4_K"), (4, 5, "q4_K"), (2, 3, "q8_0")])
+def test_decode_layers(dev, T, n_layers, wtype):
+    H, N, E, k = 512, 256, 16, 4
+    cases = [MoeCase(seed=100 + l, H=H, N=N, E=E, k=k, S=E, wtype=wtype) for l in range(n_layers)]
+    rng = np.random.default_rng(7)
+    perms = [rng.permutation(E).astype(np.int32) for _ in range(n_layers)]   # expert -> slot, per layer
+    tables = np.zeros((3, n_layers * E), np.int32)
+    for l in range(n_layers):
+        tables[:, l * E:(l + 1) * E] = perms[l]
+    layers = (qa.MoeLayer * n_layers)()
+    for l, c in enumerate(cases):
+        layers[l] = c.upload(torch)
+    x0 = rng.standard_normal((T, H)).astype(np.float32)
+
+    # oracle, layer by layer
+    x = x0.copy()
+    for l, c in enumerate(cases):
+        ids, w, _, _ = c.route(x)
+        x = c.block(x, perms[l][ids], w) + x
+    exp = x
+
+    dtab = torch.from_numpy(tables).cuda()
+    L = qa.lib()
+    dx = torch.from_numpy(x0).cuda()
+    ws = workspace(L.qwm_moe_decode_workspace_size(layers, n_layers, T))
+    qa.check(L.qwm_moe_decode(layers, n_layers, dtab.data_ptr(), n_layers * E, qa.tensor(qa.TYPE_F32, H, T, 1, dx),
+                              ws.data_ptr(), ws.numel(), None))
+    # the same layers one block at a time
+    wsb = workspace(L.qwm_moe_workspace_size(layers[0], T))
+    a = torch.from_numpy(x0).cuda()
+    for l in range(n_layers):
+        b = torch.zeros_like(a)
+        ta, tb = qa.tensor(qa.TYPE_F32, H, T, 1, a), qa.tensor(qa.TYPE_F32, H, T, 1, b)
+        qa.check(L.qwm_moe_block_resident(layers[l], l, dtab.data_ptr(), n_layers * E, ta, None, ta, tb, None, None,
+                                          wsb.data_ptr(), wsb.numel(), None))
+        a = b
+    torch.cuda.synchronize()
+    got = dx.cpu().numpy()
+    err = rel_err(got, exp)
+    print(f"decode T={T} layers={n_layers} {wtype}: rel err {err:.3e}")
+    assert err < TOL
+    assert np.array_equal(got.view(np.uint32), a.cpu().numpy().view(np.uint32)), "loop and per-block calls differ"
+
+
+def test_decode_rejects_mixed_shapes(dev):
+    a = MoeCase(seed=1, H=512, N=256, E=16, k=4, S=16)
+    b = MoeCase(seed=2, H=512, N=512, E=16, k=4, S=16)
+    layers = (qa.MoeLayer * 2)()
+    layers[0] = a.upload(torch)
+    layers[1] = b.upload(torch)
+    assert qa.lib().qwm_moe_decode_workspace_size(layers, 2, 1) == 0

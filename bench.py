@@ -33,6 +33,7 @@ Q4K_ROW_GU = H // 256 * 144          # 1152 B
 Q4K_ROW_D = N // 256 * 144           # 432 B
 SLAB = N * Q4K_ROW_GU                # 884,736 B per role per expert
 LM_ROW = H // 32 * 34                # 2176 B
+QK_K_ = 256
 CAL_BYTES = 256 << 20                # calibration copy for the PMC byte counters
 TRAFFIC_SUMMARY = {"step": os.path.join(ROOT, "profiles", "verify_step_T4_traffic.json"),
                    "ops": os.path.join(ROOT, "profiles", "verify_ops_T4_traffic.json")}
@@ -60,14 +61,15 @@ def parse():
     ap.add_argument("--accept-rate", type=float, default=0.7, help="probability that a draft equals the target")
     ap.add_argument("--path", choices=["step", "ops"], default="step",
                     help="step: the fused verify step (one launch); ops: qwm_moe_block_resident + qwm_verify_accept")
-    ap.add_argument("--workload", choices=["verify", "decode48"], default="verify",
+    ap.add_argument("--workload", choices=["verify", "decode48", "prefill"], default="verify",
                     help="verify: the metric's MTP verify step; decode48: 1-token decode through 48 stacked "
-                         "MoE blocks (qwm_moe_decode, HIP graph)")
+                         "MoE blocks (qwm_moe_decode, HIP graph); prefill: 512 tokens through one "
+                         "Qwen3-Next-shape layer's MUL_MAT_IDs (expert-grouped MFMA GEMM)")
     args = ap.parse_args()
     if args.steps is None:
-        args.steps = 256 if args.workload == "decode48" else 200
+        args.steps = {"decode48": 256, "prefill": 50}.get(args.workload, 200)
     if args.warmup is None:
-        args.warmup = 10 if args.workload == "decode48" else 20
+        args.warmup = {"decode48": 10, "prefill": 5}.get(args.workload, 20)
     return args
 
 
@@ -82,6 +84,9 @@ def main():
 
     if args.workload == "decode48":
         bench_decode(args, torch, qa)
+        return
+    if args.workload == "prefill":
+        bench_prefill(args, torch, qa)
         return
     L = qa.lib()
     dev = torch.device("cuda:0")
@@ -313,6 +318,88 @@ def bench_decode(args, torch, qa, n_layers=48):
         "roofline": {"bound": "hbm", "kernel": "whole step (48 x route + gate/up + down)", "achieved": gbs,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS, "traffic": None,
                      "bytes_per_launch": step_bytes},
+    }))
+
+
+def bench_prefill(args, torch, qa, T_pf=512, E_pf=512, k_pf=10, N_pf=512):
+    """A 512-token prefill chunk through one Qwen3-Next-shape MoE layer's
+    expert GEMMs (hidden 2048, 512 experts, FFN 512, top-10, Q4_K from
+    N(0, 0.02)): up = mul_mat_id(up, x, ids), gate = mul_mat_id(gate, x, ids),
+    down = mul_mat_id(down, act, ids) with act = silu(gate) * up between
+    them.  ids are each token's top-10 of random router logits.  The timed
+    step is the three GGML_OP_MUL_MAT_ID calls (qwm_mul_mat_id, columns
+    grouped by expert on int8 MFMA)."""
+    L = qa.lib()
+    dev = torch.device("cuda:0")
+    torch.manual_seed(args.seed)
+    stream = torch.cuda.current_stream().cuda_stream
+    slab = N_pf * H // QK_K_ * 144
+    pools = [torch.empty(E_pf * slab, dtype=torch.uint8, device=dev) for _ in range(3)]
+    tmp = torch.empty(N_pf * H, dtype=torch.float32, device=dev)
+    for r in range(3):
+        for e in range(E_pf):
+            tmp.normal_(0.0, 0.02)
+            qa.check(L.qwm_quantize(qa.TYPE_Q4_K, tmp.data_ptr(), pools[r].data_ptr() + e * slab, N_pf * H, stream))
+    del tmp
+    x = torch.randn((T_pf, 1, H), device=dev)
+    ids = torch.topk(torch.randn((T_pf, E_pf), device=dev), k_pf, dim=1).indices.to(torch.int32).contiguous()
+    gate = torch.empty((T_pf, k_pf, N_pf), device=dev)
+    up = torch.empty_like(gate)
+    act = torch.empty_like(gate)
+    down = torch.empty((T_pf, k_pf, H), device=dev)
+    t_g = qa.tensor(qa.TYPE_Q4_K, H, N_pf, E_pf, pools[0])
+    t_u = qa.tensor(qa.TYPE_Q4_K, H, N_pf, E_pf, pools[1])
+    t_d = qa.tensor(qa.TYPE_Q4_K, N_pf, H, E_pf, pools[2])
+    t_x = qa.tensor(qa.TYPE_F32, H, 1, T_pf, x)
+    t_ids = qa.tensor(qa.TYPE_I32, k_pf, T_pf, 1, ids)
+    t_act = qa.tensor(qa.TYPE_F32, N_pf, k_pf, T_pf, act)
+    need = max(L.qwm_mul_mat_id_workspace_size(t_g, t_x, t_ids), L.qwm_mul_mat_id_workspace_size(t_d, t_act, t_ids))
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    qa.check(L.qwm_workspace_init(ws.data_ptr(), ws.numel(), stream))
+
+    def gemm(t_as, t_b, out, st):
+        qa.check(L.qwm_mul_mat_id(t_as, t_b, t_ids, qa.tensor(qa.TYPE_F32, out.shape[2], k_pf, T_pf, out),
+                                  ws.data_ptr(), ws.numel(), st))
+
+    def step():
+        st = torch.cuda.current_stream().cuda_stream
+        gemm(t_u, t_x, up, st)
+        gemm(t_g, t_x, gate, st)
+        torch.mul(torch.nn.functional.silu(gate), up, out=act)
+        gemm(t_d, t_act, down, st)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    qa.check(L.qwm_profile_start(b"prefill_gemm", 3 * args.steps))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    g_ms = np.zeros(3 * args.steps, np.float32)
+    n_g = L.qwm_profile_stop(g_ms.ctypes.data, 3 * args.steps)
+    g_ms = g_ms[:n_g].reshape(-1, 3) if n_g == 3 * args.steps else None
+    used = len(np.unique(ids.cpu().numpy()))
+    w_bytes = 3 * used * slab
+    flops = 2.0 * T_pf * k_pf * (2 * N_pf * H + H * N_pf)
+    gemm_ms = float(g_ms.sum(1).mean()) if g_ms is not None else ms
+    gbs = (w_bytes + 4 * T_pf * H + 3 * 4 * T_pf * k_pf * N_pf + 4 * T_pf * k_pf * H) / (gemm_ms * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "MoE prefill tokens/s (expert GEMMs of one Qwen3-Next-shape layer), 1xMI355X",
+        "value": T_pf / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "512-token prefill chunk, one Qwen3-Next-shape MoE layer (H 2048, 512 experts, FFN 512, "
+                               "top-10, Q4_K): gate/up/down MUL_MAT_ID as expert-grouped int8 MFMA GEMMs",
+                   "experts_used": used, "gemm_ms_per_step": gemm_ms,
+                   "gemm_ms_each": g_ms.mean(0).tolist() if g_ms is not None else None},
+        "roofline": {"bound": "hbm", "kernel": "k_pf_gemm (3 launches per step)", "achieved": gbs, "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS, "traffic": None, "bytes_per_launch": w_bytes / 3},
+        "mfma": {"tops": flops / (gemm_ms * 1e-3) / 1e12, "peak_int8_tops": 5000.0,
+                 "frac": flops / (gemm_ms * 1e-3) / 5e15},
     }))
 
 

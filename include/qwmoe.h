@@ -16,6 +16,9 @@
  *  - The library allocates no device memory on the hot path.  Scratch comes
  *    from a caller-owned workspace sized by qwm_*_workspace_size() and zeroed
  *    once with qwm_workspace_init() (it keeps self-resetting counters).
+ *    The counters' places depend on the call's shape: before a workspace
+ *    serves calls of another shape (T, layer shape), initialize it again.
+ *    (qwm_mul_mat_id keeps no state between calls.)
  *  - Work is enqueued on the given hipStream_t (passed as void*); calls are
  *    asynchronous unless stated otherwise.  Calls that share a workspace must
  *    be ordered on one stream.

@@ -138,8 +138,14 @@ static int check_mmid(const qwm_tensor * as, const qwm_tensor * b, const qwm_ten
     if (!fully_contiguous(as)) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: as must be contiguous");
     if (b->nb[0] != 4 || ids->nb[0] != 4) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: b/ids must have unit element stride");
     if ((b->nb[1] | b->nb[2]) % 16) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: b rows must be 16-byte aligned");
-    if (b->ne[2] > MAX_T) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: more than 8 columns (prefill) is not handled here");
-    if (ids->ne[0] * ids->ne[1] > MAX_PAIRS) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: too many (expert, column) pairs");
+    if (b->ne[2] > MAX_T) {                     // prefill: the grouped GEMM (qwm_prefill.hip)
+        std::string why;
+        if (as->type != T_Q4_K) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: prefill batches need Q4_K weights");
+        if (!prefill_supported(as->ne[0], as->ne[1], as->ne[2], why)) return fail(QWM_ERR_UNSUPPORTED, why);
+        if (ids->ne[0] * ids->ne[1] > (1 << 22)) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: too many (expert, column) pairs");
+    } else if (ids->ne[0] * ids->ne[1] > MAX_PAIRS) {
+        return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: too many (expert, column) pairs");
+    }
     if (as->ne[0] > 2048) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: K > 2048");
     if (as->type == T_Q8_0 && as->ne[0] % 256) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: Q8_0 needs K a multiple of 256");
     if (dst) {
@@ -152,6 +158,7 @@ static int check_mmid(const qwm_tensor * as, const qwm_tensor * b, const qwm_ten
 
 size_t qwm_mul_mat_id_workspace_size(const qwm_tensor * as, const qwm_tensor * b, const qwm_tensor * ids) {
     if (check_mmid(as, b, ids, nullptr) != QWM_OK) return 0;
+    if (b->ne[2] > MAX_T) return prefill_workspace(as->ne[0], as->ne[1], as->ne[2], b->ne[2], b->ne[1], ids->ne[0]);
     return mmid_workspace(as->ne[0], b->ne[2], b->ne[1], ids->ne[0]);
 }
 
@@ -160,7 +167,9 @@ int qwm_mul_mat_id(const qwm_tensor * as, const qwm_tensor * b, const qwm_tensor
     int rc = check_mmid(as, b, ids, dst);
     if (rc != QWM_OK) return rc;
     if (!dst) return fail(QWM_ERR_ARG, "mul_mat_id: dst is NULL");
-    const size_t need = mmid_workspace(as->ne[0], b->ne[2], b->ne[1], ids->ne[0]);
+    const bool prefill = b->ne[2] > MAX_T;
+    const size_t need = prefill ? prefill_workspace(as->ne[0], as->ne[1], as->ne[2], b->ne[2], b->ne[1], ids->ne[0])
+                                : mmid_workspace(as->ne[0], b->ne[2], b->ne[1], ids->ne[0]);
     if (!workspace || ws_bytes < need) return fail(QWM_ERR_WORKSPACE, "mul_mat_id: workspace too small");
     MmidArgs a;
     a.wtype = as->type; a.as = (const uint8_t *)as->data; a.slab = as->nb[2];
@@ -170,6 +179,7 @@ int qwm_mul_mat_id(const qwm_tensor * as, const qwm_tensor * b, const qwm_tensor
     a.b_nb1 = b->nb[1]; a.b_nb2 = b->nb[2]; a.ids_nb1 = ids->nb[1];
     a.dst_nb1 = dst->nb[1]; a.dst_nb2 = dst->nb[2];
     a.dst = (float *)dst->data;
+    if (prefill) return launch_prefill(a, (uint8_t *)workspace, (hipStream_t)stream);
     return launch_mmid(a, (uint8_t *)workspace, (hipStream_t)stream);
 }
 

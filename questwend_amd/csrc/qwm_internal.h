@@ -89,6 +89,10 @@ struct MmidArgs {
 };
 size_t mmid_workspace(int64_t K, int64_t T, int64_t ne11, int64_t n_ids);
 int launch_mmid(const MmidArgs & a, uint8_t * ws, hipStream_t s);
+// prefill-sized batches (T > MAX_T), qwm_prefill.hip
+size_t prefill_workspace(int64_t K, int64_t N, int64_t n_as, int64_t T, int64_t ne11, int64_t n_ids);
+bool prefill_supported(int64_t K, int64_t N, int64_t n_as, std::string & why);
+int launch_prefill(const MmidArgs & a, uint8_t * ws, hipStream_t s);
 
 // ---- the fused verify step (qwm_step.hip) ----
 struct StepPlan {

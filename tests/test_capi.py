@@ -47,8 +47,14 @@ def test_argument_validation_without_gpu():
     ids_bad = qa.tensor(qa.TYPE_I32, 3, 2, 1)   # ids->ne[1] != b->ne[2]
     assert L.qwm_mul_mat_id(a, b, ids_bad, None, None, 0, None) == qa.ERR_ARG
     assert L.qwm_mul_mat_id(a, b, ids, qa.tensor(qa.TYPE_F32, 4, 2, 1), None, 0, None) == qa.ERR_WORKSPACE
-    wide = qa.tensor(qa.TYPE_F32, 256, 1, 9)    # 9 columns: prefill path, not the GEMV
+    wide = qa.tensor(qa.TYPE_F32, 256, 1, 9)    # 9 columns: the prefill GEMM, which needs N % 64 == 0
     assert L.qwm_mul_mat_id(a, wide, qa.tensor(qa.TYPE_I32, 2, 9, 1), None, None, 0, None) == qa.ERR_UNSUPPORTED
+    a64 = qa.tensor(qa.TYPE_Q4_K, 2048, 512, 8)
+    b64 = qa.tensor(qa.TYPE_F32, 2048, 1, 64)
+    i64 = qa.tensor(qa.TYPE_I32, 4, 64, 1)
+    assert L.qwm_mul_mat_id_workspace_size(a64, b64, i64) > 0
+    assert L.qwm_mul_mat_id(a64, b64, i64, qa.tensor(qa.TYPE_F32, 512, 4, 64), None, 0, None) == qa.ERR_WORKSPACE
+    assert L.qwm_mul_mat_id_workspace_size(qa.tensor(qa.TYPE_Q8_0, 2048, 512, 8), b64, i64) == 0   # Q4_K only
     lay = qa.MoeLayer()
     lay.router = qa.tensor(qa.TYPE_F32, 2048, 128)
     lay.gate_pool = qa.tensor(qa.TYPE_Q4_K, 2048, 768, 4)

@@ -61,15 +61,20 @@ def parse():
     ap.add_argument("--accept-rate", type=float, default=0.7, help="probability that a draft equals the target")
     ap.add_argument("--path", choices=["step", "ops"], default="step",
                     help="step: the fused verify step (one launch); ops: qwm_moe_block_resident + qwm_verify_accept")
-    ap.add_argument("--workload", choices=["verify", "decode48", "prefill"], default="verify",
+    ap.add_argument("--workload", choices=["verify", "decode48", "prefill", "missfill"], default="verify",
                     help="verify: the metric's MTP verify step; decode48: 1-token decode through 48 stacked "
                          "MoE blocks (qwm_moe_decode, HIP graph); prefill: 512 tokens through one "
-                         "Qwen3-Next-shape layer's MUL_MAT_IDs (expert-grouped MFMA GEMM)")
+                         "Qwen3-Next-shape layer's MUL_MAT_IDs (expert-grouped MFMA GEMM); missfill: T=4 verify "
+                         "batches through one Qwen3-Next-shape layer with a 128-slot LRU pool, misses copied "
+                         "from pinned host memory")
+    ap.add_argument("--popularity", choices=["sampled", "offset"], default="sampled",
+                    help="missfill: sampled = each token's top-10 drawn from Zipf(1.1) and forced through the route "
+                         "mask; offset = a fixed log-popularity logit offset (nearly every lookup then hits)")
     args = ap.parse_args()
     if args.steps is None:
-        args.steps = {"decode48": 256, "prefill": 50}.get(args.workload, 200)
+        args.steps = {"decode48": 256, "prefill": 50, "missfill": 400}.get(args.workload, 200)
     if args.warmup is None:
-        args.warmup = {"decode48": 10, "prefill": 5}.get(args.workload, 20)
+        args.warmup = {"decode48": 10, "prefill": 5, "missfill": 200}.get(args.workload, 20)
     return args
 
 
@@ -87,6 +92,9 @@ def main():
         return
     if args.workload == "prefill":
         bench_prefill(args, torch, qa)
+        return
+    if args.workload == "missfill":
+        bench_missfill(args, torch, qa)
         return
     L = qa.lib()
     dev = torch.device("cuda:0")
@@ -400,6 +408,183 @@ def bench_prefill(args, torch, qa, T_pf=512, E_pf=512, k_pf=10, N_pf=512):
                      "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS, "traffic": None, "bytes_per_launch": w_bytes / 3},
         "mfma": {"tops": flops / (gemm_ms * 1e-3) / 1e12, "peak_int8_tops": 5000.0,
                  "frac": flops / (gemm_ms * 1e-3) / 5e15},
+    }))
+
+
+def bench_missfill(args, torch, qa, E_n=512, N_n=512, k_n=10, S_n=128, skew=1.1):
+    """MTP verify batches (T = 4, new N(0, 1) inputs each step) through one
+    Qwen3-Next-shape MoE layer (hidden 2048, 512 experts + a shared expert,
+    FFN 512, top-10, Q4_K from N(0, 0.02)) whose experts live in pinned host
+    memory, with a GPU slot pool of 128 experts per role.  Zipf(1.1)
+    popularity over a seeded expert permutation enters through the route
+    mask: "sampled" (default) draws each token's 10 experts from Zipf(1.1)
+    and forces them with a +16 mask bias (the routing weights stay the
+    softmax of their own logits); "offset" adds fixed offsets log(p_e), under
+    which the router keeps choosing about the same 110 experts and the pool
+    nearly never misses.  A step is the reference's cached path: route on the
+    device, the ids read back (synchronous), the pool's LRU decisions on the
+    host with misses copied by hipMemcpyAsync on a side stream, the slot ids
+    uploaded, the compute stream waiting for the copies, then the experts on
+    slot ids.  Warmup steps bring the pool to its steady state before
+    timing."""
+    L = qa.lib()
+    dev = torch.device("cuda:0")
+    torch.manual_seed(args.seed)
+    stream = torch.cuda.current_stream().cuda_stream
+    slab = N_n * H // QK_K_ * 144
+    host = []
+    tmp = torch.empty(N_n * H, dtype=torch.float32, device=dev)
+    stage = torch.empty(E_n * slab, dtype=torch.uint8, device=dev)
+    for r in range(3):
+        for e in range(E_n):
+            tmp.normal_(0.0, 0.02)
+            qa.check(L.qwm_quantize(qa.TYPE_Q4_K, tmp.data_ptr(), stage.data_ptr() + e * slab, N_n * H, stream))
+        hr = torch.empty(E_n * slab, dtype=torch.uint8, pin_memory=True)
+        hr.copy_(stage)
+        host.append(hr)
+    sh = []
+    for r in range(3):
+        q = torch.empty(slab, dtype=torch.uint8, device=dev)
+        tmp.normal_(0.0, 0.02)
+        qa.check(L.qwm_quantize(qa.TYPE_Q4_K, tmp.data_ptr(), q.data_ptr(), N_n * H, stream))
+        sh.append(q)
+    del tmp, stage
+    router = (torch.randn((E_n, H), device=dev) * 0.02).contiguous()
+    sh_inp = (torch.randn(H, device=dev) * 0.02).contiguous()
+    pools = [torch.empty(S_n * slab, dtype=torch.uint8, device=dev) for _ in range(3)]
+    lay = qa.MoeLayer()
+    lay.gate_pool = qa.tensor(qa.TYPE_Q4_K, H, N_n, S_n, pools[0])
+    lay.up_pool = qa.tensor(qa.TYPE_Q4_K, H, N_n, S_n, pools[1])
+    lay.down_pool = qa.tensor(qa.TYPE_Q4_K, N_n, H, S_n, pools[2])
+    lay.router = qa.tensor(qa.TYPE_F32, H, E_n, 1, router)
+    lay.sh_gate = qa.tensor(qa.TYPE_Q4_K, H, N_n, 1, sh[0])
+    lay.sh_up = qa.tensor(qa.TYPE_Q4_K, H, N_n, 1, sh[1])
+    lay.sh_down = qa.tensor(qa.TYPE_Q4_K, N_n, H, 1, sh[2])
+    lay.sh_gate_inp = qa.tensor(qa.TYPE_F32, H, 1, 1, sh_inp)
+    lay.n_expert_used, lay.norm_weights, lay.weights_scale = k_n, 1, 1.0
+
+    n_all = args.warmup + args.steps
+    mrng = np.random.default_rng(args.seed)
+    perm = mrng.permutation(E_n)
+    if args.popularity == "offset":
+        rank = np.empty(E_n, np.float64)
+        rank[perm] = np.arange(1, E_n + 1)
+        rm = torch.from_numpy(np.tile((-skew * np.log(rank)).astype(np.float32), (n_all, T, 1))).to(dev)
+    else:
+        p = 1.0 / np.arange(1, E_n + 1) ** skew
+        p /= p.sum()
+        m = np.zeros((n_all, T, E_n), np.float32)
+        for s in range(n_all):
+            for t in range(T):
+                m[s, t, perm[mrng.choice(E_n, k_n, replace=False, p=p)]] = 16.0
+        rm = torch.from_numpy(m).to(dev)
+    copy = torch.cuda.Stream()
+    host_ptrs = [(ctypes.c_void_p * 1)(host[r].data_ptr()) for r in range(3)]
+    d = qa.PoolDesc()
+    d.n_layer, d.n_expert = 1, E_n
+    for r in range(3):
+        d.n_slots[r] = S_n
+        d.pool_data[r] = pools[r].data_ptr()
+        d.slab_bytes[r] = slab
+        d.host_slabs[r] = ctypes.cast(host_ptrs[r], ctypes.c_void_p)
+    pool = ctypes.c_void_p()
+    qa.check(L.qwm_pool_create(ctypes.byref(d), ctypes.c_void_p(copy.cuda_stream), ctypes.byref(pool)))
+
+    xs = torch.randn((n_all, T, H), device=dev)
+    ws = torch.empty(L.qwm_moe_workspace_size(lay, T), dtype=torch.uint8, device=dev)
+    qa.check(L.qwm_workspace_init(ws.data_ptr(), ws.numel(), stream))
+    gids = torch.empty((T, k_n), dtype=torch.int32, device=dev)
+    gw = torch.empty((T, k_n), dtype=torch.float32, device=dev)
+    hid = torch.empty(T * k_n, dtype=torch.int32, pin_memory=True)
+    hsl = torch.empty((3, T * k_n), dtype=torch.int32, pin_memory=True)
+    dsl = torch.empty((3, T * k_n), dtype=torch.int32, device=dev)
+    out = torch.empty((T, H), device=dev)
+    t_rms = [qa.tensor(qa.TYPE_F32, E_n, T, 1, rm[s]) for s in range(n_all)]
+    t_ids, t_w = qa.tensor(qa.TYPE_I32, k_n, T, 1, gids), qa.tensor(qa.TYPE_F32, k_n, T, 1, gw)
+    t_sl = [qa.tensor(qa.TYPE_I32, k_n, T, 1, dsl[r]) for r in range(3)]
+    t_out = qa.tensor(qa.TYPE_F32, H, T, 1, out)
+    t_xs = [qa.tensor(qa.TYPE_F32, H, T, 1, xs[s]) for s in range(n_all)]
+    cur = torch.cuda.current_stream()
+    n_ids = T * k_n
+    hs = [hsl[r].data_ptr() for r in range(3)]
+
+    def step(s, ev=None, unions=None):
+        if ev is not None:
+            ev[0].record(cur)
+        qa.check(L.qwm_moe_route(lay, t_xs[s], t_rms[s], t_ids, t_w, ws.data_ptr(), ws.numel(), stream))
+        if ev is not None:
+            ev[1].record(cur)
+        hid.copy_(gids.view(-1), non_blocking=True)
+        cur.synchronize()
+        if unions is not None:
+            unions.append(len(np.unique(hid.numpy())))
+        if ev is not None:
+            ev[2].record(copy)
+        qa.check(L.qwm_pool_ensure(pool, 0, hid.data_ptr(), n_ids, hs[0], hs[1], hs[2]))
+        if ev is not None:
+            ev[3].record(copy)
+        dsl.copy_(hsl, non_blocking=True)
+        qa.check(L.qwm_pool_wait(pool, stream))
+        if ev is not None:
+            ev[4].record(cur)
+        qa.check(L.qwm_moe_experts(lay, t_xs[s], t_sl[0], t_sl[1], t_sl[2], t_w, None, t_out, ws.data_ptr(),
+                                   ws.numel(), stream))
+        if ev is not None:
+            ev[5].record(cur)
+
+    for s in range(args.warmup):
+        step(s)
+    torch.cuda.synchronize()
+    st0 = qa.PoolStats()
+    qa.check(L.qwm_pool_get_stats(pool, ctypes.byref(st0)))
+    # timed run: whole-loop events only
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for s in range(args.warmup, n_all):
+        step(s)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    st1 = qa.PoolStats()
+    qa.check(L.qwm_pool_get_stats(pool, ctypes.byref(st1)))
+    # breakdown run over the same inputs again (the pool keeps evolving)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(args.steps)]
+    unions = []
+    for i, s in enumerate(range(args.warmup, n_all)):
+        step(s, evs[i], unions)
+    torch.cuda.synchronize()
+    rt = np.array([[ev[0].elapsed_time(ev[1]), ev[1].elapsed_time(ev[2]), ev[2].elapsed_time(ev[3]),
+                    ev[3].elapsed_time(ev[4]), ev[4].elapsed_time(ev[5])] for ev in evs])
+    L.qwm_pool_destroy(pool)
+    lookups = (st1.hits + st1.misses) - (st0.hits + st0.misses)
+    misses = st1.misses - st0.misses
+    miss_bytes = (st1.fetch_bytes - st0.fetch_bytes) / args.steps
+    union = float(np.mean(unions))
+    kern_ms = float(np.median(rt[:, 0]) + np.median(rt[:, 4]))
+    step_bytes = 3 * slab * union + E_n * H * 4 + 3 * slab + 2 * T * H * 4
+    gbs = step_bytes / (kern_ms * 1e-3) / 1e9
+    copy_ms = rt[:, 2] + rt[:, 3]
+    busy = copy_ms > 0.02
+    link = (miss_bytes * args.steps) / max(float(copy_ms.sum()) * 1e-3, 1e-9) / 1e9
+    print(json.dumps({
+        "metric": "MoE verify tokens/s with LRU slot-pool miss fills, one Qwen3-Next-shape layer, 1xMI355X",
+        "value": T / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "MTP verify T=4 through one Qwen3-Next-shape MoE layer (H 2048, 512 experts + shared, "
+                               "FFN 512, top-10, Q4_K) with a 128-slot LRU pool per role, experts in pinned host "
+                               "memory, Zipf(1.1) popularity through the route mask",
+                   "pool_slots": S_n, "skew": skew, "popularity": args.popularity, "distinct_experts_per_step": union},
+        "pool": {"hit_rate": 1.0 - misses / max(lookups, 1), "misses_per_step": misses / args.steps / 3,
+                 "miss_bytes_per_step": miss_bytes, "evictions": int(st1.evictions - st0.evictions)},
+        "breakdown_ms_median": {"route": float(np.median(rt[:, 0])), "ids_readback": float(np.median(rt[:, 1])),
+                                "ensure_and_copies": float(np.median(rt[:, 2])),
+                                "copies_to_experts_start": float(np.median(rt[:, 3])),
+                                "experts": float(np.median(rt[:, 4]))},
+        "host_link": {"achieved_GBs": link, "steps_with_copies": int(busy.sum()), "peak_GBs": 64.0},
+        "roofline": {"bound": "hbm", "kernel": "route + experts (selected slabs, router, shared expert)",
+                     "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
+                     "traffic": None, "bytes_per_launch": step_bytes},
     }))
 
 

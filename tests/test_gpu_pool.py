@@ -1,0 +1,178 @@
+"""GPU miss fill through the slot pool: the cached decode loop of the
+reference (route on the device, ids read back, ExpertCache::ensure on the
+host, misses copied into pool slots from pinned host slabs, then the experts
+run on slot ids), checked step by step against the oracle: the routed ids
+bit-exact, the slot sequences of every role bit-exact against the oracle
+pool, the copied slabs byte-identical to their host sources, and the MoE
+block's output within 1e-3 of the oracle block over the full expert table.
+Two layers share one pool per role, each token's experts are Zipf(1.1)
+draws forced through the route mask, and the pool holds fewer slots than a
+layer has experts (but more than one step selects), so misses evict experts
+of both layers."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from tests.helpers import bits, oracle, ptr
+from tests.moe_case import MoeCase, rel_err
+
+torch = pytest.importorskip("torch")
+import questwend_amd as qa  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    qa.lib()
+    return torch.device("cuda:0")
+
+
+def workspace(nbytes):
+    ws = torch.empty(max(256, (nbytes + 255) // 256 * 256), dtype=torch.uint8, device="cuda")
+    qa.check(qa.lib().qwm_workspace_init(ws.data_ptr(), ws.numel(), None))
+    return ws
+
+
+def pinned(a):
+    t = torch.empty(a.nbytes, dtype=torch.uint8, pin_memory=True)
+    t.numpy()[:] = np.ascontiguousarray(a).view(np.uint8).ravel()
+    return t
+
+
+def zipf_mask(rng, perm, k, T, skew=1.1, bias=16.0):
+    """Route mask that makes each token select k experts drawn without
+    replacement from Zipf(skew) popularity over the permutation `perm`: +bias
+    on the drawn experts' logits (the routing weights stay the softmax of
+    their own logits, the bias cancels in the normalization)."""
+    E = perm.size
+    p = 1.0 / np.arange(1, E + 1) ** skew
+    p /= p.sum()
+    m = np.zeros((T, E), np.float32)
+    for t in range(T):
+        m[t, perm[rng.choice(E, k, replace=False, p=p)]] = bias
+    return m
+
+
+@pytest.mark.parametrize("wtype,protect,indexed", [("q4_K", 0, 0), ("q4_K", 1, 1), ("q8_0", 0, 1)])
+def test_pool_miss_fill_decode(dev, wtype, protect, indexed):
+    H, N, E, k, T, S, n_layer, steps = 512, 256, 64, 4, 4, 20, 2, 24
+    cases = [MoeCase(seed=40 + l, H=H, N=N, E=E, k=k, S=E, shared=True, N_sh=N, wtype=wtype) for l in range(n_layer)]
+    rng = np.random.default_rng(9)
+    perms = [rng.permutation(E) for _ in range(n_layer)]
+    L = qa.lib()
+    slab = [c.gate_q.nbytes // E for c in cases[:1]][0]
+    assert cases[0].down_q.nbytes // E == slab
+
+    # device pools of S slots per role, shared by both layers
+    pool_t = [torch.full((S * slab,), 0xA5, dtype=torch.uint8, device="cuda") for _ in range(3)]
+    host = [[pinned(c.gate_q), pinned(c.up_q), pinned(c.down_q)] for c in cases]   # [layer][role]
+    host_ptrs = [(ctypes.c_void_p * n_layer)(*[host[l][r].data_ptr() for l in range(n_layer)]) for r in range(3)]
+    d = qa.PoolDesc()
+    d.n_layer, d.n_expert = n_layer, E
+    for r in range(3):
+        d.n_slots[r] = S
+        d.pool_data[r] = pool_t[r].data_ptr()
+        d.slab_bytes[r] = slab
+        d.host_slabs[r] = ctypes.cast(host_ptrs[r], ctypes.c_void_p)
+    d.protect_active, d.indexed = protect, indexed
+    copy = torch.cuda.Stream()
+    h = ctypes.c_void_p()
+    qa.check(L.qwm_pool_create(ctypes.byref(d), ctypes.c_void_p(copy.cuda_stream), ctypes.byref(h)))
+    o = oracle().qwo_pool_new(n_layer, E, ptr(np.array([S, S, S], np.int32)), protect)
+
+    layers = []
+    for c in cases:
+        c.upload(torch)
+        lay = c.layer
+        lay.gate_pool = qa.tensor(c.qa_type, H, N, S, pool_t[0])
+        lay.up_pool = qa.tensor(c.qa_type, H, N, S, pool_t[1])
+        lay.down_pool = qa.tensor(c.qa_type, N, H, S, pool_t[2])
+        layers.append(lay)
+    ws = workspace(L.qwm_moe_workspace_size(layers[0], T))
+    n_miss = 0
+    try:
+        for step in range(steps):
+            l = step % n_layer
+            c, lay = cases[l], layers[l]
+            x = rng.standard_normal((T, H)).astype(np.float32)
+            mask = zipf_mask(rng, perms[l], k, T)
+            ids, w, _, _ = c.route(x, mask)
+            dx = torch.from_numpy(x).cuda()
+            drm = torch.from_numpy(mask).cuda()
+            gids = torch.zeros((T, k), dtype=torch.int32, device="cuda")
+            gw = torch.zeros((T, k), dtype=torch.float32, device="cuda")
+            xt = qa.tensor(qa.TYPE_F32, H, T, 1, dx)
+            qa.check(L.qwm_moe_route(lay, xt, qa.tensor(qa.TYPE_F32, E, T, 1, drm), qa.tensor(qa.TYPE_I32, k, T, 1, gids),
+                                     qa.tensor(qa.TYPE_F32, k, T, 1, gw), ws.data_ptr(), ws.numel(), None))
+            hids = gids.cpu().numpy()          # the reference's D2H read of the ids (synchronous)
+            assert np.array_equal(hids, ids), f"step {step}: routed ids differ"
+            assert np.array_equal(bits(gw.cpu().numpy()), bits(w))
+
+            flat = np.ascontiguousarray(hids.ravel())
+            sl = np.zeros((3, flat.size), np.int32)
+            qa.check(L.qwm_pool_ensure(h, l, ptr(flat), flat.size, ptr(sl[0]), ptr(sl[1]), ptr(sl[2])))
+            so = np.zeros((3, flat.size), np.int32)
+            nf = ctypes.c_int()
+            assert oracle().qwo_pool_ensure(o, l, ptr(flat), flat.size, ptr(so[0]), ptr(so[1]), ptr(so[2]),
+                                            None, ctypes.byref(nf)) == 0
+            assert np.array_equal(sl, so), f"step {step}: slot sequences differ"
+
+            dsl = torch.from_numpy(sl).cuda()
+            qa.check(L.qwm_pool_wait(h, None))
+            out = torch.full((T, H), float("nan"), dtype=torch.float32, device="cuda")
+            st = [qa.tensor(qa.TYPE_I32, k, T, 1, dsl[r]) for r in range(3)]
+            qa.check(L.qwm_moe_experts(lay, xt, st[0], st[1], st[2], qa.tensor(qa.TYPE_F32, k, T, 1, gw), None,
+                                       qa.tensor(qa.TYPE_F32, H, T, 1, out), ws.data_ptr(), ws.numel(), None))
+            exp = c.block(x, ids, w)           # every expert resident: slot = expert id
+            got = out.cpu().numpy()
+            err = rel_err(got, exp)
+            assert np.isfinite(got).all() and err < TOL, f"step {step}: rel err {err:.3e}"
+        torch.cuda.synchronize()
+
+        # every occupied slot holds its key's host slab, byte for byte
+        for r in range(3):
+            keys = np.zeros(S, np.int32)
+            qa.check(L.qwm_pool_slots(h, r, ptr(keys), None))
+            dev_bytes = pool_t[r].cpu().numpy().reshape(S, slab)
+            for s, key in enumerate(keys):
+                if key < 0:
+                    continue
+                lyr, e = divmod(int(key), E)
+                src = host[lyr][r].numpy().reshape(E, slab)[e]
+                assert np.array_equal(dev_bytes[s], src), f"role {r} slot {s} key {key}"
+        stt = qa.PoolStats()
+        qa.check(L.qwm_pool_get_stats(h, ctypes.byref(stt)))
+        hmo = np.zeros(3, np.uint64)
+        oracle().qwo_pool_stats(o, ptr(hmo))
+        assert (stt.hits, stt.misses, stt.evictions) == tuple(int(v) for v in hmo)
+        assert stt.fetches == stt.misses and stt.fetch_bytes == stt.misses * slab
+        n_miss = stt.misses
+        print(f"pool {wtype} protect={protect} indexed={indexed}: hits {stt.hits} misses {stt.misses} "
+              f"evictions {stt.evictions}")
+        assert stt.evictions > 0, "the trace should overflow the pool"
+    finally:
+        L.qwm_pool_destroy(h)
+        oracle().qwo_pool_free(o)
+    assert n_miss > 0
+
+
+def test_slab_fetch_async_event(dev):
+    """One slab copy on a side stream, ordered by its done event."""
+    L = qa.lib()
+    slab, S = 589824, 3
+    src = pinned(np.random.default_rng(2).integers(0, 256, slab, dtype=np.uint8))
+    pool = torch.zeros(S * slab, dtype=torch.uint8, device="cuda")
+    copy = torch.cuda.Stream()
+    ev = torch.cuda.Event()
+    ev.record(copy)                       # creates the event
+    qa.check(L.qwm_slab_fetch_async(ctypes.c_void_p(pool.data_ptr()), slab, 2, ctypes.c_void_p(src.data_ptr()),
+                                    ctypes.c_void_p(copy.cuda_stream), ctypes.c_void_p(ev.cuda_event)))
+    torch.cuda.current_stream().wait_event(ev)
+    got = pool.cpu().numpy().reshape(S, slab)
+    assert np.array_equal(got[2], src.numpy())
+    assert not got[:2].any()

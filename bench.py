@@ -70,6 +70,8 @@ def parse():
     ap.add_argument("--popularity", choices=["sampled", "offset"], default="sampled",
                     help="missfill: sampled = each token's top-10 drawn from Zipf(1.1) and forced through the route "
                          "mask; offset = a fixed log-popularity logit offset (nearly every lookup then hits)")
+    ap.add_argument("--fetch", choices=["gather", "memcpy"], default="gather",
+                    help="missfill: how misses reach the pool (the other mode is run too and reported beside)")
     args = ap.parse_args()
     if args.steps is None:
         args.steps = {"decode48": 256, "prefill": 50, "missfill": 400}.get(args.workload, 200)
@@ -480,16 +482,6 @@ def bench_missfill(args, torch, qa, E_n=512, N_n=512, k_n=10, S_n=128, skew=1.1)
         rm = torch.from_numpy(m).to(dev)
     copy = torch.cuda.Stream()
     host_ptrs = [(ctypes.c_void_p * 1)(host[r].data_ptr()) for r in range(3)]
-    d = qa.PoolDesc()
-    d.n_layer, d.n_expert = 1, E_n
-    for r in range(3):
-        d.n_slots[r] = S_n
-        d.pool_data[r] = pools[r].data_ptr()
-        d.slab_bytes[r] = slab
-        d.host_slabs[r] = ctypes.cast(host_ptrs[r], ctypes.c_void_p)
-    pool = ctypes.c_void_p()
-    qa.check(L.qwm_pool_create(ctypes.byref(d), ctypes.c_void_p(copy.cuda_stream), ctypes.byref(pool)))
-
     xs = torch.randn((n_all, T, H), device=dev)
     ws = torch.empty(L.qwm_moe_workspace_size(lay, T), dtype=torch.uint8, device=dev)
     qa.check(L.qwm_workspace_init(ws.data_ptr(), ws.numel(), stream))
@@ -508,80 +500,105 @@ def bench_missfill(args, torch, qa, E_n=512, N_n=512, k_n=10, S_n=128, skew=1.1)
     n_ids = T * k_n
     hs = [hsl[r].data_ptr() for r in range(3)]
 
-    def step(s, ev=None, unions=None):
-        if ev is not None:
-            ev[0].record(cur)
-        qa.check(L.qwm_moe_route(lay, t_xs[s], t_rms[s], t_ids, t_w, ws.data_ptr(), ws.numel(), stream))
-        if ev is not None:
-            ev[1].record(cur)
-        hid.copy_(gids.view(-1), non_blocking=True)
-        cur.synchronize()
-        if unions is not None:
-            unions.append(len(np.unique(hid.numpy())))
-        if ev is not None:
-            ev[2].record(copy)
-        qa.check(L.qwm_pool_ensure(pool, 0, hid.data_ptr(), n_ids, hs[0], hs[1], hs[2]))
-        if ev is not None:
-            ev[3].record(copy)
-        dsl.copy_(hsl, non_blocking=True)
-        qa.check(L.qwm_pool_wait(pool, stream))
-        if ev is not None:
-            ev[4].record(cur)
-        qa.check(L.qwm_moe_experts(lay, t_xs[s], t_sl[0], t_sl[1], t_sl[2], t_w, None, t_out, ws.data_ptr(),
-                                   ws.numel(), stream))
-        if ev is not None:
-            ev[5].record(cur)
+    def run_mode(fetch_mode):
+        """A fresh pool with the given fetch mode over the same inputs."""
+        d = qa.PoolDesc()
+        d.n_layer, d.n_expert = 1, E_n
+        for r in range(3):
+            d.n_slots[r] = S_n
+            d.pool_data[r] = pools[r].data_ptr()
+            d.slab_bytes[r] = slab
+            d.host_slabs[r] = ctypes.cast(host_ptrs[r], ctypes.c_void_p)
+        d.fetch_mode = fetch_mode
+        pool = ctypes.c_void_p()
+        qa.check(L.qwm_pool_create(ctypes.byref(d), ctypes.c_void_p(copy.cuda_stream), ctypes.byref(pool)))
 
-    for s in range(args.warmup):
-        step(s)
-    torch.cuda.synchronize()
-    st0 = qa.PoolStats()
-    qa.check(L.qwm_pool_get_stats(pool, ctypes.byref(st0)))
-    # timed run: whole-loop events only
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for s in range(args.warmup, n_all):
-        step(s)
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / args.steps
-    st1 = qa.PoolStats()
-    qa.check(L.qwm_pool_get_stats(pool, ctypes.byref(st1)))
-    # breakdown run over the same inputs again (the pool keeps evolving)
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(args.steps)]
-    unions = []
-    for i, s in enumerate(range(args.warmup, n_all)):
-        step(s, evs[i], unions)
-    torch.cuda.synchronize()
-    rt = np.array([[ev[0].elapsed_time(ev[1]), ev[1].elapsed_time(ev[2]), ev[2].elapsed_time(ev[3]),
-                    ev[3].elapsed_time(ev[4]), ev[4].elapsed_time(ev[5])] for ev in evs])
-    L.qwm_pool_destroy(pool)
-    lookups = (st1.hits + st1.misses) - (st0.hits + st0.misses)
-    misses = st1.misses - st0.misses
-    miss_bytes = (st1.fetch_bytes - st0.fetch_bytes) / args.steps
-    union = float(np.mean(unions))
+        def step(s, ev=None, unions=None):
+            if ev is not None:
+                ev[0].record(cur)
+            qa.check(L.qwm_moe_route(lay, t_xs[s], t_rms[s], t_ids, t_w, ws.data_ptr(), ws.numel(), stream))
+            if ev is not None:
+                ev[1].record(cur)
+            hid.copy_(gids.view(-1), non_blocking=True)
+            cur.synchronize()
+            if unions is not None:
+                unions.append(len(np.unique(hid.numpy())))
+            if ev is not None:
+                ev[2].record(copy)
+            qa.check(L.qwm_pool_ensure(pool, 0, hid.data_ptr(), n_ids, hs[0], hs[1], hs[2]))
+            if ev is not None:
+                ev[3].record(copy)
+            dsl.copy_(hsl, non_blocking=True)
+            qa.check(L.qwm_pool_wait(pool, stream))
+            if ev is not None:
+                ev[4].record(cur)
+            qa.check(L.qwm_moe_experts(lay, t_xs[s], t_sl[0], t_sl[1], t_sl[2], t_w, None, t_out, ws.data_ptr(),
+                                       ws.numel(), stream))
+            if ev is not None:
+                ev[5].record(cur)
+
+        for s in range(args.warmup):
+            step(s)
+        torch.cuda.synchronize()
+        st0 = qa.PoolStats()
+        qa.check(L.qwm_pool_get_stats(pool, ctypes.byref(st0)))
+        # timed run: whole-loop events only
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for s in range(args.warmup, n_all):
+            step(s)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / args.steps
+        st1 = qa.PoolStats()
+        qa.check(L.qwm_pool_get_stats(pool, ctypes.byref(st1)))
+        # breakdown run over the same inputs again (the pool keeps evolving)
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(args.steps)]
+        unions = []
+        for i, s in enumerate(range(args.warmup, n_all)):
+            step(s, evs[i], unions)
+        torch.cuda.synchronize()
+        rt = np.array([[ev[0].elapsed_time(ev[1]), ev[1].elapsed_time(ev[2]), ev[2].elapsed_time(ev[3]),
+                        ev[3].elapsed_time(ev[4]), ev[4].elapsed_time(ev[5])] for ev in evs])
+        L.qwm_pool_destroy(pool)
+        lookups = (st1.hits + st1.misses) - (st0.hits + st0.misses)
+        misses = st1.misses - st0.misses
+        miss_bytes = (st1.fetch_bytes - st0.fetch_bytes) / args.steps
+        copy_ms = rt[:, 2]
+        return {"ms": ms, "rt": rt, "union": float(np.mean(unions)),
+                "pool": {"hit_rate": 1.0 - misses / max(lookups, 1), "misses_per_step": misses / args.steps / 3,
+                         "miss_bytes_per_step": miss_bytes, "evictions": int(st1.evictions - st0.evictions)},
+                "breakdown_ms_median": {"route": float(np.median(rt[:, 0])),
+                                        "ids_readback": float(np.median(rt[:, 1])),
+                                        "ensure_and_copies": float(np.median(rt[:, 2])),
+                                        "copies_to_experts_start": float(np.median(rt[:, 3])),
+                                        "experts": float(np.median(rt[:, 4]))},
+                "host_link_GBs": (miss_bytes * args.steps) / max(float(copy_ms.sum()) * 1e-3, 1e-9) / 1e9}
+
+    other = "memcpy" if args.fetch == "gather" else "gather"
+    modes = {"gather": qa.FETCH_GATHER, "memcpy": qa.FETCH_MEMCPY}
+    res_other = run_mode(modes[other])
+    res = run_mode(modes[args.fetch])
+    rt = res["rt"]
     kern_ms = float(np.median(rt[:, 0]) + np.median(rt[:, 4]))
-    step_bytes = 3 * slab * union + E_n * H * 4 + 3 * slab + 2 * T * H * 4
+    step_bytes = 3 * slab * res["union"] + E_n * H * 4 + 3 * slab + 2 * T * H * 4
     gbs = step_bytes / (kern_ms * 1e-3) / 1e9
-    copy_ms = rt[:, 2] + rt[:, 3]
-    busy = copy_ms > 0.02
-    link = (miss_bytes * args.steps) / max(float(copy_ms.sum()) * 1e-3, 1e-9) / 1e9
     print(json.dumps({
         "metric": "MoE verify tokens/s with LRU slot-pool miss fills, one Qwen3-Next-shape layer, 1xMI355X",
-        "value": T / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "value": T / (res["ms"] * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": res["ms"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
         "data": "synthetic",
         "config": {"workload": "MTP verify T=4 through one Qwen3-Next-shape MoE layer (H 2048, 512 experts + shared, "
                                "FFN 512, top-10, Q4_K) with a 128-slot LRU pool per role, experts in pinned host "
                                "memory, Zipf(1.1) popularity through the route mask",
-                   "pool_slots": S_n, "skew": skew, "popularity": args.popularity, "distinct_experts_per_step": union},
-        "pool": {"hit_rate": 1.0 - misses / max(lookups, 1), "misses_per_step": misses / args.steps / 3,
-                 "miss_bytes_per_step": miss_bytes, "evictions": int(st1.evictions - st0.evictions)},
-        "breakdown_ms_median": {"route": float(np.median(rt[:, 0])), "ids_readback": float(np.median(rt[:, 1])),
-                                "ensure_and_copies": float(np.median(rt[:, 2])),
-                                "copies_to_experts_start": float(np.median(rt[:, 3])),
-                                "experts": float(np.median(rt[:, 4]))},
-        "host_link": {"achieved_GBs": link, "steps_with_copies": int(busy.sum()), "peak_GBs": 64.0},
+                   "pool_slots": S_n, "skew": skew, "popularity": args.popularity, "fetch": args.fetch,
+                   "distinct_experts_per_step": res["union"]},
+        "pool": res["pool"],
+        "breakdown_ms_median": res["breakdown_ms_median"],
+        "host_link": {"achieved_GBs": res["host_link_GBs"], "peak_GBs": 64.0},
+        "other_fetch": {"fetch": other, "ms_per_step": res_other["ms"], "tokens_per_s": T / (res_other["ms"] * 1e-3),
+                        "host_link_GBs": res_other["host_link_GBs"], "hit_rate": res_other["pool"]["hit_rate"],
+                        "breakdown_ms_median": res_other["breakdown_ms_median"]},
         "roofline": {"bound": "hbm", "kernel": "route + experts (selected slabs, router, shared expert)",
                      "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
                      "traffic": None, "bytes_per_launch": step_bytes},

@@ -218,7 +218,21 @@ typedef struct qwm_pool_desc {
     const void * const * host_slabs[3]; /* per role: host_slabs[r][layer] = pinned [K, N, n_expert] source; may be NULL */
     int32_t protect_active;      /* 1: ActiveExpertGuard protection (TinyLFU mode); 0: reference default */
     int32_t indexed;             /* 1: O(1) indexed LRU (QWEN_GPU_LRU_INDEX=1); 0: linear scan */
+    int32_t fetch_mode;          /* QWM_FETCH_MEMCPY or QWM_FETCH_GATHER */
 } qwm_pool_desc;
+
+/* How misses reach the pool (the bytes are the same either way):
+ * MEMCPY: one hipMemcpyAsync per missed slab on the copy stream, as the
+ *   reference's fetch_slab; host slabs may be pageable (then the copies are
+ *   synchronous).
+ * GATHER: one kernel per qwm_pool_ensure call on the copy stream pulls every
+ *   missed slab of the call over the host link (about twice the rate of
+ *   per-slab copies for 576 KiB slabs).  Host slabs must be pinned
+ *   (hipHostMalloc) and, like pool_data, 16-byte aligned; slab_bytes a
+ *   multiple of 16; at most 32767 slots per role.  qwm_pool_create checks
+ *   these. */
+#define QWM_FETCH_MEMCPY 0
+#define QWM_FETCH_GATHER 1
 
 typedef struct qwm_pool_stats {
     uint64_t hits, misses, evictions, fetch_bytes, fetches;
@@ -229,7 +243,11 @@ int qwm_pool_create(const qwm_pool_desc * desc, void * copy_stream, qwm_pool ** 
 void qwm_pool_destroy(qwm_pool * pool);
 /* ids: host i32 [n] (token-major); slot_*: host i32 [n].  Issues the slab
  * copies for misses on the copy stream.  QWM_ERR_NO_VICTIM leaves the pool
- * consistent (the failing role is not published). */
+ * consistent (the failing role is not published; the misses before it are
+ * fetched).  The copies overwrite the victims' slots without waiting for
+ * other streams: the caller makes sure that no kernel still reads them (in
+ * the decode loop the synchronous read-back of the routed ids that precedes
+ * this call does). */
 int qwm_pool_ensure(qwm_pool * pool, int32_t layer, const int32_t * ids, int32_t n,
                     int32_t * slot_gate, int32_t * slot_up, int32_t * slot_down);
 /* Makes `stream` wait for every slab copy issued so far (hipStreamWaitEvent). */

@@ -12,12 +12,13 @@ import ctypes
 import os
 
 __all__ = ["lib", "QwmError", "QwmTensor", "MoeLayer", "PoolDesc", "PoolStats", "tensor", "check",
-           "TYPE_F32", "TYPE_Q8_0", "TYPE_Q4_K", "TYPE_I32"]
+           "TYPE_F32", "TYPE_Q8_0", "TYPE_Q4_K", "TYPE_I32", "FETCH_MEMCPY", "FETCH_GATHER"]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libqwmoe.so")
 
 TYPE_F32, TYPE_Q8_0, TYPE_Q4_K, TYPE_I32 = 0, 8, 12, 26
+FETCH_MEMCPY, FETCH_GATHER = 0, 1
 _TYPE_SIZE = {TYPE_F32: (4, 1), TYPE_I32: (4, 1), TYPE_Q8_0: (34, 32), TYPE_Q4_K: (144, 256)}
 
 OK, ERR_UNSUPPORTED, ERR_ARG, ERR_WORKSPACE, ERR_HIP, ERR_NO_VICTIM, ERR_STATE = 0, -1, -2, -3, -4, -5, -6
@@ -53,7 +54,7 @@ class PoolDesc(ctypes.Structure):
     _fields_ = [("n_layer", ctypes.c_int32), ("n_expert", ctypes.c_int32), ("n_slots", ctypes.c_int32 * 3),
                 ("pool_data", ctypes.c_void_p * 3), ("slab_bytes", ctypes.c_size_t * 3),
                 ("host_slabs", ctypes.c_void_p * 3), ("protect_active", ctypes.c_int32),
-                ("indexed", ctypes.c_int32)]
+                ("indexed", ctypes.c_int32), ("fetch_mode", ctypes.c_int32)]
 
 
 class PoolStats(ctypes.Structure):

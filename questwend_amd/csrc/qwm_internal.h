@@ -115,6 +115,22 @@ int launch_verify(const uint8_t * lm_head, const float * x, const float * norm_w
 
 int launch_fill_zero(void * p, size_t bytes, hipStream_t s);
 
+// ---- slab gather (qwm_fetch.hip) ----
+constexpr int GATHER_MAX = 224;   // misses per launch (kernel arguments stay under 2 KiB)
+struct GatherItem {
+    int32_t expert;   // slab index in the role's host tensor of the layer
+    int16_t slot;     // pool slot
+    int16_t role;     // 0 gate, 1 up, 2 down
+};
+struct GatherArgs {
+    const uint8_t * src[3];   // device-visible address of the layer's pinned host slabs, per role
+    uint8_t * dst[3];         // pool base, per role
+    uint64_t slab[3];         // bytes per slab (multiples of 16)
+    int32_t n, wg_per_item;
+    GatherItem item[GATHER_MAX];
+};
+int launch_slab_gather(const GatherArgs & a, hipStream_t s);
+
 // ---- qwm_quant.hip ----
 int launch_quantize(int32_t type, const float * src, void * dst, int64_t n, hipStream_t s);
 

@@ -1,7 +1,8 @@
 // qwm_pool.cpp -- the GPU slot pool: the RAM-tier decisions of QuestWend's
 // ExpertCache (core/expert_cache.cpp) over per-role pools of expert slabs in
-// HBM, with misses filled from pinned host memory by hipMemcpyAsync on a
-// copy stream.  Host code, owner thread only; it never touches kernels.
+// HBM, with misses filled from pinned host memory on a copy stream, by
+// hipMemcpyAsync per slab or by one slab-gather launch per call.  Host code,
+// owner thread only.
 //
 // Decision rules (all restated, not copied):
 //   ensure (expert_cache.cpp:1615-1645): for each id i in order, for each role
@@ -20,9 +21,13 @@
 //     demand table exists (TinyLFU admission mode): desc.protect_active.
 // The indexed mode keeps an ordered (clock, slot) set and a free-slot set,
 // giving the same victims as the scan in O(log n).
+// Fetch: MEMCPY issues one hipMemcpyAsync per missed slab as it is
+// installed (the reference's order); GATHER collects the call's misses and
+// launches one slab-gather kernel for them at the end of the call.
 #include <hip/hip_runtime_api.h>
 
 #include <cstdint>
+#include <algorithm>
 #include <limits>
 #include <set>
 #include <string>
@@ -39,6 +44,7 @@ struct qwm_pool {
         uint8_t * data = nullptr;
         size_t slab = 0;
         std::vector<const uint8_t *> host;          // per layer, pinned [*, *, n_expert]
+        std::vector<const uint8_t *> host_dev;      // GATHER: device-visible addresses of `host`
         std::vector<int32_t> slot2key;
         std::vector<uint64_t> clk;
         std::unordered_map<int32_t, int32_t> key2slot;
@@ -57,6 +63,8 @@ struct qwm_pool {
     hipStream_t copy = nullptr;
     hipEvent_t done = nullptr;
     bool pending = false;
+    bool gather = false;
+    std::vector<GatherItem> batch;                  // GATHER: this call's misses
 
     void touch(Role & R, int32_t slot) {
         const uint64_t next = clock + 1;
@@ -110,13 +118,59 @@ struct qwm_pool {
             hipError_t e = hipEventCreateWithFlags(&done, hipEventDisableTiming);
             if (e != hipSuccess) return fail(QWM_ERR_HIP, std::string("slab fetch: hipEventCreate: ") + hipGetErrorString(e));
         }
-        const uint8_t * src = R.host[layer] + (size_t)expert * R.slab;
-        hipError_t e = hipMemcpyAsync(R.data + (size_t)slot * R.slab, src, R.slab, hipMemcpyHostToDevice, copy);
-        if (e != hipSuccess) return fail(QWM_ERR_HIP, std::string("slab fetch: ") + hipGetErrorString(e));
+        if (gather) {
+            // A slot filled twice in one call (its first key was evicted again
+            // within the call) keeps the later slab, as stream-ordered copies do.
+            bool replaced = false;
+            for (GatherItem & it : batch)
+                if (it.role == r && it.slot == slot) { it.expert = expert; replaced = true; }
+            if (!replaced) batch.push_back(GatherItem{expert, (int16_t)slot, (int16_t)r});
+        } else {
+            const uint8_t * src = R.host[layer] + (size_t)expert * R.slab;
+            hipError_t e = hipMemcpyAsync(R.data + (size_t)slot * R.slab, src, R.slab, hipMemcpyHostToDevice, copy);
+            if (e != hipSuccess) return fail(QWM_ERR_HIP, std::string("slab fetch: ") + hipGetErrorString(e));
+        }
         fetch_bytes += R.slab;
         fetches++;
         pending = true;
         return QWM_OK;
+    }
+
+    // GATHER: one launch (per GATHER_MAX misses) for the call's misses.  On a
+    // launch failure the call's installs are undone (their slots are freed),
+    // so no published key points at a slot that was not filled.
+    int flush(int32_t layer) {
+        if (batch.empty()) return QWM_OK;
+        GatherArgs a{};
+        for (int r = 0; r < 3; ++r) {
+            a.src[r] = role[r].host_dev.empty() ? nullptr : role[r].host_dev[layer];
+            a.dst[r] = role[r].data;
+            a.slab[r] = role[r].slab;
+        }
+        int rc = QWM_OK;
+        for (size_t i0 = 0; i0 < batch.size() && rc == QWM_OK; i0 += GATHER_MAX) {
+            a.n = (int32_t)std::min<size_t>(GATHER_MAX, batch.size() - i0);
+            for (int32_t i = 0; i < a.n; ++i) a.item[i] = batch[i0 + i];
+            rc = launch_slab_gather(a, copy);
+        }
+        if (rc != QWM_OK)
+            for (const GatherItem & it : batch) {
+                Role & R = role[it.role];
+                const int32_t key = R.slot2key[it.slot];
+                if (key < 0) continue;
+                fetch_bytes -= R.slab;
+                fetches--;
+                if (indexed) {
+                    R.lru.erase({R.clk[it.slot], it.slot});
+                    R.free_slots.insert(it.slot);
+                }
+                R.occ[key / n_expert]--;
+                R.slot_of[key] = 0;
+                R.key2slot.erase(key);
+                R.slot2key[it.slot] = -1;
+            }
+        batch.clear();
+        return rc;
     }
 
     void publish(Role & R, int32_t slot, int32_t key, int32_t layer) {
@@ -144,6 +198,11 @@ int qwm_pool_create(const qwm_pool_desc * d, void * copy_stream, qwm_pool ** out
     p->protect = d->protect_active != 0;
     p->indexed = d->indexed != 0;
     p->copy = (hipStream_t)copy_stream;
+    p->gather = d->fetch_mode == QWM_FETCH_GATHER;
+    if (d->fetch_mode != QWM_FETCH_MEMCPY && d->fetch_mode != QWM_FETCH_GATHER) {
+        delete p;
+        return fail(QWM_ERR_ARG, "pool_create: unknown fetch_mode");
+    }
     for (int r = 0; r < 3; ++r) {
         auto & R = p->role[r];
         if (d->n_slots[r] < 1) { delete p; return fail(QWM_ERR_ARG, "pool_create: a role has no slots"); }
@@ -151,6 +210,26 @@ int qwm_pool_create(const qwm_pool_desc * d, void * copy_stream, qwm_pool ** out
         R.data = (uint8_t *)d->pool_data[r];
         R.slab = d->slab_bytes[r];
         if (d->host_slabs[r]) R.host.assign((const uint8_t * const *)d->host_slabs[r], (const uint8_t * const *)d->host_slabs[r] + d->n_layer);
+        if (p->gather && !R.host.empty()) {
+            if (R.slab % 16 || ((uintptr_t)R.data & 15) || R.n_slots > 32767) {
+                delete p;
+                return fail(QWM_ERR_ARG, "pool_create: GATHER needs 16-byte aligned pools, slab_bytes % 16 == 0 and "
+                                         "at most 32767 slots per role");
+            }
+            R.host_dev.assign((size_t)d->n_layer, nullptr);
+            for (int32_t l = 0; l < d->n_layer; ++l) {
+                if (!R.host[l]) continue;
+                void * dp = nullptr;
+                hipError_t e = hipHostGetDevicePointer(&dp, const_cast<uint8_t *>(R.host[l]), 0);
+                if (e != hipSuccess) (void)hipGetLastError();   // a refused pointer is an argument error, not sticky
+                if (e != hipSuccess || ((uintptr_t)dp & 15)) {
+                    delete p;
+                    return fail(QWM_ERR_ARG, std::string("pool_create: GATHER needs pinned (hipHostMalloc), 16-byte "
+                                                         "aligned host slabs: ") + hipGetErrorString(e));
+                }
+                R.host_dev[l] = (const uint8_t *)dp;
+            }
+        }
         R.slot2key.assign((size_t)R.n_slots, -1);
         R.clk.assign((size_t)R.n_slots, 0);
         R.slot_of.assign((size_t)d->n_layer * d->n_expert, 0);
@@ -209,7 +288,11 @@ int qwm_pool_ensure(qwm_pool * p, int32_t layer, const int32_t * ids, int32_t n,
         }
     }
     for (size_t key : changed) p->active[key] = 0;
-    if (p->pending && rc == QWM_OK) {
+    if (p->gather) {   // the misses installed before a NO_VICTIM failure are filled too
+        const int frc = p->flush(layer);
+        if (frc != QWM_OK) return frc;
+    }
+    if (p->pending && (rc == QWM_OK || p->gather)) {
         hipError_t e = hipEventRecord(p->done, p->copy);
         if (e != hipSuccess) return fail(QWM_ERR_HIP, std::string("pool_ensure: hipEventRecord: ") + hipGetErrorString(e));
     }

@@ -22,6 +22,7 @@ import questwend_amd as qa  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-3
+FETCH = {"memcpy": qa.FETCH_MEMCPY, "gather": qa.FETCH_GATHER}
 
 
 @pytest.fixture(scope="module")
@@ -58,8 +59,10 @@ def zipf_mask(rng, perm, k, T, skew=1.1, bias=16.0):
     return m
 
 
-@pytest.mark.parametrize("wtype,protect,indexed", [("q4_K", 0, 0), ("q4_K", 1, 1), ("q8_0", 0, 1)])
-def test_pool_miss_fill_decode(dev, wtype, protect, indexed):
+@pytest.mark.parametrize("wtype,protect,indexed,fetch", [("q4_K", 0, 0, "memcpy"), ("q4_K", 0, 0, "gather"),
+                                                          ("q4_K", 1, 1, "gather"), ("q8_0", 0, 1, "memcpy"),
+                                                          ("q8_0", 1, 0, "gather")])
+def test_pool_miss_fill_decode(dev, wtype, protect, indexed, fetch):
     H, N, E, k, T, S, n_layer, steps = 512, 256, 64, 4, 4, 20, 2, 24
     cases = [MoeCase(seed=40 + l, H=H, N=N, E=E, k=k, S=E, shared=True, N_sh=N, wtype=wtype) for l in range(n_layer)]
     rng = np.random.default_rng(9)
@@ -80,6 +83,7 @@ def test_pool_miss_fill_decode(dev, wtype, protect, indexed):
         d.slab_bytes[r] = slab
         d.host_slabs[r] = ctypes.cast(host_ptrs[r], ctypes.c_void_p)
     d.protect_active, d.indexed = protect, indexed
+    d.fetch_mode = FETCH[fetch]
     copy = torch.cuda.Stream()
     h = ctypes.c_void_p()
     qa.check(L.qwm_pool_create(ctypes.byref(d), ctypes.c_void_p(copy.cuda_stream), ctypes.byref(h)))
@@ -152,7 +156,7 @@ def test_pool_miss_fill_decode(dev, wtype, protect, indexed):
         assert (stt.hits, stt.misses, stt.evictions) == tuple(int(v) for v in hmo)
         assert stt.fetches == stt.misses and stt.fetch_bytes == stt.misses * slab
         n_miss = stt.misses
-        print(f"pool {wtype} protect={protect} indexed={indexed}: hits {stt.hits} misses {stt.misses} "
+        print(f"pool {wtype} protect={protect} indexed={indexed} fetch={fetch}: hits {stt.hits} misses {stt.misses} "
               f"evictions {stt.evictions}")
         assert stt.evictions > 0, "the trace should overflow the pool"
     finally:
@@ -176,3 +180,61 @@ def test_slab_fetch_async_event(dev):
     got = pool.cpu().numpy().reshape(S, slab)
     assert np.array_equal(got[2], src.numpy())
     assert not got[:2].any()
+
+
+def small_pool(n_slots, slab, host_t, fetch, copy, n_layer=1, n_expert=16):
+    pool_t = [torch.zeros(n_slots * slab, dtype=torch.uint8, device="cuda") for _ in range(3)]
+    ptrs = [(ctypes.c_void_p * n_layer)(*[host_t[r][l].data_ptr() for l in range(n_layer)]) for r in range(3)]
+    d = qa.PoolDesc()
+    d.n_layer, d.n_expert = n_layer, n_expert
+    for r in range(3):
+        d.n_slots[r] = n_slots
+        d.pool_data[r] = pool_t[r].data_ptr()
+        d.slab_bytes[r] = slab
+        d.host_slabs[r] = ctypes.cast(ptrs[r], ctypes.c_void_p)
+    d.fetch_mode = FETCH[fetch]
+    h = ctypes.c_void_p()
+    rc = qa.lib().qwm_pool_create(ctypes.byref(d), ctypes.c_void_p(copy.cuda_stream), ctypes.byref(h))
+    return rc, h, pool_t, ptrs
+
+
+@pytest.mark.parametrize("fetch", ["memcpy", "gather"])
+def test_pool_refill_within_call(dev, fetch):
+    """More distinct experts in one call than slots: a slot installed early in
+    the call is evicted and refilled later in the same call, and must end up
+    holding the later expert's slab (the copies of one call land in order)."""
+    slab, S, E = 4096 + 16 * 37, 6, 16
+    rng = np.random.default_rng(5)
+    host_t = [[pinned(rng.integers(0, 256, E * slab, dtype=np.uint8))] for _ in range(3)]
+    copy = torch.cuda.Stream()
+    rc, h, pool_t, _keep = small_pool(S, slab, host_t, fetch, copy, n_expert=E)
+    qa.check(rc)
+    L = qa.lib()
+    try:
+        for ids in ([0, 1, 2, 3, 4, 5, 6, 7, 8, 9], [9, 3, 12, 13, 14, 15, 0, 1], [2, 2, 5, 11]):
+            ids = np.array(ids, np.int32)
+            sl = np.zeros((3, ids.size), np.int32)
+            qa.check(L.qwm_pool_ensure(h, 0, ptr(ids), ids.size, ptr(sl[0]), ptr(sl[1]), ptr(sl[2])))
+            qa.check(L.qwm_pool_wait(h, None))
+            torch.cuda.synchronize()
+            for r in range(3):
+                keys = np.zeros(S, np.int32)
+                qa.check(L.qwm_pool_slots(h, r, ptr(keys), None))
+                got = pool_t[r].cpu().numpy().reshape(S, slab)
+                src = host_t[r][0].numpy().reshape(E, slab)
+                for s_, key in enumerate(keys):
+                    assert key >= 0 and np.array_equal(got[s_], src[key]), (fetch, r, s_, key)
+    finally:
+        L.qwm_pool_destroy(h)
+
+
+def test_pool_gather_needs_pinned_slabs(dev):
+    """GATHER reads host slabs from the GPU: pageable memory is refused at create."""
+    slab, S, E = 4096, 4, 16
+    pageable = [[torch.zeros(E * slab, dtype=torch.uint8)] for _ in range(3)]
+    rc, h, _, _keep = small_pool(S, slab, pageable, "gather", torch.cuda.Stream(), n_expert=E)
+    assert rc == qa.ERR_ARG and not h.value
+    assert b"pinned" in qa.lib().qwm_last_error()
+    rc, h, _, _keep = small_pool(S, slab + 8, [[pinned(np.zeros(E * (slab + 8), np.uint8))] for _ in range(3)],
+                                 "gather", torch.cuda.Stream(), n_expert=E)
+    assert rc == qa.ERR_ARG and not h.value

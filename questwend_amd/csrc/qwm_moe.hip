@@ -38,37 +38,42 @@ struct RouteKArgs {
     const int32_t * slot_tables; int64_t table_stride; int layer; int32_t * slots_ws;  // [3][T*k]
 };
 
-constexpr int RX_PITCH = 132;           // LDS pitch of the transposed x rows (floats)
-constexpr int RT_MAX_S = 2048 / 16;     // 16-wide steps of one router row
+constexpr int RX_PITCH = 132;           // LDS pitch of the transposed rows (floats; 128 steps + 4)
 
-// One kernel for the whole routing step.
+// One kernel for the whole routing step, one router row per workgroup (the
+// whole row in one round trip of coalesced 16-byte loads; H <= 2048, a
+// multiple of 256).
 //  * Router rows.  T >= 2: llamafile tinyBLAS<16, __m512> order (sgemm.cpp:
 //    600-670): per (row, token) sixteen fma accumulators over 16-wide steps,
-//    then the 16-lane tree; a wave holds 4 rows (lanes 16r + l) and all tokens,
-//    x comes from LDS transposed so lane l reads its stride-16 elements as
-//    128-bit words.  T == 1 (and the single shared-gate row, which ggml runs
+//    then the 16-lane tree.  The row and x are transposed into LDS so that
+//    lane (t, l) reads its stride-16 elements as 128-bit words; a wave holds
+//    four tokens.  T == 1 (and the single shared-gate row, which ggml runs
 //    through vec_dot_f32): ggml_vec_dot_f32's AVX-512 order (ggml-cpu/vec.cpp:
-//    11-135), one row per wave: lane L = 16j + l accumulates over 64-wide
+//    11-135), one token per wave: lane L = 16j + l accumulates over 64-wide
 //    steps, then (j0+j2, j1+j3, 0+1) and the 16-lane tree.
-//  * Q8_K of x, one 256-block per wave across the grid.
-//  * The last workgroup: per token soft_max (ggml-cpu/ops.cpp:5813-5920,
-//    vec.cpp:531 AVX-512: v_expf over 16-lane chunks, each chunk summed with
-//    the 16-lane tree into a double), top-k by probability (ties: lower expert
-//    index), weight gather, normalization (double sum, clamp 6.103515625e-5,
-//    division) and scale; then the expert union (first-occurrence order) and,
-//    in resident mode, the slot ids.
+//  * Q8_K of x (Q8_0 for Q8_0 pools), one 256-block per wave across the grid.
+//  * The last workgroup: per token (one wave each) soft_max (ggml-cpu/ops.cpp:
+//    5813-5920, vec.cpp:531 AVX-512: v_expf over 16-lane chunks, each chunk
+//    summed with the 16-lane tree into a double), top-k as k rounds of a wave
+//    maximum with ballots for the tie order (larger probability, then lower
+//    expert index), the weight sum in selection order (double), clamp
+//    6.103515625e-5, division and scale; then the expert union in
+//    first-occurrence order and, in resident mode, the slot ids.
+// R: probabilities per lane in the selection (E <= 64 R).
+template <int R>
 __global__ void __launch_bounds__(256) k_route(RouteKArgs a) {
-    __shared__ __align__(16) float smem[MAX_T * 16 * RX_PITCH];   // transposed x; later per-wave probabilities
+    __shared__ __align__(16) float smem[(4 + 1) * 16 * RX_PITCH];   // x of four tokens + the row, transposed
     __shared__ int32_t s_ids[MAX_PAIRS];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int E = a.E, H = a.H, T = a.T, k = a.k;
-    const int nsteps = H / 16;
+    const int g = blockIdx.x, G = gridDim.x;
 
     // ---- Q8_K (Q4_K pools) or Q8_0 (Q8_0 pools) of x, the inputs of the
-    // expert GEMVs, spread over every wave
+    // expert GEMVs, spread over every wave (from the last workgroup down, so
+    // that the row workgroups start their loads first)
     {
         const int nb = H / QK_K;
-        for (int jb = blockIdx.x * 4 + wave; jb < T * nb; jb += gridDim.x * 4) {
+        for (int jb = (G - 1 - g) * 4 + wave; jb < T * nb; jb += G * 4) {
             const int t = jb / nb, b = jb % nb;
             if (a.q80)
                 quantize_q80_256(a.x + (size_t)t * H + b * QK_K, a.xq_qs + (size_t)t * H + b * QK_K,
@@ -79,79 +84,88 @@ __global__ void __launch_bounds__(256) k_route(RouteKArgs a) {
         }
     }
 
-    if (blockIdx.x < a.n_row_wg && a.tiny) {
-        // all weight loads first (one round trip), then x into LDS
-        const int l = lane & 15, r = lane >> 4;
-        const int e = blockIdx.x * 16 + wave * 4 + r;
-        const int ec = min(e, E - 1);
-        const float * w = a.W + (size_t)ec * H;
-        float wv[RT_MAX_S];
+    const int rows = E + (a.sgi ? 1 : 0);
+    if (g < rows) {
+        const bool sh_row = g == E;
+        const float * w = sh_row ? a.sgi : a.W + (size_t)g * H;
+        if (a.tiny && !sh_row) {
+            float * xt = smem;                       // [4][16][RX_PITCH]
+            float * wt = smem + 4 * 16 * RX_PITCH;   // [16][RX_PITCH]
+            const int nq = H / 4;                    // float4 per row (<= 512)
+            // dst[h & 15][h >> 4] = src[h] for the float4 number q of a row
+            auto put = [&](float * dst, int q, const float4 v) {
+                const int h = 4 * q;
+                dst[((h + 0) & 15) * RX_PITCH + ((h + 0) >> 4)] = v.x;
+                dst[((h + 1) & 15) * RX_PITCH + ((h + 1) >> 4)] = v.y;
+                dst[((h + 2) & 15) * RX_PITCH + ((h + 2) >> 4)] = v.z;
+                dst[((h + 3) & 15) * RX_PITCH + ((h + 3) >> 4)] = v.w;
+            };
+            float4 wv[2];
 #pragma unroll
-        for (int st = 0; st < RT_MAX_S; ++st)
-            if (st < nsteps) wv[st] = w[16 * st + l];
-        for (int q = tid; q < T * H / 4; q += 256) {
-            const float4 v = reinterpret_cast<const float4 *>(a.x)[q];
-            const int t = (4 * q) / H, h = (4 * q) % H;
-            float * row = smem + (size_t)t * 16 * RX_PITCH;
-            row[((h + 0) & 15) * RX_PITCH + ((h + 0) >> 4)] = v.x;
-            row[((h + 1) & 15) * RX_PITCH + ((h + 1) >> 4)] = v.y;
-            row[((h + 2) & 15) * RX_PITCH + ((h + 2) >> 4)] = v.z;
-            row[((h + 3) & 15) * RX_PITCH + ((h + 3) >> 4)] = v.w;
-        }
-        __syncthreads();
-        for (int t = 0; t < T; ++t) {
-            const float * xr = smem + (size_t)t * 16 * RX_PITCH + l * RX_PITCH;
-            float acc = 0.f;
+            for (int i = 0; i < 2; ++i)
+                if (tid + 256 * i < nq) wv[i] = reinterpret_cast<const float4 *>(w)[tid + 256 * i];
+            for (int t0 = 0; t0 < T; t0 += 4) {
+                float4 xv[4][2];
 #pragma unroll
-            for (int st = 0; st < RT_MAX_S; st += 4) {
-                if (st < nsteps) {
-                    const float4 xv = *reinterpret_cast<const float4 *>(xr + st);
-                    acc = __builtin_fmaf(wv[st + 0], xv.x, acc);
-                    acc = __builtin_fmaf(wv[st + 1], xv.y, acc);
-                    acc = __builtin_fmaf(wv[st + 2], xv.z, acc);
-                    acc = __builtin_fmaf(wv[st + 3], xv.w, acc);
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+                        if (t0 + q < T && tid + 256 * i < nq)
+                            xv[q][i] = reinterpret_cast<const float4 *>(a.x + (size_t)(t0 + q) * H)[tid + 256 * i];
+                if (t0) __syncthreads();             // the previous group's readers are done with LDS
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    if (tid + 256 * i < nq) {
+                        if (t0 == 0) put(wt, tid + 256 * i, wv[i]);
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+                            if (t0 + q < T) put(xt + q * 16 * RX_PITCH, tid + 256 * i, xv[q][i]);
+                    }
+                }
+                __syncthreads();
+                const int l = lane & 15, t = t0 + (lane >> 4);
+                if (wave == 0 && t < T) {
+                    const float * xr = xt + (t - t0) * 16 * RX_PITCH + l * RX_PITCH;
+                    const float * wr = wt + l * RX_PITCH;
+                    float acc = 0.f;
+                    for (int st = 0; st < H / 16; st += 16) {
+#pragma unroll
+                        for (int u = 0; u < 16; u += 4) {
+                            const float4 x4 = *reinterpret_cast<const float4 *>(xr + st + u);
+                            const float4 w4 = *reinterpret_cast<const float4 *>(wr + st + u);
+                            acc = __builtin_fmaf(w4.x, x4.x, acc);
+                            acc = __builtin_fmaf(w4.y, x4.y, acc);
+                            acc = __builtin_fmaf(w4.z, x4.z, acc);
+                            acc = __builtin_fmaf(w4.w, x4.w, acc);
+                        }
+                    }
+                    acc = tree16_dpp(acc);
+                    if (l == 0) st_agent(a.logits + (size_t)t * E + g, a.rm ? acc + a.rm[(size_t)t * E + g] : acc);
                 }
             }
-            acc = tree16_dpp(acc);
-            if (l == 0 && e < E) st_agent(a.logits + (size_t)t * E + e, a.rm ? acc + a.rm[(size_t)t * E + e] : acc);
-        }
-    } else if (blockIdx.x < a.n_row_wg || (a.sgi && blockIdx.x == a.n_row_wg)) {
-        // one row per wave, vec_dot_f32 order; the shared-gate row is wave 0 of the extra block
-        const bool sh_row = blockIdx.x == a.n_row_wg;
-        const int e = sh_row ? E : blockIdx.x * 4 + wave;
-        if ((sh_row && wave == 0) || (!sh_row && e < E)) {
-            const float * w = sh_row ? a.sgi : a.W + (size_t)e * H;
-            const int np = H & ~63;
+        } else {
+            // ggml_vec_dot_f32's AVX-512 order, one token per wave pass
+            const int ns = H / 64;
             float wv[32];
 #pragma unroll
             for (int st = 0; st < 32; ++st)
-                if (64 * st < np) wv[st] = w[64 * st + lane];
-            for (int t = 0; t < T; ++t) {
-                const float * xt = a.x + (size_t)t * H;
+                if (st < ns) wv[st] = w[64 * st + lane];
+            for (int t = wave; t < T; t += 4) {
+                const float * xr = a.x + (size_t)t * H;
                 float xv[32];
 #pragma unroll
                 for (int st = 0; st < 32; ++st)
-                    if (64 * st < np) xv[st] = xt[64 * st + lane];
+                    if (st < ns) xv[st] = xr[64 * st + lane];
                 float acc = 0.f;
 #pragma unroll
                 for (int st = 0; st < 32; ++st)
-                    if (64 * st < np) acc = __builtin_fmaf(wv[st], xv[st], acc);
+                    if (st < ns) acc = __builtin_fmaf(wv[st], xv[st], acc);
                 acc += lane_xor32_f(acc);
                 acc += lane_xor16_f(acc);
                 acc = tree16_dpp(acc);
                 if (lane == 0) {
-                    // scalar tail as gcc -O3 vectorizes it: unfused 16/8-groups, then fma
-                    float sum = acc;
-                    int i = np;
-                    for (; H - i >= 16; i += 16)
-                        for (int q = 0; q < 16; ++q) sum = sum + w[i + q] * xt[i + q];
-                    if (H - i >= 8) {
-                        for (int q = 0; q < 8; ++q) sum = sum + w[i + q] * xt[i + q];
-                        i += 8;
-                    }
-                    for (; i < H; ++i) sum = __builtin_fmaf(w[i], xt[i], sum);
-                    if (sh_row) st_agent(a.sh_logit + t, sum);
-                    else st_agent(a.logits + (size_t)t * E + e, a.rm ? sum + a.rm[(size_t)t * E + e] : sum);
+                    if (sh_row) st_agent(a.sh_logit + t, acc);
+                    else st_agent(a.logits + (size_t)t * E + g, a.rm ? acc + a.rm[(size_t)t * E + g] : acc);
                 }
             }
         }
@@ -159,123 +173,126 @@ __global__ void __launch_bounds__(256) k_route(RouteKArgs a) {
 
     // ---- last workgroup: selection and the expert schedule
     if (!last_workgroup(a.counter)) return;
-    float * probs = smem + wave * MAX_E;
+    const int nr = (E + 63) / 64;
+    const int nfull = E & ~15;
     for (int t = wave; t < T; t += 4) {
         const float * lt = a.logits + (size_t)t * E;
+        float v[R];
         float m = -__builtin_inff();
-        for (int i = lane; i < E; i += 64) {
-            const float v = ld_agent(lt + i);
-            probs[i] = v;
-            m = fmaxf(m, v);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            v[r] = -__builtin_inff();
+            const int i = 64 * r + lane;
+            if (r < nr && i < E) v[r] = ld_agent(lt + i);
+            m = fmaxf(m, v[r]);
         }
         m = wave_max(m);
         double sum = 0.0;
-        const int nfull = E & ~15;
-        for (int c0 = 0; c0 < nfull; c0 += 64) {
-            const int i = c0 + lane;
-            float v = 0.f;
-            if (i < nfull) { v = v_expf(probs[i] - m); probs[i] = v; }
-            const float cs = tree16_dpp(v);
+        float tailv = 0.f;
 #pragma unroll
-            for (int g = 0; g < 4; ++g)
-                if (c0 + 16 * g < nfull) sum += (double)readlane_f(cs, 16 * g);
+        for (int r = 0; r < R; ++r) {
+            if (r < nr) {
+                const int i = 64 * r + lane;
+                float ev = 0.f;
+                if (i < nfull) ev = v_expf(v[r] - m);
+                else if (i < E) ev = expf(v[r] - m);          // scalar tail: libm expf on the CPU
+                const float cs = tree16_dpp(i < nfull ? ev : 0.f);
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    if (64 * r + 16 * q < nfull) sum += (double)readlane_f(cs, 16 * q);
+                if (r == (nfull >> 6)) tailv = ev;
+                v[r] = ev;
+            }
         }
-        for (int i = nfull; i < E; ++i) {           // scalar tail (libm expf on the CPU)
-            const float v = expf(probs[i] - m);
-            sum += (double)v;
-            if (lane == 0) probs[i] = v;
-        }
+        for (int i = nfull; i < E; ++i) sum += (double)readlane_f(tailv, i & 63);
         const float sc = (float)(1.0 / sum);
-        wave_sync();
-        for (int i = lane; i < E; i += 64) probs[i] = probs[i] * sc;
-        wave_sync();
-
-        // top-k: k rounds of a wave argmax (larger probability, then lower index)
-        uint32_t taken = 0;
-        int sel[MAX_K];
+        // top-k: k rounds of the wave maximum; a tie goes to the lower index
+        // (the first r, then the first lane, holding the maximum).  Lane j
+        // keeps the j-th selection; the weight sum runs in selection order.
+        float cur[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int i = 64 * r + lane;
+            cur[r] = (r < nr && i < E) ? v[r] * sc : -1.f;             // probabilities are >= 0
+        }
+        float myw = 0.f;
+        int myid = 0;
+        double wsum = 0.0;
         for (int j = 0; j < k; ++j) {
-            float bv = -__builtin_inff();
-            int bi = 0x7fffffff;
-            int slot = 0;
-            for (int i = lane; i < E; i += 64, ++slot) {
-                if (taken & (1u << slot)) continue;
-                const float p = probs[i];
-                if (p > bv || (p == bv && i < bi)) { bv = p; bi = i; }
+            float mx = cur[0];
+#pragma unroll
+            for (int r = 1; r < R; ++r) mx = fmaxf(mx, cur[r]);
+            mx = wave_max(mx);
+            int id = -1;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const unsigned long long bal = __ballot(cur[r] == mx);
+                if (id < 0 && bal) id = 64 * r + (int)__builtin_ctzll(bal);
             }
-            wave_best_first(bv, bi);
-            if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-            sel[j] = bi;
+            if (lane == j) { myw = mx; myid = id; }
+            wsum += (double)mx;
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                if (64 * r + lane == id) cur[r] = -1.f;
         }
-        if (lane == 0) {
-            float w[MAX_K];
-            for (int j = 0; j < k; ++j) w[j] = probs[sel[j]];
-            if (a.norm) {
-                double s = 0.0;
-                for (int j = 0; j < k; ++j) s += (double)w[j];
-                float ws = (float)s;
-                ws = fmaxf(fminf(ws, __builtin_inff()), 6.103515625e-5f);
-                for (int j = 0; j < k; ++j) w[j] = w[j] / ws;
-            }
-            if (a.scale != 0.0f && a.scale != 1.0f)
-                for (int j = 0; j < k; ++j) w[j] = w[j] * a.scale;
-            for (int j = 0; j < k; ++j) {
-                s_ids[t * k + j] = sel[j];
-                a.ids_ws[t * k + j] = sel[j];
-                a.w_ws[t * k + j] = w[j];
-                if (a.ids_out) a.ids_out[(size_t)t * a.ids_ld + j] = sel[j];
-                if (a.w_out) a.w_out[(size_t)t * a.w_ld + j] = w[j];
-            }
-            if (a.sh_gate) a.sh_gate[t] = 1.f / (1.f + expf(-ld_agent(a.sh_logit + t)));   // unary-ops.cpp:31
+        if (a.norm) {
+            float ws = (float)wsum;
+            ws = fmaxf(fminf(ws, __builtin_inff()), 6.103515625e-5f);
+            myw = myw / ws;
         }
+        if (a.scale != 0.0f && a.scale != 1.0f) myw = myw * a.scale;
+        if (lane < k) {
+            s_ids[t * k + lane] = myid;
+            a.ids_ws[t * k + lane] = myid;
+            a.w_ws[t * k + lane] = myw;
+            if (a.ids_out) a.ids_out[(size_t)t * a.ids_ld + lane] = myid;
+            if (a.w_out) a.w_out[(size_t)t * a.w_ld + lane] = myw;
+        }
+        if (lane == 0 && a.sh_gate) a.sh_gate[t] = 1.f / (1.f + expf(-ld_agent(a.sh_logit + t)));   // unary-ops.cpp:31
     }
     __syncthreads();
-    if (wave != 0) return;
 
-    // wave 0 alone from here: LDS hand-offs between its lanes need only wave_sync
+    // expert union through per-expert LDS tables: first pair, token mask, unit
+    int32_t * tab_first = reinterpret_cast<int32_t *>(smem);
+    uint32_t * tab_mask = reinterpret_cast<uint32_t *>(tab_first + MAX_E);
+    int32_t * tab_unit = reinterpret_cast<int32_t *>(tab_mask + MAX_E);
+    __shared__ unsigned long long s_bal[2];
     const int P = T * k;
-    __shared__ int32_t first[MAX_PAIRS], uidx[MAX_PAIRS];
-    for (int p = lane; p < P; p += 64) {
-        const int e = s_ids[p];
-        int f = p;
-        for (int q = 0; q < p; ++q)
-            if (s_ids[q] == e) { f = q; break; }
-        first[p] = f;
+    const int p = tid;
+    const int e = p < P ? s_ids[p] : 0;
+    if (p < P) { tab_first[e] = 0x7fffffff; tab_mask[e] = 0u; }
+    __syncthreads();
+    if (p < P) { atomicMin(&tab_first[e], p); atomicOr(&tab_mask[e], 1u << (p / k)); }
+    __syncthreads();
+    const bool first = p < P && tab_first[e] == p;
+    const uint32_t tmask = p < P ? tab_mask[e] : 0u;
+    const unsigned long long bal = __ballot(first);
+    if (lane == 0 && wave < 2) s_bal[wave] = bal;
+    __syncthreads();
+    const int nu = __popcll(s_bal[0]) + (P > 64 ? __popcll(s_bal[1]) : 0);
+    if (first) {
+        const int u = (wave == 1 ? __popcll(s_bal[0]) : 0) + __popcll(bal & ((1ull << lane) - 1ull));
+        a.units[u].expert = e;
+        a.units[u].n = __popc(tmask);
+        tab_unit[e] = u;
     }
-    wave_sync();
-    int base = 0;
-    for (int c0 = 0; c0 < P; c0 += 64) {
-        const int p = c0 + lane;
-        const bool isf = p < P && first[p] == p;
-        const unsigned long long bal = __ballot(isf);
-        const int below = __popcll(bal & ((1ull << lane) - 1ull));
-        if (isf) uidx[p] = base + below;
-        base += __popcll(bal);
-    }
-    wave_sync();
-    const int nu = base;
-    for (int p = lane; p < P; p += 64) {
-        const int f = first[p];
-        int pos = 0;
-        for (int q = 0; q < p; ++q) pos += first[q] == f;
-        Unit & u = a.units[uidx[f]];
-        u.pair[pos] = p;
-        if (p == f) u.expert = s_ids[p];
-        int cnt = 0;
-        for (int q = f; q < P; ++q) cnt += first[q] == f;
-        if (p == f) u.n = cnt;
-        if (a.slot_tables) {
-            const int e = s_ids[p];
+    __syncthreads();
+    if (p < P) {
+        const int t = p / k;
+        a.units[tab_unit[e]].pair[__popc(tmask & ((1u << t) - 1u))] = p;
+        if (a.slot_tables)
             for (int r = 0; r < 3; ++r)
                 a.slots_ws[r * P + p] = a.slot_tables[(size_t)r * a.table_stride + (size_t)a.layer * E + e];
+    }
+    if (tid == 0) {
+        if (a.shared) {
+            Unit & u = a.units[nu];
+            u.expert = -1;
+            u.n = T;
+            for (int i = 0; i < T; ++i) u.pair[i] = i;
         }
+        *a.n_units = nu;
     }
-    if (a.shared && lane == 0) {
-        Unit & u = a.units[nu];
-        u.expert = -1;
-        u.n = T;
-        for (int i = 0; i < T; ++i) u.pair[i] = i;
-    }
-    if (lane == 0) *a.n_units = nu;
 }
 
 // Wave steps per GEMV tile: each wave issues the weight loads of GEMV_STEPS
@@ -578,7 +595,7 @@ int launch_route(const RouteArgs & a, const MoePlan & p, uint8_t * ws, int32_t *
     r.W = a.W; r.x = a.x; r.rm = a.rm; r.sgi = a.sh_gate_inp;
     r.E = (int)a.E; r.H = (int)a.H; r.T = (int)a.T; r.k = (int)a.k; r.norm = a.norm; r.scale = a.scale;
     r.tiny = (a.T >= 2 && a.E % 4 == 0) ? 1 : 0;
-    r.n_row_wg = r.tiny ? (int)((a.E + 15) / 16) : (int)((a.E + 3) / 4);
+    r.n_row_wg = (int)a.E;
     r.logits = reinterpret_cast<float *>(ws + p.logits);
     float * sh = reinterpret_cast<float *>(ws + p.sh_gate);
     r.sh_logit = sh + p.T;
@@ -597,8 +614,12 @@ int launch_route(const RouteArgs & a, const MoePlan & p, uint8_t * ws, int32_t *
     r.shared = p.shared ? 1 : 0;
     r.slot_tables = a.slot_tables; r.table_stride = a.table_stride; r.layer = a.layer;
     r.slots_ws = reinterpret_cast<int32_t *>(ws + p.slots);
-    const int grid = r.n_row_wg + (a.sh_gate_inp ? 1 : 0);
-    QWM_TIMED("route", s, k_route<<<dim3((unsigned)grid), dim3(256), 0, s>>>(r));
+    const int quant_wgs = (int)((a.T * (a.H / QK_K) + 3) / 4);
+    const int grid = std::max((int)a.E + (a.sh_gate_inp ? 1 : 0), quant_wgs);
+    const dim3 gd((unsigned)grid);
+    if (a.E <= 128) QWM_TIMED("route", s, k_route<2><<<gd, dim3(256), 0, s>>>(r));
+    else if (a.E <= 512) QWM_TIMED("route", s, k_route<8><<<gd, dim3(256), 0, s>>>(r));
+    else QWM_TIMED("route", s, k_route<MAX_E / 64><<<gd, dim3(256), 0, s>>>(r));
     QWM_HIP_CHECK(hipGetLastError());
     return QWM_OK;
 }

@@ -259,7 +259,8 @@ int qwm_moe_route(const qwm_moe_layer * layer, const qwm_tensor * x, const qwm_t
 }
 
 static int do_experts(const qwm_moe_layer * L, const MoePlan & p, const int32_t * sg, const int32_t * su,
-                      const int32_t * sd, const float * w, const float * resid, float * out, uint8_t * ws, hipStream_t s) {
+                      const int32_t * sd, const float * w, const float * resid, float * out, uint8_t * ws, hipStream_t s,
+                      const int32_t * uslot = nullptr) {
     ExpertArgs a;
     a.wtype = L->gate_pool.type;
     a.gate = (const uint8_t *)L->gate_pool.data; a.up = (const uint8_t *)L->up_pool.data;
@@ -267,7 +268,7 @@ static int do_experts(const qwm_moe_layer * L, const MoePlan & p, const int32_t 
     a.gate_slab = L->gate_pool.nb[2]; a.up_slab = L->up_pool.nb[2]; a.down_slab = L->down_pool.nb[2];
     a.sh_gate = (const uint8_t *)L->sh_gate.data; a.sh_up = (const uint8_t *)L->sh_up.data;
     a.sh_down = (const uint8_t *)L->sh_down.data;
-    a.slot_g = sg; a.slot_u = su; a.slot_d = sd;
+    a.slot_g = sg; a.slot_u = su; a.slot_d = sd; a.uslot = uslot;
     a.weights = w; a.resid = resid; a.out = out;
     return launch_experts(a, p, ws, s);
 }
@@ -322,7 +323,8 @@ int qwm_moe_block_resident(const qwm_moe_layer * layer, int32_t layer_index, con
     const int64_t P = p.T * p.k;
     const int32_t * slots = (const int32_t *)(ws + p.slots);
     return do_experts(layer, p, slots, slots + P, slots + 2 * P, (const float *)(ws + p.w),
-                      resid ? (const float *)resid->data : nullptr, (float *)out->data, ws, s);
+                      resid ? (const float *)resid->data : nullptr, (float *)out->data, ws, s,
+                      (const int32_t *)(ws + p.uslot));
 }
 
 // ------------------------------------------------------------ layer loop --

@@ -249,6 +249,26 @@ QWM_DEV bool last_workgroup(int32_t * counter) {
     return last_workgroup(counter, (int)(gridDim.x * gridDim.y * gridDim.z));
 }
 
+// Dataflow hand-off between workgroups of one launch.  signal_count: after
+// this workgroup's agent-scope writes have completed, count one completion.
+// wait_count: until `target` completions are counted (thread 0 polls; the
+// spin is bounded, a timeout sets *err and lets the workgroup go on).
+QWM_DEV void signal_count(int32_t * c) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+QWM_DEV void wait_count(const int32_t * c, int32_t target, int32_t * err, uint32_t limit) {
+    if (threadIdx.x == 0) {
+        uint32_t spins = 0;
+        while (ld_agent(c) < target) {
+            __builtin_amdgcn_s_sleep(1);
+            if (++spins > limit) { st_agent(err, 1); break; }
+        }
+    }
+    __syncthreads();
+}
+
 // Orders LDS traffic between the lanes of one wave (no workgroup barrier).
 QWM_DEV void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

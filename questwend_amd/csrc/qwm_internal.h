@@ -43,7 +43,7 @@ struct Unit {
 struct MoePlan {
     int64_t H, N, N_sh, E, k, T;
     bool shared, shared_gate;
-    size_t counters, tile_counters, logits, ids, w, slots, sh_gate, units, n_units;
+    size_t counters, tile_counters, logits, ids, w, slots, sh_gate, units, uslot, n_units;
     size_t xq_qs, xq_d, xq_bs, xq_d0, act, act_sh, ex, ex_sh;
     size_t total;
 };
@@ -74,6 +74,7 @@ struct ExpertArgs {
     size_t gate_slab, up_slab, down_slab;                             // bytes per slot
     const uint8_t * sh_gate; const uint8_t * sh_up; const uint8_t * sh_down;
     const int32_t * slot_g; const int32_t * slot_u; const int32_t * slot_d;  // [T][k]
+    const int32_t * uslot;  // [unit][4] from the route's resident remap, or null
     const float * weights;  // [T][k]
     const float * resid;    // [T][H] or null
     float * out;            // [T][H]
@@ -98,7 +99,7 @@ int launch_prefill(const MmidArgs & a, uint8_t * ws, hipStream_t s);
 struct StepPlan {
     MoePlan moe;
     int64_t V;
-    size_t v_counter, v_pv, v_pi, lg, xq_d, xq_bs, bar, flags, total;
+    size_t v_counter, v_pv, v_pi, lg, xq_d, xq_bs, bar, flags, gu_done, tiles_done, total;
 };
 bool step_plan(const qwm_moe_layer * L, const qwm_tensor * lm_head, int64_t T, StepPlan & p, std::string & why);
 struct StepCall {

@@ -36,6 +36,7 @@ struct RouteKArgs {
     Unit * units; int32_t * n_units; int32_t * counter;
     int shared;                                      // append the shared-expert unit
     const int32_t * slot_tables; int64_t table_stride; int layer; int32_t * slots_ws;  // [3][T*k]
+    int32_t * uslot;                                 // resident mode: [unit][4] slots of each unit (gate, up, down)
 };
 
 constexpr int RX_PITCH = 132;           // LDS pitch of the transposed rows (floats; 128 steps + 4)
@@ -275,6 +276,9 @@ __global__ void __launch_bounds__(256) k_route(RouteKArgs a) {
         a.units[u].expert = e;
         a.units[u].n = __popc(tmask);
         tab_unit[e] = u;
+        if (a.slot_tables)
+            for (int r = 0; r < 3; ++r)
+                a.uslot[4 * u + r] = a.slot_tables[(size_t)r * a.table_stride + (size_t)a.layer * E + e];
     }
     __syncthreads();
     if (p < P) {
@@ -307,11 +311,50 @@ struct GateUpArgs {
     const uint8_t * gate; const uint8_t * up; size_t gate_slab, up_slab;
     const uint8_t * sh_gate; const uint8_t * sh_up;
     const int32_t * slot_g; const int32_t * slot_u;
+    const int32_t * uslot;                                        // [unit][4] or null: slots through the pairs
     const Unit * units; const int32_t * n_units; int unit_slots;  // routed unit grid rows
     const int8_t * xq_qs; const float * xq_d; const int32_t * xq_bs;
     float * act; float * act_sh;
-    int H, N, N_sh, k;
+    int H, N, N_sh, k, T;
 };
+
+// The workgroup's unit: its pairs (token-major (t, j) indices; the shared
+// expert's unit is every token) and slot.  The unit count, the unit and its
+// resident-mode slot are requested together, before the empty-unit exit, so
+// the weight loads wait for one round trip instead of three.
+template <int MAXP>
+struct UnitView {
+    int n;
+    int pair[MAXP];
+    int slot[2];
+};
+template <int MAXP>
+QWM_DEV bool load_unit(UnitView<MAXP> & V, const Unit * units, const int32_t * n_units, const int32_t * uslot,
+                       const int32_t * slot_a, const int32_t * slot_b, int u, bool shared, int T, int role_a,
+                       int role_b, int & nu) {
+    nu = *n_units;
+    if (shared) {
+        V.n = T;
+#pragma unroll
+        for (int i = 0; i < MAXP; ++i) V.pair[i] = i;
+        V.slot[0] = V.slot[1] = 0;
+        return true;
+    }
+    const Unit & U = units[u];
+    const int n = U.n;
+    int pr[MAXP];
+#pragma unroll
+    for (int i = 0; i < MAXP; ++i) pr[i] = U.pair[i];
+    int sa = 0, sb = 0;
+    if (uslot) { sa = uslot[4 * u + role_a]; sb = uslot[4 * u + role_b]; }
+    if (u >= nu) return false;
+    if (!uslot) { sa = slot_a[pr[0]]; sb = slot_b ? slot_b[pr[0]] : 0; }
+    V.n = n;
+#pragma unroll
+    for (int i = 0; i < MAXP; ++i) V.pair[i] = pr[i];
+    V.slot[0] = sa; V.slot[1] = sb;
+    return true;
+}
 
 template <class F, int LPR, int MAXP>
 __global__ void __launch_bounds__(256) k_gateup(GateUpArgs a) {
@@ -321,8 +364,9 @@ __global__ void __launch_bounds__(256) k_gateup(GateUpArgs a) {
     const int c = lane % LPR, rsub = lane / LPR;
     const int u = blockIdx.y;
     const bool shared = u == a.unit_slots;
-    if (!shared && u >= *a.n_units) return;
-    const Unit & U = a.units[shared ? *a.n_units : u];
+    UnitView<MAXP> U;
+    int nu;
+    if (!load_unit<MAXP>(U, a.units, a.n_units, a.uslot, a.slot_g, a.slot_u, u, shared, a.T, 0, 1, nu)) return;
     const int n = U.n;
     const int rows = shared ? a.N_sh : a.N;
     const size_t row_bytes = F::row_bytes(a.H);
@@ -330,8 +374,8 @@ __global__ void __launch_bounds__(256) k_gateup(GateUpArgs a) {
     const uint8_t * ubase;
     if (shared) { gbase = a.sh_gate; ubase = a.sh_up; }
     else {
-        gbase = a.gate + (size_t)a.slot_g[U.pair[0]] * a.gate_slab;
-        ubase = a.up + (size_t)a.slot_u[U.pair[0]] * a.up_slab;
+        gbase = a.gate + (size_t)U.slot[0] * a.gate_slab;
+        ubase = a.up + (size_t)U.slot[1] * a.up_slab;
     }
     const int C = a.H / 32;
     const bool active = c < C;
@@ -400,6 +444,7 @@ __global__ void __launch_bounds__(256) k_gateup(GateUpArgs a) {
 struct DownArgs {
     const uint8_t * down; size_t down_slab; const uint8_t * sh_down;
     const int32_t * slot_d;
+    const int32_t * uslot;
     const Unit * units; const int32_t * n_units; int unit_slots; int shared;
     const float * act; const float * act_sh;
     float * ex; float * ex_sh;
@@ -452,11 +497,11 @@ __global__ void __launch_bounds__(256) k_down_q4k(DownArgs a) {
     const int c8 = lane & 7, rsub = lane >> 3;
     const int u = blockIdx.y;
     const bool shared = u == a.unit_slots;
-    const int nu = *a.n_units;
-    if (!shared && u >= nu) return;
-    const Unit & U = a.units[shared ? nu : u];
+    UnitView<MAXP> U;
+    int nu;
+    if (!load_unit<MAXP>(U, a.units, a.n_units, a.uslot, a.slot_d, nullptr, u, shared, a.T, 2, 2, nu)) return;
     const int n = U.n;
-    const uint8_t * base = shared ? a.sh_down : a.down + (size_t)a.slot_d[U.pair[0]] * a.down_slab;
+    const uint8_t * base = shared ? a.sh_down : a.down + (size_t)U.slot[0] * a.down_slab;
     const int row0 = blockIdx.x * TILE;
     const int r = row0 + wave * RPS + rsub;
     // weight loads first: they do not depend on the activations
@@ -465,7 +510,10 @@ __global__ void __launch_bounds__(256) k_down_q4k(DownArgs a) {
     // quantize the unit's activation rows to Q8_K (one 256-block per wave at a time)
     for (int jb = wave; jb < n * NB; jb += 4) {
         const int i = jb / NB, b = jb % NB;
-        const float * src = shared ? a.act_sh + (size_t)U.pair[i] * (NB * QK_K) : a.act + (size_t)U.pair[i] * (NB * QK_K);
+        int pi = U.pair[0];              // U.pair[i] by selects (a dynamic index would put U in scratch)
+#pragma unroll
+        for (int q = 1; q < MAXP; ++q) if (i == q) pi = U.pair[q];
+        const float * src = shared ? a.act_sh + (size_t)pi * (NB * QK_K) : a.act + (size_t)pi * (NB * QK_K);
         quantize_block_q8K(src + b * QK_K, &s_qs[i][b * QK_K], &s_d[i][b], &s_bs[i][b * 16], lane);
     }
     __syncthreads();
@@ -501,11 +549,11 @@ __global__ void __launch_bounds__(256) k_down_q80(DownArgs a) {
     const int c8 = lane & 7, rsub = lane >> 3;
     const int u = blockIdx.y;
     const bool shared = u == a.unit_slots;
-    const int nu = *a.n_units;
-    if (!shared && u >= nu) return;
-    const Unit & U = a.units[shared ? nu : u];
+    UnitView<MAXP> U;
+    int nu;
+    if (!load_unit<MAXP>(U, a.units, a.n_units, a.uslot, a.slot_d, nullptr, u, shared, a.T, 2, 2, nu)) return;
     const int n = U.n;
-    const uint8_t * base = shared ? a.sh_down : a.down + (size_t)a.slot_d[U.pair[0]] * a.down_slab;
+    const uint8_t * base = shared ? a.sh_down : a.down + (size_t)U.slot[0] * a.down_slab;
     const int row0 = blockIdx.x * TILE;
     const int r = row0 + wave * RPS + rsub;
     W80 W[NB];
@@ -514,7 +562,10 @@ __global__ void __launch_bounds__(256) k_down_q80(DownArgs a) {
     for (int q = 0; q < NB; ++q) load_w80(W[q], rowp, 8 * q + c8);
     for (int jb = wave; jb < n * NB; jb += 4) {
         const int i = jb / NB, b = jb % NB;
-        const float * src = shared ? a.act_sh + (size_t)U.pair[i] * (NB * QK_K) : a.act + (size_t)U.pair[i] * (NB * QK_K);
+        int pi = U.pair[0];              // U.pair[i] by selects (a dynamic index would put U in scratch)
+#pragma unroll
+        for (int q = 1; q < MAXP; ++q) if (i == q) pi = U.pair[q];
+        const float * src = shared ? a.act_sh + (size_t)pi * (NB * QK_K) : a.act + (size_t)pi * (NB * QK_K);
         quantize_q80_256(src + b * QK_K, &s_qs[i][b * QK_K], &s_d[i][b * 8], lane);
     }
     __syncthreads();
@@ -577,6 +628,7 @@ bool moe_plan(const qwm_moe_layer * L, int64_t T, MoePlan & p, std::string & why
     p.sh_gate = take(sizeof(float) * (T + 1));
     p.n_units = take(sizeof(int32_t));
     p.units = take(sizeof(Unit) * (P + 1));
+    p.uslot = take(sizeof(int32_t) * 4 * (P + 1));
     p.xq_qs = take((size_t)T * p.H);
     p.xq_d = take(sizeof(float) * T * (p.H / QK_K));
     p.xq_bs = take(sizeof(int32_t) * T * (p.H / 16));
@@ -614,6 +666,7 @@ int launch_route(const RouteArgs & a, const MoePlan & p, uint8_t * ws, int32_t *
     r.shared = p.shared ? 1 : 0;
     r.slot_tables = a.slot_tables; r.table_stride = a.table_stride; r.layer = a.layer;
     r.slots_ws = reinterpret_cast<int32_t *>(ws + p.slots);
+    r.uslot = reinterpret_cast<int32_t *>(ws + p.uslot);
     const int quant_wgs = (int)((a.T * (a.H / QK_K) + 3) / 4);
     const int grid = std::max((int)a.E + (a.sh_gate_inp ? 1 : 0), quant_wgs);
     const dim3 gd((unsigned)grid);
@@ -682,14 +735,14 @@ int launch_experts(const ExpertArgs & a, const MoePlan & p, uint8_t * ws, hipStr
     GateUpArgs g;
     g.gate = a.gate; g.up = a.up; g.gate_slab = a.gate_slab; g.up_slab = a.up_slab;
     g.sh_gate = a.sh_gate; g.sh_up = a.sh_up;
-    g.slot_g = a.slot_g; g.slot_u = a.slot_u;
+    g.slot_g = a.slot_g; g.slot_u = a.slot_u; g.uslot = a.uslot;
     g.units = units; g.n_units = n_units; g.unit_slots = unit_slots;
     g.xq_qs = reinterpret_cast<const int8_t *>(ws + p.xq_qs);
     g.xq_d = reinterpret_cast<const float *>(ws + (q80 ? p.xq_d0 : p.xq_d));
     g.xq_bs = reinterpret_cast<const int32_t *>(ws + p.xq_bs);
     g.act = reinterpret_cast<float *>(ws + p.act);
     g.act_sh = reinterpret_cast<float *>(ws + p.act_sh);
-    g.H = (int)p.H; g.N = (int)p.N; g.N_sh = (int)p.N_sh; g.k = (int)p.k;
+    g.H = (int)p.H; g.N = (int)p.N; g.N_sh = (int)p.N_sh; g.k = (int)p.k; g.T = (int)p.T;
     const int lg = lanes_per_row((int)p.H);
     if (lg < 0) return fail(QWM_ERR_UNSUPPORTED, "hidden size > 2048 not tiled");
     const int rows_g = (int)std::max(p.N, p.N_sh);
@@ -702,7 +755,7 @@ int launch_experts(const ExpertArgs & a, const MoePlan & p, uint8_t * ws, hipStr
 
     DownArgs d;
     d.down = a.down; d.down_slab = a.down_slab; d.sh_down = a.sh_down;
-    d.slot_d = a.slot_d;
+    d.slot_d = a.slot_d; d.uslot = a.uslot;
     d.units = units; d.n_units = n_units; d.unit_slots = unit_slots;
     d.act = g.act; d.act_sh = g.act_sh;
     d.ex = reinterpret_cast<float *>(ws + p.ex);

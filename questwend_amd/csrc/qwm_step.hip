@@ -13,10 +13,13 @@
 //       (softmax, top-k, weights, expert union, slots) in registers and LDS:
 //       no hand-off and no serial tail
 //   P2  gate/up GEMVs over the expert union, persistent row loops with a
-//       4-deep load ring, fused SwiGLU                            -> barrier
-//   P3  down GEMVs; the last unit to finish a row tile combines it
-//       (CPU order, + shared expert, + residual)                  -> barrier
-//   P4  the verify head of qwm_vhead.h on the block's output
+//       6-deep load ring, fused SwiGLU; each finished item counts for its unit
+//   P3  down GEMVs: an item requests its weight rows, then waits for its
+//       unit's gate/up items only; the last unit to finish a row tile
+//       combines it (CPU order, + shared expert, + residual) and counts it
+//   P4  the verify head of qwm_vhead.h on the block's output: the first
+//       lm_head tiles are requested, then the workgroup waits for every
+//       combined tile
 //
 // Data that crosses workgroups inside the launch is written with agent-scope
 // stores (write-through, coherent across the XCDs' L2s) into buffers that no
@@ -25,10 +28,13 @@
 // logits, the Q8_K scales and the combine tiles are padded or aligned for
 // that), so a consumer's ordinary L2-cached load can only find that writer's
 // fresh line or none; the one multi-writer buffer (SwiGLU activations) is read
-// with agent-scope loads.  Grid barriers: one arrival counter, and a flag line
-// per workgroup that the last arriver sets, so no line is polled by more than
-// one workgroup; spins are bounded (a timeout sets an error word and the
-// result reports a = -1 instead of hanging).
+// with agent-scope loads.  The grid barrier after P0: group arrival counters,
+// and a flag line per workgroup that the last arriver sets, so no line is
+// polled by more than one workgroup.  P2 -> P3 and P3 -> P4 are completion
+// counters instead (per unit, and for the combined tiles), so no workgroup
+// waits for work it does not read.  Every wait is bounded (a timeout sets an
+// error word and the result reports a = -1 instead of hanging); the last
+// workgroup of the launch re-arms the counters.
 #include <hip/hip_runtime.h>
 
 #include "qwm_internal.h"
@@ -60,6 +66,8 @@ struct StepArgs {
     float * act; float * act_sh; float * ex; float * ex_sh;
     uint32_t * bar; uint32_t * epoch; uint32_t * flags;                         // flags: one 32-word line per workgroup
     int32_t * tile_counters; int32_t * err;
+    int32_t * gu_done;                                                          // per unit, one 32-word line each
+    int32_t * tiles_done;                                                       // combined down tiles
     VerifyArgs v;                                                               // v.x = out
 };
 
@@ -450,7 +458,7 @@ QWM_DEV void step_gateup(const StepArgs & a, int g, int G, const StepShared & S,
                 else st_agent(a.act + (size_t)U_.pair[i] * rows + r, s_act[i][r - rb]);
             }
         }
-        __syncthreads();
+        signal_count(a.gu_done + 32 * u);        // also orders s_act's reuse by the next item
     }
 }
 
@@ -476,6 +484,7 @@ QWM_DEV void step_down(const StepArgs & a, int g, int G, const StepShared & S, u
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int c8 = lane & 7, rsub = lane >> 3;
     const int U = S.nu + a.shared;
+    const int nb_r = (a.N + GU_ROWS - 1) / GU_ROWS, nb_s = (a.N_sh + GU_ROWS - 1) / GU_ROWS;   // gate/up items per unit
     int8_t (*s_qs)[MAX_NDOWN_S] = reinterpret_cast<int8_t (*)[MAX_NDOWN_S]>(smem);
     float (*s_d)[MAX_NDOWN_S / QK_K] = reinterpret_cast<float (*)[MAX_NDOWN_S / QK_K]>(smem + MAXP * MAX_NDOWN_S);
     int32_t (*s_bs)[MAX_NDOWN_S / 16] =
@@ -495,6 +504,7 @@ QWM_DEV void step_down(const StepArgs & a, int g, int G, const StepShared & S, u
         WChunkS Wb[PF][NB];
 #pragma unroll
         for (int p = 0; p < PF; ++p) load_row8<NB>(Wb[p], rp + (size_t)(4 * RPS * p) * row_bytes, c8);
+        wait_count(a.gu_done + 32 * u, shared ? nb_s : nb_r, a.err, SPIN_LIMIT);   // the unit's activations are out
         for (int jb = wave; jb < n * NB; jb += 4) {
             const int i = jb / NB, b = jb % NB;
             const float * src = shared ? a.act_sh + (size_t)U_.pair[i] * (NB * QK_K)
@@ -577,6 +587,7 @@ QWM_DEV void step_down(const StepArgs & a, int g, int G, const StepShared & S, u
                     st_agent(a.out + (size_t)t * SH + h, sacc);
                 }
             }
+            signal_count(a.tiles_done);
         }
         __syncthreads();
     }
@@ -612,18 +623,23 @@ __global__ void __launch_bounds__(256) k_step(StepArgs a) {
     if (a.E <= 128) step_select<NT, 2>(a, g, S, smem);
     else step_select<NT, STEP_MAX_E / 64>(a, g, S, smem);
     step_gateup<MAXP>(a, g, G, S, smem);
-    grid_barrier(a, 2, G, epoch);
     step_down<NT, NB_D, MAXP>(a, g, G, S, smem);
-    grid_barrier(a, 3, G, epoch);
     __syncthreads();
     constexpr int PF = NT <= 4 ? 2 : 1;
-    if (verify_body<NT, SH / 512, PF, false>(a.v, g, G, smem) && threadIdx.x == 0) {
-        // every workgroup has read the epoch and passed all barriers
-        st_agent(a.epoch, epoch + 1u);
-        if (ld_agent(a.err)) {
-            a.v.result[NT] = -1;
-            a.v.result[NT + 1] = -1;
-            st_agent(a.err, 0);
+    if (verify_body<NT, SH / 512, PF, VH_BEFORE_WAIT>(a.v, g, G, smem, a.tiles_done, SH / DN_TR, a.err, SPIN_LIMIT)) {
+        // every workgroup has read the epoch, passed the barrier and all waits:
+        // re-arm the completion counters, then the epoch
+        for (int q = threadIdx.x; q < MAX_PAIRS + 1; q += 256) st_agent(a.gu_done + 32 * q, 0);
+        if (threadIdx.x == 0) st_agent(a.tiles_done, 0);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            st_agent(a.epoch, epoch + 1u);
+            if (ld_agent(a.err)) {
+                a.v.result[NT] = -1;
+                a.v.result[NT + 1] = -1;
+                st_agent(a.err, 0);
+            }
         }
     }
 }
@@ -660,6 +676,8 @@ bool step_plan(const qwm_moe_layer * L, const qwm_tensor * lm_head, int64_t T, S
     p.xq_bs = take(sizeof(int32_t) * 32 * T * SNB);
     p.bar = take(512 + 128 * BAR_GROUPS);     // top counter, epoch, error word, group counters at 512
     p.flags = take(sizeof(uint32_t) * 32 * MAX_STEP_WG);
+    p.gu_done = take(128 * (MAX_PAIRS + 1));
+    p.tiles_done = take(128);
     p.total = o;
     return true;
 }
@@ -736,6 +754,8 @@ int launch_step(const StepCall & c, const StepPlan & p, uint8_t * ws, hipStream_
     a.err = reinterpret_cast<int32_t *>(ws + p.bar + 256);
     a.flags = reinterpret_cast<uint32_t *>(ws + p.flags);
     a.tile_counters = reinterpret_cast<int32_t *>(ws + m.tile_counters);
+    a.gu_done = reinterpret_cast<int32_t *>(ws + p.gu_done);
+    a.tiles_done = reinterpret_cast<int32_t *>(ws + p.tiles_done);
     VerifyArgs & v = a.v;
     v.W = c.lm_head; v.H = SH; v.V = (int)p.V;
     v.x = c.out; v.norm_w = c.norm_w; v.eps = c.eps;

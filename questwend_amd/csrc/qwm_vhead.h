@@ -63,12 +63,15 @@ template <int NT> struct VhSmem {
 // vocabulary rows), with `smem` holding VhSmem<NT>::bytes of LDS.  Returns
 // true in the workgroup that finished last (it wrote the result).
 // NS = H / 512 block sets per lane (H = 512 * NS), PF tiles in flight.
-// EARLY: the first weight tiles are requested before the rms_norm and
-// quantization prep instead of after it.  Right after a grid barrier the
-// late form lets the barrier's release reach every workgroup before the
-// weight stream fills the memory queues.
-template <int NT, int NS, int PF, bool EARLY = true>
-QWM_DEV bool verify_body(const VerifyArgs & a, int wg, int n_wg, uint8_t * smem) {
+// ISSUE: when the first weight tiles are requested.  VH_EARLY: before the
+// rms_norm and quantization prep; VH_LATE: after it; VH_BEFORE_WAIT: first of
+// all, then the workgroup waits until `*ready` counts `ready_target`
+// completions (the producers of x inside the same launch), so the tiles'
+// latency hides under the wait.
+enum { VH_LATE = 0, VH_EARLY = 1, VH_BEFORE_WAIT = 2 };
+template <int NT, int NS, int PF, int ISSUE = VH_EARLY>
+QWM_DEV bool verify_body(const VerifyArgs & a, int wg, int n_wg, uint8_t * smem, const int32_t * ready = nullptr,
+                         int32_t ready_target = 0, int32_t * err = nullptr, uint32_t spin_limit = 0) {
     constexpr int NG = (NT + 3) / 4;                  // token groups (MFMA A rows)
     __shared__ float s_scale[NT];
     uint4 (*s_q)[64][2] = reinterpret_cast<uint4 (*)[64][2]>(smem);
@@ -93,6 +96,13 @@ QWM_DEV bool verify_body(const VerifyArgs & a, int wg, int n_wg, uint8_t * smem)
         return a.W + r * row_bytes + lane_off;
     };
 
+    uint32_t win[PF][NS][VH_WIN];
+    if constexpr (ISSUE == VH_BEFORE_WAIT) {
+#pragma unroll
+        for (int p = 0; p < PF; ++p) load_tile<NS>(win[p], lane_ptr(min(p, n_steps - 1)));
+        wait_count(ready, ready_target, err, spin_limit);
+    }
+
     // ---- h = rms_norm(x) * norm_w (ggml-cpu/ops.cpp:4120-4160), then the x86
     // Q8_0 quantizer (ggml-cpu/arch/x86/quants.c:302-345) per (token, block)
     // item, into LDS.  Vector-memory waits complete in issue order, so every
@@ -115,8 +125,7 @@ QWM_DEV bool verify_body(const VerifyArgs & a, int wg, int n_wg, uint8_t * smem)
     __builtin_amdgcn_sched_barrier(0);
 
     // weight loads for the first steps
-    uint32_t win[PF][NS][VH_WIN];
-    if constexpr (EARLY) {
+    if constexpr (ISSUE == VH_EARLY) {
 #pragma unroll
         for (int p = 0; p < PF; ++p) load_tile<NS>(win[p], lane_ptr(min(p, n_steps - 1)));
     }
@@ -179,7 +188,7 @@ QWM_DEV bool verify_body(const VerifyArgs & a, int wg, int n_wg, uint8_t * smem)
         s_d[t][blk] = fp16_to_f32(f32_to_fp16(d));
     }
     __syncthreads();
-    if constexpr (!EARLY) {
+    if constexpr (ISSUE == VH_LATE) {
 #pragma unroll
         for (int p = 0; p < PF; ++p) load_tile<NS>(win[p], lane_ptr(min(p, n_steps - 1)));
     }

@@ -317,6 +317,68 @@ def bench_decode(args, torch, qa, n_layers=48):
     ms = min(ms_direct, ms_graph)
     step_bytes = n_layers * (K_USED * 3 * SLAB + E * H * 4 + 2 * T1 * H * 4)
     gbs = step_bytes / (ms * 1e-3) / 1e9
+    cpu = None
+    if not args.no_cpu:
+        lib = ref_cpu_lib()
+        if lib is None:
+            cpu = NO_REF
+        else:
+            # the GPU's output for the first input after every prefix of the layers,
+            # as the parity check of the sample
+            gpu_x = []
+            for nl in range(1, n_layers + 1):
+                xw.copy_(xs[0])
+                qa.check(L.qwm_moe_decode(layers, nl, tables.data_ptr(), n_layers * E, xt, ws.data_ptr(), ws.numel(),
+                                          torch.cuda.current_stream().cuda_stream))
+                gpu_x.append(xw.cpu().numpy()[0].copy())
+            host = [[p.cpu().numpy() for p in pl] for pl in pools]
+            rts = [rt.cpu().numpy() for rt in routers]
+            x_np = xs.cpu().numpy()
+            a = BlockArgs()
+            a.H, a.N, a.E, a.k, a.T, a.n_threads = H, N, E, K_USED, T1, CPU_THREADS
+            ids = np.zeros((T1, K_USED), np.int32)
+            out = np.zeros((T1, H), np.float32)
+            a.ids, a.out = ids.ctypes.data, out.ctypes.data
+            res = {}
+
+            def token(i):
+                x = np.ascontiguousarray(x_np[i % n_all])
+                for l in range(n_layers):
+                    a.router, a.gate, a.up, a.down = (rts[l].ctypes.data, host[l][0].ctypes.data,
+                                                      host[l][1].ctypes.data, host[l][2].ctypes.data)
+                    a.x = x.ctypes.data
+                    lib.qwr_cpu_moe_block(ctypes.byref(a))
+                    if i == 0:
+                        res.setdefault("layers", []).append((x.copy(), out.copy(), ids.copy()))
+                    x = out.copy()
+
+            n, secs = timed_sample(token, args.cpu_seconds)
+            errs = [rel_err(c[1][0], g) for c, g in zip(res["layers"], gpu_x)]
+            first_off = next((l + 1 for l, e_ in enumerate(errs) if e_ > 1e-3), None)
+            # every block on the CPU's own input: the single-layer parity, free of the chain's divergence
+            wsb = torch.empty(L.qwm_moe_workspace_size(layers[0], T1), dtype=torch.uint8, device=dev)
+            qa.check(L.qwm_workspace_init(wsb.data_ptr(), wsb.numel(), stream))
+            blk_err, ids_same = [], 0
+            for l, (xin, xout, cids) in enumerate(res["layers"]):
+                din = torch.from_numpy(xin).to(dev)
+                dout = torch.empty_like(din)
+                gids = torch.empty((T1, K_USED), dtype=torch.int32, device=dev)
+                tin = qa.tensor(qa.TYPE_F32, H, T1, 1, din)
+                qa.check(L.qwm_moe_block_resident(layers[l], l, tables.data_ptr(), n_layers * E, tin, None, tin,
+                                                  qa.tensor(qa.TYPE_F32, H, T1, 1, dout),
+                                                  qa.tensor(qa.TYPE_I32, K_USED, T1, 1, gids), None,
+                                                  wsb.data_ptr(), wsb.numel(), stream))
+                blk_err.append(rel_err(dout.cpu().numpy() - xin, xout - xin))
+                ids_same += int(np.array_equal(gids.cpu().numpy(), cids))
+            cpu = {"value": n / secs, "unit": "tokens/s", "cores": CPU_THREADS, "kind": "reference",
+                   "sample": f"{n} decode tokens ({secs:.1f} s) through the same 48 blocks with the reference's "
+                             f"ggml-CPU kernels (x86-64 AVX-512 build, {CPU_THREADS} OpenMP threads)",
+                   "ms_per_token": 1e3 * secs / n,
+                   "parity_first_token": {
+                       "per_block_on_cpu_input": {"max_rel_err_moe": max(blk_err), "median_rel_err_moe": float(np.median(blk_err)),
+                                                  "layers_with_identical_ids": f"{ids_same}/{n_layers}"},
+                       "chained_rel_err_per_layer": [float(f"{e_:.3g}") for e_ in errs],
+                       "chain_first_layer_above_1e-3": first_off}}
     print(json.dumps({
         "metric": "MoE decode tokens/s + achieved HBM GB/s (% of 8 TB/s), 48 stacked Q4_K blocks, 1xMI355X",
         "value": T1 / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -328,6 +390,7 @@ def bench_decode(args, torch, qa, n_layers=48):
         "roofline": {"bound": "hbm", "kernel": "whole step (48 x route + gate/up + down)", "achieved": gbs,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS, "traffic": None,
                      "bytes_per_launch": step_bytes},
+        "cpu_baseline": cpu,
     }))
 
 
@@ -392,6 +455,34 @@ def bench_prefill(args, torch, qa, T_pf=512, E_pf=512, k_pf=10, N_pf=512):
     g_ms = np.zeros(3 * args.steps, np.float32)
     n_g = L.qwm_profile_stop(g_ms.ctypes.data, 3 * args.steps)
     g_ms = g_ms[:n_g].reshape(-1, 3) if n_g == 3 * args.steps else None
+    cpu = None
+    if not args.no_cpu:
+        lib = ref_cpu_lib()
+        if lib is None:
+            cpu = NO_REF
+        else:
+            hq = [p.cpu().numpy() for p in pools]
+            xh = x.cpu().numpy()
+            ih = ids.cpu().numpy()
+            gd = down.cpu().numpy()
+            hg = np.zeros((T_pf, k_pf, N_pf), np.float32)
+            hu = np.zeros_like(hg)
+            hd = np.zeros((T_pf, k_pf, H), np.float32)
+            P_ = lambda arr: arr.ctypes.data
+
+            def cpu_step(i):
+                lib.qwr_cpu_mul_mat_id(P_(hq[1]), H, N_pf, E_pf, P_(xh), 1, T_pf, P_(ih), k_pf, P_(hu), CPU_THREADS)
+                lib.qwr_cpu_mul_mat_id(P_(hq[0]), H, N_pf, E_pf, P_(xh), 1, T_pf, P_(ih), k_pf, P_(hg), CPU_THREADS)
+                ha = np.ascontiguousarray((hg / (1.0 + np.exp(-hg)) * hu).astype(np.float32))
+                lib.qwr_cpu_mul_mat_id(P_(hq[2]), N_pf, H, E_pf, P_(ha), k_pf, T_pf, P_(ih), k_pf, P_(hd), CPU_THREADS)
+
+            n, secs = timed_sample(cpu_step, args.cpu_seconds)
+            cpu = {"value": T_pf * n / secs, "unit": "tokens/s", "cores": CPU_THREADS, "kind": "reference",
+                   "sample": f"{n} prefill steps ({secs:.1f} s): the same three MUL_MAT_IDs through the reference's "
+                             f"ggml-CPU vec_dot kernels ({CPU_THREADS} OpenMP threads; ggml's tiled AVX-512 VNNI "
+                             f"kernel for experts with >= 8 columns is not built here); down output against the "
+                             f"GPU's: rel err {rel_err(hd, gd):.2e}",
+                   "ms_per_step": 1e3 * secs / n}
     used = len(np.unique(ids.cpu().numpy()))
     w_bytes = 3 * used * slab
     flops = 2.0 * T_pf * k_pf * (2 * N_pf * H + H * N_pf)
@@ -410,6 +501,7 @@ def bench_prefill(args, torch, qa, T_pf=512, E_pf=512, k_pf=10, N_pf=512):
                      "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS, "traffic": None, "bytes_per_launch": w_bytes / 3},
         "mfma": {"tops": flops / (gemm_ms * 1e-3) / 1e12, "peak_int8_tops": 5000.0,
                  "frac": flops / (gemm_ms * 1e-3) / 5e15},
+        "cpu_baseline": cpu,
     }))
 
 
@@ -575,6 +667,40 @@ def bench_missfill(args, torch, qa, E_n=512, N_n=512, k_n=10, S_n=128, skew=1.1)
                                         "experts": float(np.median(rt[:, 4]))},
                 "host_link_GBs": (miss_bytes * args.steps) / max(float(copy_ms.sum()) * 1e-3, 1e-9) / 1e9}
 
+    cpu = None
+    if not args.no_cpu:
+        lib = ref_cpu_lib()
+        if lib is None:
+            cpu = NO_REF
+        else:
+            # every expert in host memory (the pinned slabs), the shared expert and router copied back
+            hs_np = [h.numpy() for h in host]
+            sh_np = [q.cpu().numpy() for q in sh]
+            rt_np = router.cpu().numpy()
+            si_np = sh_inp.cpu().numpy()
+            rm_np = rm.cpu().numpy()
+            x_np = xs.cpu().numpy()
+            a = BlockArgs()
+            a.H, a.N, a.E, a.k, a.T, a.n_threads = H, N_n, E_n, k_n, T, CPU_THREADS
+            a.router, a.gate, a.up, a.down = rt_np.ctypes.data, hs_np[0].ctypes.data, hs_np[1].ctypes.data, hs_np[2].ctypes.data
+            a.sh_gate, a.sh_up, a.sh_down, a.sh_inp = (sh_np[0].ctypes.data, sh_np[1].ctypes.data, sh_np[2].ctypes.data,
+                                                       si_np.ctypes.data)
+            ids_c = np.zeros((T, k_n), np.int32)
+            out_c = np.zeros((T, H), np.float32)
+            a.ids, a.out = ids_c.ctypes.data, out_c.ctypes.data
+
+            def cpu_step(i):
+                s_ = args.warmup + i % args.steps
+                xi = np.ascontiguousarray(x_np[s_])
+                ri = np.ascontiguousarray(rm_np[s_])
+                a.x, a.rm = xi.ctypes.data, ri.ctypes.data
+                lib.qwr_cpu_moe_block(ctypes.byref(a))
+
+            n, secs = timed_sample(cpu_step, args.cpu_seconds)
+            cpu = {"value": T * n / secs, "unit": "tokens/s", "cores": CPU_THREADS, "kind": "reference",
+                   "sample": f"{n} verify steps ({secs:.1f} s) of the same inputs through the reference's ggml-CPU "
+                             f"kernels with every expert in host memory ({CPU_THREADS} OpenMP threads)",
+                   "ms_per_step": 1e3 * secs / n}
     other = "memcpy" if args.fetch == "gather" else "gather"
     modes = {"gather": qa.FETCH_GATHER, "memcpy": qa.FETCH_MEMCPY}
     res_other = run_mode(modes[other])
@@ -602,6 +728,7 @@ def bench_missfill(args, torch, qa, E_n=512, N_n=512, k_n=10, S_n=128, skew=1.1)
         "roofline": {"bound": "hbm", "kernel": "route + experts (selected slabs, router, shared expert)",
                      "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
                      "traffic": None, "bytes_per_launch": step_bytes},
+        "cpu_baseline": cpu,
     }))
 
 
@@ -611,6 +738,50 @@ class StepArgs(ctypes.Structure):
                 ("up", ctypes.c_void_p), ("down", ctypes.c_void_p), ("lm_head", ctypes.c_void_p),
                 ("x", ctypes.c_void_p), ("drafts", ctypes.c_void_p), ("ids", ctypes.c_void_p), ("out", ctypes.c_void_p),
                 ("vA", ctypes.c_void_p), ("accepted", ctypes.c_void_p), ("n_threads", ctypes.c_int)]
+
+
+class BlockArgs(ctypes.Structure):
+    """qwr_block_args of oracle/ref_harness/cpu_step.cpp."""
+    _fields_ = [("H", ctypes.c_int64), ("N", ctypes.c_int64), ("E", ctypes.c_int64), ("k", ctypes.c_int64),
+                ("T", ctypes.c_int64), ("router", ctypes.c_void_p), ("rm", ctypes.c_void_p), ("gate", ctypes.c_void_p),
+                ("up", ctypes.c_void_p), ("down", ctypes.c_void_p), ("sh_gate", ctypes.c_void_p),
+                ("sh_up", ctypes.c_void_p), ("sh_down", ctypes.c_void_p), ("sh_inp", ctypes.c_void_p),
+                ("x", ctypes.c_void_p), ("out", ctypes.c_void_p), ("ids", ctypes.c_void_p), ("n_threads", ctypes.c_int)]
+
+
+def ref_cpu_lib():
+    """The reference's ggml-CPU kernels with the step/block harness (oracle/_ref), or None."""
+    so = os.path.join(ROOT, "oracle", "_ref", "libggml_leaf.so")
+    if not os.path.exists(so):
+        return None
+    lib = ctypes.CDLL(so)
+    lib.qwr_cpu_verify_step.argtypes = [ctypes.POINTER(StepArgs)]
+    lib.qwr_cpu_moe_block.argtypes = [ctypes.POINTER(BlockArgs)]
+    P, I = ctypes.c_void_p, ctypes.c_int64
+    lib.qwr_cpu_mul_mat_id.argtypes = [P, I, I, I, P, I, I, P, I, P, ctypes.c_int]
+    return lib
+
+
+def timed_sample(fn, seconds, max_runs=100000):
+    """One untimed warm-up call, then calls until `seconds` are spent; returns (runs, seconds)."""
+    fn(0)
+    n, t_total = 0, 0.0
+    while t_total < seconds and n < max_runs:
+        t0 = time.perf_counter()
+        fn(n + 1)
+        t_total += time.perf_counter() - t0
+        n += 1
+    return n, t_total
+
+
+def rel_err(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+NO_REF = {"value": None, "unit": "tokens/s", "cores": 0, "kind": "reference", "sample": "oracle/_ref not built"}
+CPU_THREADS = 16
 
 
 def cpu_baseline(args, torch, pools, router, lm, xs, drafts, ids_gpu, res_gpu):

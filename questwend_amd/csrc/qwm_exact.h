@@ -1,0 +1,165 @@
+// qwm_exact.h -- Q4_K x Q8_K row dots in ggml-CPU's exact float order.
+//
+// ggml's x86 ggml_vec_dot_q4_K_q8_K (ggml-cpu/arch/x86/quants.c:2102-2185)
+// keeps eight fp32 lanes: lane m accumulates, block after block,
+//   acc[m] = fma(y.d * fp16(x.d), (float) sumi[m], acc[m]),
+//   sumi[m] = sum_j sc_j * (dot of elements 4m .. 4m+3 of sub-block j),
+// and four lanes of mins, acc_m[l] = fma(-y.d * fp16(x.dmin), (float)
+// (mn_2l * q8s_2l + mn_2l+1 * q8s_2l+1), acc_m[l]) with q8s_j = bsums_2j +
+// bsums_2j+1; the row's value is hsum8(acc) + hsum4(acc_m) (pairs (m, m+4),
+// then (0, 2) and (1, 3), then the two halves).  The integer sums are exact
+// in any order; only the float steps have an order, and here eight GPU lanes
+// play the eight CPU lanes: lane m of a row's 8-lane group walks the row's
+// blocks in order with the same fused multiply-adds, so the result is the
+// CPU's bit for bit.  Then the SwiGLU activations, their Q8_K levels, and the
+// down projection's integer sums are the CPU's too: no quantization-boundary
+// flips between the two.
+//
+// Weights: lane m loads the 16-byte block header (d, dmin, 12 scale bytes,
+// shared by the group) and the 4 dwords of qs it needs (bytes 32p + 4m).
+// Activations (Q8_K) sit in LDS in a per-lane order: per block XS dwords,
+// lane m's 8 qs dwords contiguous (sub-block 2p+h at slot 2p+h), then the
+// block scale and the eight 32-element sums q8s.
+#pragma once
+
+#include "qwm_q4k.h"
+
+namespace qwm {
+
+constexpr int XS = 76;       // LDS dwords per Q8_K block in the exact layout (64 qs + d + 8 q8s + pad)
+
+// One wave quantizes 256 floats to Q8_K (quantize_block_q8K's arithmetic)
+// into the exact layout at `dst` (XS dwords).  Lane l owns elements 4l..4l+3,
+// i.e. qs dword l = 16p + 8h + m.
+template <bool SRC_AGENT = false, bool AGENT = false>
+QWM_DEV void quantize_block_q8K_x(const float * __restrict__ src, uint32_t * __restrict__ dst, int lane) {
+    float4 v4;
+    if constexpr (SRC_AGENT) {
+        const uint64_t * s64 = reinterpret_cast<const uint64_t *>(src) + 2 * lane;
+        const uint64_t lo = ld_agent(s64), hi = ld_agent(s64 + 1);
+        v4 = make_float4(__uint_as_float((uint32_t)lo), __uint_as_float((uint32_t)(lo >> 32)),
+                         __uint_as_float((uint32_t)hi), __uint_as_float((uint32_t)(hi >> 32)));
+    } else {
+        v4 = reinterpret_cast<const float4 *>(src)[lane];
+    }
+    const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+    float a = __builtin_fabsf(v[0]);
+    int ii = 0;
+#pragma unroll
+    for (int i = 1; i < 4; ++i)
+        if (__builtin_fabsf(v[i]) > a) { a = __builtin_fabsf(v[i]); ii = i; }
+    int idx = 4 * lane + ii;
+    wave_best_first(a, idx);
+    idx = __builtin_amdgcn_readfirstlane(idx);
+    const int c = idx & 3;
+    const float mine = c == 0 ? v[0] : c == 1 ? v[1] : c == 2 ? v[2] : v[3];
+    const float mx = readlane_f(mine, idx >> 2);
+    int q[4] = {0, 0, 0, 0};
+    float d = 0.f;
+    if (a != 0.f) {
+        const float iscale = -127.f / mx;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) q[i] = min(127, nearest_int_mul(iscale, v[i]));
+        d = 1.f / iscale;
+    }
+    const uint32_t packed = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) |
+                            ((uint32_t)(q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24);
+    const int m = lane & 7, h = (lane >> 3) & 1, p = lane >> 4;
+    // sums over 32 elements (8 lanes): quads by DPP, then quad + quad + 4
+    int sm = q[0] + q[1] + q[2] + q[3];
+    sm += dpp_i<0xB1>(sm);
+    sm += dpp_i<0x4E>(sm);
+    sm += dpp_i<0x124>(sm);                   // lane i receives lane i - 4 (same 16-lane row)
+    const uint32_t q8s = (uint32_t)(int32_t)(int16_t)sm;
+    if constexpr (AGENT) {
+        st_agent(dst + 8 * m + 2 * p + h, packed);
+        if ((lane & 7) == 4) st_agent(dst + 65 + (lane >> 3), q8s);
+        if (lane == 0) st_agent(dst + 64, __float_as_uint(d));
+    } else {
+        dst[8 * m + 2 * p + h] = packed;
+        if ((lane & 7) == 4) dst[65 + (lane >> 3)] = q8s;
+        if (lane == 0) dst[64] = __float_as_uint(d);
+    }
+}
+
+// One Q4_K block as lane m of its row's 8-lane group holds it.
+struct XBlk {
+    uint4 h;         // d, dmin (fp16 x 2), scales[0..11]
+    uint32_t q[4];   // qs bytes 32p + 4m .. +3, p = 0..3
+};
+
+QWM_DEV void load_xblk(XBlk & B, const uint8_t * blk, int m) {
+    B.h = *reinterpret_cast<const uint4 *>(blk);
+#pragma unroll
+    for (int p = 0; p < 4; ++p) B.q[p] = *reinterpret_cast<const uint32_t *>(blk + 16 + 32 * p + 4 * m);
+}
+
+// Row dots of one weight row (NB blocks in W) with n <= MAXP activation rows
+// at sx + i * NB * XS in LDS.  out[i] is valid in lane m == 0 of the group.
+template <int NB, int MAXP>
+QWM_DEV void q4k_dot8(float (&out)[MAXP], const XBlk (&W)[NB], const uint32_t * sx, int n, int m) {
+    float acc[MAXP], accm[MAXP];
+#pragma unroll
+    for (int i = 0; i < MAXP; ++i) { acc[i] = 0.f; accm[i] = 0.f; }
+    const uint32_t k1 = 0x3f3f3f3fu, k2 = 0x0f0f0f0fu, k3 = 0x03030303u, m4 = 0x0f0f0f0fu;
+    const int l = m & 3;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const XBlk & B = W[b];
+        // scales and mins as ggml unpacks them (quants.c:2133-2138)
+        const uint32_t u0 = B.h.y, u1 = B.h.z, u2 = B.h.w;
+        const uint32_t mn_hi = ((u2 >> 4) & k2) | (((u1 >> 6) & k3) << 4);
+        const uint32_t mn_lo = u1 & k1;
+        const uint32_t sc_hi = (u2 & k2) | (((u0 >> 6) & k3) << 4);
+        const uint32_t sc_lo = u0 & k1;
+        int sc[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) { sc[j] = (sc_lo >> (8 * j)) & 0xff; sc[4 + j] = (sc_hi >> (8 * j)) & 0xff; }
+        const uint32_t mw = l < 2 ? mn_lo : mn_hi;
+        const int sh = 16 * (l & 1);
+        const int mnA = (mw >> sh) & 0xff, mnB = (mw >> (sh + 8)) & 0xff;
+        const float dw = fp16_to_f32((uint16_t)(B.h.x & 0xffff));
+        const float dmw = fp16_to_f32((uint16_t)(B.h.x >> 16));
+        uint32_t wl[4], wh[4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) { wl[p] = B.q[p] & m4; wh[p] = (B.q[p] >> 4) & m4; }
+#pragma unroll
+        for (int i = 0; i < MAXP; ++i) {
+            if (i < n) {
+                const uint32_t * xb = sx + (i * NB + b) * XS;
+                const uint4 x0 = *reinterpret_cast<const uint4 *>(xb + 8 * m);
+                const uint4 x1 = *reinterpret_cast<const uint4 *>(xb + 8 * m + 4);
+                const float yd = __uint_as_float(xb[64]);
+                const int qa = (int)xb[65 + 2 * l], qb = (int)xb[66 + 2 * l];
+                int s = 0;
+                s += sc[0] * dot4(wl[0], x0.x, 0);
+                s += sc[1] * dot4(wh[0], x0.y, 0);
+                s += sc[2] * dot4(wl[1], x0.z, 0);
+                s += sc[3] * dot4(wh[1], x0.w, 0);
+                s += sc[4] * dot4(wl[2], x1.x, 0);
+                s += sc[5] * dot4(wh[2], x1.y, 0);
+                s += sc[6] * dot4(wl[3], x1.z, 0);
+                s += sc[7] * dot4(wh[3], x1.w, 0);
+                acc[i] = __builtin_fmaf(yd * dw, (float)s, acc[i]);
+                const int prod = mnA * qa + mnB * qb;
+                accm[i] = __builtin_fmaf(-yd * dmw, (float)prod, accm[i]);
+            }
+        }
+    }
+    // hsum_float_8(acc) + hsum_float_4(acc_m) (quants.c:43-49, 2181-2184)
+#pragma unroll
+    for (int i = 0; i < MAXP; ++i) {
+        if (i < n) {
+            const float t = acc[i] + dpp_f<0x12C>(acc[i]);        // lanes 0-3: a[m] + a[m + 4]
+            const float u = t + dpp_f<0x12E>(t);                   // lanes 0-1: t[m] + t[m + 2]
+            const float h8 = u + dpp_f<0x12F>(u);                  // lane 0: u[0] + u[1]
+            const float v = accm[i] + dpp_f<0x12E>(accm[i]);       // lanes 0-1: am[l] + am[l + 2]
+            const float h4 = v + dpp_f<0x12F>(v);                  // lane 0
+            out[i] = h8 + h4;
+        } else {
+            out[i] = 0.f;
+        }
+    }
+}
+
+}  // namespace qwm

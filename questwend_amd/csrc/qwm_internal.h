@@ -44,7 +44,7 @@ struct MoePlan {
     int64_t H, N, N_sh, E, k, T;
     bool shared, shared_gate;
     size_t counters, tile_counters, logits, ids, w, slots, sh_gate, units, uslot, n_units;
-    size_t xq_qs, xq_d, xq_bs, xq_d0, act, act_sh, ex, ex_sh;
+    size_t xq_qs, xq_d, xq_bs, xq_d0, xq_x, act, act_sh, ex, ex_sh;
     size_t total;
 };
 bool moe_plan(const qwm_moe_layer * L, int64_t T, MoePlan & p, std::string & why);
@@ -99,7 +99,7 @@ int launch_prefill(const MmidArgs & a, uint8_t * ws, hipStream_t s);
 struct StepPlan {
     MoePlan moe;
     int64_t V;
-    size_t v_counter, v_pv, v_pi, lg, xq_d, xq_bs, bar, flags, gu_done, tiles_done, total;
+    size_t v_counter, v_pv, v_pi, lg, xq_x, bar, flags, gu_done, tiles_done, total;
 };
 bool step_plan(const qwm_moe_layer * L, const qwm_tensor * lm_head, int64_t T, StepPlan & p, std::string & why);
 struct StepCall {

@@ -15,6 +15,7 @@
 #include "qwm_internal.h"
 #include "qwm_q4k.h"
 #include "qwm_q80.h"
+#include "qwm_exact.h"
 
 namespace qwm {
 
@@ -33,6 +34,7 @@ struct RouteKArgs {
     float * sh_gate;                                 // [T] or null
     int8_t * xq_qs; float * xq_d; int32_t * xq_bs;   // Q8_K of x
     int q80; float * xq_d0;                         // Q8_0 pools: x as Q8_0 (qs in xq_qs, scales per 32)
+    uint32_t * xq_x;                                 // Q4_K pools: x as Q8_K in the exact-dot layout [T][H/256][XS]
     Unit * units; int32_t * n_units; int32_t * counter;
     int shared;                                      // append the shared-expert unit
     const int32_t * slot_tables; int64_t table_stride; int layer; int32_t * slots_ws;  // [3][T*k]
@@ -80,8 +82,7 @@ __global__ void __launch_bounds__(256) k_route(RouteKArgs a) {
                 quantize_q80_256(a.x + (size_t)t * H + b * QK_K, a.xq_qs + (size_t)t * H + b * QK_K,
                                  a.xq_d0 + (size_t)t * (H / 32) + b * 8, lane);
             else
-                quantize_block_q8K(a.x + (size_t)t * H + b * QK_K, a.xq_qs + (size_t)t * H + b * QK_K,
-                                   a.xq_d + (size_t)t * nb + b, a.xq_bs + (size_t)t * (H / 16) + b * 16, lane);
+                quantize_block_q8K_x(a.x + (size_t)t * H + b * QK_K, a.xq_x + (size_t)(t * nb + b) * XS, lane);
         }
     }
 
@@ -314,6 +315,7 @@ struct GateUpArgs {
     const int32_t * uslot;                                        // [unit][4] or null: slots through the pairs
     const Unit * units; const int32_t * n_units; int unit_slots;  // routed unit grid rows
     const int8_t * xq_qs; const float * xq_d; const int32_t * xq_bs;
+    const uint32_t * xq_x;                                        // Q8_K of x, exact-dot layout (Q4_K pools)
     float * act; float * act_sh;
     int H, N, N_sh, k, T;
 };
@@ -430,6 +432,61 @@ __global__ void __launch_bounds__(256) k_gateup(GateUpArgs a) {
     }
 }
 
+// Q4_K gate/up in ggml-CPU's exact float order (qwm_exact.h): 8 lanes per
+// row, a workgroup owns 32 consecutive rows (4 waves x 8 rows) of one unit.
+// The unit's Q8_K activations are copied into LDS first; SwiGLU then sees the
+// CPU's gate and up values bit for bit.
+constexpr int GUX_ROWS = 32;
+
+template <int NB, int MAXP>
+__global__ void __launch_bounds__(256) k_gateup_x(GateUpArgs a) {
+    __shared__ __align__(16) uint32_t s_x[MAXP * NB * XS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int m = lane & 7, rsub = lane >> 3;
+    const int u = blockIdx.y;
+    const bool shared = u == a.unit_slots;
+    UnitView<MAXP> U;
+    int nu;
+    if (!load_unit<MAXP>(U, a.units, a.n_units, a.uslot, a.slot_g, a.slot_u, u, shared, a.T, 0, 1, nu)) return;
+    const int n = U.n;
+    const int rows = shared ? a.N_sh : a.N;
+    const int r = blockIdx.x * GUX_ROWS + wave * 8 + rsub;
+    if (blockIdx.x * GUX_ROWS >= rows) return;
+    const size_t row_bytes = (size_t)NB * 144;
+    const uint8_t * gbase = shared ? a.sh_gate : a.gate + (size_t)U.slot[0] * a.gate_slab;
+    const uint8_t * ubase = shared ? a.sh_up : a.up + (size_t)U.slot[1] * a.up_slab;
+    const int rc = min(r, rows - 1);
+    XBlk G[NB], W[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        load_xblk(G[b], gbase + (size_t)rc * row_bytes + b * 144, m);
+        load_xblk(W[b], ubase + (size_t)rc * row_bytes + b * 144, m);
+    }
+    // the unit's tokens' activation blocks into LDS (uint4 copies)
+    constexpr int Q4 = NB * XS / 4;
+    for (int q = tid; q < n * Q4; q += 256) {
+        const int i = q / Q4, o = q % Q4;
+        int pi = U.pair[0];              // U.pair[i] by selects (a dynamic index would put U in scratch)
+#pragma unroll
+        for (int qq = 1; qq < MAXP; ++qq) if (i == qq) pi = U.pair[qq];
+        const int t = shared ? pi : pi / a.k;
+        reinterpret_cast<uint4 *>(s_x)[i * Q4 + o] = reinterpret_cast<const uint4 *>(a.xq_x + (size_t)t * NB * XS)[o];
+    }
+    __syncthreads();
+    float g[MAXP], up[MAXP];
+    q4k_dot8<NB, MAXP>(g, G, s_x, n, m);
+    q4k_dot8<NB, MAXP>(up, W, s_x, n, m);
+    if (m == 0 && r < rows) {
+#pragma unroll
+        for (int i = 0; i < MAXP; ++i)
+            if (i < n) {
+                const float v = (r < rows - (rows & 15)) ? v_silu(g[i]) * up[i] : g[i] / (1.0f + expf(-g[i])) * up[i];
+                if (shared) a.act_sh[(size_t)U.pair[i] * rows + r] = v;
+                else a.act[(size_t)U.pair[i] * rows + r] = v;
+            }
+    }
+}
+
 // ---------------------------------------------------------------------
 // down: ex[p][h] = down_e[h] . Q8_K(act[p]), then the combine of the row tile
 // grid: (row tiles over H, unit slots [+1 shared]), block 256.  Each block
@@ -490,9 +547,7 @@ __global__ void __launch_bounds__(256) k_down_q4k(DownArgs a) {
     constexpr int RPS = 8;                   // rows per wave
     constexpr int TILE = 4 * RPS;
     constexpr size_t row_bytes = (size_t)NB * 144;
-    __shared__ int8_t s_qs[MAXP][MAX_NDOWN];
-    __shared__ float s_d[MAXP][MAX_NDOWN / QK_K];
-    __shared__ int32_t s_bs[MAXP][MAX_NDOWN / 16];
+    __shared__ __align__(16) uint32_t s_x[MAXP * NB * XS];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int c8 = lane & 7, rsub = lane >> 3;
     const int u = blockIdx.y;
@@ -505,28 +560,27 @@ __global__ void __launch_bounds__(256) k_down_q4k(DownArgs a) {
     const int row0 = blockIdx.x * TILE;
     const int r = row0 + wave * RPS + rsub;
     // weight loads first: they do not depend on the activations
-    WChunkS W[NB];
-    load_row8<NB>(W, base + (size_t)min(r, a.H - 1) * row_bytes, c8);
-    // quantize the unit's activation rows to Q8_K (one 256-block per wave at a time)
+    XBlk W[NB];
+    const uint8_t * rp = base + (size_t)min(r, a.H - 1) * row_bytes;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) load_xblk(W[b], rp + b * 144, c8);
+    // the unit's activation rows to Q8_K in the exact-dot layout (one 256-block per wave at a time)
     for (int jb = wave; jb < n * NB; jb += 4) {
         const int i = jb / NB, b = jb % NB;
         int pi = U.pair[0];              // U.pair[i] by selects (a dynamic index would put U in scratch)
 #pragma unroll
         for (int q = 1; q < MAXP; ++q) if (i == q) pi = U.pair[q];
         const float * src = shared ? a.act_sh + (size_t)pi * (NB * QK_K) : a.act + (size_t)pi * (NB * QK_K);
-        quantize_block_q8K(src + b * QK_K, &s_qs[i][b * QK_K], &s_d[i][b], &s_bs[i][b * 16], lane);
+        quantize_block_q8K_x(src + b * QK_K, s_x + (i * NB + b) * XS, lane);
     }
     __syncthreads();
     float acc[MAXP];
-    row8_dots<NB, MAXP, MAX_NDOWN>(acc, W, n, &s_qs[0][0], &s_d[0][0], &s_bs[0][0], c8);
+    q4k_dot8<NB, MAXP>(acc, W, s_x, n, c8);
 #pragma unroll
     for (int i = 0; i < MAXP; ++i)
-        if (i < n) {
-            const float sum = row8_sum(acc[i]);
-            if (c8 == 0 && r < a.H) {
-                if (shared) st_agent(a.ex_sh + (size_t)U.pair[i] * a.H + r, sum);
-                else st_agent(a.ex + (size_t)U.pair[i] * a.H + r, sum);
-            }
+        if (i < n && c8 == 0 && r < a.H) {
+            if (shared) st_agent(a.ex_sh + (size_t)U.pair[i] * a.H + r, acc[i]);
+            else st_agent(a.ex + (size_t)U.pair[i] * a.H + r, acc[i]);
         }
     if (!last_workgroup(a.tile_counters + blockIdx.x, nu + a.shared)) return;
     for (int q = tid; q < a.T * TILE; q += 256) {
@@ -633,6 +687,7 @@ bool moe_plan(const qwm_moe_layer * L, int64_t T, MoePlan & p, std::string & why
     p.xq_d = take(sizeof(float) * T * (p.H / QK_K));
     p.xq_bs = take(sizeof(int32_t) * T * (p.H / 16));
     p.xq_d0 = take(sizeof(float) * T * (p.H / 32));
+    p.xq_x = take(sizeof(uint32_t) * T * (p.H / QK_K) * XS);
     p.act = take(sizeof(float) * P * p.N);
     p.act_sh = take(sizeof(float) * T * (p.N_sh ? p.N_sh : 1));
     p.ex = take(sizeof(float) * P * p.H);
@@ -660,6 +715,7 @@ int launch_route(const RouteArgs & a, const MoePlan & p, uint8_t * ws, int32_t *
     r.xq_bs = reinterpret_cast<int32_t *>(ws + p.xq_bs);
     r.q80 = a.wtype == T_Q8_0;
     r.xq_d0 = reinterpret_cast<float *>(ws + p.xq_d0);
+    r.xq_x = reinterpret_cast<uint32_t *>(ws + p.xq_x);
     r.units = reinterpret_cast<Unit *>(ws + p.units);
     r.n_units = reinterpret_cast<int32_t *>(ws + p.n_units);
     r.counter = reinterpret_cast<int32_t *>(ws + p.counters);
@@ -692,6 +748,28 @@ static void launch_gateup_f(const GateUpArgs & g, int lpr, int maxp, dim3 grid, 
         case 16: launch_gateup_lpr<F, 16>(g, maxp, grid, s); break;
         case 32: launch_gateup_lpr<F, 32>(g, maxp, grid, s); break;
         default: launch_gateup_lpr<F, 64>(g, maxp, grid, s); break;
+    }
+}
+template <int NB>
+static void launch_gateup_x_nb(const GateUpArgs & g, int maxp, dim3 grid, hipStream_t s) {
+    switch (maxp) {
+        case 1: k_gateup_x<NB, 1><<<grid, 256, 0, s>>>(g); break;
+        case 2: k_gateup_x<NB, 2><<<grid, 256, 0, s>>>(g); break;
+        case 4: k_gateup_x<NB, 4><<<grid, 256, 0, s>>>(g); break;
+        default: k_gateup_x<NB, 8><<<grid, 256, 0, s>>>(g); break;
+    }
+}
+static bool launch_gateup_x(const GateUpArgs & g, int nb, int maxp, dim3 grid, hipStream_t s) {
+    switch (nb) {
+        case 1: launch_gateup_x_nb<1>(g, maxp, grid, s); return true;
+        case 2: launch_gateup_x_nb<2>(g, maxp, grid, s); return true;
+        case 3: launch_gateup_x_nb<3>(g, maxp, grid, s); return true;
+        case 4: launch_gateup_x_nb<4>(g, maxp, grid, s); return true;
+        case 5: launch_gateup_x_nb<5>(g, maxp, grid, s); return true;
+        case 6: launch_gateup_x_nb<6>(g, maxp, grid, s); return true;
+        case 7: launch_gateup_x_nb<7>(g, maxp, grid, s); return true;
+        case 8: launch_gateup_x_nb<8>(g, maxp, grid, s); return true;
+        default: return false;
     }
 }
 template <int NB>
@@ -740,6 +818,7 @@ int launch_experts(const ExpertArgs & a, const MoePlan & p, uint8_t * ws, hipStr
     g.xq_qs = reinterpret_cast<const int8_t *>(ws + p.xq_qs);
     g.xq_d = reinterpret_cast<const float *>(ws + (q80 ? p.xq_d0 : p.xq_d));
     g.xq_bs = reinterpret_cast<const int32_t *>(ws + p.xq_bs);
+    g.xq_x = reinterpret_cast<const uint32_t *>(ws + p.xq_x);
     g.act = reinterpret_cast<float *>(ws + p.act);
     g.act_sh = reinterpret_cast<float *>(ws + p.act_sh);
     g.H = (int)p.H; g.N = (int)p.N; g.N_sh = (int)p.N_sh; g.k = (int)p.k; g.T = (int)p.T;
@@ -750,7 +829,8 @@ int launch_experts(const ExpertArgs & a, const MoePlan & p, uint8_t * ws, hipStr
     dim3 grid_g((rows_g + tile_g - 1) / tile_g, grid_y);
     prof_begin("gate_up", s);
     if (q80) launch_gateup_f<FmtQ80>(g, lg, maxp, grid_g, s);
-    else launch_gateup_f<FmtQ4K>(g, lg, maxp, grid_g, s);
+    else if (!launch_gateup_x(g, (int)(p.H / QK_K), maxp, dim3((rows_g + GUX_ROWS - 1) / GUX_ROWS, grid_y), s))
+        return fail(QWM_ERR_UNSUPPORTED, "hidden size not instantiated for the exact gate/up");
     prof_end("gate_up", s);
 
     DownArgs d;

@@ -12,8 +12,8 @@
 //   P1  every workgroup repeats the selection for all tokens from the logits
 //       (softmax, top-k, weights, expert union, slots) in registers and LDS:
 //       no hand-off and no serial tail
-//   P2  gate/up GEMVs over the expert union, persistent row loops with a
-//       6-deep load ring, fused SwiGLU; each finished item counts for its unit
+//   P2  gate/up GEMVs over the expert union in ggml-CPU's exact float order
+//       (qwm_exact.h), fused SwiGLU; each finished item counts for its unit
 //   P3  down GEMVs: an item requests its weight rows, then waits for its
 //       unit's gate/up items only; the last unit to finish a row tile
 //       combines it (CPU order, + shared expert, + residual) and counts it
@@ -40,6 +40,7 @@
 #include "qwm_internal.h"
 #include "qwm_q4k.h"
 #include "qwm_vhead.h"
+#include "qwm_exact.h"
 
 namespace qwm {
 
@@ -49,6 +50,7 @@ constexpr uint32_t SPIN_LIMIT = 1u << 21;
 constexpr int MAX_NDOWN_S = 2048;        // longest down-projection input (FFN width)
 constexpr int STEP_MAX_E = 512;          // experts per layer in the fused step
 constexpr int RX_P = 132;                // pitch of the transposed router rows in LDS (floats)
+constexpr int XSP = 96;                  // workspace dwords per exact-layout Q8_K block of x (3 whole lines)
 constexpr size_t cmax(size_t x, size_t y) { return x > y ? x : y; }
 
 struct StepArgs {
@@ -62,7 +64,7 @@ struct StepArgs {
     const float * resid; float * out;                                           // [T][H]
     int32_t * ids_out; int64_t ids_ld; float * w_out; int64_t w_ld;
     float * lg;                                                                 // [E + 1][32]: logits of row e (row E: shared gate)
-    int8_t * xq_qs; float * xq_d; int32_t * xq_bs;                              // d, bsums: one 32-word line per block
+    uint32_t * xq_x;                                                            // Q8_K of x, exact-dot layout, XSP per block
     float * act; float * act_sh; float * ex; float * ex_sh;
     uint32_t * bar; uint32_t * epoch; uint32_t * flags;                         // flags: one 32-word line per workgroup
     int32_t * tile_counters; int32_t * err;
@@ -136,8 +138,7 @@ QWM_DEV void step_router(const StepArgs & a, int g, int G, uint8_t * smem) {
         const int gw = (G - 1 - g) * 4 + wave;
         for (int jb = gw; jb < NT * SNB; jb += 4 * G) {
             const int t = jb / SNB, b = jb % SNB;
-            quantize_block_q8K<true>(a.x + (size_t)t * SH + b * QK_K, a.xq_qs + (size_t)t * SH + b * QK_K,
-                                     a.xq_d + (size_t)(t * SNB + b) * 32, a.xq_bs + (size_t)(t * SNB + b) * 32, lane);
+            quantize_block_q8K_x<false, true>(a.x + (size_t)t * SH + b * QK_K, a.xq_x + (size_t)(t * SNB + b) * XSP, lane);
         }
     }
     const int rows = E + (a.sgi ? 1 : 0);
@@ -365,28 +366,24 @@ QWM_DEV void step_select(const StepArgs & a, int g, StepShared & S, uint8_t * sm
 }
 
 // ---------------------------------------------------------------- P2 ----
-// gate/up: items of GU_ROWS consecutive rows of one unit; workgroup g takes
-// items g, g + G, ...  Each wave streams GU_ROWS / 4 rows through a
-// GU_PF-deep ring with the unit's Q8_K activations in registers, decodes each
-// row chunk once for all tokens and reduces four rows' gate and up sums at a
-// time (wave_sum_scatter8).  act = silu(g) * u (the vectorized silu except
-// for the row tail the CPU runs through scalar expf) is collected in LDS and
-// leaves in one pass of stores; an item's first and last lines may be shared
-// with the neighbouring item, so the down phase reads act with agent-scope loads.
-constexpr int GU_ROWS = 48;
-constexpr int GU_PF = 6;
+// gate/up: items of GU_ROWS = 32 consecutive rows of one unit (one whole
+// 128-byte line of activations per token); workgroup g takes items g,
+// g + G, ...  Each wave owns 8 rows, 8 lanes per row, in ggml-CPU's exact
+// float order (qwm_exact.h): the unit's Q8_K activations are copied into LDS,
+// both rows' blocks are requested at once, and act = silu(g) * u (the
+// vectorized silu except for the row tail the CPU runs through scalar expf)
+// leaves as agent-scope stores.  Each finished item counts for its unit.
+constexpr int GU_ROWS = 32;
 
 template <int MAXP>
 QWM_DEV void step_gateup(const StepArgs & a, int g, int G, const StepShared & S, uint8_t * smem) {
-    constexpr int RPW = GU_ROWS / 4;             // rows per wave per item, in groups of 4
-    static_assert(RPW % 4 == 0, "rows per wave come in groups of four");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int c = lane;                          // 64 chunks of 16 B per 2048-wide row
-    const int rho = scatter_row(lane >> 4);      // row of a 4-row group this lane's sums belong to
-    float (*s_act)[GU_ROWS] = reinterpret_cast<float (*)[GU_ROWS]>(smem);
+    const int m = lane & 7, rsub = lane >> 3;
+    uint32_t * s_x = reinterpret_cast<uint32_t *>(smem);          // [MAXP][SNB][XS]
     const int nb_r = (a.N + GU_ROWS - 1) / GU_ROWS, nb_s = a.shared ? (a.N_sh + GU_ROWS - 1) / GU_ROWS : 0;
     const int items = S.nu * nb_r + nb_s;
     constexpr size_t row_bytes = (size_t)SNB * 144;
+    constexpr int Q4 = SNB * XS / 4;                               // uint4 per token in LDS
     for (int item = g; item < items; item += G) {
         const bool shared = item >= S.nu * nb_r;
         const int u = shared ? S.nu : item / nb_r;
@@ -396,69 +393,34 @@ QWM_DEV void step_gateup(const StepArgs & a, int g, int G, const StepShared & S,
         const int n = U_.n;
         const uint8_t * gbase = shared ? a.sh_gate : a.gate + (size_t)S.uslot[u][0] * a.gate_slab;
         const uint8_t * ubase = shared ? a.sh_up : a.up + (size_t)S.uslot[u][1] * a.up_slab;
-        const int rb = blk * GU_ROWS, re = min(rb + GU_ROWS, rows);
-        const int r0 = rb + wave * RPW;
-        // rows past the unit's last one re-read the last row; their sums are dropped
-        auto row_ptr = [&](const uint8_t * base, int s) { return base + (size_t)min(r0 + s, rows - 1) * row_bytes; };
-        {
-            // activations first: vector-memory waits count in issue order, so
-            // the ring's loads must be the youngest for its waits to stay partial
-            ActChunk A[MAXP];
+        const int r = blk * GU_ROWS + wave * 8 + rsub;
+        const int rc = min(r, rows - 1);                           // rows past the unit's last re-read it; dropped
+        XBlk Gw[SNB], Uw[SNB];
+#pragma unroll
+        for (int b = 0; b < SNB; ++b) {
+            load_xblk(Gw[b], gbase + (size_t)rc * row_bytes + b * 144, m);
+            load_xblk(Uw[b], ubase + (size_t)rc * row_bytes + b * 144, m);
+        }
+        for (int q = tid; q < n * Q4; q += 256) {
+            const int i = q / Q4, o = q % Q4, b = o / (XS / 4), w4 = o % (XS / 4);
+            const int tok = shared ? U_.pair[i] : U_.pair[i] / a.k;
+            reinterpret_cast<uint4 *>(s_x)[q] =
+                reinterpret_cast<const uint4 *>(a.xq_x + (size_t)(tok * SNB + b) * XSP)[w4];
+        }
+        __syncthreads();
+        float gs[MAXP], us[MAXP];
+        q4k_dot8<SNB, MAXP>(gs, Gw, s_x, n, m);
+        q4k_dot8<SNB, MAXP>(us, Uw, s_x, n, m);
+        if (m == 0 && r < rows) {
 #pragma unroll
             for (int i = 0; i < MAXP; ++i)
                 if (i < n) {
-                    const int tok = shared ? U_.pair[i] : U_.pair[i] / a.k;
-                    load_act_chunk<32, 32>(A[i], a.xq_qs + (size_t)tok * SH, a.xq_d + (size_t)tok * SNB * 32,
-                                           a.xq_bs + (size_t)tok * SNB * 32, c);
+                    const float v = (r < rows - (rows & 15)) ? v_silu(gs[i]) * us[i] : gs[i] / (1.0f + expf(-gs[i])) * us[i];
+                    if (shared) st_agent(a.act_sh + (size_t)U_.pair[i] * rows + r, v);
+                    else st_agent(a.act + (size_t)U_.pair[i] * rows + r, v);
                 }
-            WChunkS Gb[GU_PF], Ub[GU_PF];
-#pragma unroll
-            for (int p = 0; p < GU_PF; ++p) {
-                load_w_chunk_s(Gb[p], row_ptr(gbase, p), c);
-                load_w_chunk_s(Ub[p], row_ptr(ubase, p), c);
-            }
-            // straight-line ring: every wait below is a partial one
-#pragma clang loop unroll(full)
-            for (int s0 = 0; s0 < RPW; s0 += 4) {
-                float pg[MAXP][4], pu[MAXP][4];
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int s = s0 + q, p = s % GU_PF;
-                    RowChunk RG, RU;
-                    decode_chunk_s(Gb[p], c, RG);
-                    decode_chunk_s(Ub[p], c, RU);
-                    if (s + GU_PF < RPW) {
-                        load_w_chunk_s(Gb[p], row_ptr(gbase, s + GU_PF), c);
-                        load_w_chunk_s(Ub[p], row_ptr(ubase, s + GU_PF), c);
-                    }
-#pragma unroll
-                    for (int i = 0; i < MAXP; ++i)
-                        if (i < n) {
-                            pg[i][q] = token_dot(RG, A[i]);
-                            pu[i][q] = token_dot(RU, A[i]);
-                        }
-                }
-                const int r = r0 + s0 + rho;
-#pragma unroll
-                for (int i = 0; i < MAXP; ++i) {
-                    if (i < n) {
-                        float gs, us;
-                        wave_sum_scatter8(pg[i], pu[i], gs, us);
-                        if ((lane & 15) == i && r < re)
-                            s_act[i][r - rb] = (r < rows - (rows & 15)) ? v_silu(gs) * us : gs / (1.0f + expf(-gs)) * us;
-                    }
-                }
-            }
         }
-        __syncthreads();
-        for (int q = tid; q < n * GU_ROWS; q += 256) {
-            const int i = q / GU_ROWS, r = rb + q % GU_ROWS;
-            if (r < re) {
-                if (shared) st_agent(a.act_sh + (size_t)U_.pair[i] * rows + r, s_act[i][r - rb]);
-                else st_agent(a.act + (size_t)U_.pair[i] * rows + r, s_act[i][r - rb]);
-            }
-        }
-        signal_count(a.gu_done + 32 * u);        // also orders s_act's reuse by the next item
+        signal_count(a.gu_done + 32 * u);        // also orders s_x's reuse by the next item
     }
 }
 
@@ -485,12 +447,8 @@ QWM_DEV void step_down(const StepArgs & a, int g, int G, const StepShared & S, u
     const int c8 = lane & 7, rsub = lane >> 3;
     const int U = S.nu + a.shared;
     const int nb_r = (a.N + GU_ROWS - 1) / GU_ROWS, nb_s = (a.N_sh + GU_ROWS - 1) / GU_ROWS;   // gate/up items per unit
-    int8_t (*s_qs)[MAX_NDOWN_S] = reinterpret_cast<int8_t (*)[MAX_NDOWN_S]>(smem);
-    float (*s_d)[MAX_NDOWN_S / QK_K] = reinterpret_cast<float (*)[MAX_NDOWN_S / QK_K]>(smem + MAXP * MAX_NDOWN_S);
-    int32_t (*s_bs)[MAX_NDOWN_S / 16] =
-        reinterpret_cast<int32_t (*)[MAX_NDOWN_S / 16]>(smem + MAXP * MAX_NDOWN_S + MAXP * (MAX_NDOWN_S / QK_K) * 4);
-    float (*s_ex)[DN_TR] = reinterpret_cast<float (*)[DN_TR]>(
-        smem + MAXP * (MAX_NDOWN_S + (MAX_NDOWN_S / QK_K) * 4 + (MAX_NDOWN_S / 16) * 4));
+    uint32_t * s_x = reinterpret_cast<uint32_t *>(smem);                        // [MAXP][NB][XS]
+    float (*s_ex)[DN_TR] = reinterpret_cast<float (*)[DN_TR]>(smem + (size_t)MAXP * NB * XS * 4);
     for (int item = g; item < U * ntiles; item += G) {
         const int u = item / ntiles, x = item % ntiles;
         const bool shared = u == S.nu;
@@ -501,30 +459,31 @@ QWM_DEV void step_down(const StepArgs & a, int g, int G, const StepShared & S, u
         const uint8_t * rp = base + (size_t)(h0 + wave * RPS + rsub) * row_bytes;   // row of step st: + 4 * RPS * st
         // weights first: vector-memory waits count in issue order, and these
         // do not depend on the activations
-        WChunkS Wb[PF][NB];
+        XBlk Wb[PF][NB];
 #pragma unroll
-        for (int p = 0; p < PF; ++p) load_row8<NB>(Wb[p], rp + (size_t)(4 * RPS * p) * row_bytes, c8);
+        for (int p = 0; p < PF; ++p)
+#pragma unroll
+            for (int b = 0; b < NB; ++b) load_xblk(Wb[p][b], rp + (size_t)(4 * RPS * p) * row_bytes + b * 144, c8);
         wait_count(a.gu_done + 32 * u, shared ? nb_s : nb_r, a.err, SPIN_LIMIT);   // the unit's activations are out
         for (int jb = wave; jb < n * NB; jb += 4) {
             const int i = jb / NB, b = jb % NB;
             const float * src = shared ? a.act_sh + (size_t)U_.pair[i] * (NB * QK_K)
                                        : a.act + (size_t)U_.pair[i] * (NB * QK_K);
-            quantize_block_q8K<false, true>(src + b * QK_K, &s_qs[i][b * QK_K], &s_d[i][b], &s_bs[i][b * 16], lane);
+            quantize_block_q8K_x<true>(src + b * QK_K, s_x + (i * NB + b) * XS, lane);
         }
         __syncthreads();
 #pragma clang loop unroll(full)
         for (int st = 0; st < NSTEP; ++st) {
             const int p = st % PF;
             float acc[MAXP];
-            row8_dots<NB, MAXP, MAX_NDOWN_S>(acc, Wb[p], n, &s_qs[0][0], &s_d[0][0], &s_bs[0][0], c8);
-            if (st + PF < NSTEP) load_row8<NB>(Wb[p], rp + (size_t)(4 * RPS * (st + PF)) * row_bytes, c8);
+            q4k_dot8<NB, MAXP>(acc, Wb[p], s_x, n, c8);
+            if (st + PF < NSTEP)
+#pragma unroll
+                for (int b = 0; b < NB; ++b) load_xblk(Wb[p][b], rp + (size_t)(4 * RPS * (st + PF)) * row_bytes + b * 144, c8);
             const int r = h0 + (st * 4 + wave) * RPS + rsub;
 #pragma unroll
             for (int i = 0; i < MAXP; ++i)
-                if (i < n) {
-                    const float sum = row8_sum(acc[i]);
-                    if (c8 == 0) s_ex[i][r - h0] = sum;
-                }
+                if (i < n && c8 == 0) s_ex[i][r - h0] = acc[i];
         }
         __syncthreads();
         for (int q = tid; q < n * (h1 - h0); q += 256) {
@@ -597,9 +556,9 @@ template <int NT, int NB_D>
 __global__ void __launch_bounds__(256) k_step(StepArgs a) {
     constexpr int MAXP = NT <= 1 ? 1 : NT <= 2 ? 2 : NT <= 4 ? 4 : 8;
     constexpr size_t router_bytes = (size_t)5 * 16 * RX_P * 4;
-    constexpr size_t down_bytes = (size_t)MAXP * (MAX_NDOWN_S + (MAX_NDOWN_S / QK_K) * 4 + (MAX_NDOWN_S / 16) * 4 +
-                                                  DN_TR * 4);
-    constexpr size_t smem_bytes = cmax(cmax(router_bytes, down_bytes), VhSmem<NT>::bytes);
+    constexpr size_t down_bytes = (size_t)MAXP * (NB_D * XS * 4 + DN_TR * 4);
+    constexpr size_t gateup_bytes = (size_t)MAXP * SNB * XS * 4;
+    constexpr size_t smem_bytes = cmax(cmax(cmax(router_bytes, down_bytes), gateup_bytes), VhSmem<NT>::bytes);
     __shared__ __align__(16) uint8_t smem[smem_bytes];
     __shared__ StepShared S;
     __shared__ uint32_t s_epoch;
@@ -672,8 +631,7 @@ bool step_plan(const qwm_moe_layer * L, const qwm_tensor * lm_head, int64_t T, S
     p.v_pv = take(sizeof(float) * MAX_STEP_WG * T);
     p.v_pi = take(sizeof(int32_t) * MAX_STEP_WG * T);
     p.lg = take(sizeof(float) * 32 * (p.moe.E + 1));
-    p.xq_d = take(sizeof(float) * 32 * T * SNB);
-    p.xq_bs = take(sizeof(int32_t) * 32 * T * SNB);
+    p.xq_x = take(sizeof(uint32_t) * XSP * T * SNB);
     p.bar = take(512 + 128 * BAR_GROUPS);     // top counter, epoch, error word, group counters at 512
     p.flags = take(sizeof(uint32_t) * 32 * MAX_STEP_WG);
     p.gu_done = take(128 * (MAX_PAIRS + 1));
@@ -744,9 +702,7 @@ int launch_step(const StepCall & c, const StepPlan & p, uint8_t * ws, hipStream_
     a.resid = c.resid; a.out = c.out;
     a.ids_out = c.ids_out; a.ids_ld = c.ids_ld; a.w_out = c.w_out; a.w_ld = c.w_ld;
     a.lg = reinterpret_cast<float *>(ws + p.lg);
-    a.xq_qs = reinterpret_cast<int8_t *>(ws + m.xq_qs);
-    a.xq_d = reinterpret_cast<float *>(ws + p.xq_d);
-    a.xq_bs = reinterpret_cast<int32_t *>(ws + p.xq_bs);
+    a.xq_x = reinterpret_cast<uint32_t *>(ws + p.xq_x);
     a.act = reinterpret_cast<float *>(ws + m.act); a.act_sh = reinterpret_cast<float *>(ws + m.act_sh);
     a.ex = reinterpret_cast<float *>(ws + m.ex); a.ex_sh = reinterpret_cast<float *>(ws + m.ex_sh);
     a.bar = reinterpret_cast<uint32_t *>(ws + p.bar);

@@ -875,7 +875,8 @@ struct MmidPrep {
     const int32_t * ids; size_t ids_nb1;    // bytes
     int K, ne11, T, n_ids, n_as, cap;       // cap: pairs per unit
     int q80;                                // Q8_0 weights: b as Q8_0 (d per 32) instead of Q8_K
-    int8_t * qs; float * d; int32_t * bs;   // [T*ne11] rows of Q8_K or Q8_0
+    int8_t * qs; float * d; int32_t * bs;   // [T*ne11] rows of Q8_0 (Q8_0 weights)
+    uint32_t * xq;                          // [T*ne11][K/256][XS] rows of Q8_K, exact-dot layout (Q4_K weights)
     Unit * units; int32_t * n_units; int32_t * ids_ws; int32_t * err;
 };
 
@@ -891,8 +892,7 @@ __global__ void __launch_bounds__(256) k_mmid_prep(MmidPrep a) {
         if (a.q80)
             quantize_q80_256(src + b * QK_K, a.qs + (size_t)row * a.K + b * QK_K, a.d + (size_t)row * (a.K / 32) + b * 8, lane);
         else
-            quantize_block_q8K(src + b * QK_K, a.qs + (size_t)row * a.K + b * QK_K, a.d + (size_t)row * nb + b,
-                               a.bs + (size_t)row * (a.K / 16) + b * 16, lane);
+            quantize_block_q8K_x(src + b * QK_K, a.xq + (size_t)(row * nb + b) * XS, lane);
     }
     if (blockIdx.x != 0 || wave != 0) return;
     const int P = a.T * a.n_ids;
@@ -940,9 +940,53 @@ struct MmidGemv {
     const uint8_t * as; size_t slab; size_t row_bytes;
     const Unit * units; const int32_t * n_units;
     const int8_t * qs; const float * d; const int32_t * bs;
+    const uint32_t * xq;
     int K, N, ne11, n_ids;
     float * dst; size_t dst_nb1, dst_nb2;
 };
+
+// Q4_K MUL_MAT_ID columns in ggml-CPU's exact float order (qwm_exact.h): a
+// workgroup owns 32 rows (4 waves x 8 rows, 8 lanes per row) of one unit;
+// the unit's Q8_K columns are copied into LDS first.
+template <int NB, int MAXP>
+__global__ void __launch_bounds__(256) k_mmid_x(MmidGemv a) {
+    __shared__ __align__(16) uint32_t s_x[MAXP * NB * XS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int m = lane & 7, rsub = lane >> 3;
+    const int u = blockIdx.y;
+    const int nu = *a.n_units;
+    const Unit U = a.units[u];
+    if (u >= nu) return;
+    const int n = U.n;
+    const uint8_t * base = a.as + (size_t)U.expert * a.slab;
+    const int r = blockIdx.x * 32 + wave * 8 + rsub;
+    const int rc = min(r, a.N - 1);
+    XBlk W[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) load_xblk(W[b], base + (size_t)rc * a.row_bytes + b * 144, m);
+    constexpr int Q4 = NB * XS / 4;
+    for (int q = tid; q < n * Q4; q += 256) {
+        const int i = q / Q4, o = q % Q4;
+        int p = U.pair[0];
+#pragma unroll
+        for (int qq = 1; qq < MAXP; ++qq) if (i == qq) p = U.pair[qq];
+        const int row = (p / a.n_ids) * a.ne11 + (p % a.n_ids) % a.ne11;
+        reinterpret_cast<uint4 *>(s_x)[q] = reinterpret_cast<const uint4 *>(a.xq + (size_t)row * NB * XS)[o];
+    }
+    __syncthreads();
+    float acc[MAXP];
+    q4k_dot8<NB, MAXP>(acc, W, s_x, n, m);
+    if (m == 0 && r < a.N) {
+#pragma unroll
+        for (int i = 0; i < MAXP; ++i)
+            if (i < n) {
+                const int p = U.pair[i];
+                float * o = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(a.dst) + (p / a.n_ids) * a.dst_nb2 +
+                                                      (p % a.n_ids) * a.dst_nb1);
+                o[r] = acc[i];
+            }
+    }
+}
 
 template <class F, int LPR, int MAXP>
 __global__ void __launch_bounds__(256) k_mmid(MmidGemv a) {
@@ -1010,6 +1054,7 @@ size_t mmid_workspace(int64_t K, int64_t T, int64_t ne11, int64_t n_ids) {
     take(sizeof(Unit) * T * n_ids);               // units
     take(sizeof(int32_t) * 4);                    // n_units, err
     take(sizeof(int32_t) * T * n_ids);            // ids copy
+    take(sizeof(uint32_t) * rows * (K / QK_K) * XS);   // Q8_K columns, exact-dot layout
     return o;
 }
 
@@ -1021,7 +1066,8 @@ int launch_mmid(const MmidArgs & a, uint8_t * ws, hipStream_t s) {
     auto take = [&](size_t bytes) { size_t at = o; o = align_up(o + bytes, 256); return at; };
     const size_t o_qs = take((size_t)rows * a.K), o_d = take(sizeof(float) * rows * (a.K / 32)),
                  o_bs = take(sizeof(int32_t) * rows * (a.K / 16)), o_u = take(sizeof(Unit) * a.T * a.n_ids),
-                 o_n = take(sizeof(int32_t) * 4), o_ids = take(sizeof(int32_t) * a.T * a.n_ids);
+                 o_n = take(sizeof(int32_t) * 4), o_ids = take(sizeof(int32_t) * a.T * a.n_ids),
+                 o_x = take(sizeof(uint32_t) * rows * (a.K / QK_K) * XS);
     MmidPrep pr;
     pr.b = a.b; pr.b_nb1 = a.b_nb1; pr.b_nb2 = a.b_nb2; pr.ids = a.ids; pr.ids_nb1 = a.ids_nb1;
     const int maxp = pow2_maxp(a.T);
@@ -1032,21 +1078,43 @@ int launch_mmid(const MmidArgs & a, uint8_t * ws, hipStream_t s) {
     pr.bs = reinterpret_cast<int32_t *>(ws + o_bs); pr.units = reinterpret_cast<Unit *>(ws + o_u);
     pr.n_units = reinterpret_cast<int32_t *>(ws + o_n); pr.err = pr.n_units + 1;
     pr.ids_ws = reinterpret_cast<int32_t *>(ws + o_ids);
+    pr.xq = reinterpret_cast<uint32_t *>(ws + o_x);
     const int nblk = (int)(rows * (a.K / QK_K));
     QWM_TIMED("mul_mat_id_prep", s, k_mmid_prep<<<dim3((unsigned)std::max(1, std::min(256, (nblk + 3) / 4))), 256, 0, s>>>(pr));
     MmidGemv g;
     g.as = a.as; g.slab = a.slab; g.row_bytes = q80 ? (size_t)(a.K / 32) * 34 : (size_t)(a.K / QK_K) * 144;
-    g.units = pr.units; g.n_units = pr.n_units; g.qs = pr.qs; g.d = pr.d; g.bs = pr.bs;
+    g.units = pr.units; g.n_units = pr.n_units; g.qs = pr.qs; g.d = pr.d; g.bs = pr.bs; g.xq = pr.xq;
     g.K = (int)a.K; g.N = (int)a.N; g.ne11 = (int)a.ne11; g.n_ids = (int)a.n_ids;
     g.dst = a.dst; g.dst_nb1 = a.dst_nb1; g.dst_nb2 = a.dst_nb2;
     const int lpr = lanes_per_row((int)a.K);
     if (lpr < 0) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: K > 2048 not tiled");
+    if (!q80) {
+        const dim3 gx((unsigned)((a.N + 31) / 32), (unsigned)(a.T * a.n_ids));
+#define QWM_MMIDX(NB_)                                                              \
+        case NB_:                                                                   \
+            switch (maxp) {                                                         \
+                case 1: k_mmid_x<NB_, 1><<<gx, 256, 0, s>>>(g); break;              \
+                case 2: k_mmid_x<NB_, 2><<<gx, 256, 0, s>>>(g); break;              \
+                case 4: k_mmid_x<NB_, 4><<<gx, 256, 0, s>>>(g); break;              \
+                default: k_mmid_x<NB_, 8><<<gx, 256, 0, s>>>(g); break;             \
+            }                                                                       \
+            break;
+        prof_begin("mul_mat_id", s);
+        switch (a.K / QK_K) {
+            QWM_MMIDX(1) QWM_MMIDX(2) QWM_MMIDX(3) QWM_MMIDX(4)
+            QWM_MMIDX(5) QWM_MMIDX(6) QWM_MMIDX(7) QWM_MMIDX(8)
+            default: return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: K > 2048 not tiled");
+        }
+        prof_end("mul_mat_id", s);
+#undef QWM_MMIDX
+        QWM_HIP_CHECK(hipGetLastError());
+        return QWM_OK;
+    }
     const int tile = 4 * GEMV_STEPS * (WAVE / lpr);
     dim3 grid((unsigned)((a.N + tile - 1) / tile), (unsigned)(a.T * a.n_ids));
 #define QWM_MMID(LPR_, P_)                                                          \
     do {                                                                            \
-        if (q80) k_mmid<FmtQ80, LPR_, P_><<<grid, 256, 0, s>>>(g);                  \
-        else k_mmid<FmtQ4K, LPR_, P_><<<grid, 256, 0, s>>>(g);                      \
+        k_mmid<FmtQ80, LPR_, P_><<<grid, 256, 0, s>>>(g);                           \
     } while (0)
 #define QWM_MMID_P(LPR_)                                    \
     switch (maxp) {                                         \

@@ -163,3 +163,64 @@ QWM_DEV void q4k_dot8(float (&out)[MAXP], const XBlk (&W)[NB], const uint32_t * 
 }
 
 }  // namespace qwm
+
+namespace qwm {
+
+// Q8_0 x Q8_0 row dots in ggml-CPU's exact float order: the x86
+// ggml_vec_dot_q8_0_q8_0 (ggml-cpu/arch/x86/quants.c:1389-1406) keeps eight
+// fp32 lanes, lane m adding fma(fp16(x.d) * fp16(y.d), (float)(dot of
+// elements 4m .. 4m+3 of the block), acc[m]) block after block, then
+// hsum8.  Lane m of a row's 8-lane group plays CPU lane m.
+//
+// A pair of 34-byte blocks is 17 dwords: lane m takes dwords m, m+1 (the even
+// block's qs bytes 4m..4m+3 sit 2 bytes into dword m), 9+m (the odd block's),
+// and the scale dwords 0 (low half) and 8 (high half).  Activations (Q8_0) in
+// LDS: xq [MAXP][kq dwords], xd [MAXP][kd] (natural layout: lane m reads dword
+// 8b + m of block b).
+template <int NPAIR, int MAXP>
+QWM_DEV void q80_dot8(float (&out)[MAXP], const uint8_t * row, const uint32_t * xq, const float * xd, int kq, int kd,
+                      int n, int m) {
+    float acc[MAXP];
+#pragma unroll
+    for (int i = 0; i < MAXP; ++i) acc[i] = 0.f;
+    const uint32_t * rw = reinterpret_cast<const uint32_t *>(row);
+    constexpr int CH = NPAIR % 8 == 0 ? 8 : NPAIR % 4 == 0 ? 4 : NPAIR;   // pairs per chunk, dividing NPAIR
+    static_assert(NPAIR % CH == 0, "chunk must divide the row");
+#pragma unroll
+    for (int c0 = 0; c0 < NPAIR; c0 += CH) {
+        uint32_t w0[CH], w1[CH], w2[CH], s0[CH], s1[CH];
+#pragma unroll
+        for (int k = 0; k < CH; ++k) {
+            const uint32_t * pr = rw + 17 * (c0 + k);
+            w0[k] = pr[m]; w1[k] = pr[m + 1]; w2[k] = pr[9 + m]; s0[k] = pr[0]; s1[k] = pr[8];
+        }
+#pragma unroll
+        for (int k = 0; k < CH; ++k) {
+            const int b = 2 * (c0 + k);
+            const uint32_t we = __builtin_amdgcn_alignbit(w1[k], w0[k], 16);
+            const float de = fp16_to_f32((uint16_t)(s0[k] & 0xffff));
+            const float dd = fp16_to_f32((uint16_t)(s1[k] >> 16));
+#pragma unroll
+            for (int i = 0; i < MAXP; ++i) {
+                if (i < n) {
+                    const uint32_t xe = xq[i * kq + 8 * b + m], xo = xq[i * kq + 8 * b + 8 + m];
+                    const float dxe = xd[i * kd + b], dxo = xd[i * kd + b + 1];
+                    acc[i] = __builtin_fmaf(de * dxe, (float)dot4(we, xe, 0), acc[i]);
+                    acc[i] = __builtin_fmaf(dd * dxo, (float)dot4(w2[k], xo, 0), acc[i]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < MAXP; ++i) {
+        if (i < n) {
+            const float t = acc[i] + dpp_f<0x12C>(acc[i]);
+            const float u = t + dpp_f<0x12E>(t);
+            out[i] = u + dpp_f<0x12F>(u);
+        } else {
+            out[i] = 0.f;
+        }
+    }
+}
+
+}  // namespace qwm

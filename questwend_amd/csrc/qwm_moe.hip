@@ -300,10 +300,6 @@ __global__ void __launch_bounds__(256) k_route(RouteKArgs a) {
     }
 }
 
-// Wave steps per GEMV tile: each wave issues the weight loads of GEMV_STEPS
-// row steps before it computes any of them.
-constexpr int GEMV_STEPS = 4;
-
 // ---------------------------------------------------------------------
 // gate/up + SwiGLU: act[p][r] = silu(gate_e[r] . x_t) * (up_e[r] . x_t)
 // grid: (row tiles, unit slots [+1 for the shared expert]), block 256.
@@ -358,80 +354,6 @@ QWM_DEV bool load_unit(UnitView<MAXP> & V, const Unit * units, const int32_t * n
     return true;
 }
 
-template <class F, int LPR, int MAXP>
-__global__ void __launch_bounds__(256) k_gateup(GateUpArgs a) {
-    constexpr int RPI = WAVE / LPR;     // rows per wave step
-    constexpr int NIT = GEMV_STEPS;     // steps per wave; all loads issued up front
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int c = lane % LPR, rsub = lane / LPR;
-    const int u = blockIdx.y;
-    const bool shared = u == a.unit_slots;
-    UnitView<MAXP> U;
-    int nu;
-    if (!load_unit<MAXP>(U, a.units, a.n_units, a.uslot, a.slot_g, a.slot_u, u, shared, a.T, 0, 1, nu)) return;
-    const int n = U.n;
-    const int rows = shared ? a.N_sh : a.N;
-    const size_t row_bytes = F::row_bytes(a.H);
-    const uint8_t * gbase;
-    const uint8_t * ubase;
-    if (shared) { gbase = a.sh_gate; ubase = a.sh_up; }
-    else {
-        gbase = a.gate + (size_t)U.slot[0] * a.gate_slab;
-        ubase = a.up + (size_t)U.slot[1] * a.up_slab;
-    }
-    const int C = a.H / 32;
-    const bool active = c < C;
-    const int r_begin = (blockIdx.x * 4 + wave) * (NIT * RPI);
-    if (r_begin >= rows) return;
-    typename F::W G[NIT], Uw[NIT];
-#pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-        const int r = r_begin + it * RPI + rsub;
-        if (active && r < rows) {
-            F::load_w(G[it], gbase + (size_t)r * row_bytes, c);
-            F::load_w(Uw[it], ubase + (size_t)r * row_bytes, c);
-        }
-    }
-    typename F::A A[MAXP];
-#pragma unroll
-    for (int i = 0; i < MAXP; ++i) {
-        if (i < n && active) {
-            const int tok = shared ? U.pair[i] : U.pair[i] / a.k;
-            F::load_a(A[i], a.xq_qs + (size_t)tok * a.H, a.xq_d + (size_t)tok * F::d_per_row(a.H),
-                      a.xq_bs + (size_t)tok * (a.H / 16), a.H, c);
-        }
-    }
-#pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-        const int r = r_begin + it * RPI + rsub;
-        const bool valid = active && r < rows;
-        float g[MAXP], up[MAXP];
-#pragma unroll
-        for (int i = 0; i < MAXP; ++i) {
-            g[i] = 0.f; up[i] = 0.f;
-            if (i < n) {                      // n is uniform: empty token slots cost nothing
-                if (valid) {
-                    g[i] = F::dot(G[it], A[i], c);
-                    up[i] = F::dot(Uw[it], A[i], c);
-                }
-                g[i] = halves_sum<LPR>(g[i]);
-                up[i] = halves_sum<LPR>(up[i]);
-            }
-        }
-        if (r < rows) {
-#pragma unroll
-            for (int i = 0; i < MAXP; ++i) {
-                if (i < n && c == i) {
-                    const float v = (r < rows - (rows & 15)) ? v_silu(g[i]) * up[i]
-                                                            : g[i] / (1.0f + expf(-g[i])) * up[i];
-                    if (shared) a.act_sh[(size_t)U.pair[i] * rows + r] = v;
-                    else a.act[(size_t)U.pair[i] * rows + r] = v;
-                }
-            }
-        }
-    }
-}
-
 // Q4_K gate/up in ggml-CPU's exact float order (qwm_exact.h): 8 lanes per
 // row, a workgroup owns 32 consecutive rows (4 waves x 8 rows) of one unit.
 // The unit's Q8_K activations are copied into LDS first; SwiGLU then sees the
@@ -476,6 +398,52 @@ __global__ void __launch_bounds__(256) k_gateup_x(GateUpArgs a) {
     float g[MAXP], up[MAXP];
     q4k_dot8<NB, MAXP>(g, G, s_x, n, m);
     q4k_dot8<NB, MAXP>(up, W, s_x, n, m);
+    if (m == 0 && r < rows) {
+#pragma unroll
+        for (int i = 0; i < MAXP; ++i)
+            if (i < n) {
+                const float v = (r < rows - (rows & 15)) ? v_silu(g[i]) * up[i] : g[i] / (1.0f + expf(-g[i])) * up[i];
+                if (shared) a.act_sh[(size_t)U.pair[i] * rows + r] = v;
+                else a.act[(size_t)U.pair[i] * rows + r] = v;
+            }
+    }
+}
+
+// The Q8_0 form of k_gateup_x: ggml's Q8_0 dot order (q80_dot8), the unit's
+// Q8_0 activations in LDS.
+template <int NPAIR, int MAXP>
+__global__ void __launch_bounds__(256) k_gateup_x80(GateUpArgs a) {
+    constexpr int K = NPAIR * 64;
+    __shared__ __align__(16) uint32_t s_q[MAXP * K / 4];
+    __shared__ float s_d[MAXP * K / 32];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int m = lane & 7, rsub = lane >> 3;
+    const int u = blockIdx.y;
+    const bool shared = u == a.unit_slots;
+    UnitView<MAXP> U;
+    int nu;
+    if (!load_unit<MAXP>(U, a.units, a.n_units, a.uslot, a.slot_g, a.slot_u, u, shared, a.T, 0, 1, nu)) return;
+    const int n = U.n;
+    const int rows = shared ? a.N_sh : a.N;
+    const int r = blockIdx.x * GUX_ROWS + wave * 8 + rsub;
+    if (blockIdx.x * GUX_ROWS >= rows) return;
+    const size_t row_bytes = (size_t)NPAIR * 68;
+    const uint8_t * gbase = shared ? a.sh_gate : a.gate + (size_t)U.slot[0] * a.gate_slab;
+    const uint8_t * ubase = shared ? a.sh_up : a.up + (size_t)U.slot[1] * a.up_slab;
+    const int rc = min(r, rows - 1);
+    for (int q = tid; q < n * (K / 16); q += 256) {
+        const int i = q / (K / 16), o = q % (K / 16);
+        int pi = U.pair[0];              // U.pair[i] by selects (a dynamic index would put U in scratch)
+#pragma unroll
+        for (int qq = 1; qq < MAXP; ++qq) if (i == qq) pi = U.pair[qq];
+        const int t = shared ? pi : pi / a.k;
+        reinterpret_cast<uint4 *>(s_q)[i * (K / 16) + o] = reinterpret_cast<const uint4 *>(a.xq_qs + (size_t)t * K)[o];
+        if (o < K / 32) s_d[i * (K / 32) + o] = a.xq_d[(size_t)t * (K / 32) + o];
+    }
+    __syncthreads();
+    float g[MAXP], up[MAXP];
+    q80_dot8<NPAIR, MAXP>(g, gbase + (size_t)rc * row_bytes, s_q, s_d, K / 4, K / 32, n, m);
+    q80_dot8<NPAIR, MAXP>(up, ubase + (size_t)rc * row_bytes, s_q, s_d, K / 4, K / 32, n, m);
     if (m == 0 && r < rows) {
 #pragma unroll
         for (int i = 0; i < MAXP; ++i)
@@ -540,8 +508,8 @@ QWM_DEV float combine_one(const DownArgs & a, int t, int h) {
     return s;
 }
 
-// Rows go 8 lanes each (load_row8 / row8_dots, NB = FFN width / 256 Q4_K
-// blocks per row): a workgroup owns a tile of 32 rows, one wave step each.
+// Rows go 8 lanes each (q4k_dot8, NB = FFN width / 256 Q4_K blocks per
+// row): a workgroup owns a tile of 32 rows, one wave step each.
 template <int NB, int MAXP>
 __global__ void __launch_bounds__(256) k_down_q4k(DownArgs a) {
     constexpr int RPS = 8;                   // rows per wave
@@ -596,9 +564,10 @@ template <int NB, int MAXP>
 __global__ void __launch_bounds__(256) k_down_q80(DownArgs a) {
     constexpr int RPS = 8;                   // rows per wave
     constexpr int TILE = 4 * RPS;
-    constexpr size_t row_bytes = (size_t)NB * 8 * 34;
-    __shared__ __align__(16) int8_t s_qs[MAXP][MAX_NDOWN];
-    __shared__ float s_d[MAXP][MAX_NDOWN / 32];
+    constexpr int K = NB * QK_K;             // FFN width
+    constexpr size_t row_bytes = (size_t)(K / 32) * 34;
+    __shared__ __align__(16) uint32_t s_q[MAXP * K / 4];
+    __shared__ float s_d[MAXP * K / 32];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int c8 = lane & 7, rsub = lane >> 3;
     const int u = blockIdx.y;
@@ -610,39 +579,24 @@ __global__ void __launch_bounds__(256) k_down_q80(DownArgs a) {
     const uint8_t * base = shared ? a.sh_down : a.down + (size_t)U.slot[0] * a.down_slab;
     const int row0 = blockIdx.x * TILE;
     const int r = row0 + wave * RPS + rsub;
-    W80 W[NB];
     const uint8_t * rowp = base + (size_t)min(r, a.H - 1) * row_bytes;
-#pragma unroll
-    for (int q = 0; q < NB; ++q) load_w80(W[q], rowp, 8 * q + c8);
     for (int jb = wave; jb < n * NB; jb += 4) {
         const int i = jb / NB, b = jb % NB;
         int pi = U.pair[0];              // U.pair[i] by selects (a dynamic index would put U in scratch)
 #pragma unroll
         for (int q = 1; q < MAXP; ++q) if (i == q) pi = U.pair[q];
-        const float * src = shared ? a.act_sh + (size_t)pi * (NB * QK_K) : a.act + (size_t)pi * (NB * QK_K);
-        quantize_q80_256(src + b * QK_K, &s_qs[i][b * QK_K], &s_d[i][b * 8], lane);
+        const float * src = shared ? a.act_sh + (size_t)pi * K : a.act + (size_t)pi * K;
+        quantize_q80_256(src + b * QK_K, reinterpret_cast<int8_t *>(s_q + i * (K / 4)) + b * QK_K,
+                         s_d + i * (K / 32) + b * 8, lane);
     }
     __syncthreads();
     float acc[MAXP];
-#pragma unroll
-    for (int i = 0; i < MAXP; ++i) acc[i] = 0.f;
-#pragma unroll
-    for (int q = 0; q < NB; ++q)
-#pragma unroll
-        for (int i = 0; i < MAXP; ++i)
-            if (i < n) {
-                A80 A;
-                load_a80(A, s_qs[i], s_d[i], 8 * q + c8);
-                acc[i] = dot80(W[q], A, 8 * q + c8, acc[i]);
-            }
+    q80_dot8<K / 64, MAXP>(acc, rowp, s_q, s_d, K / 4, K / 32, n, c8);
 #pragma unroll
     for (int i = 0; i < MAXP; ++i)
-        if (i < n) {
-            const float sum = row8_sum(acc[i]);
-            if (c8 == 0 && r < a.H) {
-                if (shared) st_agent(a.ex_sh + (size_t)U.pair[i] * a.H + r, sum);
-                else st_agent(a.ex + (size_t)U.pair[i] * a.H + r, sum);
-            }
+        if (i < n && c8 == 0 && r < a.H) {
+            if (shared) st_agent(a.ex_sh + (size_t)U.pair[i] * a.H + r, acc[i]);
+            else st_agent(a.ex + (size_t)U.pair[i] * a.H + r, acc[i]);
         }
     if (!last_workgroup(a.tile_counters + blockIdx.x, nu + a.shared)) return;
     for (int q = tid; q < a.T * TILE; q += 256) {
@@ -733,23 +687,6 @@ int launch_route(const RouteArgs & a, const MoePlan & p, uint8_t * ws, int32_t *
     return QWM_OK;
 }
 
-template <class F, int LPR>
-static void launch_gateup_lpr(const GateUpArgs & g, int maxp, dim3 grid, hipStream_t s) {
-    switch (maxp) {
-        case 1: k_gateup<F, LPR, 1><<<grid, 256, 0, s>>>(g); break;
-        case 2: k_gateup<F, LPR, 2><<<grid, 256, 0, s>>>(g); break;
-        case 4: k_gateup<F, LPR, 4><<<grid, 256, 0, s>>>(g); break;
-        default: k_gateup<F, LPR, 8><<<grid, 256, 0, s>>>(g); break;
-    }
-}
-template <class F>
-static void launch_gateup_f(const GateUpArgs & g, int lpr, int maxp, dim3 grid, hipStream_t s) {
-    switch (lpr) {
-        case 16: launch_gateup_lpr<F, 16>(g, maxp, grid, s); break;
-        case 32: launch_gateup_lpr<F, 32>(g, maxp, grid, s); break;
-        default: launch_gateup_lpr<F, 64>(g, maxp, grid, s); break;
-    }
-}
 template <int NB>
 static void launch_gateup_x_nb(const GateUpArgs & g, int maxp, dim3 grid, hipStream_t s) {
     switch (maxp) {
@@ -772,6 +709,28 @@ static bool launch_gateup_x(const GateUpArgs & g, int nb, int maxp, dim3 grid, h
         default: return false;
     }
 }
+template <int NPAIR>
+static void launch_gateup_x80_np(const GateUpArgs & g, int maxp, dim3 grid, hipStream_t s) {
+    switch (maxp) {
+        case 1: k_gateup_x80<NPAIR, 1><<<grid, 256, 0, s>>>(g); break;
+        case 2: k_gateup_x80<NPAIR, 2><<<grid, 256, 0, s>>>(g); break;
+        case 4: k_gateup_x80<NPAIR, 4><<<grid, 256, 0, s>>>(g); break;
+        default: k_gateup_x80<NPAIR, 8><<<grid, 256, 0, s>>>(g); break;
+    }
+}
+static bool launch_gateup_x80(const GateUpArgs & g, int npair, int maxp, dim3 grid, hipStream_t s) {
+    switch (npair) {
+        case 4: launch_gateup_x80_np<4>(g, maxp, grid, s); return true;
+        case 8: launch_gateup_x80_np<8>(g, maxp, grid, s); return true;
+        case 12: launch_gateup_x80_np<12>(g, maxp, grid, s); return true;
+        case 16: launch_gateup_x80_np<16>(g, maxp, grid, s); return true;
+        case 20: launch_gateup_x80_np<20>(g, maxp, grid, s); return true;
+        case 24: launch_gateup_x80_np<24>(g, maxp, grid, s); return true;
+        case 28: launch_gateup_x80_np<28>(g, maxp, grid, s); return true;
+        case 32: launch_gateup_x80_np<32>(g, maxp, grid, s); return true;
+        default: return false;
+    }
+}
 template <int NB>
 static void launch_down_nb(const DownArgs & d, bool q80, int maxp, dim3 grid, hipStream_t s) {
     if (q80) {
@@ -791,13 +750,6 @@ static void launch_down_nb(const DownArgs & d, bool q80, int maxp, dim3 grid, hi
     }
 }
 
-static int lanes_per_row(int K) {
-    const int C = K / 32;          // 16-byte chunks per row
-    if (C > 64) return -1;         // K > 2048 is not tiled here
-    int l = 16;
-    while (l < C) l <<= 1;
-    return l;
-}
 static int pow2_maxp(int64_t T) { return T <= 1 ? 1 : T <= 2 ? 2 : T <= 4 ? 4 : 8; }
 
 int launch_experts(const ExpertArgs & a, const MoePlan & p, uint8_t * ws, hipStream_t s) {
@@ -822,14 +774,11 @@ int launch_experts(const ExpertArgs & a, const MoePlan & p, uint8_t * ws, hipStr
     g.act = reinterpret_cast<float *>(ws + p.act);
     g.act_sh = reinterpret_cast<float *>(ws + p.act_sh);
     g.H = (int)p.H; g.N = (int)p.N; g.N_sh = (int)p.N_sh; g.k = (int)p.k; g.T = (int)p.T;
-    const int lg = lanes_per_row((int)p.H);
-    if (lg < 0) return fail(QWM_ERR_UNSUPPORTED, "hidden size > 2048 not tiled");
+    if (p.H > 2048) return fail(QWM_ERR_UNSUPPORTED, "hidden size > 2048 not tiled");
     const int rows_g = (int)std::max(p.N, p.N_sh);
-    const int tile_g = 4 * GEMV_STEPS * (WAVE / lg);
-    dim3 grid_g((rows_g + tile_g - 1) / tile_g, grid_y);
     prof_begin("gate_up", s);
-    if (q80) launch_gateup_f<FmtQ80>(g, lg, maxp, grid_g, s);
-    else if (!launch_gateup_x(g, (int)(p.H / QK_K), maxp, dim3((rows_g + GUX_ROWS - 1) / GUX_ROWS, grid_y), s))
+    const dim3 grid_x((rows_g + GUX_ROWS - 1) / GUX_ROWS, grid_y);
+    if (q80 ? !launch_gateup_x80(g, (int)(p.H / 64), maxp, grid_x, s) : !launch_gateup_x(g, (int)(p.H / QK_K), maxp, grid_x, s))
         return fail(QWM_ERR_UNSUPPORTED, "hidden size not instantiated for the exact gate/up");
     prof_end("gate_up", s);
 
@@ -988,59 +937,43 @@ __global__ void __launch_bounds__(256) k_mmid_x(MmidGemv a) {
     }
 }
 
-template <class F, int LPR, int MAXP>
-__global__ void __launch_bounds__(256) k_mmid(MmidGemv a) {
-    constexpr int RPI = WAVE / LPR;
-    constexpr int NIT = GEMV_STEPS;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// The Q8_0 form of k_mmid_x: ggml's Q8_0 dot order, the unit's Q8_0 columns in LDS.
+template <int NPAIR, int MAXP>
+__global__ void __launch_bounds__(256) k_mmid_x80(MmidGemv a) {
+    constexpr int K = NPAIR * 64;
+    __shared__ __align__(16) uint32_t s_q[MAXP * K / 4];
+    __shared__ float s_d[MAXP * K / 32];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int m = lane & 7, rsub = lane >> 3;
     const int u = blockIdx.y;
-    if (u >= *a.n_units) return;
-    const Unit & U = a.units[u];
+    const int nu = *a.n_units;
+    const Unit U = a.units[u];
+    if (u >= nu) return;
     const int n = U.n;
-    const int c = lane % LPR, rsub = lane / LPR;
-    const int C = a.K / 32;
-    const bool active = c < C;
     const uint8_t * base = a.as + (size_t)U.expert * a.slab;
-    const int r_begin = (blockIdx.x * 4 + wave) * (NIT * RPI);
-    if (r_begin >= a.N) return;
-    typename F::W W[NIT];
+    const int r = blockIdx.x * 32 + wave * 8 + rsub;
+    const int rc = min(r, a.N - 1);
+    for (int q = tid; q < n * (K / 16); q += 256) {
+        const int i = q / (K / 16), o = q % (K / 16);
+        int p = U.pair[0];
 #pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-        const int r = r_begin + it * RPI + rsub;
-        if (active && r < a.N) F::load_w(W[it], base + (size_t)r * a.row_bytes, c);
+        for (int qq = 1; qq < MAXP; ++qq) if (i == qq) p = U.pair[qq];
+        const int row = (p / a.n_ids) * a.ne11 + (p % a.n_ids) % a.ne11;
+        reinterpret_cast<uint4 *>(s_q)[i * (K / 16) + o] = reinterpret_cast<const uint4 *>(a.qs + (size_t)row * K)[o];
+        if (o < K / 32) s_d[i * (K / 32) + o] = a.d[(size_t)row * (K / 32) + o];
     }
-    typename F::A A[MAXP];
+    __syncthreads();
+    float acc[MAXP];
+    q80_dot8<NPAIR, MAXP>(acc, base + (size_t)rc * a.row_bytes, s_q, s_d, K / 4, K / 32, n, m);
+    if (m == 0 && r < a.N) {
 #pragma unroll
-    for (int i = 0; i < MAXP; ++i)
-        if (i < n && active) {
-            const int p = U.pair[i];
-            const int row = (p / a.n_ids) * a.ne11 + (p % a.n_ids) % a.ne11;
-            F::load_a(A[i], a.qs + (size_t)row * a.K, a.d + (size_t)row * F::d_per_row(a.K), a.bs + (size_t)row * (a.K / 16),
-                      a.K, c);
-        }
-#pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-        const int r = r_begin + it * RPI + rsub;
-        const bool valid = active && r < a.N;
-        float acc[MAXP];
-#pragma unroll
-        for (int i = 0; i < MAXP; ++i) {
-            acc[i] = 0.f;
+        for (int i = 0; i < MAXP; ++i)
             if (i < n) {
-                if (valid) acc[i] = F::dot(W[it], A[i], c);
-                acc[i] = lane_sum<LPR>(acc[i]);
+                const int p = U.pair[i];
+                float * o = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(a.dst) + (p / a.n_ids) * a.dst_nb2 +
+                                                      (p % a.n_ids) * a.dst_nb1);
+                o[r] = acc[i];
             }
-        }
-        if (r < a.N) {
-#pragma unroll
-            for (int i = 0; i < MAXP; ++i)
-                if (i < n && c == i) {
-                    const int p = U.pair[i];
-                    float * o = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(a.dst) + (p / a.n_ids) * a.dst_nb2 +
-                                                          (p % a.n_ids) * a.dst_nb1);
-                    o[r] = acc[i];
-                }
-        }
     }
 }
 
@@ -1086,8 +1019,7 @@ int launch_mmid(const MmidArgs & a, uint8_t * ws, hipStream_t s) {
     g.units = pr.units; g.n_units = pr.n_units; g.qs = pr.qs; g.d = pr.d; g.bs = pr.bs; g.xq = pr.xq;
     g.K = (int)a.K; g.N = (int)a.N; g.ne11 = (int)a.ne11; g.n_ids = (int)a.n_ids;
     g.dst = a.dst; g.dst_nb1 = a.dst_nb1; g.dst_nb2 = a.dst_nb2;
-    const int lpr = lanes_per_row((int)a.K);
-    if (lpr < 0) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: K > 2048 not tiled");
+    if (a.K > 2048) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: K > 2048 not tiled");
     if (!q80) {
         const dim3 gx((unsigned)((a.N + 31) / 32), (unsigned)(a.T * a.n_ids));
 #define QWM_MMIDX(NB_)                                                              \
@@ -1110,28 +1042,24 @@ int launch_mmid(const MmidArgs & a, uint8_t * ws, hipStream_t s) {
         QWM_HIP_CHECK(hipGetLastError());
         return QWM_OK;
     }
-    const int tile = 4 * GEMV_STEPS * (WAVE / lpr);
-    dim3 grid((unsigned)((a.N + tile - 1) / tile), (unsigned)(a.T * a.n_ids));
-#define QWM_MMID(LPR_, P_)                                                          \
-    do {                                                                            \
-        k_mmid<FmtQ80, LPR_, P_><<<grid, 256, 0, s>>>(g);                           \
-    } while (0)
-#define QWM_MMID_P(LPR_)                                    \
-    switch (maxp) {                                         \
-        case 1: QWM_MMID(LPR_, 1); break;                   \
-        case 2: QWM_MMID(LPR_, 2); break;                   \
-        case 4: QWM_MMID(LPR_, 4); break;                   \
-        default: QWM_MMID(LPR_, 8); break;                  \
-    }
+    const dim3 gx((unsigned)((a.N + 31) / 32), (unsigned)(a.T * a.n_ids));
+#define QWM_MMIDX80(NP_)                                                            \
+    case NP_:                                                                       \
+        switch (maxp) {                                                             \
+            case 1: k_mmid_x80<NP_, 1><<<gx, 256, 0, s>>>(g); break;                \
+            case 2: k_mmid_x80<NP_, 2><<<gx, 256, 0, s>>>(g); break;                \
+            case 4: k_mmid_x80<NP_, 4><<<gx, 256, 0, s>>>(g); break;                \
+            default: k_mmid_x80<NP_, 8><<<gx, 256, 0, s>>>(g); break;               \
+        }                                                                           \
+        break;
     prof_begin("mul_mat_id", s);
-    switch (lpr) {
-        case 16: QWM_MMID_P(16); break;
-        case 32: QWM_MMID_P(32); break;
-        default: QWM_MMID_P(64); break;
+    switch (a.K / 64) {                       // pairs of Q8_0 blocks per row
+        QWM_MMIDX80(4) QWM_MMIDX80(8) QWM_MMIDX80(12) QWM_MMIDX80(16)
+        QWM_MMIDX80(20) QWM_MMIDX80(24) QWM_MMIDX80(28) QWM_MMIDX80(32)
+        default: return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: K > 2048 not tiled");
     }
     prof_end("mul_mat_id", s);
-#undef QWM_MMID_P
-#undef QWM_MMID
+#undef QWM_MMIDX80
     QWM_HIP_CHECK(hipGetLastError());
     return QWM_OK;
 }

@@ -429,7 +429,7 @@ QWM_DEV void step_gateup(const StepArgs & a, int g, int G, const StepShared & S,
 // (whole 32-row lines); items (unit, tile) go to workgroups g, g + G, ...
 // The workgroup requests the tile's first weight rows, quantizes the unit's
 // activations to Q8_K in LDS and streams the rest of the tile, 8 lanes per
-// row (load_row8 / row8_dots), outputs collected in LDS and written as whole
+// row (q4k_dot8), outputs collected in LDS and written as whole
 // lines; then it takes the tile's ticket, and the last of the U units
 // combines the tile for every token (runtime.cpp:3815-3817 for T == 1,
 // 4544-4550 for T > 1; then the shared expert and the residual).

@@ -1,6 +1,6 @@
 """GPU parity of the decode loop over stacked MoE blocks (qwm_moe_decode:
 x = x + MoE_l(x) for every layer, slots remapped on the device from per-layer
-tables) against the oracle applied layer by layer (bit for bit with Q4_K
+tables) against the oracle applied layer by layer (bit for bit, Q4_K and Q8_0
 slabs), and bit for bit against the same layers through
 qwm_moe_block_resident one call at a time."""
 import numpy as np
@@ -70,8 +70,7 @@ def test_decode_layers(dev, T, n_layers, wtype):
     err = rel_err(got, exp)
     print(f"decode T={T} layers={n_layers} {wtype}: rel err {err:.3e}")
     assert err < TOL
-    if wtype == "q4_K":
-        assert np.array_equal(got.view(np.uint32), exp.view(np.uint32)), "Q4_K decode loop not bit-exact"
+    assert np.array_equal(got.view(np.uint32), exp.view(np.uint32)), f"{wtype} decode loop not bit-exact"
     assert np.array_equal(got.view(np.uint32), a.cpu().numpy().view(np.uint32)), "loop and per-block calls differ"
 
 

@@ -1,11 +1,10 @@
 """GPU parity of the MoE block against the oracle (ggml-CPU restated), through
 the C ABI of libqwmoe.  Expert ids and routing weights must be bit-exact
-(the router reproduces the CPU's floating-point order).  With Q4_K slabs the
-expert GEMVs also follow ggml's x86 float order, so block outputs and
-MUL_MAT_ID results must equal the oracle bit for bit (with a shared expert:
-within 1e-6, its sigmoid gate runs through the device expf instead of libm's).
-Q8_0 slabs keep the 1e-3 bar of the north star (block sums are exact
-integers; the fp32 order across blocks differs)."""
+(the router reproduces the CPU's floating-point order).  The expert GEMVs
+follow ggml's x86 float order for Q4_K and Q8_0 slabs alike, so block outputs
+and MUL_MAT_ID results must equal the oracle bit for bit (with a shared
+expert: within 1e-6, its sigmoid gate runs through the device expf instead of
+libm's)."""
 import numpy as np
 import pytest
 
@@ -118,11 +117,10 @@ def test_moe_block_parity(dev, cfg):
     assert err < TOL
     for t in range(T):
         assert rel_err(got[t], exp[t]) < TOL
-    if cfg.get("wtype", "q4_K") == "q4_K":
-        if cfg["shared"]:
-            assert err < 1e-6
-        else:
-            assert np.array_equal(bits(got), bits(exp)), "Q4_K block output not bit-exact"
+    if cfg["shared"]:
+        assert err < 1e-6
+    else:
+        assert np.array_equal(bits(got), bits(exp)), f"{cfg.get('wtype', 'q4_K')} block output not bit-exact"
 
 
 @pytest.mark.parametrize("seed,T", [(1, 2), (12, 2), (1, 4)])
@@ -210,8 +208,7 @@ def test_mul_mat_id_op(dev, K, N, n_as, n_ids, ne11, T, wt):
     for t in range(T):
         for e in range(n_ids):
             assert rel_err(got[t, e], exp[t, e]) < TOL
-    if wt == "q4_K":
-        assert np.array_equal(bits(got), bits(exp)), "Q4_K MUL_MAT_ID not bit-exact"
+    assert np.array_equal(bits(got), bits(exp)), f"{wt} MUL_MAT_ID not bit-exact"
 
 
 def test_mul_mat_id_rejects_bad_shapes(dev):

@@ -21,7 +21,6 @@ torch = pytest.importorskip("torch")
 import questwend_amd as qa  # noqa: E402
 
 pytestmark = pytest.mark.gpu
-TOL = 1e-3
 FETCH = {"memcpy": qa.FETCH_MEMCPY, "gather": qa.FETCH_GATHER}
 
 
@@ -135,7 +134,7 @@ def test_pool_miss_fill_decode(dev, wtype, protect, indexed, fetch):
             exp = c.block(x, ids, w)           # every expert resident: slot = expert id
             got = out.cpu().numpy()
             err = rel_err(got, exp)
-            assert np.isfinite(got).all() and err < TOL, f"step {step}: rel err {err:.3e}"
+            assert np.isfinite(got).all() and err < 1e-6, f"step {step}: rel err {err:.3e}"   # shared gate: device expf
         torch.cuda.synchronize()
 
         # every occupied slot holds its key's host slab, byte for byte

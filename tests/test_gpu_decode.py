@@ -81,3 +81,46 @@ def test_decode_rejects_mixed_shapes(dev):
     layers[0] = a.upload(torch)
     layers[1] = b.upload(torch)
     assert qa.lib().qwm_moe_decode_workspace_size(layers, 2, 1) == 0
+
+
+@pytest.mark.parametrize("T,n_layers", [(1, 3), (4, 4)])
+def test_decode_graph_replay(dev, T, n_layers):
+    """The decode loop captured into a HIP graph (through torch.cuda.graph)
+    and replayed three times, with eager work and synchronizations between
+    the replays: every replay equals the eager loop on the same input bit for
+    bit (the kernels re-arm their own counters; the loop records no memset)."""
+    H, N, E, k = 512, 256, 16, 4
+    cases = [MoeCase(seed=300 + l, H=H, N=N, E=E, k=k, S=E) for l in range(n_layers)]
+    rng = np.random.default_rng(11)
+    tables = np.zeros((3, n_layers * E), np.int32)
+    for l in range(n_layers):
+        tables[:, l * E:(l + 1) * E] = rng.permutation(E).astype(np.int32)
+    layers = (qa.MoeLayer * n_layers)()
+    for l, c in enumerate(cases):
+        layers[l] = c.upload(torch)
+    L = qa.lib()
+    dtab = torch.from_numpy(tables).cuda()
+    nbytes = L.qwm_moe_decode_workspace_size(layers, n_layers, T)
+    ws_e, ws_g = workspace(nbytes), workspace(nbytes)
+    xs = [rng.standard_normal((T, H)).astype(np.float32) for _ in range(3)]
+
+    def eager(x0):
+        dx = torch.from_numpy(x0).cuda()
+        qa.check(L.qwm_moe_decode(layers, n_layers, dtab.data_ptr(), n_layers * E, qa.tensor(qa.TYPE_F32, H, T, 1, dx),
+                                  ws_e.data_ptr(), ws_e.numel(), None))
+        torch.cuda.synchronize()
+        return dx.cpu().numpy()
+
+    gx = torch.zeros((T, H), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        qa.check(L.qwm_moe_decode(layers, n_layers, dtab.data_ptr(), n_layers * E, qa.tensor(qa.TYPE_F32, H, T, 1, gx),
+                                  ws_g.data_ptr(), ws_g.numel(), torch.cuda.current_stream().cuda_stream))
+    for rep, x0 in enumerate(xs):
+        exp = eager(x0)
+        gx.copy_(torch.from_numpy(x0).cuda())
+        graph.replay()
+        torch.cuda.synchronize()
+        got = gx.cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), exp.view(np.uint32)), f"replay {rep} differs from the eager loop"

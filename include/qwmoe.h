@@ -45,6 +45,7 @@ extern "C" {
 #define QWM_ERR_HIP         (-4)
 #define QWM_ERR_NO_VICTIM   (-5)
 #define QWM_ERR_STATE       (-6)
+#define QWM_ERR_IO          (-7)
 
 /* ggml_type values used on this path (ggml.h:390-420) */
 #define QWM_TYPE_F32   0
@@ -258,6 +259,24 @@ int qwm_pool_get_stats(const qwm_pool * pool, qwm_pool_stats * out);
 int qwm_pool_slot_of_row(const qwm_pool * pool, int32_t role, int32_t layer, int32_t * out);
 /* Per-slot key (layer * n_expert + expert, -1 free) and clock of one role. */
 int qwm_pool_slots(const qwm_pool * pool, int32_t role, int32_t * keys, uint64_t * clocks);
+
+/* File tier (ExpertCache::fetch_parallel's file path, expert_cache.cpp:
+ * 1194-1440, with its persistent readers, expert_io_workers.h): misses of
+ * (role, layer) are read from `path` at offset + expert * slab_bytes instead
+ * of host_slabs.  At the end of each qwm_pool_ensure call, reader threads
+ * pread the call's missed slabs into a pinned staging ring and each slab is
+ * copied to its slot on the copy stream as soon as its read is complete, in
+ * the order of the misses (so qwm_pool_ensure returns after the reads; the
+ * copies complete asynchronously, as with the other fetch modes).  A failed
+ * read returns QWM_ERR_IO and un-publishes that miss and the later ones of
+ * the call (their experts are not resident afterwards).  The file must hold
+ * offset + n_expert * slab_bytes bytes (QWM_ERR_ARG otherwise); the pool
+ * keeps the descriptor open until qwm_pool_destroy or the next attach of the
+ * same (role, layer). */
+int qwm_pool_attach_file(qwm_pool * pool, int32_t role, int32_t layer, const char * path, uint64_t offset);
+/* Reader threads (1..64, default 8) and staging slabs (0: as many as fit in
+ * 64 MiB, the reference's batch size) of the file tier. */
+int qwm_pool_set_io(qwm_pool * pool, int32_t n_threads, int32_t staging_slabs);
 
 /* One slab copy: pool_data + slot * slab_bytes <- pinned_src (async H2D on
  * copy_stream), then records done_event (a hipEvent_t, may be NULL)

@@ -21,7 +21,7 @@ TYPE_F32, TYPE_Q8_0, TYPE_Q4_K, TYPE_I32 = 0, 8, 12, 26
 FETCH_MEMCPY, FETCH_GATHER = 0, 1
 _TYPE_SIZE = {TYPE_F32: (4, 1), TYPE_I32: (4, 1), TYPE_Q8_0: (34, 32), TYPE_Q4_K: (144, 256)}
 
-OK, ERR_UNSUPPORTED, ERR_ARG, ERR_WORKSPACE, ERR_HIP, ERR_NO_VICTIM, ERR_STATE = 0, -1, -2, -3, -4, -5, -6
+OK, ERR_UNSUPPORTED, ERR_ARG, ERR_WORKSPACE, ERR_HIP, ERR_NO_VICTIM, ERR_STATE, ERR_IO = 0, -1, -2, -3, -4, -5, -6, -7
 
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32
@@ -100,6 +100,8 @@ def lib():
         "qwm_pool_get_stats": (ctypes.c_int, [_P, ctypes.POINTER(PoolStats)]),
         "qwm_pool_slot_of_row": (ctypes.c_int, [_P, _I32, _I32, _P]),
         "qwm_pool_slots": (ctypes.c_int, [_P, _I32, _P, _P]),
+        "qwm_pool_attach_file": (ctypes.c_int, [_P, _I32, _I32, ctypes.c_char_p, ctypes.c_uint64]),
+        "qwm_pool_set_io": (ctypes.c_int, [_P, _I32, _I32]),
         "qwm_slab_fetch_async": (ctypes.c_int, [_P, _SZ, _I32, _P, _P, _P]),
         "qwm_quantize": (ctypes.c_int, [_I32, _P, _P, _I64, _P]),
         "qwm_profile_start": (ctypes.c_int, [ctypes.c_char_p, _I32]),

@@ -24,19 +24,131 @@
 // Fetch: MEMCPY issues one hipMemcpyAsync per missed slab as it is
 // installed (the reference's order); GATHER collects the call's misses and
 // launches one slab-gather kernel for them at the end of the call.
+// File tier (ExpertCache::fetch_parallel's file path, expert_cache.cpp:
+// 1194-1440): a (role, layer) attached to a file takes its missed slabs from
+// file offset + expert * slab.  At the end of the call persistent reader
+// threads pread them into a pinned staging ring, and the owner copies each
+// slab to its slot on the copy stream as soon as its read is complete, in
+// the order of the misses; a staging batch is reused only after its copies
+// have left it.
 #include <hip/hip_runtime_api.h>
 
+#include <fcntl.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <cerrno>
+#include <condition_variable>
 #include <cstdint>
+#include <cstring>
 #include <algorithm>
+#include <functional>
 #include <limits>
+#include <mutex>
 #include <set>
 #include <string>
+#include <thread>
 #include <unordered_map>
 #include <vector>
 
 #include "qwm_internal.h"
 
 using namespace qwm;
+
+namespace {
+
+// pread until n bytes are in (0), or errno / -1 at end of file.
+int read_full(int fd, uint8_t * dst, size_t n, uint64_t off) {
+    while (n) {
+        const ssize_t r = pread(fd, dst, n, (off_t)off);
+        if (r < 0) {
+            if (errno == EINTR) continue;
+            return errno;
+        }
+        if (r == 0) return -1;
+        dst += r; n -= (size_t)r; off += (uint64_t)r;
+    }
+    return 0;
+}
+
+// Persistent reader threads.  begin(n, fn) hands out jobs 0..n-1 (each run
+// once, by whichever reader claims it); wait(j) returns job j's status once
+// it has run; end() returns when no reader is inside a job of the batch.
+class Readers {
+public:
+    ~Readers() { stop_all(); }
+    void start(int n) {
+        if ((int)th_.size() == n) return;
+        stop_all();
+        stop_ = false;
+        for (int i = 0; i < n; ++i) th_.emplace_back([this] { loop(); });
+    }
+    void begin(int n, std::function<int(int)> fn) {
+        std::lock_guard<std::mutex> lk(mu_);
+        fn_ = std::move(fn);
+        n_ = n;
+        next_ = 0;
+        status_.assign((size_t)n, PENDING);
+        ++gen_;
+        go_.notify_all();
+    }
+    int wait(int j) {
+        std::unique_lock<std::mutex> lk(mu_);
+        done_.wait(lk, [&] { return status_[(size_t)j] != PENDING; });
+        return status_[(size_t)j];
+    }
+    void end() {
+        std::unique_lock<std::mutex> lk(mu_);
+        next_ = n_;                                   // unclaimed jobs are not run
+        done_.wait(lk, [&] { return active_ == 0; });
+    }
+
+private:
+    static constexpr int PENDING = -2;
+    void loop() {
+        uint64_t seen = 0;
+        std::unique_lock<std::mutex> lk(mu_);
+        for (;;) {
+            go_.wait(lk, [&] { return stop_ || gen_ != seen; });
+            if (stop_) return;
+            seen = gen_;
+            ++active_;
+            while (next_ < n_) {
+                const int j = next_++;
+                lk.unlock();
+                const int st = fn_(j);
+                lk.lock();
+                status_[(size_t)j] = st;
+                done_.notify_all();
+            }
+            --active_;
+            done_.notify_all();
+        }
+    }
+    void stop_all() {
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            stop_ = true;
+        }
+        go_.notify_all();
+        for (auto & t : th_) t.join();
+        th_.clear();
+    }
+    std::mutex mu_;
+    std::condition_variable go_, done_;
+    std::vector<std::thread> th_;
+    std::function<int(int)> fn_;
+    std::vector<int> status_;
+    int n_ = 0, next_ = 0, active_ = 0;
+    uint64_t gen_ = 0;
+    bool stop_ = false;
+};
+
+struct FileJob {
+    int32_t role, expert, slot;
+};
+
+}  // namespace
 
 struct qwm_pool {
     struct Role {
@@ -53,6 +165,8 @@ struct qwm_pool {
         std::unordered_map<int32_t, uint64_t> count;
         std::set<std::pair<uint64_t, int32_t>> lru; // indexed mode: occupied (clock, slot)
         std::set<int32_t> free_slots;               // indexed mode
+        std::vector<int> fd;                        // file tier: per layer, -1 = none
+        std::vector<uint64_t> foff;                 // file tier: per layer, offset of expert 0
     };
     int n_layer = 0, n_expert = 0;
     bool protect = false, indexed = false;
@@ -65,6 +179,26 @@ struct qwm_pool {
     bool pending = false;
     bool gather = false;
     std::vector<GatherItem> batch;                  // GATHER: this call's misses
+    // file tier
+    std::vector<FileJob> fjobs;                     // this call's misses from files
+    Readers readers;
+    int io_threads = 8, staging_slabs = 0;          // 0: as many slabs as fit in 64 MiB
+    uint8_t * staging = nullptr;
+    size_t staging_stride = 0;
+    int staging_n = 0;
+    hipEvent_t staging_free = nullptr;              // recorded after each batch's copies
+    bool staging_busy = false;
+
+    ~qwm_pool() {   // every flush ended with no reader inside a job
+        for (auto & R : role)
+            for (int f : R.fd)
+                if (f >= 0) close(f);
+        if (staging_free) {
+            (void)hipEventSynchronize(staging_free);
+            (void)hipEventDestroy(staging_free);
+        }
+        if (staging) (void)hipHostFree(staging);
+    }
 
     void touch(Role & R, int32_t slot) {
         const uint64_t next = clock + 1;
@@ -113,12 +247,15 @@ struct qwm_pool {
 
     int fetch(int r, int32_t layer, int32_t expert, int32_t slot) {
         Role & R = role[r];
-        if (R.host.empty() || !R.host[layer]) return QWM_OK;   // no host tier: metadata only
+        const bool from_file = !R.fd.empty() && R.fd[layer] >= 0;
+        if (!from_file && (R.host.empty() || !R.host[layer])) return QWM_OK;   // no host tier: metadata only
         if (!done) {   // created on first use, so decision-only pools need no GPU
             hipError_t e = hipEventCreateWithFlags(&done, hipEventDisableTiming);
             if (e != hipSuccess) return fail(QWM_ERR_HIP, std::string("slab fetch: hipEventCreate: ") + hipGetErrorString(e));
         }
-        if (gather) {
+        if (from_file) {
+            fjobs.push_back(FileJob{r, expert, slot});
+        } else if (gather) {
             // A slot filled twice in one call (its first key was evicted again
             // within the call) keeps the later slab, as stream-ordered copies do.
             bool replaced = false;
@@ -154,22 +291,88 @@ struct qwm_pool {
             rc = launch_slab_gather(a, copy);
         }
         if (rc != QWM_OK)
-            for (const GatherItem & it : batch) {
-                Role & R = role[it.role];
-                const int32_t key = R.slot2key[it.slot];
-                if (key < 0) continue;
-                fetch_bytes -= R.slab;
-                fetches--;
-                if (indexed) {
-                    R.lru.erase({R.clk[it.slot], it.slot});
-                    R.free_slots.insert(it.slot);
-                }
-                R.occ[key / n_expert]--;
-                R.slot_of[key] = 0;
-                R.key2slot.erase(key);
-                R.slot2key[it.slot] = -1;
-            }
+            for (const GatherItem & it : batch) unpublish(it.role, it.slot);
         batch.clear();
+        return rc;
+    }
+
+    // Frees the slot of an install whose slab was not filled (its key no
+    // longer resolves), as if the miss had not been taken.
+    void unpublish(int r, int32_t slot) {
+        Role & R = role[r];
+        const int32_t key = R.slot2key[slot];
+        if (key < 0) return;
+        fetch_bytes -= R.slab;
+        fetches--;
+        if (indexed) {
+            R.lru.erase({R.clk[slot], slot});
+            R.free_slots.insert(slot);
+        }
+        R.occ[key / n_expert]--;
+        R.slot_of[key] = 0;
+        R.key2slot.erase(key);
+        R.slot2key[slot] = -1;
+    }
+
+    // File tier: this call's misses, read by the readers into the staging ring
+    // and copied to their slots in order.  On a failed read or copy the failed
+    // job and every later one are unpublished.
+    int flush_files(int32_t layer) {
+        if (fjobs.empty()) return QWM_OK;
+        size_t max_slab = 0;
+        for (const auto & R : role) max_slab = std::max(max_slab, R.slab);
+        if (!staging) {
+            staging_stride = (max_slab + 4095) & ~(size_t)4095;
+            staging_n = staging_slabs > 0 ? staging_slabs : (int)std::max<size_t>(1, ((size_t)64 << 20) / staging_stride);
+            hipError_t e = hipHostMalloc((void **)&staging, (size_t)staging_n * staging_stride, hipHostMallocDefault);
+            if (e == hipSuccess && !staging_free) e = hipEventCreateWithFlags(&staging_free, hipEventDisableTiming);
+            if (e != hipSuccess) {
+                staging = nullptr;
+                for (const FileJob & j : fjobs) unpublish(j.role, j.slot);
+                fjobs.clear();
+                return fail(QWM_ERR_HIP, std::string("file tier: pinned staging: ") + hipGetErrorString(e));
+            }
+        }
+        readers.start(io_threads);
+        int rc = QWM_OK;
+        size_t bad = fjobs.size();
+        for (size_t b0 = 0; b0 < fjobs.size() && rc == QWM_OK; b0 += (size_t)staging_n) {
+            const int bn = (int)std::min<size_t>((size_t)staging_n, fjobs.size() - b0);
+            if (staging_busy) {
+                hipError_t e = hipEventSynchronize(staging_free);   // the previous batch's copies are out
+                if (e != hipSuccess) { rc = fail(QWM_ERR_HIP, std::string("file tier: ") + hipGetErrorString(e)); bad = b0; break; }
+                staging_busy = false;
+            }
+            readers.begin(bn, [this, b0, layer](int j) {
+                const FileJob & fj = fjobs[b0 + (size_t)j];
+                const Role & R = role[fj.role];
+                return read_full(R.fd[layer], staging + (size_t)j * staging_stride, R.slab,
+                                 R.foff[layer] + (uint64_t)fj.expert * R.slab);
+            });
+            for (int j = 0; j < bn; ++j) {
+                const int st = readers.wait(j);
+                const FileJob & fj = fjobs[b0 + (size_t)j];
+                Role & R = role[fj.role];
+                if (st != 0) {
+                    rc = fail(QWM_ERR_IO, "file tier: reading the slab of expert " + std::to_string(fj.expert) +
+                                              " (role " + std::to_string(fj.role) + ", layer " + std::to_string(layer) +
+                                              "): " + (st < 0 ? std::string("end of file") : std::string(strerror(st))));
+                    bad = b0 + (size_t)j;
+                    break;
+                }
+                hipError_t e = hipMemcpyAsync(R.data + (size_t)fj.slot * R.slab, staging + (size_t)j * staging_stride,
+                                              R.slab, hipMemcpyHostToDevice, copy);
+                if (e != hipSuccess) {
+                    rc = fail(QWM_ERR_HIP, std::string("file tier: ") + hipGetErrorString(e));
+                    bad = b0 + (size_t)j;
+                    break;
+                }
+            }
+            readers.end();                               // no reader still writes this batch's staging
+            if (hipEventRecord(staging_free, copy) == hipSuccess) staging_busy = true;
+        }
+        for (size_t i = bad; i < fjobs.size(); ++i) unpublish(fjobs[i].role, fjobs[i].slot);
+        fjobs.clear();
         return rc;
     }
 
@@ -288,14 +491,15 @@ int qwm_pool_ensure(qwm_pool * p, int32_t layer, const int32_t * ids, int32_t n,
         }
     }
     for (size_t key : changed) p->active[key] = 0;
-    if (p->gather) {   // the misses installed before a NO_VICTIM failure are filled too
-        const int frc = p->flush(layer);
-        if (frc != QWM_OK) return frc;
-    }
-    if (p->pending && (rc == QWM_OK || p->gather)) {
+    // the misses installed before a NO_VICTIM failure are filled too
+    const int grc = p->gather ? p->flush(layer) : QWM_OK;
+    const int frc = p->flush_files(layer);
+    if (p->pending) {   // covers every copy issued so far, also after a failure
         hipError_t e = hipEventRecord(p->done, p->copy);
         if (e != hipSuccess) return fail(QWM_ERR_HIP, std::string("pool_ensure: hipEventRecord: ") + hipGetErrorString(e));
     }
+    if (grc != QWM_OK) return grc;
+    if (frc != QWM_OK) return frc;
     return rc;
 }
 
@@ -327,6 +531,42 @@ int qwm_pool_slots(const qwm_pool * p, int32_t role, int32_t * keys, uint64_t * 
         if (keys) keys[s] = R.slot2key[s];
         if (clocks) clocks[s] = R.clk[s];
     }
+    return QWM_OK;
+}
+
+int qwm_pool_attach_file(qwm_pool * p, int32_t role, int32_t layer, const char * path, uint64_t offset) {
+    if (!p || !path || role < 0 || role > 2 || layer < 0 || layer >= p->n_layer)
+        return fail(QWM_ERR_ARG, "pool_attach_file: bad argument");
+    auto & R = p->role[role];
+    if (!R.data) return fail(QWM_ERR_ARG, "pool_attach_file: the role has no device pool");
+    const int fd = open(path, O_RDONLY | O_CLOEXEC);
+    if (fd < 0) return fail(QWM_ERR_IO, std::string("pool_attach_file: ") + path + ": " + strerror(errno));
+    struct stat st;
+    const uint64_t need = offset + (uint64_t)p->n_expert * R.slab;
+    if (fstat(fd, &st) != 0 || (uint64_t)st.st_size < need) {
+        close(fd);
+        return fail(QWM_ERR_ARG, std::string("pool_attach_file: ") + path + " is shorter than offset + n_expert * slab_bytes");
+    }
+    if (R.fd.empty()) {
+        R.fd.assign((size_t)p->n_layer, -1);
+        R.foff.assign((size_t)p->n_layer, 0);
+    }
+    if (R.fd[layer] >= 0) close(R.fd[layer]);
+    R.fd[layer] = fd;
+    R.foff[layer] = offset;
+    return QWM_OK;
+}
+
+int qwm_pool_set_io(qwm_pool * p, int32_t n_threads, int32_t staging_slabs) {
+    if (!p || n_threads < 1 || n_threads > 64 || staging_slabs < 0) return fail(QWM_ERR_ARG, "pool_set_io: bad argument");
+    p->io_threads = n_threads;
+    if (staging_slabs != p->staging_slabs && p->staging) {   // re-sized on the next miss
+        if (p->staging_busy) QWM_HIP_CHECK(hipEventSynchronize(p->staging_free));
+        p->staging_busy = false;
+        QWM_HIP_CHECK(hipHostFree(p->staging));
+        p->staging = nullptr;
+    }
+    p->staging_slabs = staging_slabs;
     return QWM_OK;
 }
 

@@ -171,3 +171,39 @@ def test_pool_exhaustion_is_reported_and_consistent():
     k, _ = g.state(0)
     assert sorted(k.tolist()) == [0, 1]          # nothing was evicted or published
     assert g.ensure(0, [16])[0] == qa.ERR_ARG    # expert id out of range
+
+
+def test_pool_attach_file_checks_without_gpu(tmp_path):
+    """The file tier's set-up errors, on a pool whose device memory is never
+    touched: a missing file is an I/O error, a file shorter than offset +
+    n_expert * slab_bytes an argument error (both with the path in the
+    message), as are a role without a device pool and bad reader settings."""
+    L = qa.lib()
+    d = qa.PoolDesc()
+    d.n_layer, d.n_expert = 2, 8
+    for r in range(3):
+        d.n_slots[r] = 4
+        d.pool_data[r] = 4096 if r < 2 else None        # never dereferenced here
+        d.slab_bytes[r] = 1000
+    h = ctypes.c_void_p()
+    qa.check(L.qwm_pool_create(ctypes.byref(d), None, ctypes.byref(h)))
+    try:
+        missing = str(tmp_path / "none.bin").encode()
+        assert L.qwm_pool_attach_file(h, 0, 0, missing, 0) == qa.ERR_IO
+        assert missing in L.qwm_last_error()
+        short = tmp_path / "short.bin"
+        short.write_bytes(b"\0" * (100 + 8 * 1000 - 1))
+        assert L.qwm_pool_attach_file(h, 0, 1, str(short).encode(), 100) == qa.ERR_ARG
+        assert b"shorter" in L.qwm_last_error()
+        short.write_bytes(b"\0" * (100 + 8 * 1000))
+        assert L.qwm_pool_attach_file(h, 0, 1, str(short).encode(), 100) == qa.OK
+        assert L.qwm_pool_attach_file(h, 1, 1, str(short).encode(), 100) == qa.OK
+        assert L.qwm_pool_attach_file(h, 2, 0, str(short).encode(), 0) == qa.ERR_ARG     # no device pool
+        assert L.qwm_pool_attach_file(h, 3, 0, str(short).encode(), 0) == qa.ERR_ARG     # no such role
+        assert L.qwm_pool_attach_file(h, 0, 2, str(short).encode(), 0) == qa.ERR_ARG     # no such layer
+        assert L.qwm_pool_set_io(h, 0, 0) == qa.ERR_ARG
+        assert L.qwm_pool_set_io(h, 65, 0) == qa.ERR_ARG
+        assert L.qwm_pool_set_io(h, 4, -1) == qa.ERR_ARG
+        assert L.qwm_pool_set_io(h, 4, 3) == qa.OK
+    finally:
+        L.qwm_pool_destroy(h)

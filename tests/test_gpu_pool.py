@@ -58,10 +58,35 @@ def zipf_mask(rng, perm, k, T, skew=1.1, bias=16.0):
     return m
 
 
+def write_slab_file(path, host, head=4133):
+    """Every (layer, role) slab array of `host` ([layer][role] tensors) in one
+    file behind a `head`-byte header (offsets not aligned to anything), as a
+    model file holds its expert tensors; returns offsets [layer][role]."""
+    offs, pos = [], head
+    with open(path, "wb") as f:
+        f.write(b"\x5a" * head)
+        for row in host:
+            offs.append([])
+            for t in row:
+                b = t.numpy().tobytes()
+                offs[-1].append(pos)
+                f.write(b)
+                f.write(b"\x00" * 37)
+                pos += len(b) + 37
+    return offs
+
+
 @pytest.mark.parametrize("wtype,protect,indexed,fetch", [("q4_K", 0, 0, "memcpy"), ("q4_K", 0, 0, "gather"),
                                                           ("q4_K", 1, 1, "gather"), ("q8_0", 0, 1, "memcpy"),
-                                                          ("q8_0", 1, 0, "gather")])
-def test_pool_miss_fill_decode(dev, wtype, protect, indexed, fetch):
+                                                          ("q8_0", 1, 0, "gather"), ("q4_K", 0, 1, "file"),
+                                                          ("q8_0", 1, 0, "file")])
+def test_pool_miss_fill_decode(dev, tmp_path, wtype, protect, indexed, fetch):
+    """Decode steps over two layers sharing a pool smaller than the routed
+    experts (Zipf popularity), misses filled from pinned host slabs (per-slab
+    copies or one gather launch per call) or from a file through the reader
+    threads and a 5-slab staging ring: slot sequences equal the oracle's, every
+    occupied slot holds its slab byte for byte, and every MoE output matches
+    the oracle."""
     H, N, E, k, T, S, n_layer, steps = 512, 256, 64, 4, 4, 20, 2, 24
     cases = [MoeCase(seed=40 + l, H=H, N=N, E=E, k=k, S=E, shared=True, N_sh=N, wtype=wtype) for l in range(n_layer)]
     rng = np.random.default_rng(9)
@@ -80,12 +105,19 @@ def test_pool_miss_fill_decode(dev, wtype, protect, indexed, fetch):
         d.n_slots[r] = S
         d.pool_data[r] = pool_t[r].data_ptr()
         d.slab_bytes[r] = slab
-        d.host_slabs[r] = ctypes.cast(host_ptrs[r], ctypes.c_void_p)
+        d.host_slabs[r] = None if fetch == "file" else ctypes.cast(host_ptrs[r], ctypes.c_void_p)
     d.protect_active, d.indexed = protect, indexed
-    d.fetch_mode = FETCH[fetch]
+    d.fetch_mode = FETCH["memcpy" if fetch == "file" else fetch]
     copy = torch.cuda.Stream()
     h = ctypes.c_void_p()
     qa.check(L.qwm_pool_create(ctypes.byref(d), ctypes.c_void_p(copy.cuda_stream), ctypes.byref(h)))
+    if fetch == "file":
+        path = str(tmp_path / "slabs.bin")
+        offs = write_slab_file(path, host)
+        for l in range(n_layer):
+            for r in range(3):
+                qa.check(L.qwm_pool_attach_file(h, r, l, path.encode(), offs[l][r]))
+        qa.check(L.qwm_pool_set_io(h, 4, 5))
     o = oracle().qwo_pool_new(n_layer, E, ptr(np.array([S, S, S], np.int32)), protect)
 
     layers = []
@@ -237,3 +269,69 @@ def test_pool_gather_needs_pinned_slabs(dev):
     rc, h, _, _keep = small_pool(S, slab + 8, [[pinned(np.zeros(E * (slab + 8), np.uint8))] for _ in range(3)],
                                  "gather", torch.cuda.Stream(), n_expert=E)
     assert rc == qa.ERR_ARG and not h.value
+
+
+def test_pool_file_read_failure_unpublishes(dev, tmp_path):
+    """A file tier whose file was cut short after attach: the call returns
+    QWM_ERR_IO naming the failed slab, the miss that failed and every later
+    miss of the call are not resident afterwards (no key points at an unfilled
+    slot), the earlier ones are and hold their slabs; once the file is whole
+    again the same call fills every slot byte for byte."""
+    L = qa.lib()
+    E, S, slab = 8, 4, 8192
+    rng = np.random.default_rng(5)
+    host = [[torch.from_numpy(rng.integers(0, 256, E * slab, dtype=np.uint8)) for _ in range(3)]]
+    path = tmp_path / "slabs.bin"
+    offs = write_slab_file(str(path), host)
+    whole = path.read_bytes()
+    pool_t = [torch.zeros(S * slab, dtype=torch.uint8, device="cuda") for _ in range(3)]
+    d = qa.PoolDesc()
+    d.n_layer, d.n_expert = 1, E
+    for r in range(3):
+        d.n_slots[r], d.pool_data[r], d.slab_bytes[r] = S, pool_t[r].data_ptr(), slab
+    d.fetch_mode = qa.FETCH_MEMCPY
+    copy = torch.cuda.Stream()
+    h = ctypes.c_void_p()
+    qa.check(L.qwm_pool_create(ctypes.byref(d), ctypes.c_void_p(copy.cuda_stream), ctypes.byref(h)))
+    try:
+        for r in range(3):
+            qa.check(L.qwm_pool_attach_file(h, r, 0, str(path).encode(), offs[0][r]))
+        qa.check(L.qwm_pool_set_io(h, 3, 2))
+        path.write_bytes(whole[:offs[0][0] + 6 * slab + 100])   # role 0 up to expert 5 only; roles 1, 2 gone
+        ids = np.array([1, 5, 2], np.int32)
+        out = np.zeros((3, 3), np.int32)
+        rc = L.qwm_pool_ensure(h, 0, ptr(ids), 3, ptr(out[0]), ptr(out[1]), ptr(out[2]))
+        assert rc == qa.ERR_IO
+        assert b"end of file" in L.qwm_last_error()
+        qa.check(L.qwm_pool_wait(h, None))
+        torch.cuda.synchronize()
+        resident = []
+        for r in range(3):
+            keys = np.zeros(S, np.int32)
+            qa.check(L.qwm_pool_slots(h, r, ptr(keys), None))
+            resident.append(sorted(int(k) for k in keys if k >= 0))
+            row = np.zeros(E, np.int32)
+            qa.check(L.qwm_pool_slot_of_row(h, r, 0, ptr(row)))
+            assert sorted(int(e) for e in np.nonzero(row)[0]) == [e for e in resident[-1] if row[e] != 0]
+        assert resident == [[1], [], []], resident         # misses in order: (1, gate) read, (1, up) failed
+        st = qa.PoolStats()
+        qa.check(L.qwm_pool_get_stats(h, ctypes.byref(st)))
+        assert st.fetches == 1 and st.fetch_bytes == slab
+        keys = np.zeros(S, np.int32)
+        qa.check(L.qwm_pool_slots(h, 0, ptr(keys), None))
+        s1 = int(np.nonzero(keys == 1)[0][0])
+        assert np.array_equal(pool_t[0].cpu().numpy()[s1 * slab:(s1 + 1) * slab],
+                              host[0][0].numpy()[slab:2 * slab])
+
+        path.write_bytes(whole)
+        rc = L.qwm_pool_ensure(h, 0, ptr(ids), 3, ptr(out[0]), ptr(out[1]), ptr(out[2]))
+        assert rc == qa.OK, L.qwm_last_error()
+        qa.check(L.qwm_pool_wait(h, None))
+        torch.cuda.synchronize()
+        for r in range(3):
+            dev_bytes = pool_t[r].cpu().numpy().reshape(S, slab)
+            src = host[0][r].numpy().reshape(E, slab)
+            for i, e in enumerate(ids):
+                assert np.array_equal(dev_bytes[out[r, i]], src[e]), f"role {r} expert {e}"
+    finally:
+        L.qwm_pool_destroy(h)

@@ -19,6 +19,7 @@ import ctypes
 import json
 import os
 import sys
+import tempfile
 import time
 
 import numpy as np
@@ -70,7 +71,7 @@ def parse():
     ap.add_argument("--popularity", choices=["sampled", "offset"], default="sampled",
                     help="missfill: sampled = each token's top-10 drawn from Zipf(1.1) and forced through the route "
                          "mask; offset = a fixed log-popularity logit offset (nearly every lookup then hits)")
-    ap.add_argument("--fetch", choices=["gather", "memcpy"], default="gather",
+    ap.add_argument("--fetch", choices=["gather", "memcpy", "file"], default="gather",
                     help="missfill: how misses reach the pool (the other mode is run too and reported beside)")
     args = ap.parse_args()
     if args.steps is None:
@@ -592,18 +593,33 @@ def bench_missfill(args, torch, qa, E_n=512, N_n=512, k_n=10, S_n=128, skew=1.1)
     n_ids = T * k_n
     hs = [hsl[r].data_ptr() for r in range(3)]
 
-    def run_mode(fetch_mode):
-        """A fresh pool with the given fetch mode over the same inputs."""
+    def run_mode(fetch):
+        """A fresh pool with the given fetch mode over the same inputs.  "file":
+        the slabs come from a file (the three roles' expert arrays back to
+        back), read by the pool's reader threads; the file was just written,
+        so its pages are in the host's page cache (no device I/O is timed), and
+        the staged slabs reach the pool by slab-gather launches."""
         d = qa.PoolDesc()
         d.n_layer, d.n_expert = 1, E_n
         for r in range(3):
             d.n_slots[r] = S_n
             d.pool_data[r] = pools[r].data_ptr()
             d.slab_bytes[r] = slab
-            d.host_slabs[r] = ctypes.cast(host_ptrs[r], ctypes.c_void_p)
-        d.fetch_mode = fetch_mode
+            d.host_slabs[r] = None if fetch == "file" else ctypes.cast(host_ptrs[r], ctypes.c_void_p)
+        d.fetch_mode = qa.FETCH_MEMCPY if fetch == "memcpy" else qa.FETCH_GATHER   # file: gathers from the staging
         pool = ctypes.c_void_p()
         qa.check(L.qwm_pool_create(ctypes.byref(d), ctypes.c_void_p(copy.cuda_stream), ctypes.byref(pool)))
+        if fetch == "file":
+            fd, path = tempfile.mkstemp(prefix="qwm_slabs_", suffix=".bin")
+            with os.fdopen(fd, "wb") as f:
+                for r in range(3):
+                    f.write(host[r].numpy().tobytes())
+            try:
+                for r in range(3):
+                    qa.check(L.qwm_pool_attach_file(pool, r, 0, path.encode(), r * E_n * slab))
+            finally:
+                os.unlink(path)   # the pool holds its descriptor
+            qa.check(L.qwm_pool_set_io(pool, 8, 0))
 
         def step(s, ev=None, unions=None):
             if ev is not None:
@@ -701,10 +717,8 @@ def bench_missfill(args, torch, qa, E_n=512, N_n=512, k_n=10, S_n=128, skew=1.1)
                    "sample": f"{n} verify steps ({secs:.1f} s) of the same inputs through the reference's ggml-CPU "
                              f"kernels with every expert in host memory ({CPU_THREADS} OpenMP threads)",
                    "ms_per_step": 1e3 * secs / n}
-    other = "memcpy" if args.fetch == "gather" else "gather"
-    modes = {"gather": qa.FETCH_GATHER, "memcpy": qa.FETCH_MEMCPY}
-    res_other = run_mode(modes[other])
-    res = run_mode(modes[args.fetch])
+    others = {m: run_mode(m) for m in ("gather", "memcpy", "file") if m != args.fetch}
+    res = run_mode(args.fetch)
     rt = res["rt"]
     kern_ms = float(np.median(rt[:, 0]) + np.median(rt[:, 4]))
     step_bytes = 3 * slab * res["union"] + E_n * H * 4 + 3 * slab + 2 * T * H * 4
@@ -722,9 +736,9 @@ def bench_missfill(args, torch, qa, E_n=512, N_n=512, k_n=10, S_n=128, skew=1.1)
         "pool": res["pool"],
         "breakdown_ms_median": res["breakdown_ms_median"],
         "host_link": {"achieved_GBs": res["host_link_GBs"], "peak_GBs": 64.0},
-        "other_fetch": {"fetch": other, "ms_per_step": res_other["ms"], "tokens_per_s": T / (res_other["ms"] * 1e-3),
-                        "host_link_GBs": res_other["host_link_GBs"], "hit_rate": res_other["pool"]["hit_rate"],
-                        "breakdown_ms_median": res_other["breakdown_ms_median"]},
+        "other_fetch": {m: {"ms_per_step": o["ms"], "tokens_per_s": T / (o["ms"] * 1e-3),
+                            "host_link_GBs": o["host_link_GBs"], "hit_rate": o["pool"]["hit_rate"],
+                            "breakdown_ms_median": o["breakdown_ms_median"]} for m, o in others.items()},
         "roofline": {"bound": "hbm", "kernel": "route + experts (selected slabs, router, shared expert)",
                      "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
                      "traffic": None, "bytes_per_launch": step_bytes},

@@ -33,7 +33,8 @@ __global__ __launch_bounds__(GATHER_THREADS) void k_slab_gather(GatherArgs a) {
     const size_t beg = (size_t)part * GATHER_CHUNK16;
     if (beg >= n16) return;
     const size_t end = beg + GATHER_CHUNK16 < n16 ? beg + GATHER_CHUNK16 : n16;
-    const uint4 * src = reinterpret_cast<const uint4 *>(a.src[r] + (size_t)it.expert * a.slab[r]);
+    const size_t stride = a.src_stride[r] ? a.src_stride[r] : a.slab[r];
+    const uint4 * src = reinterpret_cast<const uint4 *>(a.src[r] + (size_t)it.expert * stride);
     uint4 * dst = reinterpret_cast<uint4 *>(a.dst[r] + (size_t)it.slot * a.slab[r]);
     for (size_t i = beg + (size_t)threadIdx.x * GATHER_UNROLL; i < end; i += GATHER_THREADS * GATHER_UNROLL) {
         uint4 v[GATHER_UNROLL];

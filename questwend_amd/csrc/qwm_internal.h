@@ -127,6 +127,7 @@ struct GatherArgs {
     const uint8_t * src[3];   // device-visible address of the layer's pinned host slabs, per role
     uint8_t * dst[3];         // pool base, per role
     uint64_t slab[3];         // bytes per slab (multiples of 16)
+    uint64_t src_stride[3];   // bytes between source slabs (0: slab)
     int32_t n, wg_per_item;
     GatherItem item[GATHER_MAX];
 };

@@ -184,6 +184,7 @@ struct qwm_pool {
     Readers readers;
     int io_threads = 8, staging_slabs = 0;          // 0: as many slabs as fit in 64 MiB
     uint8_t * staging = nullptr;
+    const uint8_t * staging_dev = nullptr;          // GATHER: device-visible address of the staging
     size_t staging_stride = 0;
     int staging_n = 0;
     hipEvent_t staging_free = nullptr;              // recorded after each batch's copies
@@ -325,6 +326,11 @@ struct qwm_pool {
             staging_stride = (max_slab + 4095) & ~(size_t)4095;
             staging_n = staging_slabs > 0 ? staging_slabs : (int)std::max<size_t>(1, ((size_t)64 << 20) / staging_stride);
             hipError_t e = hipHostMalloc((void **)&staging, (size_t)staging_n * staging_stride, hipHostMallocDefault);
+            if (e == hipSuccess && gather) {
+                void * dp = nullptr;
+                e = hipHostGetDevicePointer(&dp, staging, 0);
+                staging_dev = (const uint8_t *)dp;
+            }
             if (e == hipSuccess && !staging_free) e = hipEventCreateWithFlags(&staging_free, hipEventDisableTiming);
             if (e != hipSuccess) {
                 staging = nullptr;
@@ -349,16 +355,43 @@ struct qwm_pool {
                 return read_full(R.fd[layer], staging + (size_t)j * staging_stride, R.slab,
                                  R.foff[layer] + (uint64_t)fj.expert * R.slab);
             });
+            // GATHER: one slab-gather launch per FILE_GATHER_GROUP completed reads
+            constexpr int FILE_GATHER_GROUP = 8;
+            GatherArgs ga{};
+            for (int r = 0; r < 3; ++r) {
+                ga.src[r] = staging_dev;
+                ga.dst[r] = role[r].data;
+                ga.slab[r] = role[r].slab;
+                ga.src_stride[r] = staging_stride;
+            }
+            int g0 = 0;                                  // first job of the pending gather group
+            auto launch_group = [&](int g1) {            // jobs [g0, g1) of this batch
+                ga.n = g1 - g0;
+                for (int i = 0; i < ga.n; ++i) {
+                    const FileJob & gj = fjobs[b0 + (size_t)(g0 + i)];
+                    ga.item[i] = GatherItem{g0 + i, (int16_t)gj.slot, (int16_t)gj.role};
+                }
+                const int lrc = ga.n > 0 ? launch_slab_gather(ga, copy) : QWM_OK;
+                if (lrc == QWM_OK) g0 = g1;
+                return lrc;
+            };
             for (int j = 0; j < bn; ++j) {
                 const int st = readers.wait(j);
                 const FileJob & fj = fjobs[b0 + (size_t)j];
                 Role & R = role[fj.role];
                 if (st != 0) {
+                    if (gather && launch_group(j) != QWM_OK) { rc = QWM_ERR_HIP; bad = b0 + (size_t)g0; break; }
                     rc = fail(QWM_ERR_IO, "file tier: reading the slab of expert " + std::to_string(fj.expert) +
                                               " (role " + std::to_string(fj.role) + ", layer " + std::to_string(layer) +
                                               "): " + (st < 0 ? std::string("end of file") : std::string(strerror(st))));
                     bad = b0 + (size_t)j;
                     break;
+                }
+                if (gather) {
+                    if (j + 1 - g0 < FILE_GATHER_GROUP && j + 1 < bn) continue;
+                    const int lrc = launch_group(j + 1);
+                    if (lrc != QWM_OK) { rc = lrc; bad = b0 + (size_t)g0; break; }
+                    continue;
                 }
                 hipError_t e = hipMemcpyAsync(R.data + (size_t)fj.slot * R.slab, staging + (size_t)j * staging_stride,
                                               R.slab, hipMemcpyHostToDevice, copy);
@@ -539,6 +572,9 @@ int qwm_pool_attach_file(qwm_pool * p, int32_t role, int32_t layer, const char *
         return fail(QWM_ERR_ARG, "pool_attach_file: bad argument");
     auto & R = p->role[role];
     if (!R.data) return fail(QWM_ERR_ARG, "pool_attach_file: the role has no device pool");
+    if (p->gather && (R.slab % 16 || ((uintptr_t)R.data & 15) || R.n_slots > 32767))
+        return fail(QWM_ERR_ARG, "pool_attach_file: GATHER needs 16-byte aligned pools, slab_bytes % 16 == 0 and at "
+                                 "most 32767 slots per role");
     const int fd = open(path, O_RDONLY | O_CLOEXEC);
     if (fd < 0) return fail(QWM_ERR_IO, std::string("pool_attach_file: ") + path + ": " + strerror(errno));
     struct stat st;

@@ -79,12 +79,13 @@ def write_slab_file(path, host, head=4133):
 @pytest.mark.parametrize("wtype,protect,indexed,fetch", [("q4_K", 0, 0, "memcpy"), ("q4_K", 0, 0, "gather"),
                                                           ("q4_K", 1, 1, "gather"), ("q8_0", 0, 1, "memcpy"),
                                                           ("q8_0", 1, 0, "gather"), ("q4_K", 0, 1, "file"),
-                                                          ("q8_0", 1, 0, "file")])
+                                                          ("q8_0", 1, 0, "file"), ("q4_K", 1, 0, "file_gather")])
 def test_pool_miss_fill_decode(dev, tmp_path, wtype, protect, indexed, fetch):
     """Decode steps over two layers sharing a pool smaller than the routed
     experts (Zipf popularity), misses filled from pinned host slabs (per-slab
     copies or one gather launch per call) or from a file through the reader
-    threads and a 5-slab staging ring: slot sequences equal the oracle's, every
+    threads and a 5-slab staging ring (then per-slab copies, or gather
+    launches from the staging): slot sequences equal the oracle's, every
     occupied slot holds its slab byte for byte, and every MoE output matches
     the oracle."""
     H, N, E, k, T, S, n_layer, steps = 512, 256, 64, 4, 4, 20, 2, 24
@@ -105,13 +106,13 @@ def test_pool_miss_fill_decode(dev, tmp_path, wtype, protect, indexed, fetch):
         d.n_slots[r] = S
         d.pool_data[r] = pool_t[r].data_ptr()
         d.slab_bytes[r] = slab
-        d.host_slabs[r] = None if fetch == "file" else ctypes.cast(host_ptrs[r], ctypes.c_void_p)
+        d.host_slabs[r] = None if fetch.startswith("file") else ctypes.cast(host_ptrs[r], ctypes.c_void_p)
     d.protect_active, d.indexed = protect, indexed
-    d.fetch_mode = FETCH["memcpy" if fetch == "file" else fetch]
+    d.fetch_mode = FETCH[{"file": "memcpy", "file_gather": "gather"}.get(fetch, fetch)]
     copy = torch.cuda.Stream()
     h = ctypes.c_void_p()
     qa.check(L.qwm_pool_create(ctypes.byref(d), ctypes.c_void_p(copy.cuda_stream), ctypes.byref(h)))
-    if fetch == "file":
+    if fetch.startswith("file"):
         path = str(tmp_path / "slabs.bin")
         offs = write_slab_file(path, host)
         for l in range(n_layer):
@@ -271,7 +272,8 @@ def test_pool_gather_needs_pinned_slabs(dev):
     assert rc == qa.ERR_ARG and not h.value
 
 
-def test_pool_file_read_failure_unpublishes(dev, tmp_path):
+@pytest.mark.parametrize("mode", ["memcpy", "gather"])
+def test_pool_file_read_failure_unpublishes(dev, tmp_path, mode):
     """A file tier whose file was cut short after attach: the call returns
     QWM_ERR_IO naming the failed slab, the miss that failed and every later
     miss of the call are not resident afterwards (no key points at an unfilled
@@ -289,7 +291,7 @@ def test_pool_file_read_failure_unpublishes(dev, tmp_path):
     d.n_layer, d.n_expert = 1, E
     for r in range(3):
         d.n_slots[r], d.pool_data[r], d.slab_bytes[r] = S, pool_t[r].data_ptr(), slab
-    d.fetch_mode = qa.FETCH_MEMCPY
+    d.fetch_mode = FETCH[mode]
     copy = torch.cuda.Stream()
     h = ctypes.c_void_p()
     qa.check(L.qwm_pool_create(ctypes.byref(d), ctypes.c_void_p(copy.cuda_stream), ctypes.byref(h)))

@@ -260,6 +260,18 @@ int qwm_pool_slot_of_row(const qwm_pool * pool, int32_t role, int32_t layer, int
 /* Per-slot key (layer * n_expert + expert, -1 free) and clock of one role. */
 int qwm_pool_slots(const qwm_pool * pool, int32_t role, int32_t * keys, uint64_t * clocks);
 
+/* Cache profiles (ExpertCache::save_profile / load_prefetch,
+ * expert_cache.cpp:1485-1538), in the reference's text format:
+ * "QWENEXPCACHE 1", "n_layer n_expert", then "role layer expert count" per
+ * key that ensure has counted (roles in order, keys ascending here).
+ * load: a missing or incompatible profile installs nothing and returns
+ * QWM_OK (cold start); otherwise entries in range, largest count first (equal
+ * counts in file order), are installed into free slots until their role's
+ * pool is full, skipping resident keys, their slabs fetched as misses are
+ * (qwm_pool_wait orders them).  *n_installed (may be NULL) gets the count. */
+int qwm_pool_save_profile(const qwm_pool * pool, const char * path);
+int qwm_pool_load_profile(qwm_pool * pool, const char * path, int64_t * n_installed);
+
 /* File tier (ExpertCache::fetch_parallel's file path, expert_cache.cpp:
  * 1194-1440, with its persistent readers, expert_io_workers.h): misses of
  * (role, layer) are read from `path` at offset + expert * slab_bytes instead

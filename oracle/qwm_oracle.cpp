@@ -24,6 +24,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
+#include <cstdio>
 #include <cstring>
 #include <limits>
 #include <stdexcept>
@@ -923,6 +924,70 @@ QWO_API int qwo_pool_ensure(qwo_pool * p, int layer, const int32_t * ids, int n,
     if (n_fetch) *n_fetch = nf;
     return rc;
 }
+// ExpertCache::save_profile (expert_cache.cpp:1485-1500) as text into buf
+// (cap bytes): "QWENEXPCACHE 1", "n_layer n_expert", then "role layer expert
+// count" for every counted key, roles in order, keys ascending (the
+// reference walks its count map in hash order; the loader below reads any
+// order).  Returns the text length, or -1 if it does not fit.
+QWO_API int qwo_pool_save_profile(const qwo_pool * p, char * buf, int cap) {
+    std::string s = "QWENEXPCACHE 1\n" + std::to_string(p->n_layer) + " " + std::to_string(p->n_expert) + "\n";
+    for (int r = 0; r < 3; ++r) {
+        std::vector<std::pair<int, uint64_t>> kv(p->role[r].count.begin(), p->role[r].count.end());
+        std::sort(kv.begin(), kv.end());
+        for (const auto & c : kv)
+            s += std::to_string(r) + " " + std::to_string(c.first / p->n_expert) + " " +
+                 std::to_string(c.first % p->n_expert) + " " + std::to_string(c.second) + "\n";
+    }
+    if ((int)s.size() + 1 > cap) return -1;
+    std::memcpy(buf, s.c_str(), s.size() + 1);
+    return (int)s.size();
+}
+
+// ExpertCache::load_prefetch (expert_cache.cpp:1502-1538) from profile text:
+// a header other than "QWENEXPCACHE 1" with this pool's n_layer and n_expert
+// is a cold start (nothing installed, returns 0).  Entries with role, layer
+// and expert in range are ordered by count, largest first (a stable order:
+// equal counts keep the text's order, where the reference's std::sort leaves
+// it unspecified); each is installed -- lowest free slot, drop-free, clock +
+// 1, uncounted -- unless its role's pool is full or the key is resident.
+// fetch_log as in qwo_pool_ensure.  Returns the number of installs.
+QWO_API int qwo_pool_load_profile(qwo_pool * p, const char * text, int32_t * fetch_log) {
+    int ver = 0, nl = 0, ne = 0, used = 0;
+    if (std::sscanf(text, "QWENEXPCACHE %d%n", &ver, &used) != 1 || ver != 1) return 0;
+    text += used;
+    if (std::sscanf(text, "%d %d%n", &nl, &ne, &used) != 2 || nl != p->n_layer || ne != p->n_expert) return 0;
+    text += used;
+    struct Ent { int r, l, e; unsigned long long c; };
+    std::vector<Ent> ents;
+    Ent en;
+    while (std::sscanf(text, "%d %d %d %llu%n", &en.r, &en.l, &en.e, &en.c, &used) == 4) {
+        text += used;
+        if (en.r >= 0 && en.r < 3 && en.l >= 0 && en.l < p->n_layer && en.e >= 0 && en.e < p->n_expert) ents.push_back(en);
+    }
+    std::stable_sort(ents.begin(), ents.end(), [](const Ent & a, const Ent & b) { return a.c > b.c; });
+    int n = 0;
+    for (const Ent & x : ents) {
+        auto & R = p->role[x.r];
+        if ((int)R.key2slot.size() >= R.n_slots) continue;
+        const int key = x.l * p->n_expert + x.e;
+        if (R.key2slot.count(key)) continue;
+        int slot = 0;
+        while (R.slot2key[(size_t)slot] >= 0) ++slot;
+        if (fetch_log) {
+            fetch_log[4 * n + 0] = x.r; fetch_log[4 * n + 1] = x.l;
+            fetch_log[4 * n + 2] = x.e; fetch_log[4 * n + 3] = slot;
+        }
+        R.key2slot.emplace(key, slot);
+        R.slot2key[(size_t)slot] = key;
+        R.occ[(size_t)x.l]++;
+        R.slot_of[(size_t)key] = slot;
+        p->clock += 1;
+        R.clk[(size_t)slot] = p->clock;
+        ++n;
+    }
+    return n;
+}
+
 QWO_API void qwo_pool_stats(const qwo_pool * p, uint64_t * out3) {
     out3[0] = p->hits; out3[1] = p->misses; out3[2] = p->evictions;
 }

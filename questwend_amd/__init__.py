@@ -102,6 +102,8 @@ def lib():
         "qwm_pool_slots": (ctypes.c_int, [_P, _I32, _P, _P]),
         "qwm_pool_attach_file": (ctypes.c_int, [_P, _I32, _I32, ctypes.c_char_p, ctypes.c_uint64]),
         "qwm_pool_set_io": (ctypes.c_int, [_P, _I32, _I32]),
+        "qwm_pool_save_profile": (ctypes.c_int, [_P, ctypes.c_char_p]),
+        "qwm_pool_load_profile": (ctypes.c_int, [_P, ctypes.c_char_p, _P]),
         "qwm_slab_fetch_async": (ctypes.c_int, [_P, _SZ, _I32, _P, _P, _P]),
         "qwm_quantize": (ctypes.c_int, [_I32, _P, _P, _I64, _P]),
         "qwm_profile_start": (ctypes.c_int, [ctypes.c_char_p, _I32]),

@@ -39,6 +39,7 @@
 
 #include <cerrno>
 #include <condition_variable>
+#include <cstdio>
 #include <cstdint>
 #include <cstring>
 #include <algorithm>
@@ -565,6 +566,77 @@ int qwm_pool_slots(const qwm_pool * p, int32_t role, int32_t * keys, uint64_t * 
         if (clocks) clocks[s] = R.clk[s];
     }
     return QWM_OK;
+}
+
+// ExpertCache::save_profile (expert_cache.cpp:1485-1500): the same text
+// format; roles in order, keys ascending within a role.
+int qwm_pool_save_profile(const qwm_pool * p, const char * path) {
+    if (!p || !path) return fail(QWM_ERR_ARG, "pool_save_profile: NULL argument");
+    FILE * f = std::fopen(path, "wb");
+    if (!f) return fail(QWM_ERR_IO, std::string("pool_save_profile: ") + path + ": " + strerror(errno));
+    bool ok = std::fprintf(f, "QWENEXPCACHE 1\n%d %d\n", p->n_layer, p->n_expert) > 0;
+    for (int r = 0; r < 3 && ok; ++r) {
+        std::vector<std::pair<int32_t, uint64_t>> kv(p->role[r].count.begin(), p->role[r].count.end());
+        std::sort(kv.begin(), kv.end());
+        for (const auto & c : kv)
+            ok = ok && std::fprintf(f, "%d %d %d %llu\n", r, c.first / p->n_expert, c.first % p->n_expert,
+                                    (unsigned long long)c.second) > 0;
+    }
+    ok = (std::fclose(f) == 0) && ok;
+    if (!ok) return fail(QWM_ERR_IO, std::string("pool_save_profile: writing ") + path + " failed");
+    return QWM_OK;
+}
+
+// ExpertCache::load_prefetch (expert_cache.cpp:1502-1538): a missing or
+// incompatible profile is a cold start (nothing installed, QWM_OK).  The
+// in-range entries, largest count first (equal counts in file order), are
+// installed while their role's pool has a free slot and the key is not
+// resident; the slabs are fetched as ensure fetches misses.
+int qwm_pool_load_profile(qwm_pool * p, const char * path, int64_t * n_installed) {
+    if (!p || !path) return fail(QWM_ERR_ARG, "pool_load_profile: NULL argument");
+    if (n_installed) *n_installed = 0;
+    FILE * f = std::fopen(path, "rb");
+    if (!f) return QWM_OK;
+    int ver = 0, nl = 0, ne = 0;
+    if (std::fscanf(f, "QWENEXPCACHE %d", &ver) != 1 || ver != 1 || std::fscanf(f, "%d %d", &nl, &ne) != 2 ||
+        nl != p->n_layer || ne != p->n_expert) {
+        std::fclose(f);
+        return QWM_OK;
+    }
+    struct Ent { int r, l, e; unsigned long long c; };
+    std::vector<Ent> ents;
+    Ent en;
+    while (std::fscanf(f, "%d %d %d %llu", &en.r, &en.l, &en.e, &en.c) == 4)
+        if (en.r >= 0 && en.r < 3 && en.l >= 0 && en.l < p->n_layer && en.e >= 0 && en.e < p->n_expert) ents.push_back(en);
+    std::fclose(f);
+    std::stable_sort(ents.begin(), ents.end(), [](const Ent & a, const Ent & b) { return a.c > b.c; });
+    int rc = QWM_OK, cur = -1;
+    int64_t n = 0;
+    auto flush_layer = [&](int layer) {          // the fetch batches are per layer
+        if (layer < 0) return QWM_OK;
+        const int grc = p->gather ? p->flush(layer) : QWM_OK;
+        const int frc = p->flush_files(layer);
+        return grc != QWM_OK ? grc : frc;
+    };
+    for (const Ent & x : ents) {
+        auto & R = p->role[x.r];
+        if ((int)R.key2slot.size() >= R.n_slots) continue;
+        const int32_t key = x.l * p->n_expert + x.e;
+        if (R.key2slot.count(key)) continue;
+        if (x.l != cur) {
+            if ((rc = flush_layer(cur)) != QWM_OK) break;
+            cur = x.l;
+        }
+        const int32_t slot = p->pick(R);         // the lowest free slot
+        if ((rc = p->fetch(x.r, x.l, x.e, slot)) != QWM_OK) break;
+        p->publish(R, slot, key, x.l);
+        ++n;
+    }
+    const int lrc = flush_layer(cur);
+    if (rc == QWM_OK) rc = lrc;
+    if (p->pending) QWM_HIP_CHECK(hipEventRecord(p->done, p->copy));
+    if (n_installed) *n_installed = n;
+    return rc;
 }
 
 int qwm_pool_attach_file(qwm_pool * p, int32_t role, int32_t layer, const char * path, uint64_t offset) {

@@ -207,3 +207,89 @@ def test_pool_attach_file_checks_without_gpu(tmp_path):
         assert L.qwm_pool_set_io(h, 4, 3) == qa.OK
     finally:
         L.qwm_pool_destroy(h)
+
+
+def oracle_profile_text(o):
+    buf = ctypes.create_string_buffer(1 << 20)
+    n = oracle().qwo_pool_save_profile(o.h, buf, len(buf))
+    assert n >= 0
+    return buf.value
+
+
+def load_profile(g, path):
+    n = ctypes.c_int64(-1)
+    qa.check(qa.lib().qwm_pool_load_profile(g.h, str(path).encode(), ctypes.byref(n)))
+    return n.value
+
+
+@pytest.mark.parametrize("indexed", [0, 1])
+def test_pool_profile_roundtrip_matches_oracle(tmp_path, indexed):
+    """save_profile after a Zipf trace writes the oracle's text byte for byte;
+    load_prefetch of it into fresh, smaller pools installs the same experts
+    into the same slots with the same clocks, counting nothing."""
+    rng = np.random.default_rng(23)
+    n_layer, n_expert, slots = 3, 64, [40, 33, 47]
+    g = GpuPool(n_layer, n_expert, slots, 0, indexed)
+    o = OraclePool(n_layer, n_expert, slots)
+    pop = 1.0 / np.arange(1, n_expert + 1) ** 1.1
+    pop /= pop.sum()
+    perm = rng.permutation(n_expert)
+    for step in range(150):
+        layer = int(rng.integers(0, n_layer))
+        ids = np.concatenate([perm[rng.choice(n_expert, 6, replace=False, p=pop)] for _ in range(4)])
+        assert g.ensure(layer, ids)[0] == o.ensure(layer, ids)[0] == 0
+    path = tmp_path / "cache.profile"
+    qa.check(qa.lib().qwm_pool_save_profile(g.h, str(path).encode()))
+    text = path.read_bytes()
+    assert text == oracle_profile_text(o)
+    assert text.startswith(b"QWENEXPCACHE 1\n3 64\n")
+
+    small = [20, 9, 31]
+    g2 = GpuPool(n_layer, n_expert, small, 0, indexed)
+    o2 = OraclePool(n_layer, n_expert, small)
+    n_g = load_profile(g2, path)
+    n_o = oracle().qwo_pool_load_profile(o2.h, text, None)
+    assert n_g == n_o == sum(small)
+    for r in range(3):
+        kg, cg = g2.state(r)
+        ko, co = o2.state(r)
+        assert np.array_equal(kg, ko) and np.array_equal(cg, co)
+    st = qa.PoolStats()
+    qa.check(qa.lib().qwm_pool_get_stats(g2.h, ctypes.byref(st)))
+    assert (st.hits, st.misses, st.evictions) == (0, 0, 0) and st.clock == sum(small)
+    # a second load finds every pool full: nothing more is installed
+    assert load_profile(g2, path) == 0
+
+
+def test_pool_profile_known_answer(tmp_path):
+    """A hand-made profile, 1 layer x 4 experts, 2 slots per role: per role the
+    two largest counts win, the larger into the lower slot; entries out of
+    range are ignored; equal counts keep the file's order; the clock runs
+    over the installs in count order across roles."""
+    path = tmp_path / "p.txt"
+    path.write_text("QWENEXPCACHE 1\n1 4\n"
+                    "0 0 0 5\n0 0 1 9\n0 0 2 7\n0 0 3 1\n"     # gate: 1 (9), 2 (7)
+                    "1 0 3 4\n1 0 0 4\n1 0 1 2\n"              # up: 3 and 0 tie at 4: file order
+                    "2 0 2 8\n2 1 0 99\n3 0 0 99\n2 0 9 99\n")  # down: 2 only; the rest out of range
+    g = GpuPool(1, 4, [2, 2, 2])
+    assert load_profile(g, path) == 5
+    # count order: gate 1 (9), down 2 (8), gate 2 (7), up 3 (4), up 0 (4)
+    assert [g.state(r)[0].tolist() for r in range(3)] == [[1, 2], [3, 0], [2, -1]]
+    assert [g.state(r)[1].tolist() for r in range(3)] == [[1, 3], [4, 5], [2, 0]]
+    o = OraclePool(1, 4, [2, 2, 2])
+    assert oracle().qwo_pool_load_profile(o.h, path.read_bytes(), None) == 5
+    for r in range(3):
+        assert np.array_equal(g.state(r)[0], o.state(r)[0]) and np.array_equal(g.state(r)[1], o.state(r)[1])
+
+
+@pytest.mark.parametrize("text", [None, b"QWENEXPCACHE 2\n1 4\n0 0 1 9\n", b"QWENEXPCACHE 1\n2 4\n0 0 1 9\n",
+                                  b"QWENEXPCACHE 1\n1 5\n0 0 1 9\n", b"garbage\n"])
+def test_pool_profile_cold_start(tmp_path, text):
+    """A missing profile, another version or another pool shape installs
+    nothing and is not an error (the reference's cold start)."""
+    path = tmp_path / "p.txt"
+    if text is not None:
+        path.write_bytes(text)
+    g = GpuPool(1, 4, [2, 2, 2])
+    assert load_profile(g, path) == 0
+    assert all((g.state(r)[0] == -1).all() for r in range(3))

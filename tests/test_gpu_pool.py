@@ -337,3 +337,50 @@ def test_pool_file_read_failure_unpublishes(dev, tmp_path, mode):
                 assert np.array_equal(dev_bytes[out[r, i]], src[e]), f"role {r} expert {e}"
     finally:
         L.qwm_pool_destroy(h)
+
+
+@pytest.mark.parametrize("mode", ["memcpy", "gather", "file"])
+def test_pool_profile_prefetch_fills_slabs(dev, tmp_path, mode):
+    """load_prefetch over two layers: the installed slots hold their experts'
+    slabs byte for byte once qwm_pool_wait has ordered the copies, whichever
+    way the slabs arrive (per-slab copies, gather, file tier)."""
+    L = qa.lib()
+    n_layer, E, S, slab = 2, 8, 3, 4096
+    rng = np.random.default_rng(8)
+    host = [[pinned(rng.integers(0, 256, E * slab, dtype=np.uint8)) for _ in range(3)] for _ in range(n_layer)]
+    host_ptrs = [(ctypes.c_void_p * n_layer)(*[host[l][r].data_ptr() for l in range(n_layer)]) for r in range(3)]
+    pool_t = [torch.zeros(S * slab, dtype=torch.uint8, device="cuda") for _ in range(3)]
+    d = qa.PoolDesc()
+    d.n_layer, d.n_expert = n_layer, E
+    for r in range(3):
+        d.n_slots[r], d.pool_data[r], d.slab_bytes[r] = S, pool_t[r].data_ptr(), slab
+        d.host_slabs[r] = None if mode == "file" else ctypes.cast(host_ptrs[r], ctypes.c_void_p)
+    d.fetch_mode = FETCH["memcpy" if mode == "memcpy" else "gather"]
+    copy = torch.cuda.Stream()
+    h = ctypes.c_void_p()
+    qa.check(L.qwm_pool_create(ctypes.byref(d), ctypes.c_void_p(copy.cuda_stream), ctypes.byref(h)))
+    try:
+        if mode == "file":
+            path = str(tmp_path / "slabs.bin")
+            offs = write_slab_file(path, host)
+            for l in range(n_layer):
+                for r in range(3):
+                    qa.check(L.qwm_pool_attach_file(h, r, l, path.encode(), offs[l][r]))
+        lines = [f"{r} {l} {e} {int(c)}" for r in range(3) for l in range(n_layer) for e in range(E)
+                 for c in [rng.integers(1, 1000)]]
+        prof = tmp_path / "cache.profile"
+        prof.write_text(f"QWENEXPCACHE 1\n{n_layer} {E}\n" + "\n".join(lines) + "\n")
+        n = ctypes.c_int64()
+        qa.check(L.qwm_pool_load_profile(h, str(prof).encode(), ctypes.byref(n)))
+        assert n.value == 3 * S
+        qa.check(L.qwm_pool_wait(h, None))
+        torch.cuda.synchronize()
+        for r in range(3):
+            keys = np.zeros(S, np.int32)
+            qa.check(L.qwm_pool_slots(h, r, ptr(keys), None))
+            dev_bytes = pool_t[r].cpu().numpy().reshape(S, slab)
+            for s, key in enumerate(keys):
+                lyr, e = divmod(int(key), E)
+                assert np.array_equal(dev_bytes[s], host[lyr][r].numpy().reshape(E, slab)[e]), f"role {r} slot {s}"
+    finally:
+        L.qwm_pool_destroy(h)

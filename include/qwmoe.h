@@ -286,6 +286,24 @@ int qwm_pool_load_profile(qwm_pool * pool, const char * path, int64_t * n_instal
  * keeps the descriptor open until qwm_pool_destroy or the next attach of the
  * same (role, layer). */
 int qwm_pool_attach_file(qwm_pool * pool, int32_t role, int32_t layer, const char * path, uint64_t offset);
+/* GGUF model files (Model::tensor_file_offset, core/model.cpp:454-458 and
+ * 636-677): a tensor's ggml type, shape and absolute file offset (the data
+ * section, the end of the tensor infos rounded up to general.alignment, plus
+ * the tensor's offset).  nbytes = 0 for a type not sized here (sized: F32,
+ * F16, BF16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K..Q6_K).  QWM_ERR_IO: the
+ * file cannot be opened; QWM_ERR_ARG: not GGUF v2/v3, malformed, or no such
+ * tensor. */
+typedef struct qwm_gguf_tensor {
+    int32_t type, n_dims;
+    int64_t ne[4];
+    uint64_t offset, nbytes;
+} qwm_gguf_tensor;
+int qwm_gguf_find_tensor(const char * path, const char * name, qwm_gguf_tensor * out);
+/* Attaches blk.<first_block + l>.ffn_{gate,up,down}_exps.weight (the names of
+ * expert_cache.cpp:88-93) of a GGUF file to the file tier, for every layer l
+ * of the pool; each must hold n_expert slabs of the role's slab_bytes
+ * (QWM_ERR_ARG otherwise, naming the tensor). */
+int qwm_pool_attach_gguf(qwm_pool * pool, const char * path, int32_t first_block);
 /* Reader threads (1..64, default 8) and staging slabs (0: as many as fit in
  * 64 MiB, the reference's batch size) of the file tier. */
 int qwm_pool_set_io(qwm_pool * pool, int32_t n_threads, int32_t staging_slabs);

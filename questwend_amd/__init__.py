@@ -65,6 +65,12 @@ class PoolStats(ctypes.Structure):
 _lib = None
 
 
+class GgufTensor(ctypes.Structure):
+    """struct qwm_gguf_tensor."""
+    _fields_ = [("type", ctypes.c_int32), ("n_dims", ctypes.c_int32), ("ne", ctypes.c_int64 * 4),
+                ("offset", ctypes.c_uint64), ("nbytes", ctypes.c_uint64)]
+
+
 def lib():
     """Loads libqwmoe.so (built in-tree by __graft_entry__.build()); raises if absent."""
     global _lib
@@ -102,6 +108,8 @@ def lib():
         "qwm_pool_slots": (ctypes.c_int, [_P, _I32, _P, _P]),
         "qwm_pool_attach_file": (ctypes.c_int, [_P, _I32, _I32, ctypes.c_char_p, ctypes.c_uint64]),
         "qwm_pool_set_io": (ctypes.c_int, [_P, _I32, _I32]),
+        "qwm_gguf_find_tensor": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(GgufTensor)]),
+        "qwm_pool_attach_gguf": (ctypes.c_int, [_P, ctypes.c_char_p, _I32]),
         "qwm_pool_save_profile": (ctypes.c_int, [_P, ctypes.c_char_p]),
         "qwm_pool_load_profile": (ctypes.c_int, [_P, ctypes.c_char_p, _P]),
         "qwm_slab_fetch_async": (ctypes.c_int, [_P, _SZ, _I32, _P, _P, _P]),

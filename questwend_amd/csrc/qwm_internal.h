@@ -133,6 +133,11 @@ struct GatherArgs {
 };
 int launch_slab_gather(const GatherArgs & a, hipStream_t s);
 
+// ---- qwm_pool.cpp: what qwm_gguf.cpp needs of a pool ----
+int32_t pool_n_layer(const qwm_pool * p);
+int32_t pool_n_expert(const qwm_pool * p);
+size_t pool_slab_bytes(const qwm_pool * p, int role);
+
 // ---- qwm_quant.hip ----
 int launch_quantize(int32_t type, const float * src, void * dst, int64_t n, hipStream_t s);
 

@@ -423,6 +423,12 @@ struct qwm_pool {
     }
 };
 
+namespace qwm {
+int32_t pool_n_layer(const qwm_pool * p) { return p->n_layer; }
+int32_t pool_n_expert(const qwm_pool * p) { return p->n_expert; }
+size_t pool_slab_bytes(const qwm_pool * p, int role) { return p->role[role].slab; }
+}  // namespace qwm
+
 extern "C" {
 
 int qwm_pool_create(const qwm_pool_desc * d, void * copy_stream, qwm_pool ** out) {

@@ -14,6 +14,7 @@ import ctypes
 import numpy as np
 import pytest
 
+from tests.gguf_file import GGML_Q4_K, T_STR, write_gguf
 from tests.helpers import bits, oracle, ptr
 from tests.moe_case import MoeCase, rel_err
 
@@ -339,13 +340,14 @@ def test_pool_file_read_failure_unpublishes(dev, tmp_path, mode):
         L.qwm_pool_destroy(h)
 
 
-@pytest.mark.parametrize("mode", ["memcpy", "gather", "file"])
+@pytest.mark.parametrize("mode", ["memcpy", "gather", "file", "gguf"])
 def test_pool_profile_prefetch_fills_slabs(dev, tmp_path, mode):
     """load_prefetch over two layers: the installed slots hold their experts'
     slabs byte for byte once qwm_pool_wait has ordered the copies, whichever
-    way the slabs arrive (per-slab copies, gather, file tier)."""
+    way the slabs arrive (per-slab copies, gather, file tier, or the file tier
+    over the expert tensors of a GGUF model file)."""
     L = qa.lib()
-    n_layer, E, S, slab = 2, 8, 3, 4096
+    n_layer, E, S, slab = 2, 8, 3, 4608          # Q4_K [256, 32] per expert
     rng = np.random.default_rng(8)
     host = [[pinned(rng.integers(0, 256, E * slab, dtype=np.uint8)) for _ in range(3)] for _ in range(n_layer)]
     host_ptrs = [(ctypes.c_void_p * n_layer)(*[host[l][r].data_ptr() for l in range(n_layer)]) for r in range(3)]
@@ -354,7 +356,7 @@ def test_pool_profile_prefetch_fills_slabs(dev, tmp_path, mode):
     d.n_layer, d.n_expert = n_layer, E
     for r in range(3):
         d.n_slots[r], d.pool_data[r], d.slab_bytes[r] = S, pool_t[r].data_ptr(), slab
-        d.host_slabs[r] = None if mode == "file" else ctypes.cast(host_ptrs[r], ctypes.c_void_p)
+        d.host_slabs[r] = None if mode in ("file", "gguf") else ctypes.cast(host_ptrs[r], ctypes.c_void_p)
     d.fetch_mode = FETCH["memcpy" if mode == "memcpy" else "gather"]
     copy = torch.cuda.Stream()
     h = ctypes.c_void_p()
@@ -366,6 +368,13 @@ def test_pool_profile_prefetch_fills_slabs(dev, tmp_path, mode):
             for l in range(n_layer):
                 for r in range(3):
                     qa.check(L.qwm_pool_attach_file(h, r, l, path.encode(), offs[l][r]))
+        if mode == "gguf":
+            path = str(tmp_path / "model.gguf")
+            ne = {"gate": [256, 32, E], "up": [256, 32, E], "down": [256, 32, E]}
+            ts = [(f"blk.{5 + l}.ffn_{role}_exps.weight", GGML_Q4_K, ne[role], host[l][r].numpy().tobytes())
+                  for l in range(n_layer) for r, role in enumerate(("gate", "up", "down"))]
+            write_gguf(path, [("general.architecture", T_STR, "qwen3moe")], ts, alignment=64)
+            qa.check(L.qwm_pool_attach_gguf(h, path.encode(), 5))
         lines = [f"{r} {l} {e} {int(c)}" for r in range(3) for l in range(n_layer) for e in range(E)
                  for c in [rng.integers(1, 1000)]]
         prof = tmp_path / "cache.profile"

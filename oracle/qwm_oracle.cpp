@@ -44,12 +44,14 @@ constexpr int QK8_0 = 32;
 struct block_q4_K { uint16_t d, dmin; uint8_t scales[12]; uint8_t qs[QK_K / 2]; };
 struct block_q8_K { float d; int8_t qs[QK_K]; int16_t bsums[QK_K / 16]; };
 struct block_q8_0 { uint16_t d; int8_t qs[QK8_0]; };
+struct block_q6_K { uint8_t ql[QK_K / 2]; uint8_t qh[QK_K / 4]; int8_t scales[QK_K / 16]; uint16_t d; };
+static_assert(sizeof(block_q6_K) == 210, "q6_K");
 static_assert(sizeof(block_q4_K) == 144, "q4_K");
 static_assert(sizeof(block_q8_K) == 292, "q8_K");
 static_assert(sizeof(block_q8_0) == 34, "q8_0");
 
 // ggml_type values (ggml.h:390-420).
-constexpr int T_F32 = 0, T_Q8_0 = 8, T_Q4_K = 12, T_Q8_K = 15;
+constexpr int T_F32 = 0, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14, T_Q8_K = 15;
 
 inline uint32_t f2u(float f) { uint32_t u; std::memcpy(&u, &f, 4); return u; }
 inline float u2f(uint32_t u) { float f; std::memcpy(&f, &u, 4); return f; }
@@ -387,6 +389,49 @@ float vec_dot_q4_K_q8_K(int n, const block_q4_K * x, const block_q8_K * y) {
     return hsum8(acc) + hsum4(acc_m);
 }
 
+// The 6-bit value of element e (0..255) of a Q6_K block, 0..63
+// (ggml-quants.c:1940-1970 before its -32): element 128j + 32k + l takes the
+// low (k < 2) or high (k >= 2) nibble of ql[64j + 32(k & 1) + l] and bits
+// 2k, 2k+1 of qh[32j + l] as its top two bits.
+inline int q6_value(const block_q6_K & b, int e) {
+    const int j = e / 128, k = (e % 128) / 32, l = e % 32;
+    const uint8_t q = b.ql[64 * j + 32 * (k & 1) + l];
+    return ((k < 2 ? q & 15 : q >> 4) | (((b.qh[32 * j + l] >> (2 * k)) & 3) << 4));
+}
+
+// dequantize_row_q6_K (ggml-quants.c:1940-1970): d * scale[e / 16] * (q - 32).
+void dequantize_row_q6_K(const block_q6_K * x, float * y, int64_t k) {
+    for (int64_t i = 0; i < k / QK_K; ++i) {
+        const float d = fp16_to_fp32(x[i].d);
+        for (int e = 0; e < QK_K; ++e) y[i * QK_K + e] = d * x[i].scales[e / 16] * (q6_value(x[i], e) - 32);
+    }
+}
+
+// ggml_vec_dot_q6_K_q8_K, x86 AVX2 branch (ggml-cpu/arch/x86/quants.c:
+// 2490-2566): eight int32 lanes per block, lane m gathering, over the eight
+// 32-value chunks c, scale[2c + (m >= 4)] times the dot of chunk values
+// 4m..4m+3 (6-bit values without the -32), minus 32 * (bsums[2m] * scale[2m]
+// + bsums[2m+1] * scale[2m+1]); then acc[m] = fma(y.d * fp16(x.d),
+// (float)lane, acc[m]) block after block and hsum8.
+float vec_dot_q6_K_q8_K(int n, const block_q6_K * x, const block_q8_K * y) {
+    float acc[8] = {0};
+    for (int i = 0; i < n / QK_K; ++i) {
+        const float d = y[i].d * fp16_to_fp32(x[i].d);
+        int32_t lane[8] = {0};
+        for (int c = 0; c < 8; ++c)
+            for (int m = 0; m < 8; ++m) {
+                int32_t s = 0;
+                for (int e = 32 * c + 4 * m; e < 32 * c + 4 * m + 4; ++e) s += q6_value(x[i], e) * y[i].qs[e];
+                lane[m] += x[i].scales[2 * c + (m >= 4)] * s;
+            }
+        for (int m = 0; m < 8; ++m) {
+            lane[m] -= 32 * (y[i].bsums[2 * m] * x[i].scales[2 * m] + y[i].bsums[2 * m + 1] * x[i].scales[2 * m + 1]);
+            acc[m] = fmaf(d, (float)lane[m], acc[m]);
+        }
+    }
+    return hsum8(acc);
+}
+
 // ggml-cpu/arch/x86/quants.c:1372-1402 (AVX2 branch); tinyBLAS_Q0_AVX
 // (llamafile/sgemm.cpp:1625-1660) accumulates in the same lane order.
 float vec_dot_q8_0_q8_0(int n, const block_q8_0 * x, const block_q8_0 * y) {
@@ -530,6 +575,7 @@ size_t row_bytes(int type, int64_t k) {
         case T_F32: return (size_t)k * 4;
         case T_Q8_0: return (size_t)(k / QK8_0) * sizeof(block_q8_0);
         case T_Q4_K: return (size_t)(k / QK_K) * sizeof(block_q4_K);
+        case T_Q6_K: return (size_t)(k / QK_K) * sizeof(block_q6_K);
         case T_Q8_K: return (size_t)(k / QK_K) * sizeof(block_q8_K);
     }
     throw std::invalid_argument("unsupported ggml type");
@@ -538,6 +584,7 @@ size_t row_bytes(int type, int64_t k) {
 int vec_dot_type(int type) {
     switch (type) {
         case T_Q4_K: return T_Q8_K;
+        case T_Q6_K: return T_Q8_K;
         case T_Q8_0: return T_Q8_0;
         case T_F32: return T_F32;
     }
@@ -553,6 +600,7 @@ void from_float(int vtype, const float * x, void * y, int64_t k) {
 float dot_row(int type, int k, const void * w, const void * xq) {
     switch (type) {
         case T_Q4_K: return vec_dot_q4_K_q8_K(k, (const block_q4_K *)w, (const block_q8_K *)xq);
+        case T_Q6_K: return vec_dot_q6_K_q8_K(k, (const block_q6_K *)w, (const block_q8_K *)xq);
         case T_Q8_0: return vec_dot_q8_0_q8_0(k, (const block_q8_0 *)w, (const block_q8_0 *)xq);
         case T_F32: return vec_dot_f32(k, (const float *)w, (const float *)xq);
     }
@@ -631,6 +679,8 @@ QWO_API void qwo_quantize_q8_K(const float * x, void * y, int64_t k) { quantize_
 QWO_API void qwo_quantize_q8_0_ref(const float * x, void * y, int64_t k) { quantize_row_q8_0_ref(x, (block_q8_0 *)y, k); }
 QWO_API void qwo_quantize_q8_0_x86(const float * x, void * y, int64_t k) { quantize_row_q8_0_x86(x, (block_q8_0 *)y, k); }
 QWO_API float qwo_vec_dot_q4_K_q8_K(int n, const void * x, const void * y) { return vec_dot_q4_K_q8_K(n, (const block_q4_K *)x, (const block_q8_K *)y); }
+QWO_API float qwo_vec_dot_q6_K_q8_K(int n, const void * x, const void * y) { return vec_dot_q6_K_q8_K(n, (const block_q6_K *)x, (const block_q8_K *)y); }
+QWO_API void qwo_dequantize_q6_K(const void * x, float * y, int64_t k) { dequantize_row_q6_K((const block_q6_K *)x, y, k); }
 QWO_API float qwo_vec_dot_q8_0_q8_0(int n, const void * x, const void * y) { return vec_dot_q8_0_q8_0(n, (const block_q8_0 *)x, (const block_q8_0 *)y); }
 QWO_API float qwo_vec_dot_f32(int n, const float * x, const float * y) { return vec_dot_f32(n, x, y); }
 QWO_API float qwo_sgemm_dot_f32(int k, const float * a, const float * b) { return sgemm_dot_f32(k, a, b); }
@@ -713,6 +763,7 @@ struct qwo_moe_args {
     const float * sh_gate_inp;      // optional f32 [H]
     float * out;                    // [T][H]
     float * gate_out; float * up_out; float * act_out; float * experts_out;  // optional
+    int down_type;                  // type of the down pool; 0: weight_type (Q4_K_M files store some as Q6_K)
 };
 
 QWO_API int qwo_moe_block(const qwo_moe_args * a) {
@@ -723,7 +774,8 @@ QWO_API int qwo_moe_block(const qwo_moe_args * a) {
         mul_mat_id(a->weight_type, a->up_pool, H, N, a->n_slots, a->x, 1, T, a->slot_u, k, up.data());
         mul_mat_id(a->weight_type, a->gate_pool, H, N, a->n_slots, a->x, 1, T, a->slot_g, k, gate.data());
         for (int64_t r = 0; r < T * k; ++r) vec_swiglu((int)N, act.data() + r * N, gate.data() + r * N, up.data() + r * N);
-        mul_mat_id(a->weight_type, a->down_pool, N, H, a->n_slots, act.data(), k, T, a->slot_d, k, ex.data());
+        mul_mat_id(a->down_type ? a->down_type : a->weight_type, a->down_pool, N, H, a->n_slots, act.data(), k, T,
+                   a->slot_d, k, ex.data());
         for (int64_t t = 0; t < T; ++t) {
             float * o = a->out + t * H;
             const float * w = a->weights + t * k;
@@ -750,7 +802,7 @@ QWO_API int qwo_moe_block(const qwo_moe_args * a) {
                 vec_silu((int)Ns, s.data() + t * Ns, g.data() + t * Ns);
                 for (int64_t i = 0; i < Ns; ++i) s[t * Ns + i] = s[t * Ns + i] * u[t * Ns + i];
             }
-            mul_mat(a->weight_type, a->sh_down, Ns, H, s.data(), T, sh.data());
+            mul_mat(a->down_type ? a->down_type : a->weight_type, a->sh_down, Ns, H, s.data(), T, sh.data());
             for (int64_t t = 0; t < T; ++t) {
                 float gsc = 1.0f;
                 if (a->sh_gate_inp) {

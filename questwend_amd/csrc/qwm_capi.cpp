@@ -26,6 +26,7 @@ static size_t type_size(int32_t type) {
         case T_I32: return 4;
         case T_Q8_0: return 34;
         case T_Q4_K: return 144;
+        case T_Q6_K: return 210;
     }
     return 0;
 }
@@ -33,6 +34,7 @@ static int64_t block_len(int32_t type) {
     switch (type) {
         case T_Q8_0: return 32;
         case T_Q4_K: return 256;
+        case T_Q6_K: return 256;
     }
     return 1;
 }
@@ -127,7 +129,10 @@ int qwm_profile_stop(float * durations_ms, int32_t capacity) {
 
 static int check_mmid(const qwm_tensor * as, const qwm_tensor * b, const qwm_tensor * ids, const qwm_tensor * dst) {
     if (!as || !b || !ids) return fail(QWM_ERR_ARG, "mul_mat_id: NULL tensor");
-    if (as->type != T_Q4_K && as->type != T_Q8_0) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: weights must be Q4_K or Q8_0");
+    if (as->type != T_Q4_K && as->type != T_Q8_0 && as->type != T_Q6_K)
+        return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: weights must be Q4_K, Q6_K or Q8_0");
+    if (as->type == T_Q6_K && ((uintptr_t)as->data % 4))   // rows and slabs may start 2 bytes off: handled
+        return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: Q6_K weights need 4-byte aligned data");
     if (b->type != T_F32 || ids->type != T_I32) return fail(QWM_ERR_ARG, "mul_mat_id: b must be f32 and ids i32");
     // ggml.c:3418-3428
     if (as->ne[3] != 1 || b->ne[3] != 1 || ids->ne[2] != 1 || ids->ne[3] != 1)
@@ -191,18 +196,26 @@ static int check_layer(const qwm_moe_layer * L, int64_t T, MoePlan & p) {
     if (L->router.type != T_F32 || !contiguous_rows(&L->router)) return fail(QWM_ERR_UNSUPPORTED, "moe: router must be contiguous f32 [H, E]");
     const qwm_tensor * pools[3] = {&L->gate_pool, &L->up_pool, &L->down_pool};
     for (const qwm_tensor * t : pools) {
-        if (t->type != T_Q4_K && t->type != T_Q8_0) return fail(QWM_ERR_UNSUPPORTED, "moe: pools must be Q4_K or Q8_0");
-        if (t->type != L->gate_pool.type) return fail(QWM_ERR_UNSUPPORTED, "moe: mixed pool types");
+        if (t->type != T_Q4_K && t->type != T_Q8_0 && t->type != T_Q6_K)
+            return fail(QWM_ERR_UNSUPPORTED, "moe: pools must be Q4_K, Q8_0 or (down only) Q6_K");
         if (!fully_contiguous(t)) return fail(QWM_ERR_UNSUPPORTED, "moe: pools must be contiguous");
     }
+    // gate and up of one type; down the same, or Q6_K beside Q4_K (Q4_K_M files)
+    if (L->up_pool.type != L->gate_pool.type || L->gate_pool.type == T_Q6_K ||
+        (L->down_pool.type != L->gate_pool.type && !(L->down_pool.type == T_Q6_K && L->gate_pool.type == T_Q4_K)))
+        return fail(QWM_ERR_UNSUPPORTED, "moe: mixed pool types (only a Q6_K down pool beside Q4_K gate/up is handled)");
+    if (L->down_pool.type == T_Q6_K && ((uintptr_t)L->down_pool.data % 4))
+        return fail(QWM_ERR_UNSUPPORTED, "moe: Q6_K pools need 4-byte aligned data");
     if (L->gate_pool.ne[0] != L->router.ne[0] || L->up_pool.ne[0] != L->router.ne[0] ||
         L->up_pool.ne[1] != L->gate_pool.ne[1] || L->down_pool.ne[0] != L->gate_pool.ne[1] ||
         L->down_pool.ne[1] != L->router.ne[0])
         return fail(QWM_ERR_ARG, "moe: pool shapes disagree (gate/up [H, N, S], down [N, H, S])");
     if (L->sh_gate.data) {
         if (!L->sh_up.data || !L->sh_down.data) return fail(QWM_ERR_ARG, "moe: shared expert needs gate, up and down");
-        if (L->sh_gate.type != L->gate_pool.type || L->sh_up.type != L->gate_pool.type || L->sh_down.type != L->gate_pool.type)
-            return fail(QWM_ERR_UNSUPPORTED, "moe: shared expert type must match the pools");
+        if (L->sh_gate.type != L->gate_pool.type || L->sh_up.type != L->gate_pool.type || L->sh_down.type != L->down_pool.type)
+            return fail(QWM_ERR_UNSUPPORTED, "moe: shared expert types must match the pools'");
+        if (L->sh_down.type == T_Q6_K && ((uintptr_t)L->sh_down.data % 4))
+            return fail(QWM_ERR_UNSUPPORTED, "moe: Q6_K shared down must be 4-byte aligned");
         if (L->sh_gate.ne[0] != L->router.ne[0] || L->sh_up.ne[1] != L->sh_gate.ne[1] || L->sh_down.ne[0] != L->sh_gate.ne[1] ||
             L->sh_down.ne[1] != L->router.ne[0])
             return fail(QWM_ERR_ARG, "moe: shared expert shapes disagree");
@@ -263,6 +276,7 @@ static int do_experts(const qwm_moe_layer * L, const MoePlan & p, const int32_t 
                       const int32_t * uslot = nullptr) {
     ExpertArgs a;
     a.wtype = L->gate_pool.type;
+    a.down_type = L->down_pool.type;
     a.gate = (const uint8_t *)L->gate_pool.data; a.up = (const uint8_t *)L->up_pool.data;
     a.down = (const uint8_t *)L->down_pool.data;
     a.gate_slab = L->gate_pool.nb[2]; a.up_slab = L->up_pool.nb[2]; a.down_slab = L->down_pool.nb[2];

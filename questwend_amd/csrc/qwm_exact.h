@@ -223,4 +223,99 @@ QWM_DEV void q80_dot8(float (&out)[MAXP], const uint8_t * row, const uint32_t * 
     }
 }
 
+// Q6_K x Q8_K row dots in ggml-CPU's exact float order: the x86
+// ggml_vec_dot_q6_K_q8_K (ggml-cpu/arch/x86/quants.c:2490-2566) keeps eight
+// int32 lanes per block, lane m gathering over the eight 32-value chunks c
+// scale[2c + (m >= 4)] times the dot of chunk values 4m..4m+3 (6-bit values
+// 0..63), minus 32 * (bsums[2m] * scale[2m] + bsums[2m+1] * scale[2m+1]),
+// then acc[m] = fma(y.d * fp16(x.d), (float)lane, acc[m]) block after block,
+// and hsum8.  Lane m of a row's 8-lane group plays CPU lane m.
+//
+// Q6_K blocks are 210 bytes (ql [128], qh [64], int8 scales [16], fp16 d), so
+// a block starts 2 bytes off dword alignment when its byte offset does: then
+// each needed dword is joined from the two aligned dwords around it
+// (v_alignbit) and d is a 16-bit load; no access leaves the block's bytes
+// and the 2 before it.  Lane m needs ql dwords 64j + 32h + 4m (j, h in 0..1:
+// chunk 4j + k takes the low (k < 2) or high nibbles of half h = k & 1) and
+// qh dwords 128 + 32j + 4m (bits 2k, 2k+1 are the values' top bits).  The
+// chunk bsums come from the activations in LDS: chunk m's values 0..15 are
+// dwords 8m' + m of lanes m' = 0..3, values 16..31 those of m' = 4..7.
+template <int NB, int MAXP>
+QWM_DEV void q6k_dot8(float (&out)[MAXP], const uint8_t * row, const uint32_t * sx, int n, int m) {
+    float acc[MAXP];
+#pragma unroll
+    for (int i = 0; i < MAXP; ++i) acc[i] = 0.f;
+    const int hm = m >= 4 ? 8 : 0;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const uint8_t * bp = row + 210 * b;
+        const int s = (int)((uintptr_t)bp & 2);
+        const uint32_t * A = reinterpret_cast<const uint32_t *>(bp - s);
+        auto get = [&](int r) -> uint32_t {        // the 4 bytes at bp + r, r % 4 == 0
+            const uint32_t lo = A[r >> 2];
+            if (!s) return lo;
+            return __builtin_amdgcn_alignbit(A[(r >> 2) + 1], lo, 16);
+        };
+        uint32_t ql[2][2], qh[2], sc[4];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            ql[j][0] = get(64 * j + 4 * m);
+            ql[j][1] = get(64 * j + 32 + 4 * m);
+            qh[j] = get(128 + 32 * j + 4 * m);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) sc[q] = get(192 + 4 * q);
+        const float dw = fp16_to_f32(*reinterpret_cast<const uint16_t *>(bp + 208));
+        int scc[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) scc[c] = (int)(int8_t)(uint8_t)(sc[c >> 1] >> (16 * (c & 1) + hm));
+        const int mq = m >> 1;
+        const uint32_t wm = mq == 0 ? sc[0] : mq == 1 ? sc[1] : mq == 2 ? sc[2] : sc[3];
+        const int sA = (int)(int8_t)(uint8_t)(wm >> (16 * (m & 1))), sB = (int)(int8_t)(uint8_t)(wm >> (16 * (m & 1) + 8));
+        uint32_t q6[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const int j = c >> 2, k = c & 3;
+            const uint32_t w = ql[j][k & 1];
+            q6[c] = ((k < 2 ? w : w >> 4) & 0x0f0f0f0fu) | (((qh[j] >> (2 * k)) & 0x03030303u) << 4);
+        }
+#pragma unroll
+        for (int i = 0; i < MAXP; ++i) {
+            if (i < n) {
+                const uint32_t * xb = sx + (i * NB + b) * XS;
+                const uint4 x0 = *reinterpret_cast<const uint4 *>(xb + 8 * m);
+                const uint4 x1 = *reinterpret_cast<const uint4 *>(xb + 8 * m + 4);
+                const float yd = __uint_as_float(xb[64]);
+                int isum = 0;
+                isum += scc[0] * dot4(q6[0], x0.x, 0);
+                isum += scc[1] * dot4(q6[1], x0.y, 0);
+                isum += scc[2] * dot4(q6[2], x0.z, 0);
+                isum += scc[3] * dot4(q6[3], x0.w, 0);
+                isum += scc[4] * dot4(q6[4], x1.x, 0);
+                isum += scc[5] * dot4(q6[5], x1.y, 0);
+                isum += scc[6] * dot4(q6[6], x1.z, 0);
+                isum += scc[7] * dot4(q6[7], x1.w, 0);
+                int bA = 0, bB = 0;
+#pragma unroll
+                for (int mm = 0; mm < 4; ++mm) {
+                    bA = dot4(xb[8 * mm + m], 0x01010101u, bA);
+                    bB = dot4(xb[8 * (mm + 4) + m], 0x01010101u, bB);
+                }
+                isum -= 32 * (bA * sA + bB * sB);
+                acc[i] = __builtin_fmaf(yd * dw, (float)isum, acc[i]);
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < MAXP; ++i) {
+        if (i < n) {
+            const float t = acc[i] + dpp_f<0x12C>(acc[i]);
+            const float u = t + dpp_f<0x12E>(t);
+            out[i] = u + dpp_f<0x12F>(u);
+        } else {
+            out[i] = 0.f;
+        }
+    }
+}
+
 }  // namespace qwm

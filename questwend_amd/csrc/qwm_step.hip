@@ -615,7 +615,7 @@ constexpr int MAX_STEP_WG = 1024;
 bool step_plan(const qwm_moe_layer * L, const qwm_tensor * lm_head, int64_t T, StepPlan & p, std::string & why) {
     if (!moe_plan(L, T, p.moe, why)) return false;
     if (p.moe.H != SH) { why = "the fused step is built for hidden size 2048"; return false; }
-    if (L->gate_pool.type != T_Q4_K) { why = "the fused step needs Q4_K expert pools"; return false; }
+    if (L->gate_pool.type != T_Q4_K || L->down_pool.type != T_Q4_K) { why = "the fused step needs Q4_K expert pools"; return false; }
     if (p.moe.N != 512 && p.moe.N != 768 && p.moe.N != 1024 && p.moe.N != 2048) {
         why = "the fused step is built for FFN widths 512, 768, 1024 and 2048";
         return false;

@@ -36,7 +36,7 @@ def oracle():
         if not os.path.exists(ORACLE_SO):
             raise RuntimeError("oracle/liboracle.so missing: run __graft_entry__.build()")
         lib = ctypes.CDLL(ORACLE_SO)
-        for name in ["qwo_vec_dot_q4_K_q8_K", "qwo_vec_dot_q8_0_q8_0", "qwo_vec_dot_f32",
+        for name in ["qwo_vec_dot_q4_K_q8_K", "qwo_vec_dot_q8_0_q8_0", "qwo_vec_dot_q6_K_q8_K", "qwo_vec_dot_f32",
                      "qwo_sgemm_dot_f32", "qwo_v_expf", "qwo_v_silu", "qwo_fp16_to_fp32"]:
             getattr(lib, name).restype = F32
         lib.qwo_v_expf.argtypes = [F32]
@@ -74,7 +74,8 @@ def ref():
     global _ref
     if _ref is None:
         lib = ctypes.CDLL(REF_LEAF_SO)
-        for name in ["qwr_vec_dot_q4_K_q8_K", "qwr_vec_dot_q8_0_q8_0", "qwr_vec_dot_f32", "qwr_sum"]:
+        for name in ["qwr_vec_dot_q4_K_q8_K", "qwr_vec_dot_q8_0_q8_0", "qwr_vec_dot_q6_K_q8_K", "qwr_vec_dot_f32",
+                     "qwr_sum"]:
             getattr(lib, name).restype = F32
         lib.qwr_argmax.restype = ctypes.c_int
         _ref = lib
@@ -125,3 +126,19 @@ def quantize_q8_0_model(w):
 
 def bits(a):
     return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+Q6K_BYTES = 210
+GGML_Q6_K = 14
+
+
+def random_q6_K(rng, rows, K, d=2e-3):
+    """rows x K weights as random Q6_K blocks (ggml-common.h block_q6_K: ql
+    [128], qh [64], int8 scales [16], fp16 d): every 6-bit value and every
+    int8 scale occurs; d around `d`.  A valid block needs no quantizer."""
+    nb = rows * (K // 256)
+    b = np.zeros((nb, Q6K_BYTES), np.uint8)
+    b[:, :192] = rng.integers(0, 256, (nb, 192), dtype=np.uint8)
+    b[:, 192:208] = rng.integers(-128, 128, (nb, 16), dtype=np.int16).astype(np.int8).view(np.uint8)
+    b[:, 208:210] = (np.abs(rng.standard_normal(nb)) * d + d / 8).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    return b.reshape(-1)

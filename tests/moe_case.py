@@ -9,7 +9,8 @@ import ctypes
 import numpy as np
 
 import questwend_amd as qa
-from tests.helpers import GGML_Q4_K, GGML_Q8_0, I64, F32, oracle, ptr, quantize_q4_K, quantize_q8_0_model
+from tests.helpers import (GGML_Q4_K, GGML_Q6_K, GGML_Q8_0, I64, F32, oracle, ptr, quantize_q4_K, quantize_q8_0_model,
+                           random_q6_K)
 
 
 class QwoMoeArgs(ctypes.Structure):
@@ -20,14 +21,17 @@ class QwoMoeArgs(ctypes.Structure):
                 ("x", ctypes.c_void_p), ("sh_gate", ctypes.c_void_p), ("sh_up", ctypes.c_void_p),
                 ("sh_down", ctypes.c_void_p), ("N_sh", ctypes.c_int64), ("sh_gate_inp", ctypes.c_void_p),
                 ("out", ctypes.c_void_p), ("gate_out", ctypes.c_void_p), ("up_out", ctypes.c_void_p),
-                ("act_out", ctypes.c_void_p), ("experts_out", ctypes.c_void_p)]
+                ("act_out", ctypes.c_void_p), ("experts_out", ctypes.c_void_p), ("down_type", ctypes.c_int)]
 
 
 class MoeCase:
-    def __init__(self, seed, H=2048, N=768, E=128, k=8, S=16, shared=False, N_sh=512, sh_gate=True, wtype="q4_K"):
-        """wtype: "q4_K" or "q8_0" expert slabs (the model-file quantizers)."""
+    def __init__(self, seed, H=2048, N=768, E=128, k=8, S=16, shared=False, N_sh=512, sh_gate=True, wtype="q4_K",
+                 down="same"):
+        """wtype: "q4_K" or "q8_0" expert slabs (the model-file quantizers);
+        down="q6_K": random Q6_K down slabs (routed and shared) beside Q4_K
+        gate/up, as Q4_K_M model files store some layers."""
         rng = np.random.default_rng(seed)
-        assert wtype in ("q4_K", "q8_0")
+        assert wtype in ("q4_K", "q8_0") and down in ("same", "q6_K")
         self.wtype = wtype
         self.ggml_type = GGML_Q4_K if wtype == "q4_K" else GGML_Q8_0
         self.qa_type = qa.TYPE_Q4_K if wtype == "q4_K" else qa.TYPE_Q8_0
@@ -38,10 +42,16 @@ class MoeCase:
         self.gate_q = quantize((rng.standard_normal((S, N, H)) * 0.02).astype(np.float32))
         self.up_q = quantize((rng.standard_normal((S, N, H)) * 0.02).astype(np.float32))
         self.down_q = quantize((rng.standard_normal((S, H, N)) * 0.02).astype(np.float32))
+        self.down_ggml, self.down_qa = self.ggml_type, self.qa_type
+        if down == "q6_K":
+            self.down_q = random_q6_K(rng, S * H, N, 1e-4)
+            self.down_ggml, self.down_qa = GGML_Q6_K, qa.TYPE_Q6_K
         if shared:
             self.shg_q = quantize((rng.standard_normal((N_sh, H)) * 0.02).astype(np.float32))
             self.shu_q = quantize((rng.standard_normal((N_sh, H)) * 0.02).astype(np.float32))
             self.shd_q = quantize((rng.standard_normal((H, N_sh)) * 0.02).astype(np.float32))
+            if down == "q6_K":
+                self.shd_q = random_q6_K(rng, H, N_sh, 1e-4)
             self.sh_inp = (rng.standard_normal(H) * 0.02).astype(np.float32) if sh_gate else None
         self.rng = rng
 
@@ -64,6 +74,7 @@ class MoeCase:
         a = QwoMoeArgs()
         a.H, a.N, a.k, a.T = self.H, self.N, self.k, T
         a.weight_type = self.ggml_type
+        a.down_type = self.down_ggml
         a.gate_pool, a.up_pool, a.down_pool = self.gate_q.ctypes.data, self.up_q.ctypes.data, self.down_q.ctypes.data
         a.n_slots = self.S
         slots = np.ascontiguousarray(slots, np.int32)
@@ -87,13 +98,13 @@ class MoeCase:
         L = qa.MoeLayer()
         L.gate_pool = qa.tensor(self.qa_type, self.H, self.N, self.S, self.d_gate)
         L.up_pool = qa.tensor(self.qa_type, self.H, self.N, self.S, self.d_up)
-        L.down_pool = qa.tensor(self.qa_type, self.N, self.H, self.S, self.d_down)
+        L.down_pool = qa.tensor(self.down_qa, self.N, self.H, self.S, self.d_down)
         L.router = qa.tensor(qa.TYPE_F32, self.H, self.E, 1, self.d_router)
         if self.shared:
             self.d_shg, self.d_shu, self.d_shd = dev(self.shg_q), dev(self.shu_q), dev(self.shd_q)
             L.sh_gate = qa.tensor(self.qa_type, self.H, self.N_sh, 1, self.d_shg)
             L.sh_up = qa.tensor(self.qa_type, self.H, self.N_sh, 1, self.d_shu)
-            L.sh_down = qa.tensor(self.qa_type, self.N_sh, self.H, 1, self.d_shd)
+            L.sh_down = qa.tensor(self.down_qa, self.N_sh, self.H, 1, self.d_shd)
             if self.sh_inp is not None:
                 self.d_shinp = dev(self.sh_inp)
                 L.sh_gate_inp = qa.tensor(qa.TYPE_F32, self.H, 1, 1, self.d_shinp)

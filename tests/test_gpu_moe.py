@@ -1,14 +1,15 @@
 """GPU parity of the MoE block against the oracle (ggml-CPU restated), through
 the C ABI of libqwmoe.  Expert ids and routing weights must be bit-exact
 (the router reproduces the CPU's floating-point order).  The expert GEMVs
-follow ggml's x86 float order for Q4_K and Q8_0 slabs alike, so block outputs
+follow ggml's x86 float order for Q4_K, Q8_0 and Q6_K slabs, so block outputs
 and MUL_MAT_ID results must equal the oracle bit for bit (with a shared
 expert: within 1e-6, its sigmoid gate runs through the device expf instead of
 libm's)."""
 import numpy as np
 import pytest
 
-from tests.helpers import GGML_Q4_K, GGML_Q8_0, I64, bits, oracle, ptr, quantize_q4_K, quantize_q8_0_model
+from tests.helpers import (GGML_Q4_K, GGML_Q6_K, GGML_Q8_0, I64, bits, oracle, ptr, quantize_q4_K, quantize_q8_0_model,
+                           random_q6_K)
 from tests.moe_case import MoeCase, rel_err
 
 torch = pytest.importorskip("torch")
@@ -101,11 +102,15 @@ def experts_gpu(case, x, slots, weights, resid=None):
     dict(N=768, E=128, k=8, T=1, shared=False, wtype="q8_0"),   # Q8_0 expert slabs
     dict(N=768, E=128, k=8, T=4, shared=False, wtype="q8_0"),
     dict(N=512, E=512, k=10, T=4, shared=True, wtype="q8_0"),
+    dict(N=768, E=128, k=8, T=1, shared=False, down="q6_K"),    # Q6_K down slabs beside Q4_K gate/up
+    dict(N=768, E=128, k=8, T=4, shared=False, down="q6_K"),
+    dict(N=512, E=512, k=10, T=4, shared=True, down="q6_K"),
+    dict(N=1280, E=64, k=4, T=3, shared=False, down="q6_K"),    # 5 blocks per row: odd rows start off alignment
 ])
 def test_moe_block_parity(dev, cfg):
     T = cfg["T"]
     case = MoeCase(seed=11 + T, N=cfg["N"], E=cfg["E"], k=cfg["k"], S=24, shared=cfg["shared"],
-                   wtype=cfg.get("wtype", "q4_K"))
+                   wtype=cfg.get("wtype", "q4_K"), down=cfg.get("down", "same"))
     case.upload(torch)
     x = case.rng.standard_normal((T, case.H)).astype(np.float32)
     ids, w, _, _ = case.route(x)
@@ -173,17 +178,22 @@ def test_moe_block_residual(dev):
     assert np.array_equal(bits(got), bits(exp))
 
 
-@pytest.mark.parametrize("wt", ["q4_K", "q8_0"])
+@pytest.mark.parametrize("wt", ["q4_K", "q8_0", "q6_K"])
 @pytest.mark.parametrize("K,N,n_as,n_ids,ne11,T", [(2048, 768, 8, 8, 1, 1), (2048, 768, 8, 8, 1, 4),
                                                   (768, 2048, 8, 8, 8, 4), (512, 2048, 6, 10, 10, 2),
                                                   (256, 64, 4, 3, 3, 2)])
 def test_mul_mat_id_op(dev, K, N, n_as, n_ids, ne11, T, wt):
     """GGML_OP_MUL_MAT_ID contract, including broadcast b (ne11 = 1) and
-    repeated experts across columns, for Q4_K and Q8_0 slabs."""
+    repeated experts across columns, for Q4_K, Q8_0 and Q6_K slabs (Q6_K rows
+    of an odd number of blocks start 2 bytes off dword alignment)."""
     rng = np.random.default_rng(K + N + T)
     w = (rng.standard_normal((n_as, N, K)) * 0.02).astype(np.float32)
-    q = quantize_q4_K(w) if wt == "q4_K" else quantize_q8_0_model(w)
-    gtype, ttype = (GGML_Q4_K, qa.TYPE_Q4_K) if wt == "q4_K" else (GGML_Q8_0, qa.TYPE_Q8_0)
+    if wt == "q6_K":
+        q = random_q6_K(rng, n_as * N, K)      # random valid blocks: every 6-bit value and int8 scale
+    else:
+        q = quantize_q4_K(w) if wt == "q4_K" else quantize_q8_0_model(w)
+    gtype, ttype = {"q4_K": (GGML_Q4_K, qa.TYPE_Q4_K), "q8_0": (GGML_Q8_0, qa.TYPE_Q8_0),
+                    "q6_K": (GGML_Q6_K, qa.TYPE_Q6_K)}[wt]
     b = rng.standard_normal((T, ne11, K)).astype(np.float32)
     ids = np.stack([rng.permutation(n_as)[:n_ids] if n_ids <= n_as else rng.integers(0, n_as, n_ids)
                     for _ in range(T)]).astype(np.int32)

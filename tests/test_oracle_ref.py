@@ -160,3 +160,47 @@ def test_argmax_last_index_on_ties():
     for _ in range(50):
         v = rng.integers(-3, 4, 1000).astype(np.float32)
         assert oracle().qwo_argmax(v.size, ptr(v)) == ref().qwr_argmax(v.size, ptr(v))
+
+
+@pytest.mark.parametrize("K", [256, 768, 2048])
+def test_vec_dot_q6_K_q8_K_bits(K):
+    """The oracle's Q6_K dot equals the reference's x86 kernel bit for bit,
+    over random blocks with every 6-bit value and int8 scale, against Q8_K
+    activations from the reference quantizer (including +-127 saturation)."""
+    from tests.helpers import Q6K_BYTES, random_q6_K
+    rng = np.random.default_rng(K + 6)
+    q = random_q6_K(rng, 200, K)
+    x = rng.standard_normal((200, K)).astype(np.float32)
+    x[::7, ::13] *= 50.0
+    y = np.zeros(200 * (K // 256) * Q8K_BYTES, np.uint8)
+    ref().qwr_quantize_q8_K(ptr(x), ptr(y), I64(x.size))
+    rb, yb = K // 256 * Q6K_BYTES, K // 256 * Q8K_BYTES
+    for i in range(200):
+        a = oracle().qwo_vec_dot_q6_K_q8_K(K, ptr(q[i * rb:]), ptr(y[i * yb:]))
+        b = ref().qwr_vec_dot_q6_K_q8_K(K, ptr(q[i * rb:]), ptr(y[i * yb:]))
+        assert np.float32(a).view(np.uint32) == np.float32(b).view(np.uint32), i
+
+
+def test_q6_K_dequant_matches_reference_and_dot():
+    """dequantize_row_q6_K equals the reference's; the oracle's dot equals the
+    float64 dot of the dequantized row with the dequantized Q8_K row to fp32
+    rounding (a closed form independent of the lane order)."""
+    from tests.helpers import Q6K_BYTES, random_q6_K
+    rng = np.random.default_rng(66)
+    K = 1024
+    q = random_q6_K(rng, 50, K)
+    a = np.zeros(50 * K, np.float32)
+    b = np.zeros_like(a)
+    oracle().qwo_dequantize_q6_K(ptr(q), ptr(a), I64(a.size))
+    ref().qwr_dequantize_q6_K(ptr(q), ptr(b), I64(b.size))
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    x = rng.standard_normal((50, K)).astype(np.float32)
+    y = np.zeros(50 * (K // 256) * Q8K_BYTES, np.uint8)
+    ref().qwr_quantize_q8_K(ptr(x), ptr(y), I64(x.size))
+    yb = y.reshape(50, K // 256, Q8K_BYTES)
+    yd = yb[:, :, :4].copy().view(np.float32)[:, :, 0]
+    yq = yb[:, :, 4:260].view(np.int8).astype(np.float64) * yd[:, :, None]
+    for i in range(50):
+        exact = float(np.dot(a[i * K:(i + 1) * K].astype(np.float64), yq[i].reshape(-1)))
+        got = oracle().qwo_vec_dot_q6_K_q8_K(K, ptr(q[i * K // 256 * Q6K_BYTES:]), ptr(y[i * (K // 256) * Q8K_BYTES:]))
+        assert abs(got - exact) <= 1e-5 * np.abs(a[i * K:(i + 1) * K] * yq[i].reshape(-1)).sum() + 1e-6

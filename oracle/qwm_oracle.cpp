@@ -45,13 +45,15 @@ struct block_q4_K { uint16_t d, dmin; uint8_t scales[12]; uint8_t qs[QK_K / 2]; 
 struct block_q8_K { float d; int8_t qs[QK_K]; int16_t bsums[QK_K / 16]; };
 struct block_q8_0 { uint16_t d; int8_t qs[QK8_0]; };
 struct block_q6_K { uint8_t ql[QK_K / 2]; uint8_t qh[QK_K / 4]; int8_t scales[QK_K / 16]; uint16_t d; };
+struct block_q5_K { uint16_t d, dmin; uint8_t scales[12]; uint8_t qh[QK_K / 8]; uint8_t qs[QK_K / 2]; };
+static_assert(sizeof(block_q5_K) == 176, "q5_K");
 static_assert(sizeof(block_q6_K) == 210, "q6_K");
 static_assert(sizeof(block_q4_K) == 144, "q4_K");
 static_assert(sizeof(block_q8_K) == 292, "q8_K");
 static_assert(sizeof(block_q8_0) == 34, "q8_0");
 
 // ggml_type values (ggml.h:390-420).
-constexpr int T_F32 = 0, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14, T_Q8_K = 15;
+constexpr int T_F32 = 0, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_Q8_K = 15;
 
 inline uint32_t f2u(float f) { uint32_t u; std::memcpy(&u, &f, 4); return u; }
 inline float u2f(uint32_t u) { float f; std::memcpy(&f, &u, 4); return f; }
@@ -389,6 +391,47 @@ float vec_dot_q4_K_q8_K(int n, const block_q4_K * x, const block_q8_K * y) {
     return hsum8(acc) + hsum4(acc_m);
 }
 
+// Q5_K (ggml-common.h:340-356): the Q4_K header and nibble layout plus a
+// fifth bit per value, bit 2j (low nibbles of 32-byte group j) or 2j + 1
+// (high nibbles) of qh[l] for the group's byte l.
+inline int q5_value(const block_q5_K & b, int e) {
+    const int j = e / 64, h = (e % 64) / 32, l = e % 32;
+    const uint8_t q = b.qs[32 * j + l];
+    return (h ? q >> 4 : q & 15) | (((b.qh[l] >> (2 * j + h)) & 1) << 4);
+}
+
+// ggml_vec_dot_q5_K_q8_K, x86 AVX2 branch (ggml-cpu/arch/x86/quants.c:
+// 1958-2046): scales and mins unpacked as for Q4_K; eight int32 lanes per
+// block, lane m = sum over the eight 32-value sub-blocks s of scale[s] times
+// the dot of sub-block values 4m..4m+3; acc[m] = fma(y.d * fp16(x.d),
+// (float)lane, acc[m]); the mins go to one float per row:
+// summs += (-y.d * fp16(x.dmin)) * (sum_j min[j] * (bsums[2j] + bsums[2j+1])),
+// a statement gcc contracts into a fused multiply-add (-ffp-contract=fast,
+// the GNU C default); result hsum8(acc) + summs.
+float vec_dot_q5_K_q8_K(int n, const block_q5_K * x, const block_q8_K * y) {
+    float acc[8] = {0};
+    float summs = 0.f;
+    for (int i = 0; i < n / QK_K; ++i) {
+        uint8_t sc[8], mn[8];
+        for (int j = 0; j < 8; ++j) get_scale_min_k4(j, x[i].scales, &sc[j], &mn[j]);
+        const float d = y[i].d * fp16_to_fp32(x[i].d);
+        const float dmin = -y[i].d * fp16_to_fp32(x[i].dmin);
+        int32_t msum = 0;
+        for (int j = 0; j < 8; ++j) msum += mn[j] * (y[i].bsums[2 * j] + y[i].bsums[2 * j + 1]);
+        summs = fmaf(dmin, (float)msum, summs);
+        for (int m = 0; m < 8; ++m) {
+            int32_t lane = 0;
+            for (int s = 0; s < 8; ++s) {
+                int32_t t = 0;
+                for (int e = 32 * s + 4 * m; e < 32 * s + 4 * m + 4; ++e) t += q5_value(x[i], e) * y[i].qs[e];
+                lane += sc[s] * t;
+            }
+            acc[m] = fmaf(d, (float)lane, acc[m]);
+        }
+    }
+    return hsum8(acc) + summs;
+}
+
 // The 6-bit value of element e (0..255) of a Q6_K block, 0..63
 // (ggml-quants.c:1940-1970 before its -32): element 128j + 32k + l takes the
 // low (k < 2) or high (k >= 2) nibble of ql[64j + 32(k & 1) + l] and bits
@@ -576,6 +619,7 @@ size_t row_bytes(int type, int64_t k) {
         case T_Q8_0: return (size_t)(k / QK8_0) * sizeof(block_q8_0);
         case T_Q4_K: return (size_t)(k / QK_K) * sizeof(block_q4_K);
         case T_Q6_K: return (size_t)(k / QK_K) * sizeof(block_q6_K);
+        case T_Q5_K: return (size_t)(k / QK_K) * sizeof(block_q5_K);
         case T_Q8_K: return (size_t)(k / QK_K) * sizeof(block_q8_K);
     }
     throw std::invalid_argument("unsupported ggml type");
@@ -585,6 +629,7 @@ int vec_dot_type(int type) {
     switch (type) {
         case T_Q4_K: return T_Q8_K;
         case T_Q6_K: return T_Q8_K;
+        case T_Q5_K: return T_Q8_K;
         case T_Q8_0: return T_Q8_0;
         case T_F32: return T_F32;
     }
@@ -601,6 +646,7 @@ float dot_row(int type, int k, const void * w, const void * xq) {
     switch (type) {
         case T_Q4_K: return vec_dot_q4_K_q8_K(k, (const block_q4_K *)w, (const block_q8_K *)xq);
         case T_Q6_K: return vec_dot_q6_K_q8_K(k, (const block_q6_K *)w, (const block_q8_K *)xq);
+        case T_Q5_K: return vec_dot_q5_K_q8_K(k, (const block_q5_K *)w, (const block_q8_K *)xq);
         case T_Q8_0: return vec_dot_q8_0_q8_0(k, (const block_q8_0 *)w, (const block_q8_0 *)xq);
         case T_F32: return vec_dot_f32(k, (const float *)w, (const float *)xq);
     }
@@ -679,6 +725,7 @@ QWO_API void qwo_quantize_q8_K(const float * x, void * y, int64_t k) { quantize_
 QWO_API void qwo_quantize_q8_0_ref(const float * x, void * y, int64_t k) { quantize_row_q8_0_ref(x, (block_q8_0 *)y, k); }
 QWO_API void qwo_quantize_q8_0_x86(const float * x, void * y, int64_t k) { quantize_row_q8_0_x86(x, (block_q8_0 *)y, k); }
 QWO_API float qwo_vec_dot_q4_K_q8_K(int n, const void * x, const void * y) { return vec_dot_q4_K_q8_K(n, (const block_q4_K *)x, (const block_q8_K *)y); }
+QWO_API float qwo_vec_dot_q5_K_q8_K(int n, const void * x, const void * y) { return vec_dot_q5_K_q8_K(n, (const block_q5_K *)x, (const block_q8_K *)y); }
 QWO_API float qwo_vec_dot_q6_K_q8_K(int n, const void * x, const void * y) { return vec_dot_q6_K_q8_K(n, (const block_q6_K *)x, (const block_q8_K *)y); }
 QWO_API void qwo_dequantize_q6_K(const void * x, float * y, int64_t k) { dequantize_row_q6_K((const block_q6_K *)x, y, k); }
 QWO_API float qwo_vec_dot_q8_0_q8_0(int n, const void * x, const void * y) { return vec_dot_q8_0_q8_0(n, (const block_q8_0 *)x, (const block_q8_0 *)y); }

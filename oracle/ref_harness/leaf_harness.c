@@ -5,7 +5,8 @@
  *   quantize_row_q4_K_ref, quantize_row_q8_K_ref, quantize_row_q8_0_ref,
  *   dequantize_row_q4_K, dequantize_row_q6_K (ggml/src/ggml-quants.c)
  *   quantize_row_q8_0, quantize_row_q8_K, ggml_vec_dot_q4_K_q8_K,
- *   ggml_vec_dot_q6_K_q8_K, ggml_vec_dot_q8_0_q8_0 (ggml/src/ggml-cpu/arch/x86/quants.c)
+ *   ggml_vec_dot_q5_K_q8_K, ggml_vec_dot_q6_K_q8_K, ggml_vec_dot_q8_0_q8_0
+ *                                 (ggml/src/ggml-cpu/arch/x86/quants.c)
  *   ggml_vec_dot_f32              (ggml/src/ggml-cpu/vec.cpp)           */
 #include "ggml-common.h"
 #include "ggml-quants.h"
@@ -18,6 +19,7 @@ void ggml_vec_dot_f32(int n, float * s, size_t bs, const float * x, size_t bx, c
 void ggml_vec_dot_q4_K_q8_K(int n, float * s, size_t bs, const void * vx, size_t bx, const void * vy, size_t by, int nrc);
 void ggml_vec_dot_q8_0_q8_0(int n, float * s, size_t bs, const void * vx, size_t bx, const void * vy, size_t by, int nrc);
 void ggml_vec_dot_q6_K_q8_K(int n, float * s, size_t bs, const void * vx, size_t bx, const void * vy, size_t by, int nrc);
+void ggml_vec_dot_q5_K_q8_K(int n, float * s, size_t bs, const void * vx, size_t bx, const void * vy, size_t by, int nrc);
 void quantize_row_q8_0(const float * x, void * y, int64_t k);
 void quantize_row_q8_K(const float * x, void * y, int64_t k);
 
@@ -28,6 +30,7 @@ QWR_API void qwr_quantize_q8_K(const float * x, void * y, int64_t k) { quantize_
 QWR_API void qwr_quantize_q8_0_ref(const float * x, void * y, int64_t k) { quantize_row_q8_0_ref(x, (block_q8_0 *) y, k); }
 QWR_API void qwr_quantize_q8_0(const float * x, void * y, int64_t k) { quantize_row_q8_0(x, y, k); }
 QWR_API float qwr_vec_dot_q4_K_q8_K(int n, const void * x, const void * y) { float s; ggml_vec_dot_q4_K_q8_K(n, &s, 0, x, 0, y, 0, 1); return s; }
+QWR_API float qwr_vec_dot_q5_K_q8_K(int n, const void * x, const void * y) { float s; ggml_vec_dot_q5_K_q8_K(n, &s, 0, x, 0, y, 0, 1); return s; }
 QWR_API float qwr_vec_dot_q6_K_q8_K(int n, const void * x, const void * y) { float s; ggml_vec_dot_q6_K_q8_K(n, &s, 0, x, 0, y, 0, 1); return s; }
 QWR_API void qwr_dequantize_q6_K(const void * x, float * y, int64_t k) { dequantize_row_q6_K((const block_q6_K *) x, y, k); }
 QWR_API float qwr_vec_dot_q8_0_q8_0(int n, const void * x, const void * y) { float s; ggml_vec_dot_q8_0_q8_0(n, &s, 0, x, 0, y, 0, 1); return s; }

@@ -12,14 +12,15 @@ import ctypes
 import os
 
 __all__ = ["lib", "QwmError", "QwmTensor", "MoeLayer", "PoolDesc", "PoolStats", "tensor", "check",
-           "TYPE_F32", "TYPE_Q8_0", "TYPE_Q4_K", "TYPE_Q6_K", "TYPE_I32", "FETCH_MEMCPY", "FETCH_GATHER"]
+           "TYPE_F32", "TYPE_Q8_0", "TYPE_Q4_K", "TYPE_Q5_K", "TYPE_Q6_K", "TYPE_I32", "FETCH_MEMCPY", "FETCH_GATHER"]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libqwmoe.so")
 
-TYPE_F32, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q6_K, TYPE_I32 = 0, 8, 12, 14, 26
+TYPE_F32, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_I32 = 0, 8, 12, 13, 14, 26
 FETCH_MEMCPY, FETCH_GATHER = 0, 1
-_TYPE_SIZE = {TYPE_F32: (4, 1), TYPE_I32: (4, 1), TYPE_Q8_0: (34, 32), TYPE_Q4_K: (144, 256), TYPE_Q6_K: (210, 256)}
+_TYPE_SIZE = {TYPE_F32: (4, 1), TYPE_I32: (4, 1), TYPE_Q8_0: (34, 32), TYPE_Q4_K: (144, 256), TYPE_Q5_K: (176, 256),
+              TYPE_Q6_K: (210, 256)}
 
 OK, ERR_UNSUPPORTED, ERR_ARG, ERR_WORKSPACE, ERR_HIP, ERR_NO_VICTIM, ERR_STATE, ERR_IO = 0, -1, -2, -3, -4, -5, -6, -7
 

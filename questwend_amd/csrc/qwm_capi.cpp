@@ -27,6 +27,7 @@ static size_t type_size(int32_t type) {
         case T_Q8_0: return 34;
         case T_Q4_K: return 144;
         case T_Q6_K: return 210;
+        case T_Q5_K: return 176;
     }
     return 0;
 }
@@ -35,6 +36,7 @@ static int64_t block_len(int32_t type) {
         case T_Q8_0: return 32;
         case T_Q4_K: return 256;
         case T_Q6_K: return 256;
+        case T_Q5_K: return 256;
     }
     return 1;
 }
@@ -129,8 +131,10 @@ int qwm_profile_stop(float * durations_ms, int32_t capacity) {
 
 static int check_mmid(const qwm_tensor * as, const qwm_tensor * b, const qwm_tensor * ids, const qwm_tensor * dst) {
     if (!as || !b || !ids) return fail(QWM_ERR_ARG, "mul_mat_id: NULL tensor");
-    if (as->type != T_Q4_K && as->type != T_Q8_0 && as->type != T_Q6_K)
-        return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: weights must be Q4_K, Q6_K or Q8_0");
+    if (as->type != T_Q4_K && as->type != T_Q8_0 && as->type != T_Q6_K && as->type != T_Q5_K)
+        return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: weights must be Q4_K, Q5_K, Q6_K or Q8_0");
+    if (as->type == T_Q5_K && ((uintptr_t)as->data % 16))
+        return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: Q5_K weights need 16-byte aligned data");
     if (as->type == T_Q6_K && ((uintptr_t)as->data % 4))   // rows and slabs may start 2 bytes off: handled
         return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: Q6_K weights need 4-byte aligned data");
     if (b->type != T_F32 || ids->type != T_I32) return fail(QWM_ERR_ARG, "mul_mat_id: b must be f32 and ids i32");
@@ -196,14 +200,17 @@ static int check_layer(const qwm_moe_layer * L, int64_t T, MoePlan & p) {
     if (L->router.type != T_F32 || !contiguous_rows(&L->router)) return fail(QWM_ERR_UNSUPPORTED, "moe: router must be contiguous f32 [H, E]");
     const qwm_tensor * pools[3] = {&L->gate_pool, &L->up_pool, &L->down_pool};
     for (const qwm_tensor * t : pools) {
-        if (t->type != T_Q4_K && t->type != T_Q8_0 && t->type != T_Q6_K)
-            return fail(QWM_ERR_UNSUPPORTED, "moe: pools must be Q4_K, Q8_0 or (down only) Q6_K");
+        if (t->type != T_Q4_K && t->type != T_Q8_0 && t->type != T_Q5_K && t->type != T_Q6_K)
+            return fail(QWM_ERR_UNSUPPORTED, "moe: pools must be Q4_K, Q5_K, Q8_0 or (down only) Q6_K");
         if (!fully_contiguous(t)) return fail(QWM_ERR_UNSUPPORTED, "moe: pools must be contiguous");
     }
-    // gate and up of one type; down the same, or Q6_K beside Q4_K (Q4_K_M files)
-    if (L->up_pool.type != L->gate_pool.type || L->gate_pool.type == T_Q6_K ||
-        (L->down_pool.type != L->gate_pool.type && !(L->down_pool.type == T_Q6_K && L->gate_pool.type == T_Q4_K)))
-        return fail(QWM_ERR_UNSUPPORTED, "moe: mixed pool types (only a Q6_K down pool beside Q4_K gate/up is handled)");
+    // gate and up of one type; down the same, or Q6_K beside Q4_K / Q5_K (K-quant "_M" files)
+    const int32_t gt = L->gate_pool.type;
+    if (L->up_pool.type != gt || gt == T_Q6_K ||
+        (L->down_pool.type != gt && !(L->down_pool.type == T_Q6_K && (gt == T_Q4_K || gt == T_Q5_K))))
+        return fail(QWM_ERR_UNSUPPORTED, "moe: mixed pool types (only a Q6_K down pool beside Q4_K or Q5_K gate/up is handled)");
+    for (const qwm_tensor * t : pools)
+        if (t->type == T_Q5_K && ((uintptr_t)t->data % 16)) return fail(QWM_ERR_UNSUPPORTED, "moe: Q5_K pools need 16-byte aligned data");
     if (L->down_pool.type == T_Q6_K && ((uintptr_t)L->down_pool.data % 4))
         return fail(QWM_ERR_UNSUPPORTED, "moe: Q6_K pools need 4-byte aligned data");
     if (L->gate_pool.ne[0] != L->router.ne[0] || L->up_pool.ne[0] != L->router.ne[0] ||

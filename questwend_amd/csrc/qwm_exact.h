@@ -318,4 +318,81 @@ QWM_DEV void q6k_dot8(float (&out)[MAXP], const uint8_t * row, const uint32_t * 
     }
 }
 
+// Q5_K x Q8_K row dots in ggml-CPU's exact float order: the x86
+// ggml_vec_dot_q5_K_q8_K (ggml-cpu/arch/x86/quants.c:1958-2046) keeps eight
+// int32 lanes per block, lane m gathering scale[s] times the dot of values
+// 4m..4m+3 of each 32-value sub-block s (5-bit values: the Q4_K nibble plus
+// bit s of qh byte 4m..4m+3), then acc[m] = fma(y.d * fp16(x.d), (float)lane,
+// acc[m]); the mins go to one float per row, summs = fma(-y.d * fp16(x.dmin),
+// (float)sum_j(min[j] * (bsums[2j] + bsums[2j+1])), summs) (gcc contracts
+// that statement), and the result is hsum8(acc) + summs.  Lane m of a row's
+// 8-lane group plays CPU lane m; every lane keeps summs.  176-byte blocks
+// keep dword alignment.
+template <int NB, int MAXP>
+QWM_DEV void q5k_dot8(float (&out)[MAXP], const uint8_t * row, const uint32_t * sx, int n, int m) {
+    float acc[MAXP], summs[MAXP];
+#pragma unroll
+    for (int i = 0; i < MAXP; ++i) { acc[i] = 0.f; summs[i] = 0.f; }
+    const uint32_t k1 = 0x3f3f3f3fu, k2 = 0x0f0f0f0fu, k3 = 0x03030303u;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const uint8_t * bp = row + 176 * b;
+        const uint4 h = *reinterpret_cast<const uint4 *>(bp);
+        const uint32_t qh = *reinterpret_cast<const uint32_t *>(bp + 16 + 4 * m);
+        uint32_t q[4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) q[p] = *reinterpret_cast<const uint32_t *>(bp + 48 + 32 * p + 4 * m);
+        const uint32_t u0 = h.y, u1 = h.z, u2 = h.w;
+        const uint32_t sc_lo = u0 & k1, sc_hi = (u2 & k2) | (((u0 >> 6) & k3) << 4);
+        const uint32_t mn_lo = u1 & k1, mn_hi = ((u2 >> 4) & k2) | (((u1 >> 6) & k3) << 4);
+        int sc[8], mn[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            sc[j] = (sc_lo >> (8 * j)) & 0xff; sc[4 + j] = (sc_hi >> (8 * j)) & 0xff;
+            mn[j] = (mn_lo >> (8 * j)) & 0xff; mn[4 + j] = (mn_hi >> (8 * j)) & 0xff;
+        }
+        const float dw = fp16_to_f32((uint16_t)(h.x & 0xffff));
+        const float dmw = fp16_to_f32((uint16_t)(h.x >> 16));
+        uint32_t wl[4], wh[4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            wl[p] = (q[p] & 0x0f0f0f0fu) | (((qh >> (2 * p)) & 0x01010101u) << 4);
+            wh[p] = ((q[p] >> 4) & 0x0f0f0f0fu) | (((qh >> (2 * p + 1)) & 0x01010101u) << 4);
+        }
+#pragma unroll
+        for (int i = 0; i < MAXP; ++i) {
+            if (i < n) {
+                const uint32_t * xb = sx + (i * NB + b) * XS;
+                const uint4 x0 = *reinterpret_cast<const uint4 *>(xb + 8 * m);
+                const uint4 x1 = *reinterpret_cast<const uint4 *>(xb + 8 * m + 4);
+                const float yd = __uint_as_float(xb[64]);
+                int s = 0;
+                s += sc[0] * dot4(wl[0], x0.x, 0);
+                s += sc[1] * dot4(wh[0], x0.y, 0);
+                s += sc[2] * dot4(wl[1], x0.z, 0);
+                s += sc[3] * dot4(wh[1], x0.w, 0);
+                s += sc[4] * dot4(wl[2], x1.x, 0);
+                s += sc[5] * dot4(wh[2], x1.y, 0);
+                s += sc[6] * dot4(wl[3], x1.z, 0);
+                s += sc[7] * dot4(wh[3], x1.w, 0);
+                acc[i] = __builtin_fmaf(yd * dw, (float)s, acc[i]);
+                int ms = 0;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) ms += mn[j] * (int)xb[65 + j];
+                summs[i] = __builtin_fmaf(-yd * dmw, (float)ms, summs[i]);
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < MAXP; ++i) {
+        if (i < n) {
+            const float t = acc[i] + dpp_f<0x12C>(acc[i]);
+            const float u = t + dpp_f<0x12E>(t);
+            out[i] = (u + dpp_f<0x12F>(u)) + summs[i];
+        } else {
+            out[i] = 0.f;
+        }
+    }
+}
+
 }  // namespace qwm

@@ -12,7 +12,7 @@
 namespace qwm {
 
 // ggml_type values (ggml.h:390-420)
-enum : int32_t { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14, T_Q8_K = 15, T_I32 = 26 };
+enum : int32_t { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_Q8_K = 15, T_I32 = 26 };
 
 void set_error(const std::string & msg);
 int fail(int code, const std::string & msg);
@@ -70,7 +70,7 @@ int launch_route(const RouteArgs & a, const MoePlan & p, uint8_t * ws, int32_t *
 
 struct ExpertArgs {
     int32_t wtype;          // gate and up pools (and the shared expert's)
-    int32_t down_type;      // down pools: wtype, or Q6_K beside Q4_K gate/up
+    int32_t down_type;      // down pools: wtype, or Q6_K beside Q4_K / Q5_K gate/up
     const uint8_t * gate; const uint8_t * up; const uint8_t * down;   // pool bases
     size_t gate_slab, up_slab, down_slab;                             // bytes per slot
     const uint8_t * sh_gate; const uint8_t * sh_up; const uint8_t * sh_down;

@@ -409,6 +409,51 @@ __global__ void __launch_bounds__(256) k_gateup_x(GateUpArgs a) {
     }
 }
 
+// k_gateup_x for Q5_K gate/up pools: the same mapping and activations,
+// rows through q5k_dot8.
+template <int NB, int MAXP>
+__global__ void __launch_bounds__(256) k_gateup_x5(GateUpArgs a) {
+    __shared__ __align__(16) uint32_t s_x[MAXP * NB * XS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int m = lane & 7, rsub = lane >> 3;
+    const int u = blockIdx.y;
+    const bool shared = u == a.unit_slots;
+    UnitView<MAXP> U;
+    int nu;
+    if (!load_unit<MAXP>(U, a.units, a.n_units, a.uslot, a.slot_g, a.slot_u, u, shared, a.T, 0, 1, nu)) return;
+    const int n = U.n;
+    const int rows = shared ? a.N_sh : a.N;
+    const int r = blockIdx.x * GUX_ROWS + wave * 8 + rsub;
+    if (blockIdx.x * GUX_ROWS >= rows) return;
+    const size_t row_bytes = (size_t)NB * 176;
+    const uint8_t * gbase = shared ? a.sh_gate : a.gate + (size_t)U.slot[0] * a.gate_slab;
+    const uint8_t * ubase = shared ? a.sh_up : a.up + (size_t)U.slot[1] * a.up_slab;
+    const int rc = min(r, rows - 1);
+    // the unit's tokens' activation blocks into LDS (uint4 copies)
+    constexpr int Q4 = NB * XS / 4;
+    for (int q = tid; q < n * Q4; q += 256) {
+        const int i = q / Q4, o = q % Q4;
+        int pi = U.pair[0];              // U.pair[i] by selects (a dynamic index would put U in scratch)
+#pragma unroll
+        for (int qq = 1; qq < MAXP; ++qq) if (i == qq) pi = U.pair[qq];
+        const int t = shared ? pi : pi / a.k;
+        reinterpret_cast<uint4 *>(s_x)[i * Q4 + o] = reinterpret_cast<const uint4 *>(a.xq_x + (size_t)t * NB * XS)[o];
+    }
+    __syncthreads();
+    float g[MAXP], up[MAXP];
+    q5k_dot8<NB, MAXP>(g, gbase + (size_t)rc * row_bytes, s_x, n, m);
+    q5k_dot8<NB, MAXP>(up, ubase + (size_t)rc * row_bytes, s_x, n, m);
+    if (m == 0 && r < rows) {
+#pragma unroll
+        for (int i = 0; i < MAXP; ++i)
+            if (i < n) {
+                const float v = (r < rows - (rows & 15)) ? v_silu(g[i]) * up[i] : g[i] / (1.0f + expf(-g[i])) * up[i];
+                if (shared) a.act_sh[(size_t)U.pair[i] * rows + r] = v;
+                else a.act[(size_t)U.pair[i] * rows + r] = v;
+            }
+    }
+}
+
 // The Q8_0 form of k_gateup_x: ggml's Q8_0 dot order (q80_dot8), the unit's
 // Q8_0 activations in LDS.
 template <int NPAIR, int MAXP>
@@ -602,6 +647,50 @@ __global__ void __launch_bounds__(256) k_down_q6k(DownArgs a) {
     }
 }
 
+// k_down_q4k for Q5_K down pools (Q5_K_S/M model files): rows through q5k_dot8.
+template <int NB, int MAXP>
+__global__ void __launch_bounds__(256) k_down_q5k(DownArgs a) {
+    constexpr int RPS = 8;                   // rows per wave
+    constexpr int TILE = 4 * RPS;
+    constexpr size_t row_bytes = (size_t)NB * 176;
+    __shared__ __align__(16) uint32_t s_x[MAXP * NB * XS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int c8 = lane & 7, rsub = lane >> 3;
+    const int u = blockIdx.y;
+    const bool shared = u == a.unit_slots;
+    UnitView<MAXP> U;
+    int nu;
+    if (!load_unit<MAXP>(U, a.units, a.n_units, a.uslot, a.slot_d, nullptr, u, shared, a.T, 2, 2, nu)) return;
+    const int n = U.n;
+    const uint8_t * base = shared ? a.sh_down : a.down + (size_t)U.slot[0] * a.down_slab;
+    const int row0 = blockIdx.x * TILE;
+    const int r = row0 + wave * RPS + rsub;
+    const uint8_t * rp = base + (size_t)min(r, a.H - 1) * row_bytes;
+    // the unit's activation rows to Q8_K in the exact-dot layout (one 256-block per wave at a time)
+    for (int jb = wave; jb < n * NB; jb += 4) {
+        const int i = jb / NB, b = jb % NB;
+        int pi = U.pair[0];              // U.pair[i] by selects (a dynamic index would put U in scratch)
+#pragma unroll
+        for (int q = 1; q < MAXP; ++q) if (i == q) pi = U.pair[q];
+        const float * src = shared ? a.act_sh + (size_t)pi * (NB * QK_K) : a.act + (size_t)pi * (NB * QK_K);
+        quantize_block_q8K_x(src + b * QK_K, s_x + (i * NB + b) * XS, lane);
+    }
+    __syncthreads();
+    float acc[MAXP];
+    q5k_dot8<NB, MAXP>(acc, rp, s_x, n, c8);
+#pragma unroll
+    for (int i = 0; i < MAXP; ++i)
+        if (i < n && c8 == 0 && r < a.H) {
+            if (shared) st_agent(a.ex_sh + (size_t)U.pair[i] * a.H + r, acc[i]);
+            else st_agent(a.ex + (size_t)U.pair[i] * a.H + r, acc[i]);
+        }
+    if (!last_workgroup(a.tile_counters + blockIdx.x, nu + a.shared)) return;
+    for (int q = tid; q < a.T * TILE; q += 256) {
+        const int t = q / TILE, h = row0 + q % TILE;
+        if (h < a.H) a.out[(size_t)t * a.H + h] = combine_one(a, t, h);
+    }
+}
+
 // The Q8_0 form of k_down_q4k: weight blocks of 32 (one per lane per step of
 // the row), activations quantized to Q8_0 in LDS (ggml's x86 quantizer, the
 // vec_dot_type of Q8_0).
@@ -754,6 +843,28 @@ static bool launch_gateup_x(const GateUpArgs & g, int nb, int maxp, dim3 grid, h
         default: return false;
     }
 }
+template <int NB>
+static void launch_gateup_x5_nb(const GateUpArgs & g, int maxp, dim3 grid, hipStream_t s) {
+    switch (maxp) {
+        case 1: k_gateup_x5<NB, 1><<<grid, 256, 0, s>>>(g); break;
+        case 2: k_gateup_x5<NB, 2><<<grid, 256, 0, s>>>(g); break;
+        case 4: k_gateup_x5<NB, 4><<<grid, 256, 0, s>>>(g); break;
+        default: k_gateup_x5<NB, 8><<<grid, 256, 0, s>>>(g); break;
+    }
+}
+static bool launch_gateup_x5(const GateUpArgs & g, int nb, int maxp, dim3 grid, hipStream_t s) {
+    switch (nb) {
+        case 1: launch_gateup_x5_nb<1>(g, maxp, grid, s); return true;
+        case 2: launch_gateup_x5_nb<2>(g, maxp, grid, s); return true;
+        case 3: launch_gateup_x5_nb<3>(g, maxp, grid, s); return true;
+        case 4: launch_gateup_x5_nb<4>(g, maxp, grid, s); return true;
+        case 5: launch_gateup_x5_nb<5>(g, maxp, grid, s); return true;
+        case 6: launch_gateup_x5_nb<6>(g, maxp, grid, s); return true;
+        case 7: launch_gateup_x5_nb<7>(g, maxp, grid, s); return true;
+        case 8: launch_gateup_x5_nb<8>(g, maxp, grid, s); return true;
+        default: return false;
+    }
+}
 template <int NPAIR>
 static void launch_gateup_x80_np(const GateUpArgs & g, int maxp, dim3 grid, hipStream_t s) {
     switch (maxp) {
@@ -777,8 +888,17 @@ static bool launch_gateup_x80(const GateUpArgs & g, int npair, int maxp, dim3 gr
     }
 }
 template <int NB>
-static void launch_down_nb(const DownArgs & d, bool q80, bool q6, int maxp, dim3 grid, hipStream_t s) {
-    if (q6) {
+static void launch_down_nb(const DownArgs & d, bool q80, int32_t dtype, int maxp, dim3 grid, hipStream_t s) {
+    if (dtype == T_Q5_K) {
+        switch (maxp) {
+            case 1: k_down_q5k<NB, 1><<<grid, 256, 0, s>>>(d); break;
+            case 2: k_down_q5k<NB, 2><<<grid, 256, 0, s>>>(d); break;
+            case 4: k_down_q5k<NB, 4><<<grid, 256, 0, s>>>(d); break;
+            default: k_down_q5k<NB, 8><<<grid, 256, 0, s>>>(d); break;
+        }
+        return;
+    }
+    if (dtype == T_Q6_K) {
         switch (maxp) {
             case 1: k_down_q6k<NB, 1><<<grid, 256, 0, s>>>(d); break;
             case 2: k_down_q6k<NB, 2><<<grid, 256, 0, s>>>(d); break;
@@ -807,10 +927,11 @@ static void launch_down_nb(const DownArgs & d, bool q80, bool q6, int maxp, dim3
 static int pow2_maxp(int64_t T) { return T <= 1 ? 1 : T <= 2 ? 2 : T <= 4 ? 4 : 8; }
 
 int launch_experts(const ExpertArgs & a, const MoePlan & p, uint8_t * ws, hipStream_t s) {
-    if (a.wtype != T_Q4_K && a.wtype != T_Q8_0) return fail(QWM_ERR_UNSUPPORTED, "expert pools must be Q4_K or Q8_0");
+    if (a.wtype != T_Q4_K && a.wtype != T_Q8_0 && a.wtype != T_Q5_K)
+        return fail(QWM_ERR_UNSUPPORTED, "expert gate/up pools must be Q4_K, Q5_K or Q8_0");
     const bool q80 = a.wtype == T_Q8_0;
-    const bool q6d = a.down_type == T_Q6_K;
-    if (q6d && a.wtype != T_Q4_K) return fail(QWM_ERR_UNSUPPORTED, "Q6_K down pools go with Q4_K gate/up pools");
+    if (a.down_type != a.wtype && !(a.down_type == T_Q6_K && (a.wtype == T_Q4_K || a.wtype == T_Q5_K)))
+        return fail(QWM_ERR_UNSUPPORTED, "down pools: the gate/up type, or Q6_K beside Q4_K / Q5_K");
     const int maxp = pow2_maxp(p.T);
     const int P = (int)(p.T * p.k);
     const int unit_slots = P;
@@ -834,7 +955,9 @@ int launch_experts(const ExpertArgs & a, const MoePlan & p, uint8_t * ws, hipStr
     const int rows_g = (int)std::max(p.N, p.N_sh);
     prof_begin("gate_up", s);
     const dim3 grid_x((rows_g + GUX_ROWS - 1) / GUX_ROWS, grid_y);
-    if (q80 ? !launch_gateup_x80(g, (int)(p.H / 64), maxp, grid_x, s) : !launch_gateup_x(g, (int)(p.H / QK_K), maxp, grid_x, s))
+    if (q80 ? !launch_gateup_x80(g, (int)(p.H / 64), maxp, grid_x, s)
+            : a.wtype == T_Q5_K ? !launch_gateup_x5(g, (int)(p.H / QK_K), maxp, grid_x, s)
+                                : !launch_gateup_x(g, (int)(p.H / QK_K), maxp, grid_x, s))
         return fail(QWM_ERR_UNSUPPORTED, "hidden size not instantiated for the exact gate/up");
     prof_end("gate_up", s);
 
@@ -857,14 +980,14 @@ int launch_experts(const ExpertArgs & a, const MoePlan & p, uint8_t * ws, hipStr
     if (grid_d.x > (unsigned)MAX_TILES) return fail(QWM_ERR_UNSUPPORTED, "hidden size needs too many down tiles");
     prof_begin("down", s);
     switch (nb_d) {
-        case 1: launch_down_nb<1>(d, q80, q6d, maxp, grid_d, s); break;
-        case 2: launch_down_nb<2>(d, q80, q6d, maxp, grid_d, s); break;
-        case 3: launch_down_nb<3>(d, q80, q6d, maxp, grid_d, s); break;
-        case 4: launch_down_nb<4>(d, q80, q6d, maxp, grid_d, s); break;
-        case 5: launch_down_nb<5>(d, q80, q6d, maxp, grid_d, s); break;
-        case 6: launch_down_nb<6>(d, q80, q6d, maxp, grid_d, s); break;
-        case 7: launch_down_nb<7>(d, q80, q6d, maxp, grid_d, s); break;
-        default: launch_down_nb<8>(d, q80, q6d, maxp, grid_d, s); break;
+        case 1: launch_down_nb<1>(d, q80, a.down_type, maxp, grid_d, s); break;
+        case 2: launch_down_nb<2>(d, q80, a.down_type, maxp, grid_d, s); break;
+        case 3: launch_down_nb<3>(d, q80, a.down_type, maxp, grid_d, s); break;
+        case 4: launch_down_nb<4>(d, q80, a.down_type, maxp, grid_d, s); break;
+        case 5: launch_down_nb<5>(d, q80, a.down_type, maxp, grid_d, s); break;
+        case 6: launch_down_nb<6>(d, q80, a.down_type, maxp, grid_d, s); break;
+        case 7: launch_down_nb<7>(d, q80, a.down_type, maxp, grid_d, s); break;
+        default: launch_down_nb<8>(d, q80, a.down_type, maxp, grid_d, s); break;
     }
     prof_end("down", s);
 
@@ -1031,6 +1154,44 @@ __global__ void __launch_bounds__(256) k_mmid_x6(MmidGemv a) {
     }
 }
 
+// k_mmid_x for Q5_K weights: rows through q5k_dot8.
+template <int NB, int MAXP>
+__global__ void __launch_bounds__(256) k_mmid_x5(MmidGemv a) {
+    __shared__ __align__(16) uint32_t s_x[MAXP * NB * XS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int m = lane & 7, rsub = lane >> 3;
+    const int u = blockIdx.y;
+    const int nu = *a.n_units;
+    const Unit U = a.units[u];
+    if (u >= nu) return;
+    const int n = U.n;
+    const uint8_t * base = a.as + (size_t)U.expert * a.slab;
+    const int r = blockIdx.x * 32 + wave * 8 + rsub;
+    const int rc = min(r, a.N - 1);
+    constexpr int Q4 = NB * XS / 4;
+    for (int q = tid; q < n * Q4; q += 256) {
+        const int i = q / Q4, o = q % Q4;
+        int p = U.pair[0];
+#pragma unroll
+        for (int qq = 1; qq < MAXP; ++qq) if (i == qq) p = U.pair[qq];
+        const int row = (p / a.n_ids) * a.ne11 + (p % a.n_ids) % a.ne11;
+        reinterpret_cast<uint4 *>(s_x)[q] = reinterpret_cast<const uint4 *>(a.xq + (size_t)row * NB * XS)[o];
+    }
+    __syncthreads();
+    float acc[MAXP];
+    q5k_dot8<NB, MAXP>(acc, base + (size_t)rc * a.row_bytes, s_x, n, m);
+    if (m == 0 && r < a.N) {
+#pragma unroll
+        for (int i = 0; i < MAXP; ++i)
+            if (i < n) {
+                const int p = U.pair[i];
+                float * o = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(a.dst) + (p / a.n_ids) * a.dst_nb2 +
+                                                      (p % a.n_ids) * a.dst_nb1);
+                o[r] = acc[i];
+            }
+    }
+}
+
 // The Q8_0 form of k_mmid_x: ggml's Q8_0 dot order, the unit's Q8_0 columns in LDS.
 template <int NPAIR, int MAXP>
 __global__ void __launch_bounds__(256) k_mmid_x80(MmidGemv a) {
@@ -1086,8 +1247,8 @@ size_t mmid_workspace(int64_t K, int64_t T, int64_t ne11, int64_t n_ids) {
 }
 
 int launch_mmid(const MmidArgs & a, uint8_t * ws, hipStream_t s) {
-    if (a.wtype != T_Q4_K && a.wtype != T_Q8_0 && a.wtype != T_Q6_K)
-        return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: weights must be Q4_K, Q6_K or Q8_0");
+    if (a.wtype != T_Q4_K && a.wtype != T_Q8_0 && a.wtype != T_Q6_K && a.wtype != T_Q5_K)
+        return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: weights must be Q4_K, Q5_K, Q6_K or Q8_0");
     const bool q80 = a.wtype == T_Q8_0;
     const int64_t rows = a.T * a.ne11;
     size_t o = 0;
@@ -1111,7 +1272,8 @@ int launch_mmid(const MmidArgs & a, uint8_t * ws, hipStream_t s) {
     QWM_TIMED("mul_mat_id_prep", s, k_mmid_prep<<<dim3((unsigned)std::max(1, std::min(256, (nblk + 3) / 4))), 256, 0, s>>>(pr));
     MmidGemv g;
     g.as = a.as; g.slab = a.slab;
-    g.row_bytes = q80 ? (size_t)(a.K / 32) * 34 : (size_t)(a.K / QK_K) * (a.wtype == T_Q6_K ? 210 : 144);
+    g.row_bytes = q80 ? (size_t)(a.K / 32) * 34
+                      : (size_t)(a.K / QK_K) * (a.wtype == T_Q6_K ? 210 : a.wtype == T_Q5_K ? 176 : 144);
     g.units = pr.units; g.n_units = pr.n_units; g.qs = pr.qs; g.d = pr.d; g.bs = pr.bs; g.xq = pr.xq;
     g.K = (int)a.K; g.N = (int)a.N; g.ne11 = (int)a.ne11; g.n_ids = (int)a.n_ids;
     g.dst = a.dst; g.dst_nb1 = a.dst_nb1; g.dst_nb2 = a.dst_nb2;
@@ -1126,6 +1288,13 @@ int launch_mmid(const MmidArgs & a, uint8_t * ws, hipStream_t s) {
                     case 2: k_mmid_x6<NB_, 2><<<gx, 256, 0, s>>>(g); break;         \
                     case 4: k_mmid_x6<NB_, 4><<<gx, 256, 0, s>>>(g); break;         \
                     default: k_mmid_x6<NB_, 8><<<gx, 256, 0, s>>>(g); break;        \
+                }                                                                   \
+            else if (a.wtype == T_Q5_K)                                             \
+                switch (maxp) {                                                     \
+                    case 1: k_mmid_x5<NB_, 1><<<gx, 256, 0, s>>>(g); break;         \
+                    case 2: k_mmid_x5<NB_, 2><<<gx, 256, 0, s>>>(g); break;         \
+                    case 4: k_mmid_x5<NB_, 4><<<gx, 256, 0, s>>>(g); break;         \
+                    default: k_mmid_x5<NB_, 8><<<gx, 256, 0, s>>>(g); break;        \
                 }                                                                   \
             else                                                                    \
                 switch (maxp) {                                                     \

@@ -36,7 +36,7 @@ def oracle():
         if not os.path.exists(ORACLE_SO):
             raise RuntimeError("oracle/liboracle.so missing: run __graft_entry__.build()")
         lib = ctypes.CDLL(ORACLE_SO)
-        for name in ["qwo_vec_dot_q4_K_q8_K", "qwo_vec_dot_q8_0_q8_0", "qwo_vec_dot_q6_K_q8_K", "qwo_vec_dot_f32",
+        for name in ["qwo_vec_dot_q4_K_q8_K", "qwo_vec_dot_q8_0_q8_0", "qwo_vec_dot_q6_K_q8_K", "qwo_vec_dot_q5_K_q8_K", "qwo_vec_dot_f32",
                      "qwo_sgemm_dot_f32", "qwo_v_expf", "qwo_v_silu", "qwo_fp16_to_fp32"]:
             getattr(lib, name).restype = F32
         lib.qwo_v_expf.argtypes = [F32]
@@ -74,7 +74,7 @@ def ref():
     global _ref
     if _ref is None:
         lib = ctypes.CDLL(REF_LEAF_SO)
-        for name in ["qwr_vec_dot_q4_K_q8_K", "qwr_vec_dot_q8_0_q8_0", "qwr_vec_dot_q6_K_q8_K", "qwr_vec_dot_f32",
+        for name in ["qwr_vec_dot_q4_K_q8_K", "qwr_vec_dot_q8_0_q8_0", "qwr_vec_dot_q6_K_q8_K", "qwr_vec_dot_q5_K_q8_K", "qwr_vec_dot_f32",
                      "qwr_sum"]:
             getattr(lib, name).restype = F32
         lib.qwr_argmax.restype = ctypes.c_int
@@ -141,4 +141,20 @@ def random_q6_K(rng, rows, K, d=2e-3):
     b[:, :192] = rng.integers(0, 256, (nb, 192), dtype=np.uint8)
     b[:, 192:208] = rng.integers(-128, 128, (nb, 16), dtype=np.int16).astype(np.int8).view(np.uint8)
     b[:, 208:210] = (np.abs(rng.standard_normal(nb)) * d + d / 8).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    return b.reshape(-1)
+
+
+Q5K_BYTES = 176
+GGML_Q5_K = 13
+
+
+def random_q5_K(rng, rows, K, d=2e-3):
+    """rows x K weights as random Q5_K blocks (ggml-common.h block_q5_K: fp16
+    d, fp16 dmin, 12 packed 6-bit scale/min bytes, qh [32], qs [128]): every
+    5-bit value, scale and min occurs; d and dmin around `d`."""
+    nb = rows * (K // 256)
+    b = np.zeros((nb, Q5K_BYTES), np.uint8)
+    b[:, 0:2] = (np.abs(rng.standard_normal(nb)) * d + d / 8).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    b[:, 2:4] = (np.abs(rng.standard_normal(nb)) * d / 4).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    b[:, 4:] = rng.integers(0, 256, (nb, Q5K_BYTES - 4), dtype=np.uint8)
     return b.reshape(-1)

@@ -9,8 +9,8 @@ import ctypes
 import numpy as np
 
 import questwend_amd as qa
-from tests.helpers import (GGML_Q4_K, GGML_Q6_K, GGML_Q8_0, I64, F32, oracle, ptr, quantize_q4_K, quantize_q8_0_model,
-                           random_q6_K)
+from tests.helpers import (GGML_Q4_K, GGML_Q5_K, GGML_Q6_K, GGML_Q8_0, I64, F32, oracle, ptr, quantize_q4_K,
+                           quantize_q8_0_model, random_q5_K, random_q6_K)
 
 
 class QwoMoeArgs(ctypes.Structure):
@@ -27,15 +27,20 @@ class QwoMoeArgs(ctypes.Structure):
 class MoeCase:
     def __init__(self, seed, H=2048, N=768, E=128, k=8, S=16, shared=False, N_sh=512, sh_gate=True, wtype="q4_K",
                  down="same"):
-        """wtype: "q4_K" or "q8_0" expert slabs (the model-file quantizers);
+        """wtype: "q4_K" or "q8_0" expert slabs (the model-file quantizers), or
+        "q5_K" (random valid blocks);
         down="q6_K": random Q6_K down slabs (routed and shared) beside Q4_K
         gate/up, as Q4_K_M model files store some layers."""
         rng = np.random.default_rng(seed)
-        assert wtype in ("q4_K", "q8_0") and down in ("same", "q6_K")
+        assert wtype in ("q4_K", "q8_0", "q5_K") and down in ("same", "q6_K")
         self.wtype = wtype
-        self.ggml_type = GGML_Q4_K if wtype == "q4_K" else GGML_Q8_0
-        self.qa_type = qa.TYPE_Q4_K if wtype == "q4_K" else qa.TYPE_Q8_0
-        quantize = quantize_q4_K if wtype == "q4_K" else quantize_q8_0_model
+        self.ggml_type = {"q4_K": GGML_Q4_K, "q8_0": GGML_Q8_0, "q5_K": GGML_Q5_K}[wtype]
+        self.qa_type = {"q4_K": qa.TYPE_Q4_K, "q8_0": qa.TYPE_Q8_0, "q5_K": qa.TYPE_Q5_K}[wtype]
+        if wtype == "q5_K":        # random valid blocks (every 5-bit value, scale and min occurs)
+            def quantize(w):
+                return random_q5_K(rng, int(np.prod(w.shape[:-1])), w.shape[-1], 1e-4)
+        else:
+            quantize = quantize_q4_K if wtype == "q4_K" else quantize_q8_0_model
         self.H, self.N, self.E, self.k, self.S = H, N, E, k, S
         self.shared, self.N_sh, self.has_sh_gate = shared, N_sh, sh_gate
         self.router = (rng.standard_normal((E, H)) * 0.02).astype(np.float32)

@@ -8,8 +8,8 @@ libm's)."""
 import numpy as np
 import pytest
 
-from tests.helpers import (GGML_Q4_K, GGML_Q6_K, GGML_Q8_0, I64, bits, oracle, ptr, quantize_q4_K, quantize_q8_0_model,
-                           random_q6_K)
+from tests.helpers import (GGML_Q4_K, GGML_Q5_K, GGML_Q6_K, GGML_Q8_0, I64, bits, oracle, ptr, quantize_q4_K,
+                           quantize_q8_0_model, random_q5_K, random_q6_K)
 from tests.moe_case import MoeCase, rel_err
 
 torch = pytest.importorskip("torch")
@@ -106,6 +106,9 @@ def experts_gpu(case, x, slots, weights, resid=None):
     dict(N=768, E=128, k=8, T=4, shared=False, down="q6_K"),
     dict(N=512, E=512, k=10, T=4, shared=True, down="q6_K"),
     dict(N=1280, E=64, k=4, T=3, shared=False, down="q6_K"),    # 5 blocks per row: odd rows start off alignment
+    dict(N=768, E=128, k=8, T=1, shared=False, wtype="q5_K"),   # Q5_K slabs (Q5_K_S/M model files)
+    dict(N=512, E=512, k=10, T=4, shared=True, wtype="q5_K"),
+    dict(N=768, E=128, k=8, T=4, shared=False, wtype="q5_K", down="q6_K"),
 ])
 def test_moe_block_parity(dev, cfg):
     T = cfg["T"]
@@ -178,7 +181,7 @@ def test_moe_block_residual(dev):
     assert np.array_equal(bits(got), bits(exp))
 
 
-@pytest.mark.parametrize("wt", ["q4_K", "q8_0", "q6_K"])
+@pytest.mark.parametrize("wt", ["q4_K", "q8_0", "q6_K", "q5_K"])
 @pytest.mark.parametrize("K,N,n_as,n_ids,ne11,T", [(2048, 768, 8, 8, 1, 1), (2048, 768, 8, 8, 1, 4),
                                                   (768, 2048, 8, 8, 8, 4), (512, 2048, 6, 10, 10, 2),
                                                   (256, 64, 4, 3, 3, 2)])
@@ -190,10 +193,12 @@ def test_mul_mat_id_op(dev, K, N, n_as, n_ids, ne11, T, wt):
     w = (rng.standard_normal((n_as, N, K)) * 0.02).astype(np.float32)
     if wt == "q6_K":
         q = random_q6_K(rng, n_as * N, K)      # random valid blocks: every 6-bit value and int8 scale
+    elif wt == "q5_K":
+        q = random_q5_K(rng, n_as * N, K)
     else:
         q = quantize_q4_K(w) if wt == "q4_K" else quantize_q8_0_model(w)
     gtype, ttype = {"q4_K": (GGML_Q4_K, qa.TYPE_Q4_K), "q8_0": (GGML_Q8_0, qa.TYPE_Q8_0),
-                    "q6_K": (GGML_Q6_K, qa.TYPE_Q6_K)}[wt]
+                    "q6_K": (GGML_Q6_K, qa.TYPE_Q6_K), "q5_K": (GGML_Q5_K, qa.TYPE_Q5_K)}[wt]
     b = rng.standard_normal((T, ne11, K)).astype(np.float32)
     ids = np.stack([rng.permutation(n_as)[:n_ids] if n_ids <= n_as else rng.integers(0, n_as, n_ids)
                     for _ in range(T)]).astype(np.int32)

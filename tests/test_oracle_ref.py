@@ -204,3 +204,21 @@ def test_q6_K_dequant_matches_reference_and_dot():
         exact = float(np.dot(a[i * K:(i + 1) * K].astype(np.float64), yq[i].reshape(-1)))
         got = oracle().qwo_vec_dot_q6_K_q8_K(K, ptr(q[i * K // 256 * Q6K_BYTES:]), ptr(y[i * (K // 256) * Q8K_BYTES:]))
         assert abs(got - exact) <= 1e-5 * np.abs(a[i * K:(i + 1) * K] * yq[i].reshape(-1)).sum() + 1e-6
+
+
+@pytest.mark.parametrize("K", [256, 1024, 2048])
+def test_vec_dot_q5_K_q8_K_bits(K):
+    """The oracle's Q5_K dot (eight lanes plus the fused scalar mins sum)
+    equals the reference's x86 kernel bit for bit over random blocks."""
+    from tests.helpers import Q5K_BYTES, random_q5_K
+    rng = np.random.default_rng(K + 5)
+    q = random_q5_K(rng, 200, K)
+    x = rng.standard_normal((200, K)).astype(np.float32)
+    x[::5, ::11] *= 40.0
+    y = np.zeros(200 * (K // 256) * Q8K_BYTES, np.uint8)
+    ref().qwr_quantize_q8_K(ptr(x), ptr(y), I64(x.size))
+    rb, yb = K // 256 * Q5K_BYTES, K // 256 * Q8K_BYTES
+    for i in range(200):
+        a = oracle().qwo_vec_dot_q5_K_q8_K(K, ptr(q[i * rb:]), ptr(y[i * yb:]))
+        b = ref().qwr_vec_dot_q5_K_q8_K(K, ptr(q[i * rb:]), ptr(y[i * yb:]))
+        assert np.float32(a).view(np.uint32) == np.float32(b).view(np.uint32), i

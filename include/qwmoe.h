@@ -260,6 +260,21 @@ int qwm_pool_slot_of_row(const qwm_pool * pool, int32_t role, int32_t layer, int
 /* Per-slot key (layer * n_expert + expert, -1 free) and clock of one role. */
 int qwm_pool_slots(const qwm_pool * pool, int32_t role, int32_t * keys, uint64_t * clocks);
 
+/* One layer of the cached decode path (decode_cached, runtime.cpp:5292-5341)
+ * in one call: qwm_moe_route, the routed ids read back to the host
+ * (synchronizes `stream`, as the reference's D2H read does),
+ * qwm_pool_ensure(pool, layer_index, ...) with the misses copied on the
+ * pool's copy stream, the slot ids uploaded, qwm_pool_wait(pool, stream),
+ * then qwm_moe_experts on the slot ids (resid may be NULL).  ids_host
+ * (i32 [T * k], may be NULL) receives the routed ids.  The layer's pools are
+ * the pool's device tensors.  Not capturable into a graph (host round trip).
+ * Pool errors (QWM_ERR_NO_VICTIM, QWM_ERR_IO) are returned before the
+ * experts run. */
+size_t qwm_moe_cached_workspace_size(const qwm_moe_layer * layer, int64_t T);
+int qwm_moe_cached_step(const qwm_moe_layer * layer, qwm_pool * pool, int32_t layer_index, const qwm_tensor * x,
+                        const qwm_tensor * rm, const qwm_tensor * resid, qwm_tensor * out, int32_t * ids_host,
+                        void * workspace, size_t ws_bytes, void * stream);
+
 /* Cache profiles (ExpertCache::save_profile / load_prefetch,
  * expert_cache.cpp:1485-1538), in the reference's text format:
  * "QWENEXPCACHE 1", "n_layer n_expert", then "role layer expert count" per

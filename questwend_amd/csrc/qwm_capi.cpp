@@ -368,6 +368,54 @@ static int check_layers(const qwm_moe_layer * layers, int32_t n_layers, int64_t 
     return QWM_OK;
 }
 
+// ---------------------------------------------------- cached layer step --
+// decode_cached's per-layer expert path (runtime.cpp:5292-5341): route on the
+// device, the ids read back (synchronous), the pool's decisions and copies,
+// the slot ids uploaded, the compute stream waiting for the copies, the
+// experts on the slot ids.  Workspace: the MoE workspace, then ids [T k] i32,
+// weights [T k] f32 and slots [3][T k] i32.
+static size_t cached_extra(const MoePlan & p) {
+    const size_t n = (size_t)(p.T * p.k);
+    return align_up(4 * n, 256) * 2 + align_up(12 * n, 256);
+}
+
+size_t qwm_moe_cached_workspace_size(const qwm_moe_layer * layer, int64_t T) {
+    MoePlan p;
+    if (check_layer(layer, T, p) != QWM_OK) return 0;
+    return align_up(p.total, 256) + cached_extra(p);
+}
+
+int qwm_moe_cached_step(const qwm_moe_layer * layer, qwm_pool * pool, int32_t layer_index, const qwm_tensor * x,
+                        const qwm_tensor * rm, const qwm_tensor * resid, qwm_tensor * out, int32_t * ids_host,
+                        void * workspace, size_t ws_bytes, void * stream) {
+    if (!pool || !x || !out) return fail(QWM_ERR_ARG, "moe_cached_step: NULL argument");
+    MoePlan p;
+    int rc = check_layer(layer, x->ne[1], p);
+    if (rc != QWM_OK) return rc;
+    const size_t base = align_up(p.total, 256);
+    if (!workspace || ws_bytes < base + cached_extra(p)) return fail(QWM_ERR_WORKSPACE, "moe_cached_step: workspace too small");
+    const int64_t n = p.T * p.k;
+    uint8_t * ws = (uint8_t *)workspace;
+    int32_t * d_ids = (int32_t *)(ws + base);
+    float * d_w = (float *)(ws + base + align_up(4 * (size_t)n, 256));
+    int32_t * d_sl = (int32_t *)(ws + base + 2 * align_up(4 * (size_t)n, 256));
+    hipStream_t s = (hipStream_t)stream;
+    qwm_tensor t_ids, t_w, t_sl[3];
+    qwm_tensor_init(&t_ids, QWM_TYPE_I32, p.k, p.T, 1, d_ids);
+    qwm_tensor_init(&t_w, QWM_TYPE_F32, p.k, p.T, 1, d_w);
+    for (int r = 0; r < 3; ++r) qwm_tensor_init(&t_sl[r], QWM_TYPE_I32, p.k, p.T, 1, d_sl + r * n);
+    if ((rc = qwm_moe_route(layer, x, rm, &t_ids, &t_w, ws, p.total, stream)) != QWM_OK) return rc;
+    std::vector<int32_t> ids((size_t)n), sl((size_t)(3 * n));
+    QWM_HIP_CHECK(hipMemcpyAsync(ids.data(), d_ids, 4 * (size_t)n, hipMemcpyDeviceToHost, s));
+    QWM_HIP_CHECK(hipStreamSynchronize(s));
+    if (ids_host) std::copy(ids.begin(), ids.end(), ids_host);
+    if ((rc = qwm_pool_ensure(pool, layer_index, ids.data(), (int32_t)n, sl.data(), sl.data() + n, sl.data() + 2 * n)) != QWM_OK)
+        return rc;
+    QWM_HIP_CHECK(hipMemcpyAsync(d_sl, sl.data(), 12 * (size_t)n, hipMemcpyHostToDevice, s));
+    if ((rc = qwm_pool_wait(pool, stream)) != QWM_OK) return rc;
+    return qwm_moe_experts(layer, x, &t_sl[0], &t_sl[1], &t_sl[2], &t_w, resid, out, ws, p.total, stream);
+}
+
 size_t qwm_moe_decode_workspace_size(const qwm_moe_layer * layers, int32_t n_layers, int64_t T) {
     MoePlan p;
     if (check_layers(layers, n_layers, T, p) != QWM_OK) return 0;

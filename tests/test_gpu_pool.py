@@ -393,3 +393,74 @@ def test_pool_profile_prefetch_fills_slabs(dev, tmp_path, mode):
                 assert np.array_equal(dev_bytes[s], host[lyr][r].numpy().reshape(E, slab)[e]), f"role {r} slot {s}"
     finally:
         L.qwm_pool_destroy(h)
+
+
+@pytest.mark.parametrize("fetch", ["memcpy", "gather"])
+def test_moe_cached_step_matches_oracle(dev, fetch):
+    """qwm_moe_cached_step (route, ids read back, ensure, slots up, wait,
+    experts in one call) over a Zipf trace on two layers sharing a pool that
+    overflows: routed ids equal the oracle's, the pool ends in the oracle
+    pool's state (keys and clocks), and every output matches the oracle block
+    with every expert resident (within 1e-6: the shared gate's expf)."""
+    H, N, E, k, T, S, n_layer, steps = 512, 256, 64, 4, 4, 20, 2, 16
+    cases = [MoeCase(seed=70 + l, H=H, N=N, E=E, k=k, S=E, shared=True, N_sh=N) for l in range(n_layer)]
+    rng = np.random.default_rng(13)
+    perms = [rng.permutation(E) for _ in range(n_layer)]
+    L = qa.lib()
+    slab = cases[0].gate_q.nbytes // E
+    pool_t = [torch.full((S * slab,), 0x5A, dtype=torch.uint8, device="cuda") for _ in range(3)]
+    host = [[pinned(c.gate_q), pinned(c.up_q), pinned(c.down_q)] for c in cases]
+    host_ptrs = [(ctypes.c_void_p * n_layer)(*[host[l][r].data_ptr() for l in range(n_layer)]) for r in range(3)]
+    d = qa.PoolDesc()
+    d.n_layer, d.n_expert = n_layer, E
+    for r in range(3):
+        d.n_slots[r], d.pool_data[r], d.slab_bytes[r] = S, pool_t[r].data_ptr(), slab
+        d.host_slabs[r] = ctypes.cast(host_ptrs[r], ctypes.c_void_p)
+    d.fetch_mode = FETCH[fetch]
+    copy = torch.cuda.Stream()
+    h = ctypes.c_void_p()
+    qa.check(L.qwm_pool_create(ctypes.byref(d), ctypes.c_void_p(copy.cuda_stream), ctypes.byref(h)))
+    o = oracle().qwo_pool_new(n_layer, E, ptr(np.array([S, S, S], np.int32)), 0)
+    layers = []
+    for c in cases:
+        c.upload(torch)
+        lay = c.layer
+        lay.gate_pool = qa.tensor(c.qa_type, H, N, S, pool_t[0])
+        lay.up_pool = qa.tensor(c.qa_type, H, N, S, pool_t[1])
+        lay.down_pool = qa.tensor(c.qa_type, N, H, S, pool_t[2])
+        layers.append(lay)
+    ws = workspace(L.qwm_moe_cached_workspace_size(layers[0], T))
+    try:
+        for step in range(steps):
+            l = step % n_layer
+            x = rng.standard_normal((T, H)).astype(np.float32)
+            mask = zipf_mask(rng, perms[l], k, T)
+            ids, w, _, _ = cases[l].route(x, mask)
+            dx, drm = torch.from_numpy(x).cuda(), torch.from_numpy(mask).cuda()
+            out = torch.full((T, H), float("nan"), dtype=torch.float32, device="cuda")
+            hids = np.zeros(T * k, np.int32)
+            qa.check(L.qwm_moe_cached_step(layers[l], h, l, qa.tensor(qa.TYPE_F32, H, T, 1, dx),
+                                           qa.tensor(qa.TYPE_F32, E, T, 1, drm), None,
+                                           qa.tensor(qa.TYPE_F32, H, T, 1, out), ptr(hids), ws.data_ptr(), ws.numel(),
+                                           None))
+            assert np.array_equal(hids.reshape(T, k), ids), f"step {step}: routed ids differ"
+            so = np.zeros((3, T * k), np.int32)
+            flat = np.ascontiguousarray(ids.ravel())
+            nf = ctypes.c_int()
+            assert oracle().qwo_pool_ensure(o, l, ptr(flat), flat.size, ptr(so[0]), ptr(so[1]), ptr(so[2]), None,
+                                            ctypes.byref(nf)) == 0
+            got = out.cpu().numpy()
+            exp = cases[l].block(x, ids, w)
+            assert np.isfinite(got).all() and rel_err(got, exp) < 1e-6, f"step {step}: rel err {rel_err(got, exp):.3e}"
+        for r in range(3):
+            kg, cg = np.zeros(S, np.int32), np.zeros(S, np.uint64)
+            ko, co = np.zeros(S, np.int32), np.zeros(S, np.uint64)
+            qa.check(L.qwm_pool_slots(h, r, ptr(kg), ptr(cg)))
+            oracle().qwo_pool_slots(o, r, ptr(ko), ptr(co))
+            assert np.array_equal(kg, ko) and np.array_equal(cg, co)
+        st = qa.PoolStats()
+        qa.check(L.qwm_pool_get_stats(h, ctypes.byref(st)))
+        assert st.evictions > 0
+    finally:
+        L.qwm_pool_destroy(h)
+        oracle().qwo_pool_free(o)

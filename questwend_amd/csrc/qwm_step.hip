@@ -35,587 +35,21 @@
 // waits for work it does not read.  Every wait is bounded (a timeout sets an
 // error word and the result reports a = -1 instead of hanging); the last
 // workgroup of the launch re-arms the counters.
-#include <hip/hip_runtime.h>
-
-#include "qwm_internal.h"
-#include "qwm_q4k.h"
-#include "qwm_vhead.h"
-#include "qwm_exact.h"
-
-namespace qwm {
-
-constexpr int SH = 2048;                 // hidden size of the fused step
-constexpr int SNB = SH / QK_K;           // Q8_K blocks per token
-constexpr uint32_t SPIN_LIMIT = 1u << 21;
-constexpr int MAX_NDOWN_S = 2048;        // longest down-projection input (FFN width)
-constexpr int STEP_MAX_E = 512;          // experts per layer in the fused step
-constexpr int RX_P = 132;                // pitch of the transposed router rows in LDS (floats)
-constexpr int XSP = 96;                  // workspace dwords per exact-layout Q8_K block of x (3 whole lines)
-constexpr size_t cmax(size_t x, size_t y) { return x > y ? x : y; }
-
-struct StepArgs {
-    const float * W_r; const float * x; const float * rm; const float * sgi;   // router [E][H], x [T][H]
-    int E, k, norm, tiny; float scale;
-    int N, N_sh, shared;
-    const uint8_t * gate; const uint8_t * up; const uint8_t * down;
-    size_t gate_slab, up_slab, down_slab;
-    const uint8_t * sh_gate; const uint8_t * sh_up; const uint8_t * sh_down;
-    const int32_t * slot_tables; int64_t table_stride; int layer;
-    const float * resid; float * out;                                           // [T][H]
-    int32_t * ids_out; int64_t ids_ld; float * w_out; int64_t w_ld;
-    float * lg;                                                                 // [E + 1][32]: logits of row e (row E: shared gate)
-    uint32_t * xq_x;                                                            // Q8_K of x, exact-dot layout, XSP per block
-    float * act; float * act_sh; float * ex; float * ex_sh;
-    uint32_t * bar; uint32_t * epoch; uint32_t * flags;                         // flags: one 32-word line per workgroup
-    int32_t * tile_counters; int32_t * err;
-    int32_t * gu_done;                                                          // per unit, one 32-word line each
-    int32_t * tiles_done;                                                       // combined down tiles
-    VerifyArgs v;                                                               // v.x = out
-};
-
-// Per-workgroup copy of the expert schedule (phase P1).
-struct StepShared {
-    int32_t ids[MAX_PAIRS];
-    float w[MAX_PAIRS];
-    float shg[MAX_T];
-    Unit units[MAX_PAIRS + 1];
-    int32_t uslot[MAX_PAIRS + 1][3];
-    int32_t nu;
-    int32_t slot_of[3 * STEP_MAX_E];   // this layer's slot tables, [role][expert]
-};
-
-// Grid barrier number `i` (1, 2, 3) of launch `epoch`.  Arrivals count in
-// BAR_GROUPS group counters (workgroup g in group g % BAR_GROUPS, one line
-// each); the last arrival of a group re-arms its counter and counts the group
-// at the top counter.  The last group's last workgroup re-arms the top counter
-// and then sets every workgroup's flag line to epoch * 4 + i; the others poll
-// their own line.
-constexpr int BAR_GROUPS = 16;
-
-QWM_DEV void grid_barrier(const StepArgs & a, int i, int G, uint32_t epoch) {
-    __shared__ int s_rel;
-    __builtin_amdgcn_s_waitcnt(0);               // this wave's agent-scope writes have completed
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const int grp = blockIdx.x % BAR_GROUPS;
-        const int groups = G < BAR_GROUPS ? G : BAR_GROUPS;
-        const uint32_t in_grp = (uint32_t)((G - 1 - grp) / BAR_GROUPS + 1);
-        uint32_t * gc = a.bar + 128 + 32 * grp;
-        bool rel = false;
-        if (__hip_atomic_fetch_add(gc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == in_grp - 1) {
-            st_agent(gc, 0u);
-            __builtin_amdgcn_s_waitcnt(0);           // re-armed before the group counts as arrived
-            rel = __hip_atomic_fetch_add(a.bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)groups - 1;
-        }
-        s_rel = rel;
-    }
-    __syncthreads();
-    const uint32_t v = epoch * 4u + (uint32_t)i;
-    if (s_rel) {
-        if (threadIdx.x == 0) st_agent(a.bar, 0u);
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        for (int q = threadIdx.x; q < G * 32; q += 256) st_agent(a.flags + q, v);   // whole lines
-    } else if (threadIdx.x == 0) {
-        const uint32_t * f = a.flags + (size_t)blockIdx.x * 32;
-        uint32_t spins = 0;
-        while (ld_agent(f) != v) {
-            __builtin_amdgcn_s_sleep(1);
-            if (++spins > SPIN_LIMIT) { st_agent(a.err, 1); break; }
-        }
-    }
-    __syncthreads();
-}
-
-// ---------------------------------------------------------------- P0 ----
-// Router rows e = g, g + G, ... (row E: the shared-expert gate row) and the
-// Q8_K blocks of x (waves counted from the end of the grid).
-template <int NT>
-QWM_DEV void step_router(const StepArgs & a, int g, int G, uint8_t * smem) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int E = a.E;
-    {
-        const int gw = (G - 1 - g) * 4 + wave;
-        for (int jb = gw; jb < NT * SNB; jb += 4 * G) {
-            const int t = jb / SNB, b = jb % SNB;
-            quantize_block_q8K_x<false, true>(a.x + (size_t)t * SH + b * QK_K, a.xq_x + (size_t)(t * SNB + b) * XSP, lane);
-        }
-    }
-    const int rows = E + (a.sgi ? 1 : 0);
-    if (g >= rows) return;                       // uniform per workgroup; no barrier follows inside
-    float * xt = reinterpret_cast<float *>(smem);            // [4][16][RX_P]: x of four tokens, transposed
-    float * wt = xt + 4 * 16 * RX_P;                         // [16][RX_P]: one router row, transposed
-    // 16 x 128 transposes into LDS: dst[h & 15][h >> 4] = src[h]; thread tid
-    // owns float4 number tid and tid + 256 of a 2048-float row
-    auto put = [&](float * dst, const float4 (&v)[2]) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int h = 4 * (tid + 256 * i);
-            dst[((h + 0) & 15) * RX_P + ((h + 0) >> 4)] = v[i].x;
-            dst[((h + 1) & 15) * RX_P + ((h + 1) >> 4)] = v[i].y;
-            dst[((h + 2) & 15) * RX_P + ((h + 2) >> 4)] = v[i].z;
-            dst[((h + 3) & 15) * RX_P + ((h + 3) >> 4)] = v[i].w;
-        }
-    };
-    auto get = [&](float4 (&v)[2], const float * src) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i) v[i] = reinterpret_cast<const float4 *>(src)[tid + 256 * i];
-    };
-    if (a.tiny) {
-        // llamafile tinyBLAS<16> order (sgemm.cpp:600-670): lane (t, l) runs one
-        // fma chain over 16-wide steps, then the 16-lane tree.  Tokens in groups
-        // of four (x of one group staged in LDS with the first row, one round
-        // trip); one row at a time.
-        for (int t0 = 0; t0 < NT; t0 += 4) {
-            float4 xv[4][2], wv[2];
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-                if (t0 + q < NT) get(xv[q], a.x + (size_t)(t0 + q) * SH);
-            for (int e = g; e < E; e += G) {
-                get(wv, a.W_r + (size_t)e * SH);
-                __syncthreads();                 // the previous row's readers are done with LDS
-                if (e == g) {
-#pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        if (t0 + q < NT) put(xt + q * 16 * RX_P, xv[q]);
-                }
-                put(wt, wv);
-                __syncthreads();
-                const int l = lane & 15, t = t0 + (lane >> 4);
-                if (wave == 0 && t < NT) {
-                    const float * xr = xt + (t - t0) * 16 * RX_P + l * RX_P;
-                    const float * wr = wt + l * RX_P;
-                    float acc = 0.f;
-#pragma unroll 8
-                    for (int s = 0; s < SH / 16; s += 4) {
-                        const float4 x4 = *reinterpret_cast<const float4 *>(xr + s);
-                        const float4 w4 = *reinterpret_cast<const float4 *>(wr + s);
-                        acc = __builtin_fmaf(w4.x, x4.x, acc);
-                        acc = __builtin_fmaf(w4.y, x4.y, acc);
-                        acc = __builtin_fmaf(w4.z, x4.z, acc);
-                        acc = __builtin_fmaf(w4.w, x4.w, acc);
-                    }
-                    acc = tree16_dpp(acc);
-                    if (l == 0) st_agent(a.lg + (size_t)e * 32 + t, a.rm ? acc + a.rm[(size_t)t * E + e] : acc);
-                }
-            }
-            __syncthreads();
-        }
-    }
-    for (int e = g; e < rows; e += G) {
-        const bool sh_row = e == E;
-        if (a.tiny && !sh_row) continue;
-        // ggml_vec_dot_f32's AVX-512 order (vec.cpp:11-135), one token per wave pass
-        const float * w = sh_row ? a.sgi : a.W_r + (size_t)e * SH;
-        float wv[SH / 64];
-#pragma unroll
-        for (int s = 0; s < SH / 64; ++s) wv[s] = w[64 * s + lane];
-        for (int t = wave; t < NT; t += 4) {
-            const float * xr = a.x + (size_t)t * SH;
-            float xv[SH / 64];
-#pragma unroll
-            for (int s = 0; s < SH / 64; ++s) xv[s] = xr[64 * s + lane];
-            float acc = 0.f;
-#pragma unroll
-            for (int s = 0; s < SH / 64; ++s) acc = __builtin_fmaf(wv[s], xv[s], acc);
-            acc += lane_xor32_f(acc);
-            acc += lane_xor16_f(acc);
-            acc = tree16_dpp(acc);
-            if (lane == 0) st_agent(a.lg + (size_t)e * 32 + t, (a.rm && !sh_row) ? acc + a.rm[(size_t)t * E + e] : acc);
-        }
-    }
-}
-
-// ---------------------------------------------------------------- P1 ----
-// The selection of route_experts (runtime.cpp:2693-2734) for every token, in
-// every workgroup: soft_max (ops.cpp:5813-5920, vec.cpp:531: v_expf over
-// 16-lane chunks, each chunk's 16-lane tree added to a double sum in order,
-// scaled by 1/sum), top-k (larger probability, then lower index), weight
-// normalization (double sum, clamp 6.103515625e-5, division), scale; then
-// the expert union in first-occurrence order and each unit's slots.
-//
-// One wave per token; top-k as k rounds of a wave maximum with ballots for
-// the tie order, the weight normalization one lane per selected expert.
-// R: probabilities per lane (E <= 64 * R).
-template <int NT, int R>
-QWM_DEV void step_select(const StepArgs & a, int g, StepShared & S, uint8_t * smem) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int E = a.E, k = a.k;
-    const int nr = (E + 63) / 64;
-    const int nfull = E & ~15;
-    const unsigned long long below = (1ull << lane) - 1ull;
-    for (int t = wave; t < NT; t += 4) {
-        const float shl = a.sgi ? a.lg[(size_t)E * 32 + t] : 0.f;      // shared-expert gate logit
-        float v[R];
-        float m = -__builtin_inff();
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            v[r] = -__builtin_inff();
-            const int i = 64 * r + lane;
-            if (r < nr && i < E) v[r] = a.lg[(size_t)i * 32 + t];
-            m = fmaxf(m, v[r]);
-        }
-        m = wave_max(m);
-        double sum = 0.0;
-        float tailv = 0.f;
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            if (r < nr) {
-                const int i = 64 * r + lane;
-                float ev = 0.f;
-                if (i < nfull) ev = v_expf(v[r] - m);
-                else if (i < E) ev = expf(v[r] - m);          // scalar tail: libm expf on the CPU
-                const float cs = tree16_dpp(i < nfull ? ev : 0.f);
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    if (64 * r + 16 * q < nfull) sum += (double)readlane_f(cs, 16 * q);
-                if (r == (nfull >> 6)) tailv = ev;
-                v[r] = ev;
-            }
-        }
-        for (int i = nfull; i < E; ++i) sum += (double)readlane_f(tailv, i & 63);
-        const float sc = (float)(1.0 / sum);
-        // top-k: k rounds of the wave maximum; a tie goes to the lower index
-        // (the first r, then the first lane, holding the maximum).  Lane j
-        // keeps the j-th selection; the weight sum runs in selection order.
-        float cur[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int i = 64 * r + lane;
-            v[r] = v[r] * sc;
-            cur[r] = (r < nr && i < E) ? v[r] : -1.f;                  // probabilities are >= 0
-        }
-        float myw = 0.f;
-        int myid = 0;
-        double wsum = 0.0;
-        for (int j = 0; j < k; ++j) {
-            float m = cur[0];
-#pragma unroll
-            for (int r = 1; r < R; ++r) m = fmaxf(m, cur[r]);
-            m = wave_max(m);
-            int id = -1;
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const unsigned long long bal = __ballot(cur[r] == m);
-                if (id < 0 && bal) id = 64 * r + (int)__builtin_ctzll(bal);
-            }
-            if (lane == j) { myw = m; myid = id; }
-            wsum += (double)m;
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-                if (64 * r + lane == id) cur[r] = -1.f;
-        }
-        if (a.norm) {
-            float ws = (float)wsum;
-            ws = fmaxf(fminf(ws, __builtin_inff()), 6.103515625e-5f);
-            myw = myw / ws;
-        }
-        if (a.scale != 0.0f && a.scale != 1.0f) myw = myw * a.scale;
-        if (lane < k) {
-            S.ids[t * k + lane] = myid;
-            S.w[t * k + lane] = myw;
-            if (g == 0) {
-                if (a.ids_out) a.ids_out[(size_t)t * a.ids_ld + lane] = myid;
-                if (a.w_out) a.w_out[(size_t)t * a.w_ld + lane] = myw;
-            }
-        }
-        if (lane == 0) S.shg[t] = a.sgi ? 1.f / (1.f + expf(-shl)) : 1.f;   // unary-ops.cpp:31
-    }
-    __syncthreads();
-    // expert union through per-expert LDS tables: first pair, token mask, unit
-    int32_t * tab_first = reinterpret_cast<int32_t *>(smem);
-    uint32_t * tab_mask = reinterpret_cast<uint32_t *>(tab_first + MAX_E);
-    int32_t * tab_unit = reinterpret_cast<int32_t *>(tab_mask + MAX_E);
-    __shared__ unsigned long long s_bal[2];
-    const int P = NT * k;
-    const int p = tid;
-    const int e = p < P ? S.ids[p] : 0;
-    if (p < P) { tab_first[e] = 0x7fffffff; tab_mask[e] = 0u; }
-    __syncthreads();
-    if (p < P) { atomicMin(&tab_first[e], p); atomicOr(&tab_mask[e], 1u << (p / k)); }
-    __syncthreads();
-    const bool first = p < P && tab_first[e] == p;
-    const uint32_t tmask = p < P ? tab_mask[e] : 0u;
-    const unsigned long long bal = __ballot(first);
-    if (lane == 0 && wave < 2) s_bal[wave] = bal;
-    __syncthreads();
-    const int nu = __popcll(s_bal[0]) + (P > 64 ? __popcll(s_bal[1]) : 0);
-    if (first) {
-        const int u = (wave == 1 ? __popcll(s_bal[0]) : 0) + __popcll(bal & below);
-        S.units[u].expert = e;
-        S.units[u].n = __popc(tmask);
-        tab_unit[e] = u;
-    }
-    __syncthreads();
-    if (p < P) {
-        const int t = p / k;
-        S.units[tab_unit[e]].pair[__popc(tmask & ((1u << t) - 1u))] = p;
-    }
-    __syncthreads();
-    for (int u = tid; u < nu; u += 256)
-        for (int r = 0; r < 3; ++r) S.uslot[u][r] = S.slot_of[r * E + S.units[u].expert];
-    if (tid == 0) {
-        if (a.shared) {
-            S.units[nu].expert = -1;
-            S.units[nu].n = NT;
-            for (int i = 0; i < NT; ++i) S.units[nu].pair[i] = i;
-        }
-        S.nu = nu;
-    }
-    __syncthreads();
-}
-
-// ---------------------------------------------------------------- P2 ----
-// gate/up: items of GU_ROWS = 32 consecutive rows of one unit (one whole
-// 128-byte line of activations per token); workgroup g takes items g,
-// g + G, ...  Each wave owns 8 rows, 8 lanes per row, in ggml-CPU's exact
-// float order (qwm_exact.h): the unit's Q8_K activations are copied into LDS,
-// both rows' blocks are requested at once, and act = silu(g) * u (the
-// vectorized silu except for the row tail the CPU runs through scalar expf)
-// leaves as agent-scope stores.  Each finished item counts for its unit.
-constexpr int GU_ROWS = 32;
-
-template <int MAXP>
-QWM_DEV void step_gateup(const StepArgs & a, int g, int G, const StepShared & S, uint8_t * smem) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int m = lane & 7, rsub = lane >> 3;
-    uint32_t * s_x = reinterpret_cast<uint32_t *>(smem);          // [MAXP][SNB][XS]
-    const int nb_r = (a.N + GU_ROWS - 1) / GU_ROWS, nb_s = a.shared ? (a.N_sh + GU_ROWS - 1) / GU_ROWS : 0;
-    const int items = S.nu * nb_r + nb_s;
-    constexpr size_t row_bytes = (size_t)SNB * 144;
-    constexpr int Q4 = SNB * XS / 4;                               // uint4 per token in LDS
-    for (int item = g; item < items; item += G) {
-        const bool shared = item >= S.nu * nb_r;
-        const int u = shared ? S.nu : item / nb_r;
-        const int blk = shared ? item - S.nu * nb_r : item % nb_r;
-        const int rows = shared ? a.N_sh : a.N;
-        const Unit & U_ = S.units[u];
-        const int n = U_.n;
-        const uint8_t * gbase = shared ? a.sh_gate : a.gate + (size_t)S.uslot[u][0] * a.gate_slab;
-        const uint8_t * ubase = shared ? a.sh_up : a.up + (size_t)S.uslot[u][1] * a.up_slab;
-        const int r = blk * GU_ROWS + wave * 8 + rsub;
-        const int rc = min(r, rows - 1);                           // rows past the unit's last re-read it; dropped
-        XBlk Gw[SNB], Uw[SNB];
-#pragma unroll
-        for (int b = 0; b < SNB; ++b) {
-            load_xblk(Gw[b], gbase + (size_t)rc * row_bytes + b * 144, m);
-            load_xblk(Uw[b], ubase + (size_t)rc * row_bytes + b * 144, m);
-        }
-        for (int q = tid; q < n * Q4; q += 256) {
-            const int i = q / Q4, o = q % Q4, b = o / (XS / 4), w4 = o % (XS / 4);
-            const int tok = shared ? U_.pair[i] : U_.pair[i] / a.k;
-            reinterpret_cast<uint4 *>(s_x)[q] =
-                reinterpret_cast<const uint4 *>(a.xq_x + (size_t)(tok * SNB + b) * XSP)[w4];
-        }
-        __syncthreads();
-        float gs[MAXP], us[MAXP];
-        q4k_dot8<SNB, MAXP>(gs, Gw, s_x, n, m);
-        q4k_dot8<SNB, MAXP>(us, Uw, s_x, n, m);
-        if (m == 0 && r < rows) {
-#pragma unroll
-            for (int i = 0; i < MAXP; ++i)
-                if (i < n) {
-                    const float v = (r < rows - (rows & 15)) ? v_silu(gs[i]) * us[i] : gs[i] / (1.0f + expf(-gs[i])) * us[i];
-                    if (shared) st_agent(a.act_sh + (size_t)U_.pair[i] * rows + r, v);
-                    else st_agent(a.act + (size_t)U_.pair[i] * rows + r, v);
-                }
-        }
-        signal_count(a.gu_done + 32 * u);        // also orders s_x's reuse by the next item
-    }
-}
-
-// ---------------------------------------------------------------- P3 ----
-// down + combine: each unit's rows are cut into the same 16 tiles of 128 rows
-// (whole 32-row lines); items (unit, tile) go to workgroups g, g + G, ...
-// The workgroup requests the tile's first weight rows, quantizes the unit's
-// activations to Q8_K in LDS and streams the rest of the tile, 8 lanes per
-// row (q4k_dot8), outputs collected in LDS and written as whole
-// lines; then it takes the tile's ticket, and the last of the U units
-// combines the tile for every token (runtime.cpp:3815-3817 for T == 1,
-// 4544-4550 for T > 1; then the shared expert and the residual).
-constexpr int DN_TR = 128;
-
-template <int NT, int NB, int MAXP>
-QWM_DEV void step_down(const StepArgs & a, int g, int G, const StepShared & S, uint8_t * smem) {
-    constexpr int RPS = 8;                       // rows per wave step
-    constexpr int TR = DN_TR;                    // 16 tiles of 128 rows
-    constexpr int NSTEP = TR / (4 * RPS);        // wave steps per tile
-    constexpr int PF = NB <= 3 ? NSTEP : NB <= 4 ? 3 : 1;   // steps in flight
-    constexpr int ntiles = SH / TR;
-    constexpr size_t row_bytes = (size_t)NB * 144;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int c8 = lane & 7, rsub = lane >> 3;
-    const int U = S.nu + a.shared;
-    const int nb_r = (a.N + GU_ROWS - 1) / GU_ROWS, nb_s = (a.N_sh + GU_ROWS - 1) / GU_ROWS;   // gate/up items per unit
-    uint32_t * s_x = reinterpret_cast<uint32_t *>(smem);                        // [MAXP][NB][XS]
-    float (*s_ex)[DN_TR] = reinterpret_cast<float (*)[DN_TR]>(smem + (size_t)MAXP * NB * XS * 4);
-    for (int item = g; item < U * ntiles; item += G) {
-        const int u = item / ntiles, x = item % ntiles;
-        const bool shared = u == S.nu;
-        const Unit & U_ = S.units[u];
-        const int n = U_.n;
-        const uint8_t * base = shared ? a.sh_down : a.down + (size_t)S.uslot[u][2] * a.down_slab;
-        const int h0 = x * TR, h1 = h0 + TR;
-        const uint8_t * rp = base + (size_t)(h0 + wave * RPS + rsub) * row_bytes;   // row of step st: + 4 * RPS * st
-        // weights first: vector-memory waits count in issue order, and these
-        // do not depend on the activations
-        XBlk Wb[PF][NB];
-#pragma unroll
-        for (int p = 0; p < PF; ++p)
-#pragma unroll
-            for (int b = 0; b < NB; ++b) load_xblk(Wb[p][b], rp + (size_t)(4 * RPS * p) * row_bytes + b * 144, c8);
-        wait_count(a.gu_done + 32 * u, shared ? nb_s : nb_r, a.err, SPIN_LIMIT);   // the unit's activations are out
-        for (int jb = wave; jb < n * NB; jb += 4) {
-            const int i = jb / NB, b = jb % NB;
-            const float * src = shared ? a.act_sh + (size_t)U_.pair[i] * (NB * QK_K)
-                                       : a.act + (size_t)U_.pair[i] * (NB * QK_K);
-            quantize_block_q8K_x<true>(src + b * QK_K, s_x + (i * NB + b) * XS, lane);
-        }
-        __syncthreads();
-#pragma clang loop unroll(full)
-        for (int st = 0; st < NSTEP; ++st) {
-            const int p = st % PF;
-            float acc[MAXP];
-            q4k_dot8<NB, MAXP>(acc, Wb[p], s_x, n, c8);
-            if (st + PF < NSTEP)
-#pragma unroll
-                for (int b = 0; b < NB; ++b) load_xblk(Wb[p][b], rp + (size_t)(4 * RPS * (st + PF)) * row_bytes + b * 144, c8);
-            const int r = h0 + (st * 4 + wave) * RPS + rsub;
-#pragma unroll
-            for (int i = 0; i < MAXP; ++i)
-                if (i < n && c8 == 0) s_ex[i][r - h0] = acc[i];
-        }
-        __syncthreads();
-        for (int q = tid; q < n * (h1 - h0); q += 256) {
-            const int i = q / (h1 - h0), h = h0 + q % (h1 - h0);
-            if (shared) st_agent(a.ex_sh + (size_t)U_.pair[i] * SH + h, s_ex[i][h - h0]);
-            else st_agent(a.ex + (size_t)U_.pair[i] * SH + h, s_ex[i][h - h0]);
-        }
-        if (last_workgroup(a.tile_counters + x, U)) {
-            // every expert output of the tile is in: combine it, two outputs per
-            // thread per pass with all their loads issued before any arithmetic
-            const int k = a.k;
-            const int TRh = h1 - h0;
-            for (int q0 = tid; q0 < NT * TRh; q0 += 512) {
-                float ev[2][MAX_K], shv[2], rv[2];
-#pragma unroll
-                for (int o = 0; o < 2; ++o) {
-                    const int q = min(q0 + 256 * o, NT * TRh - 1);
-                    const int t = q / TRh, h = h0 + q % TRh;
-                    const float * e = a.ex + (size_t)t * k * SH + h;
-#pragma unroll
-                    for (int j = 0; j < MAX_K; ++j) ev[o][j] = j < k ? e[(size_t)j * SH] : 0.f;
-                    shv[o] = a.shared ? a.ex_sh[(size_t)t * SH + h] : 0.f;
-                    rv[o] = a.resid ? a.resid[(size_t)t * SH + h] : 0.f;
-                }
-#pragma unroll
-                for (int o = 0; o < 2; ++o) {
-                    const int q = q0 + 256 * o;
-                    if (q >= NT * TRh) break;
-                    const int t = q / TRh, h = h0 + q % TRh;
-                    const float * wt = S.w + t * k;
-                    float sacc;
-                    if (NT == 1) {
-                        // vec_dot_f32 with n = k <= 16: a 16-group, else an
-                        // 8-group, of unfused products, then fused multiply-adds
-                        sacc = 0.0f;
-                        if (k >= 16) {
-#pragma unroll
-                            for (int l = 0; l < 16; ++l) sacc = sacc + ev[o][l] * wt[l];
-                        } else {
-                            const int g8 = k >= 8 ? 8 : 0;
-#pragma unroll
-                            for (int l = 0; l < 8; ++l)
-                                if (l < g8) sacc = sacc + ev[o][l] * wt[l];
-#pragma unroll
-                            for (int l = 0; l < 16; ++l)
-                                if (l >= g8 && l < k) sacc = __builtin_fmaf(ev[o][l], wt[l], sacc);
-                        }
-                    } else {
-                        sacc = ev[o][0] * wt[0];
-#pragma unroll
-                        for (int j = 1; j < MAX_K; ++j)
-                            if (j < k) sacc = sacc + ev[o][j] * wt[j];
-                    }
-                    if (a.shared) {
-                        float vv = shv[o];
-                        if (a.sgi) vv = vv * S.shg[t];
-                        sacc = sacc + vv;
-                    }
-                    if (a.resid) sacc = sacc + rv[o];
-                    st_agent(a.out + (size_t)t * SH + h, sacc);
-                }
-            }
-            signal_count(a.tiles_done);
-        }
-        __syncthreads();
-    }
-}
-
-template <int NT, int NB_D>
-__global__ void __launch_bounds__(256) k_step(StepArgs a) {
-    constexpr int MAXP = NT <= 1 ? 1 : NT <= 2 ? 2 : NT <= 4 ? 4 : 8;
-    constexpr size_t router_bytes = (size_t)5 * 16 * RX_P * 4;
-    constexpr size_t down_bytes = (size_t)MAXP * (NB_D * XS * 4 + DN_TR * 4);
-    constexpr size_t gateup_bytes = (size_t)MAXP * SNB * XS * 4;
-    constexpr size_t smem_bytes = cmax(cmax(cmax(router_bytes, down_bytes), gateup_bytes), VhSmem<NT>::bytes);
-    __shared__ __align__(16) uint8_t smem[smem_bytes];
-    __shared__ StepShared S;
-    __shared__ uint32_t s_epoch;
-    const int g = blockIdx.x, G = gridDim.x;
-    if (threadIdx.x == 0) s_epoch = ld_agent(a.epoch);   // constant until the last workgroup of this launch
-    __syncthreads();
-    const uint32_t epoch = s_epoch;
-
-    // the layer's slot tables, requested first and kept in LDS for the selection
-    constexpr int SLQ = 3 * STEP_MAX_E / 256;
-    int32_t sl[SLQ];
-#pragma unroll
-    for (int q = 0; q < SLQ; ++q) {
-        const int idx = threadIdx.x + 256 * q;
-        sl[q] = idx < 3 * a.E ? a.slot_tables[(size_t)(idx / a.E) * a.table_stride + (size_t)a.layer * a.E + idx % a.E] : 0;
-    }
-    step_router<NT>(a, g, G, smem);
-#pragma unroll
-    for (int q = 0; q < SLQ; ++q) S.slot_of[threadIdx.x + 256 * q] = sl[q];
-    grid_barrier(a, 1, G, epoch);
-    if (a.E <= 128) step_select<NT, 2>(a, g, S, smem);
-    else step_select<NT, STEP_MAX_E / 64>(a, g, S, smem);
-    step_gateup<MAXP>(a, g, G, S, smem);
-    step_down<NT, NB_D, MAXP>(a, g, G, S, smem);
-    __syncthreads();
-    constexpr int PF = NT <= 4 ? 2 : 1;
-    if (verify_body<NT, SH / 512, PF, VH_BEFORE_WAIT>(a.v, g, G, smem, a.tiles_done, SH / DN_TR, a.err, SPIN_LIMIT)) {
-        // every workgroup has read the epoch, passed the barrier and all waits:
-        // re-arm the completion counters, then the epoch
-        for (int q = threadIdx.x; q < MAX_PAIRS + 1; q += 256) st_agent(a.gu_done + 32 * q, 0);
-        if (threadIdx.x == 0) st_agent(a.tiles_done, 0);
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            st_agent(a.epoch, epoch + 1u);
-            if (ld_agent(a.err)) {
-                a.v.result[NT] = -1;
-                a.v.result[NT + 1] = -1;
-                st_agent(a.err, 0);
-            }
-        }
-    }
-}
-
-}  // namespace qwm
+#include "qwm_step_kernel.h"
 
 // ======================================================================
 // host side
 // ======================================================================
 namespace qwm {
 
-constexpr int MAX_STEP_WG = 1024;
 
 bool step_plan(const qwm_moe_layer * L, const qwm_tensor * lm_head, int64_t T, StepPlan & p, std::string & why) {
     if (!moe_plan(L, T, p.moe, why)) return false;
     if (p.moe.H != SH) { why = "the fused step is built for hidden size 2048"; return false; }
-    if (L->gate_pool.type != T_Q4_K || L->down_pool.type != T_Q4_K) { why = "the fused step needs Q4_K expert pools"; return false; }
+    if (L->gate_pool.type != T_Q4_K || (L->down_pool.type != T_Q4_K && L->down_pool.type != T_Q6_K)) {
+        why = "the fused step needs Q4_K gate/up pools and Q4_K or Q6_K down pools";
+        return false;
+    }
     if (p.moe.N != 512 && p.moe.N != 768 && p.moe.N != 1024 && p.moe.N != 2048) {
         why = "the fused step is built for FFN widths 512, 768, 1024 and 2048";
         return false;
@@ -638,50 +72,6 @@ bool step_plan(const qwm_moe_layer * L, const qwm_tensor * lm_head, int64_t T, S
     p.tiles_done = take(128);
     p.total = o;
     return true;
-}
-
-template <int NT, int NB_D>
-static int step_grid() {
-    static int grid = 0;
-    if (!grid) {
-        int dev = 0, cus = 0, per_cu = 0;
-        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-            return -1;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(k_step<NT, NB_D>), 256, 0) != hipSuccess)
-            return -1;
-        grid = std::min(std::min(per_cu, 2) * cus, MAX_STEP_WG);
-    }
-    return grid;
-}
-
-template <int NT, int NB_D>
-static int launch_step_t(StepArgs & a, hipStream_t s) {
-    const int G = step_grid<NT, NB_D>();
-    if (G <= 0) return fail(QWM_ERR_HIP, "fused step: occupancy query failed");
-    const int U_max = NT * a.k + a.shared;
-    if (G < U_max) return fail(QWM_ERR_UNSUPPORTED, "fused step: fewer co-resident workgroups than expert units");
-    if ((int64_t)a.v.V < 8LL * G) return fail(QWM_ERR_UNSUPPORTED, "fused step: vocabulary too small for the grid");
-    // An ordinary launch of exactly the co-resident grid (the occupancy query
-    // above): the cooperative launch API gives the same residency but costs
-    // ~20 us between consecutive launches on this stack.  If other work holds
-    // CUs, the missing workgroups start as it drains; the bounded spins report
-    // a = -1 rather than wait without end.
-    prof_begin("step", s);
-    k_step<NT, NB_D><<<dim3((unsigned)G), dim3(256), 0, s>>>(a);
-    prof_end("step", s);
-    const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return fail(QWM_ERR_HIP, std::string("fused step launch: ") + hipGetErrorString(e));
-    return QWM_OK;
-}
-
-template <int NT>
-static int launch_step_nt(StepArgs & a, int nb_d, hipStream_t s) {
-    switch (nb_d) {
-        case 2: return launch_step_t<NT, 2>(a, s);
-        case 3: return launch_step_t<NT, 3>(a, s);
-        case 4: return launch_step_t<NT, 4>(a, s);
-        default: return launch_step_t<NT, 8>(a, s);
-    }
 }
 
 int launch_step(const StepCall & c, const StepPlan & p, uint8_t * ws, hipStream_t s) {
@@ -720,15 +110,15 @@ int launch_step(const StepCall & c, const StepPlan & p, uint8_t * ws, hipStream_
     v.pi = reinterpret_cast<int32_t *>(ws + p.v_pi);
     v.counter = reinterpret_cast<int32_t *>(ws + p.v_counter);
     const int nb_d = (int)(m.N / QK_K);          // step_plan: 2, 3, 4 or 8
+    a.d6 = L->down_pool.type == T_Q6_K ? 1 : 0;   // step_plan: Q4_K, or Q6_K down
     switch (m.T) {
         case 1: return launch_step_nt<1>(a, nb_d, s);
         case 2: return launch_step_nt<2>(a, nb_d, s);
         case 3: return launch_step_nt<3>(a, nb_d, s);
         case 4: return launch_step_nt<4>(a, nb_d, s);
         case 5: return launch_step_nt<5>(a, nb_d, s);
-        case 6: return launch_step_nt<6>(a, nb_d, s);
-        case 7: return launch_step_nt<7>(a, nb_d, s);
-        default: return launch_step_nt<8>(a, nb_d, s);
+        case 8: return launch_step_t8(a, nb_d, s);
+        default: return launch_step_hi(a, (int)m.T, nb_d, s);
     }
 }
 

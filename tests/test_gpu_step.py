@@ -57,6 +57,8 @@ def slot_tables(case, ids):
     dict(T=8, E=128, k=8, N=768),
     dict(T=4, E=512, k=10, N=512, shared=True),
     dict(T=2, E=512, k=10, N=512, shared=True, sh_gate=False),
+    dict(T=4, E=128, k=8, N=768, down="q6_K"),                  # Q6_K down slabs (Q4_K_M last layers)
+    dict(T=3, E=512, k=10, N=512, shared=True, down="q6_K"),
 ])
 def test_fused_step(dev, lm_head, cfg):
     T = cfg.pop("T")

@@ -147,11 +147,12 @@ static int check_mmid(const qwm_tensor * as, const qwm_tensor * b, const qwm_ten
     if (!fully_contiguous(as)) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: as must be contiguous");
     if (b->nb[0] != 4 || ids->nb[0] != 4) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: b/ids must have unit element stride");
     if ((b->nb[1] | b->nb[2]) % 16) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: b rows must be 16-byte aligned");
-    if (b->ne[2] > MAX_T) {                     // prefill: the grouped GEMM (qwm_prefill.hip)
+    if (b->ne[2] > MAX_T && as->type == T_Q4_K) {   // prefill: the grouped GEMM (qwm_prefill.hip)
         std::string why;
-        if (as->type != T_Q4_K) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: prefill batches need Q4_K weights");
         if (!prefill_supported(as->ne[0], as->ne[1], as->ne[2], why)) return fail(QWM_ERR_UNSUPPORTED, why);
         if (ids->ne[0] * ids->ne[1] > (1 << 22)) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: too many (expert, column) pairs");
+    } else if (b->ne[2] > MAX_T) {              // other types: the GEMV path over column chunks
+        if (ids->ne[0] > MAX_PAIRS) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: too many ids per column");
     } else if (ids->ne[0] * ids->ne[1] > MAX_PAIRS) {
         return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: too many (expert, column) pairs");
     }
@@ -165,10 +166,15 @@ static int check_mmid(const qwm_tensor * as, const qwm_tensor * b, const qwm_ten
     return QWM_OK;
 }
 
+// Columns per GEMV launch when a batch of more than MAX_T columns of a type
+// without the prefill GEMM is split (the pair table holds MAX_PAIRS pairs).
+static int64_t mmid_chunk(int64_t n_ids) { return std::max<int64_t>(1, std::min<int64_t>(MAX_T, MAX_PAIRS / n_ids)); }
+
 size_t qwm_mul_mat_id_workspace_size(const qwm_tensor * as, const qwm_tensor * b, const qwm_tensor * ids) {
     if (check_mmid(as, b, ids, nullptr) != QWM_OK) return 0;
-    if (b->ne[2] > MAX_T) return prefill_workspace(as->ne[0], as->ne[1], as->ne[2], b->ne[2], b->ne[1], ids->ne[0]);
-    return mmid_workspace(as->ne[0], b->ne[2], b->ne[1], ids->ne[0]);
+    if (b->ne[2] > MAX_T && as->type == T_Q4_K)
+        return prefill_workspace(as->ne[0], as->ne[1], as->ne[2], b->ne[2], b->ne[1], ids->ne[0]);
+    return mmid_workspace(as->ne[0], std::min<int64_t>(b->ne[2], mmid_chunk(ids->ne[0])), b->ne[1], ids->ne[0]);
 }
 
 int qwm_mul_mat_id(const qwm_tensor * as, const qwm_tensor * b, const qwm_tensor * ids, qwm_tensor * dst,
@@ -176,9 +182,10 @@ int qwm_mul_mat_id(const qwm_tensor * as, const qwm_tensor * b, const qwm_tensor
     int rc = check_mmid(as, b, ids, dst);
     if (rc != QWM_OK) return rc;
     if (!dst) return fail(QWM_ERR_ARG, "mul_mat_id: dst is NULL");
-    const bool prefill = b->ne[2] > MAX_T;
+    const bool prefill = b->ne[2] > MAX_T && as->type == T_Q4_K;
+    const int64_t chunk = std::min<int64_t>(b->ne[2], mmid_chunk(ids->ne[0]));
     const size_t need = prefill ? prefill_workspace(as->ne[0], as->ne[1], as->ne[2], b->ne[2], b->ne[1], ids->ne[0])
-                                : mmid_workspace(as->ne[0], b->ne[2], b->ne[1], ids->ne[0]);
+                                : mmid_workspace(as->ne[0], chunk, b->ne[1], ids->ne[0]);
     if (!workspace || ws_bytes < need) return fail(QWM_ERR_WORKSPACE, "mul_mat_id: workspace too small");
     MmidArgs a;
     a.wtype = as->type; a.as = (const uint8_t *)as->data; a.slab = as->nb[2];
@@ -189,7 +196,17 @@ int qwm_mul_mat_id(const qwm_tensor * as, const qwm_tensor * b, const qwm_tensor
     a.dst_nb1 = dst->nb[1]; a.dst_nb2 = dst->nb[2];
     a.dst = (float *)dst->data;
     if (prefill) return launch_prefill(a, (uint8_t *)workspace, (hipStream_t)stream);
-    return launch_mmid(a, (uint8_t *)workspace, (hipStream_t)stream);
+    // column chunks in order on one stream (each launch rewrites the workspace after the previous one)
+    const int64_t T = b->ne[2];
+    for (int64_t t0 = 0; t0 < T; t0 += chunk) {
+        MmidArgs c = a;
+        c.T = std::min(chunk, T - t0);
+        c.b = (const float *)((const uint8_t *)b->data + t0 * b->nb[2]);
+        c.ids = (const int32_t *)((const uint8_t *)ids->data + t0 * ids->nb[1]);
+        c.dst = (float *)((uint8_t *)dst->data + t0 * dst->nb[2]);
+        if ((rc = launch_mmid(c, (uint8_t *)workspace, (hipStream_t)stream)) != QWM_OK) return rc;
+    }
+    return QWM_OK;
 }
 
 // ------------------------------------------------------------- MoE block --

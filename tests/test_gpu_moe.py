@@ -231,3 +231,33 @@ def test_mul_mat_id_rejects_bad_shapes(dev):
     b = qa.tensor(qa.TYPE_F32, 512, 1, 1, 0)      # K mismatch
     ids = qa.tensor(qa.TYPE_I32, 2, 1, 1, 0)
     assert qa.lib().qwm_mul_mat_id(t, b, ids, qa.tensor(qa.TYPE_F32, 4, 2, 1, 0), None, 0, None) == qa.ERR_ARG
+
+
+@pytest.mark.parametrize("wt", ["q8_0", "q6_K", "q5_K"])
+def test_mul_mat_id_wide_batch(dev, wt):
+    """A batch of 40 columns x 10 ids (prefill-sized) with weights that have
+    no grouped GEMM runs as GEMV launches over column chunks: bit-exact
+    against the oracle, with ne11 = 1 broadcast and with per-id rows."""
+    rng = np.random.default_rng(40)
+    K, N, n_as, n_ids, T = 512, 256, 16, 10, 40
+    w = (rng.standard_normal((n_as, N, K)) * 0.02).astype(np.float32)
+    q = {"q8_0": lambda: quantize_q8_0_model(w), "q6_K": lambda: random_q6_K(rng, n_as * N, K),
+         "q5_K": lambda: random_q5_K(rng, n_as * N, K)}[wt]()
+    gtype, ttype = {"q8_0": (GGML_Q8_0, qa.TYPE_Q8_0), "q6_K": (GGML_Q6_K, qa.TYPE_Q6_K),
+                    "q5_K": (GGML_Q5_K, qa.TYPE_Q5_K)}[wt]
+    for ne11 in (1, n_ids):
+        b = rng.standard_normal((T, ne11, K)).astype(np.float32)
+        ids = np.stack([rng.permutation(n_as)[:n_ids] for _ in range(T)]).astype(np.int32)
+        exp = np.zeros((T, n_ids, N), np.float32)
+        assert oracle().qwo_mul_mat_id(gtype, ptr(q), I64(K), I64(N), I64(n_as), ptr(b), I64(ne11), I64(T),
+                                       ptr(ids), I64(n_ids), ptr(exp)) == 0
+        das, db, dids = torch.from_numpy(q).cuda(), torch.from_numpy(b).cuda(), torch.from_numpy(ids).cuda()
+        dst = torch.zeros((T, n_ids, N), dtype=torch.float32, device="cuda")
+        tas = qa.tensor(ttype, K, N, n_as, das)
+        tb = qa.tensor(qa.TYPE_F32, K, ne11, T, db)
+        tids = qa.tensor(qa.TYPE_I32, n_ids, T, 1, dids)
+        ws = workspace(qa.lib().qwm_mul_mat_id_workspace_size(tas, tb, tids))
+        qa.check(qa.lib().qwm_mul_mat_id(tas, tb, tids, qa.tensor(qa.TYPE_F32, N, n_ids, T, dst), ws.data_ptr(),
+                                         ws.numel(), None))
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(dst.cpu().numpy()), bits(exp)), f"{wt} ne11={ne11}"

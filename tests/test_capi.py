@@ -54,7 +54,11 @@ def test_argument_validation_without_gpu():
     i64 = qa.tensor(qa.TYPE_I32, 4, 64, 1)
     assert L.qwm_mul_mat_id_workspace_size(a64, b64, i64) > 0
     assert L.qwm_mul_mat_id(a64, b64, i64, qa.tensor(qa.TYPE_F32, 512, 4, 64), None, 0, None) == qa.ERR_WORKSPACE
-    assert L.qwm_mul_mat_id_workspace_size(qa.tensor(qa.TYPE_Q8_0, 2048, 512, 8), b64, i64) == 0   # Q4_K only
+    # other types: GEMV launches over column chunks, whose workspace holds one chunk
+    assert 0 < L.qwm_mul_mat_id_workspace_size(qa.tensor(qa.TYPE_Q8_0, 2048, 512, 8), b64, i64) < \
+        L.qwm_mul_mat_id_workspace_size(a64, b64, i64)
+    i200 = qa.tensor(qa.TYPE_I32, 200, 64, 1)     # more ids per column than the pair table holds
+    assert L.qwm_mul_mat_id_workspace_size(qa.tensor(qa.TYPE_Q8_0, 2048, 512, 256), b64, i200) == 0
     lay = qa.MoeLayer()
     lay.router = qa.tensor(qa.TYPE_F32, 2048, 128)
     lay.gate_pool = qa.tensor(qa.TYPE_Q4_K, 2048, 768, 4)

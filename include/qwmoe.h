@@ -287,6 +287,22 @@ int qwm_moe_cached_step(const qwm_moe_layer * layer, qwm_pool * pool, int32_t la
 int qwm_pool_save_profile(const qwm_pool * pool, const char * path);
 int qwm_pool_load_profile(qwm_pool * pool, const char * path, int64_t * n_installed);
 
+/* Per-layer quotas (ExpertCache::compute_quota / rebalance,
+ * expert_cache.cpp:509-625): one quota per layer from the access counts
+ * summed over the roles -- every layer first gets up to n_used experts (the
+ * model's n_expert_used) while every role's pool has slots left, then the
+ * counts, largest first (ties: larger key first), each give their layer one
+ * more while slots remain.  From then on a miss of a layer at or over its
+ * quota recycles one of that layer's slots, any other miss takes a slot from
+ * a layer over its quota (least recently used first; none: the global LRU),
+ * and the indexed mode's shortcut is off.  Then the hottest experts inside
+ * each layer's quota are installed, all three roles, up to fill_budget
+ * experts (*n_filled, may be NULL).  quota_out: host i32 [n_layer], may be NULL.
+ * clear_counts: ExpertCache::clear_counts. */
+int qwm_pool_rebalance(qwm_pool * pool, int32_t n_used, int64_t fill_budget, int32_t * quota_out,
+                       int64_t * n_filled);
+int qwm_pool_clear_counts(qwm_pool * pool);
+
 /* File tier (ExpertCache::fetch_parallel's file path, expert_cache.cpp:
  * 1194-1440, with its persistent readers, expert_io_workers.h): misses of
  * (role, layer) are read from `path` at offset + expert * slab_bytes instead

@@ -25,6 +25,7 @@
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
+#include <functional>
 #include <cstring>
 #include <limits>
 #include <stdexcept>
@@ -938,9 +939,61 @@ struct qwo_pool {
         std::vector<int32_t> slot_of;
         std::vector<int> occ;
         std::unordered_map<int, uint64_t> count;
+        std::vector<int> quota;         // per layer, after a rebalance
     } role[3];
     std::vector<uint8_t> active;
+    bool quota_on = false;
 };
+
+// pick_victim (expert_cache.cpp:1129-1170, activation scores off): the lowest
+// free slot; else, without quotas, the minimum clock among unprotected
+// occupied slots; with quotas (after a rebalance) a layer at or over its
+// quota takes from its own slots and any other layer from layers over their
+// quotas, and if that finds nothing, the global minimum clock.
+static int qwo_pick(const qwo_pool * p, const qwo_pool::Role & R, int layer) {
+    const bool self = p->quota_on && R.quota[(size_t)layer] >= 0 && R.occ[(size_t)layer] >= R.quota[(size_t)layer];
+    int victim = -1;
+    uint64_t best = UINT64_MAX;
+    for (int s = 0; s < R.n_slots; ++s) {
+        const int ks = R.slot2key[(size_t)s];
+        if (ks < 0) return s;
+        if (p->protect && p->active[(size_t)ks]) continue;
+        if (p->quota_on) {
+            const int kl = ks / p->n_expert;
+            if (self) { if (kl != layer) continue; }
+            else if (R.occ[(size_t)kl] <= R.quota[(size_t)kl]) continue;
+        }
+        if (R.clk[(size_t)s] < best) { best = R.clk[(size_t)s]; victim = s; }
+    }
+    if (victim >= 0 || !p->quota_on) return victim;
+    for (int s = 0; s < R.n_slots; ++s) {
+        const int ks = R.slot2key[(size_t)s];
+        if (p->protect && ks >= 0 && p->active[(size_t)ks]) continue;
+        if (R.clk[(size_t)s] < best) { best = R.clk[(size_t)s]; victim = s; }
+    }
+    return victim;
+}
+
+// install (expert_cache.cpp:1173-1180): pick, drop, publish with clock + 1.
+static int qwo_install(qwo_pool * p, qwo_pool::Role & R, int key, int layer) {
+    const int victim = qwo_pick(p, R, layer);
+    if (victim < 0) return -1;
+    const int old = R.slot2key[(size_t)victim];
+    if (old >= 0) {
+        R.occ[(size_t)(old / p->n_expert)]--;
+        R.slot_of[(size_t)old] = 0;
+        R.key2slot.erase(old);
+        R.slot2key[(size_t)victim] = -1;
+        p->evictions++;
+    }
+    R.key2slot.emplace(key, victim);
+    R.slot2key[(size_t)victim] = key;
+    R.occ[(size_t)layer]++;
+    R.slot_of[(size_t)key] = victim;
+    p->clock += 1;
+    R.clk[(size_t)victim] = p->clock;
+    return victim;
+}
 
 QWO_API qwo_pool * qwo_pool_new(int n_layer, int n_expert, const int32_t * n_slots, int protect) {
     auto * p = new qwo_pool();
@@ -988,34 +1041,13 @@ QWO_API int qwo_pool_ensure(qwo_pool * p, int layer, const int32_t * ids, int n,
                 continue;
             }
             p->misses++;
-            int victim = -1;
-            uint64_t best = UINT64_MAX;
-            for (int s = 0; s < R.n_slots; ++s) {
-                const int ks = R.slot2key[(size_t)s];
-                if (ks < 0) { victim = s; break; }
-                if (p->protect && p->active[(size_t)ks]) continue;
-                if (R.clk[(size_t)s] < best) { best = R.clk[(size_t)s]; victim = s; }
-            }
+            const int victim = qwo_install(p, R, key, layer);
             if (victim < 0) { rc = -1; break; }
-            const int old = R.slot2key[(size_t)victim];
-            if (old >= 0) {
-                R.occ[(size_t)(old / p->n_expert)]--;
-                R.slot_of[(size_t)old] = 0;
-                R.key2slot.erase(old);
-                R.slot2key[(size_t)victim] = -1;
-                p->evictions++;
-            }
             if (fetch_log) {
                 fetch_log[4 * nf + 0] = r; fetch_log[4 * nf + 1] = layer;
                 fetch_log[4 * nf + 2] = e; fetch_log[4 * nf + 3] = victim;
             }
             ++nf;
-            R.key2slot.emplace(key, victim);
-            R.slot2key[(size_t)victim] = key;
-            R.occ[(size_t)layer]++;
-            R.slot_of[(size_t)key] = victim;
-            p->clock += 1;
-            R.clk[(size_t)victim] = p->clock;
             outs[r][i] = victim;
         }
     }
@@ -1086,6 +1118,62 @@ QWO_API int qwo_pool_load_profile(qwo_pool * p, const char * text, int32_t * fet
     }
     return n;
 }
+
+// ExpertCache::compute_quota + rebalance (expert_cache.cpp:509-625), one
+// pool per role shared by every layer: per-key counts summed over the roles,
+// entries ordered by (count, key) descending; floor: each layer up to n_used
+// while every role has a slot left; then one more per entry beyond its
+// layer's first n_used (quota < n_expert) while slots remain.  Quotas on;
+// then up to fill_budget experts, hottest first within each layer's quota,
+// installed in every role that lacks them.  quota_out [n_layer] (optional).
+// Returns the experts filled, or -1 when an install finds no victim.
+QWO_API int qwo_pool_rebalance(qwo_pool * p, int n_used, int64_t fill_budget, int32_t * quota_out) {
+    const int L = p->n_layer, E = p->n_expert;
+    std::unordered_map<int, uint64_t> cnt;
+    for (const auto & R : p->role)
+        for (const auto & kv : R.count) cnt[kv.first] += kv.second;
+    std::vector<std::pair<uint64_t, int>> ents;
+    for (const auto & kv : cnt) ents.emplace_back(kv.second, kv.first);
+    std::sort(ents.begin(), ents.end(), std::greater<std::pair<uint64_t, int>>());
+    std::vector<int> quota((size_t)L, 0);
+    if (!cnt.empty()) {
+        int64_t rem[3] = {p->role[0].n_slots, p->role[1].n_slots, p->role[2].n_slots};
+        auto take = [&]() {
+            if (rem[0] <= 0 || rem[1] <= 0 || rem[2] <= 0) return false;
+            rem[0]--; rem[1]--; rem[2]--;
+            return true;
+        };
+        for (int l = 0; l < L; ++l)
+            while (quota[(size_t)l] < n_used && take()) quota[(size_t)l]++;
+        std::vector<int> seen((size_t)L, 0);
+        for (const auto & e : ents) {
+            const int l = e.second / E;
+            if (seen[(size_t)l]++ < n_used) continue;
+            if (quota[(size_t)l] >= E) continue;
+            if (!take()) continue;
+            quota[(size_t)l]++;
+        }
+    }
+    for (auto & R : p->role) R.quota = quota;
+    p->quota_on = true;
+    if (quota_out) for (int l = 0; l < L; ++l) quota_out[l] = quota[(size_t)l];
+    std::vector<int> seen((size_t)L, 0);
+    int filled = 0;
+    for (const auto & e : ents) {
+        if (filled >= fill_budget) break;
+        const int key = e.second, l = key / E;
+        if (seen[(size_t)l] >= quota[(size_t)l]) continue;
+        seen[(size_t)l]++;
+        bool all = true;
+        for (const auto & R : p->role) all = all && R.key2slot.count(key);
+        if (all) continue;
+        for (auto & R : p->role)
+            if (!R.key2slot.count(key) && qwo_install(p, R, key, l) < 0) return -1;
+        ++filled;
+    }
+    return filled;
+}
+QWO_API void qwo_pool_clear_counts(qwo_pool * p) { for (auto & R : p->role) R.count.clear(); }
 
 QWO_API void qwo_pool_stats(const qwo_pool * p, uint64_t * out3) {
     out3[0] = p->hits; out3[1] = p->misses; out3[2] = p->evictions;

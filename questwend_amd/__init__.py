@@ -109,6 +109,8 @@ def lib():
         "qwm_pool_slots": (ctypes.c_int, [_P, _I32, _P, _P]),
         "qwm_pool_attach_file": (ctypes.c_int, [_P, _I32, _I32, ctypes.c_char_p, ctypes.c_uint64]),
         "qwm_pool_set_io": (ctypes.c_int, [_P, _I32, _I32]),
+        "qwm_pool_rebalance": (ctypes.c_int, [_P, _I32, _I64, _P, _P]),
+        "qwm_pool_clear_counts": (ctypes.c_int, [_P]),
         "qwm_moe_cached_workspace_size": (_SZ, [ctypes.POINTER(MoeLayer), _I64]),
         "qwm_moe_cached_step": (ctypes.c_int, [ctypes.POINTER(MoeLayer), _P, _I32, T, T, T, T, _P, _P, _SZ, _P]),
         "qwm_gguf_find_tensor": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(GgufTensor)]),

@@ -166,11 +166,13 @@ struct qwm_pool {
         std::unordered_map<int32_t, uint64_t> count;
         std::set<std::pair<uint64_t, int32_t>> lru; // indexed mode: occupied (clock, slot)
         std::set<int32_t> free_slots;               // indexed mode
+        std::vector<int32_t> quota;                 // per layer, after a rebalance
         std::vector<int> fd;                        // file tier: per layer, -1 = none
         std::vector<uint64_t> foff;                 // file tier: per layer, offset of expert 0
     };
     int n_layer = 0, n_expert = 0;
     bool protect = false, indexed = false;
+    bool quota_on = false;                          // per-layer quotas steer the victims (after a rebalance)
     uint64_t clock = 0;
     uint64_t hits = 0, misses = 0, evictions = 0, fetch_bytes = 0, fetches = 0;
     Role role[3];
@@ -212,7 +214,8 @@ struct qwm_pool {
         clock = next;
     }
 
-    int32_t pick(const Role & R) const {
+    int32_t pick(const Role & R, int32_t layer) const {
+        if (quota_on) return pick_quota(R, layer);
         if (indexed) {
             if (!R.free_slots.empty()) return *R.free_slots.begin();
             for (const auto & cs : R.lru) {
@@ -228,6 +231,32 @@ struct qwm_pool {
             const int32_t k = R.slot2key[s];
             if (k < 0) return s;
             if (protect && active[(size_t)k]) continue;
+            if (R.clk[s] < best) { best = R.clk[s]; victim = s; }
+        }
+        return victim;
+    }
+
+    // pick_victim with per-layer quotas (expert_cache.cpp:1142-1170): a free
+    // slot first; a layer at or over its quota recycles one of its own slots,
+    // any other layer takes from a layer over its quota; least recently used
+    // among those (strict <: the lowest slot on ties); none: the global LRU.
+    int32_t pick_quota(const Role & R, int32_t layer) const {
+        const bool self = R.quota[layer] >= 0 && R.occ[layer] >= R.quota[layer];
+        int32_t victim = -1;
+        uint64_t best = std::numeric_limits<uint64_t>::max();
+        for (int32_t s = 0; s < R.n_slots; ++s) {
+            const int32_t k = R.slot2key[s];
+            if (k < 0) return s;
+            if (protect && active[(size_t)k]) continue;
+            const int32_t kl = k / n_expert;
+            if (self) { if (kl != layer) continue; }
+            else if (R.occ[kl] <= R.quota[kl]) continue;
+            if (R.clk[s] < best) { best = R.clk[s]; victim = s; }
+        }
+        if (victim >= 0) return victim;
+        for (int32_t s = 0; s < R.n_slots; ++s) {
+            const int32_t k = R.slot2key[s];
+            if (protect && k >= 0 && active[(size_t)k]) continue;
             if (R.clk[s] < best) { best = R.clk[s]; victim = s; }
         }
         return victim;
@@ -522,7 +551,7 @@ int qwm_pool_ensure(qwm_pool * p, int32_t layer, const int32_t * ids, int32_t n,
                 continue;
             }
             p->misses++;
-            const int32_t victim = p->pick(R);
+            const int32_t victim = p->pick(R, layer);
             if (victim < 0) { rc = fail(QWM_ERR_NO_VICTIM, "No unprotected GPU cache victim"); break; }
             p->drop(R, victim);
             if ((rc = p->fetch(r, layer, e, victim)) != QWM_OK) break;   // victim stays free on failure
@@ -633,7 +662,7 @@ int qwm_pool_load_profile(qwm_pool * p, const char * path, int64_t * n_installed
             if ((rc = flush_layer(cur)) != QWM_OK) break;
             cur = x.l;
         }
-        const int32_t slot = p->pick(R);         // the lowest free slot
+        const int32_t slot = p->pick(R, x.l);    // the lowest free slot
         if ((rc = p->fetch(x.r, x.l, x.e, slot)) != QWM_OK) break;
         p->publish(R, slot, key, x.l);
         ++n;
@@ -643,6 +672,96 @@ int qwm_pool_load_profile(qwm_pool * p, const char * path, int64_t * n_installed
     if (p->pending) QWM_HIP_CHECK(hipEventRecord(p->done, p->copy));
     if (n_installed) *n_installed = n;
     return rc;
+}
+
+// ExpertCache::compute_quota and rebalance (expert_cache.cpp:509-625): one
+// quota per layer from the counts summed over the roles (entries by count,
+// then key, both descending): first every layer up to n_used experts while
+// every role's pool has slots left, then greedily one more expert per entry
+// beyond its layer's first n_used, while slots remain.  The quotas then steer
+// every later victim (pick_quota), and the hottest experts within each
+// layer's quota are installed, all three roles together, up to fill_budget
+// experts.
+int qwm_pool_rebalance(qwm_pool * p, int32_t n_used, int64_t fill_budget, int32_t * quota_out, int64_t * n_filled) {
+    if (!p || n_used < 1 || fill_budget < 0) return fail(QWM_ERR_ARG, "pool_rebalance: bad argument");
+    if (n_filled) *n_filled = 0;
+    const int32_t L = p->n_layer, E = p->n_expert;
+    std::unordered_map<int32_t, uint64_t> cnt;
+    for (const auto & R : p->role)
+        for (const auto & kv : R.count) cnt[kv.first] += kv.second;
+    std::vector<std::pair<uint64_t, int32_t>> ents;   // (count, key)
+    ents.reserve(cnt.size());
+    for (const auto & kv : cnt) ents.emplace_back(kv.second, kv.first);
+    std::sort(ents.begin(), ents.end(), std::greater<std::pair<uint64_t, int32_t>>());
+    std::vector<int32_t> quota((size_t)L, 0);
+    if (!cnt.empty()) {
+        int64_t rem[3];
+        for (int r = 0; r < 3; ++r) rem[r] = p->role[r].n_slots;
+        auto take = [&]() {
+            for (int r = 0; r < 3; ++r)
+                if (rem[r] <= 0) return false;
+            for (int r = 0; r < 3; ++r) rem[r]--;
+            return true;
+        };
+        for (int32_t l = 0; l < L; ++l)
+            while (quota[l] < n_used && take()) quota[l]++;
+        std::vector<int32_t> seen((size_t)L, 0);
+        for (const auto & e : ents) {
+            const int32_t l = e.second / E;
+            if (seen[l]++ < n_used) continue;
+            if (quota[l] >= E) continue;
+            if (!take()) continue;
+            quota[l]++;
+        }
+    }
+    for (auto & R : p->role) R.quota = quota;
+    p->quota_on = true;
+    if (quota_out) std::copy(quota.begin(), quota.end(), quota_out);
+    int rc = QWM_OK, cur = -1;
+    int64_t filled = 0;
+    auto flush_layer = [&](int layer) {
+        if (layer < 0) return QWM_OK;
+        const int grc = p->gather ? p->flush(layer) : QWM_OK;
+        const int frc = p->flush_files(layer);
+        return grc != QWM_OK ? grc : frc;
+    };
+    std::vector<int32_t> seen((size_t)L, 0);
+    for (const auto & e : ents) {
+        if (filled >= fill_budget) break;
+        const int32_t key = e.second, l = key / E, ex = key % E;
+        if (seen[l] >= quota[l]) continue;
+        seen[l]++;
+        bool all = true;
+        for (const auto & R : p->role) all = all && R.key2slot.count(key);
+        if (all) continue;
+        if (l != cur) {
+            if ((rc = flush_layer(cur)) != QWM_OK) break;
+            cur = l;
+        }
+        for (int r = 0; r < 3 && rc == QWM_OK; ++r) {
+            auto & R = p->role[r];
+            if (R.key2slot.count(key)) continue;
+            const int32_t victim = p->pick(R, l);
+            if (victim < 0) { rc = fail(QWM_ERR_NO_VICTIM, "No unprotected GPU cache victim"); break; }
+            p->drop(R, victim);
+            if ((rc = p->fetch(r, l, ex, victim)) != QWM_OK) break;
+            p->publish(R, victim, key, l);
+        }
+        if (rc != QWM_OK) break;
+        ++filled;
+    }
+    const int lrc = flush_layer(cur);
+    if (rc == QWM_OK) rc = lrc;
+    if (p->pending) QWM_HIP_CHECK(hipEventRecord(p->done, p->copy));
+    if (n_filled) *n_filled = filled;
+    return rc;
+}
+
+// ExpertCache::clear_counts (expert_cache.cpp:557-559).
+int qwm_pool_clear_counts(qwm_pool * p) {
+    if (!p) return fail(QWM_ERR_ARG, "pool_clear_counts: NULL pool");
+    for (auto & R : p->role) R.count.clear();
+    return QWM_OK;
 }
 
 int qwm_pool_attach_file(qwm_pool * p, int32_t role, int32_t layer, const char * path, uint64_t offset) {

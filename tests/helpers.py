@@ -56,6 +56,8 @@ def oracle():
         lib.qwo_pool_slot_of_row.argtypes = [P, ctypes.c_int, ctypes.c_int, P]
         lib.qwo_pool_slots.argtypes = [P, ctypes.c_int, P, P]
         lib.qwo_pool_save_profile.argtypes = [P, ctypes.c_char_p, ctypes.c_int]
+        lib.qwo_pool_rebalance.argtypes = [P, ctypes.c_int, I64, P]
+        lib.qwo_pool_clear_counts.argtypes = [P]
         lib.qwo_pool_load_profile.argtypes = [P, ctypes.c_char_p, P]
         lib.qwo_route.argtypes = [I64, I64, I64, P, P, P, ctypes.c_int, ctypes.c_int, F32, P, P, P, P, P]
         lib.qwo_mul_mat_id.argtypes = [ctypes.c_int, P, I64, I64, I64, P, I64, I64, P, I64, P]

@@ -297,3 +297,76 @@ def test_pool_profile_cold_start(tmp_path, text):
     g = GpuPool(1, 4, [2, 2, 2])
     assert load_profile(g, path) == 0
     assert all((g.state(r)[0] == -1).all() for r in range(3))
+
+
+def rebalance(g, n_used, budget):
+    q = np.zeros(g.n_layer, np.int32)
+    n = ctypes.c_int64(-1)
+    rc = qa.lib().qwm_pool_rebalance(g.h, n_used, budget, ptr(q), ctypes.byref(n))
+    return rc, q, n.value
+
+
+@pytest.mark.parametrize("indexed,protect", [(0, 0), (1, 0), (1, 1)])
+def test_pool_rebalance_matches_oracle(indexed, protect):
+    """compute_quota + rebalance after a trace whose layers route with
+    different spreads, then more ensure calls under the quotas: quotas,
+    filled experts, every call's slots and the final pool state equal the
+    oracle's (the indexed mode falls back to the scan once quotas are on)."""
+    rng = np.random.default_rng(31 + indexed + 2 * protect)
+    n_layer, n_expert, slots, n_used = 4, 64, [60, 50, 70], 6
+    g = GpuPool(n_layer, n_expert, slots, protect, indexed)
+    g.n_layer = n_layer
+    o = OraclePool(n_layer, n_expert, slots, protect)
+    pops = []
+    for l in range(n_layer):                       # layer l: Zipf skew 0.6 .. 1.5
+        p = 1.0 / np.arange(1, n_expert + 1) ** (0.6 + 0.3 * l)
+        pops.append((rng.permutation(n_expert), p / p.sum()))
+
+    def trace(steps):
+        for _ in range(steps):
+            l = int(rng.integers(0, n_layer))
+            perm, p = pops[l]
+            ids = np.concatenate([perm[rng.choice(n_expert, n_used, replace=False, p=p)] for _ in range(2)])
+            rg, sg = g.ensure(l, ids)
+            ro, so = o.ensure(l, ids)
+            assert rg == ro
+            if rg == 0:
+                assert np.array_equal(sg, so)
+
+    trace(120)
+    rc, qg, ng = rebalance(g, n_used, 1000)
+    qo = np.zeros(n_layer, np.int32)
+    no = oracle().qwo_pool_rebalance(o.h, n_used, 1000, ptr(qo))
+    assert rc == qa.OK and np.array_equal(qg, qo) and ng == no, (qg, qo, ng, no)
+    assert qg.sum() <= min(slots) and (qg >= n_used).all()
+    for r in range(3):
+        assert all(np.array_equal(a, b) for a, b in zip(g.state(r), o.state(r)))
+    trace(120)
+    for r in range(3):
+        assert all(np.array_equal(a, b) for a, b in zip(g.state(r), o.state(r)))
+
+
+def test_pool_quota_known_answer():
+    """2 layers x 4 experts, 5 slots per role, n_used 2.  Counts (summed over
+    the roles) 10, 9, 8 for layer 0's experts 0-2 and 7, 1 for layer 1's
+    experts 0-1: the floor gives each layer 2 (4 slots), the greedy gives
+    layer 0's third entry the last slot: quotas [3, 2].  All five experts are
+    already resident, so nothing is filled.  Then a miss of layer 1 (at its
+    quota) recycles layer 1's least recently used slot, although the global
+    LRU slot belongs to layer 0."""
+    g = GpuPool(2, 4, [5, 5, 5])
+    g.n_layer = 2
+    for e, n in [(0, 10), (1, 9), (2, 8)]:
+        for _ in range(n):
+            assert g.ensure(0, [e])[0] == 0
+    assert g.ensure(1, [1])[0] == 0
+    for _ in range(7):
+        assert g.ensure(1, [0])[0] == 0
+    rc, q, n = rebalance(g, 2, 100)
+    assert rc == qa.OK and q.tolist() == [3, 2] and n == 0
+    keys_before = g.state(0)[0].copy()
+    slot_l1e1 = int(np.nonzero(keys_before == 4 + 1)[0][0])
+    rc, slots = g.ensure(1, [2])
+    assert rc == 0 and slots[0][0] == slot_l1e1          # layer 1's LRU slot, not layer 0's
+    k = g.state(0)[0]
+    assert sorted(k.tolist()) == [0, 1, 2, 4, 6]

@@ -464,3 +464,47 @@ def test_moe_cached_step_matches_oracle(dev, fetch):
     finally:
         L.qwm_pool_destroy(h)
         oracle().qwo_pool_free(o)
+
+
+@pytest.mark.parametrize("mode", ["memcpy", "gather"])
+def test_pool_rebalance_fills_slabs(dev, mode):
+    """qwm_pool_rebalance's reshape installs fetch their slabs like misses:
+    after counts on two layers (ensure calls) and a rebalance that moves the
+    pool towards the hotter layer, every occupied slot holds its slab."""
+    L = qa.lib()
+    n_layer, E, S, slab = 2, 16, 6, 4608
+    rng = np.random.default_rng(12)
+    host = [[pinned(rng.integers(0, 256, E * slab, dtype=np.uint8)) for _ in range(3)] for _ in range(n_layer)]
+    host_ptrs = [(ctypes.c_void_p * n_layer)(*[host[l][r].data_ptr() for l in range(n_layer)]) for r in range(3)]
+    pool_t = [torch.zeros(S * slab, dtype=torch.uint8, device="cuda") for _ in range(3)]
+    d = qa.PoolDesc()
+    d.n_layer, d.n_expert = n_layer, E
+    for r in range(3):
+        d.n_slots[r], d.pool_data[r], d.slab_bytes[r] = S, pool_t[r].data_ptr(), slab
+        d.host_slabs[r] = ctypes.cast(host_ptrs[r], ctypes.c_void_p)
+    d.fetch_mode = FETCH[mode]
+    copy = torch.cuda.Stream()
+    h = ctypes.c_void_p()
+    qa.check(L.qwm_pool_create(ctypes.byref(d), ctypes.c_void_p(copy.cuda_stream), ctypes.byref(h)))
+    try:
+        out = np.zeros((3, 2), np.int32)
+        for step in range(30):                       # layer 1 hot over many experts, layer 0 over two
+            l = 1 if step % 3 else 0
+            ids = rng.choice(E, 2, replace=False).astype(np.int32) if l else np.array([0, 1], np.int32)
+            qa.check(L.qwm_pool_ensure(h, l, ptr(ids), 2, ptr(out[0]), ptr(out[1]), ptr(out[2])))
+        q = np.zeros(n_layer, np.int32)
+        n = ctypes.c_int64()
+        qa.check(L.qwm_pool_rebalance(h, 1, 100, ptr(q), ctypes.byref(n)))
+        qa.check(L.qwm_pool_wait(h, None))
+        torch.cuda.synchronize()
+        assert q.sum() == S and q[1] > q[0]
+        for r in range(3):
+            keys = np.zeros(S, np.int32)
+            qa.check(L.qwm_pool_slots(h, r, ptr(keys), None))
+            dev_bytes = pool_t[r].cpu().numpy().reshape(S, slab)
+            for s, key in enumerate(keys):
+                if key >= 0:
+                    lyr, e = divmod(int(key), E)
+                    assert np.array_equal(dev_bytes[s], host[lyr][r].numpy().reshape(E, slab)[e]), (r, s, key)
+    finally:
+        L.qwm_pool_destroy(h)

@@ -175,6 +175,19 @@ __global__ void __launch_bounds__(256) k_route(RouteKArgs a) {
 
     // ---- last workgroup: selection and the expert schedule
     if (!last_workgroup(a.counter)) return;
+    // The layer's slot-table rows (resident mode, E <= 512), requested before
+    // the logits: they are read only by the union at the end, so their round
+    // trip overlaps the selection's.
+    constexpr bool PRE = R <= 8;
+    constexpr int SQ = PRE ? (3 * 64 * R + 255) / 256 : 1;
+    int32_t slq[SQ];
+    if (PRE && a.slot_tables) {
+#pragma unroll
+        for (int q = 0; q < SQ; ++q) {
+            const int idx = tid + 256 * q;
+            slq[q] = idx < 3 * E ? a.slot_tables[(size_t)(idx / E) * a.table_stride + (size_t)a.layer * E + idx % E] : 0;
+        }
+    }
     const int nr = (E + 63) / 64;
     const int nfull = E & ~15;
     for (int t = wave; t < T; t += 4) {
@@ -258,6 +271,13 @@ __global__ void __launch_bounds__(256) k_route(RouteKArgs a) {
     int32_t * tab_first = reinterpret_cast<int32_t *>(smem);
     uint32_t * tab_mask = reinterpret_cast<uint32_t *>(tab_first + MAX_E);
     int32_t * tab_unit = reinterpret_cast<int32_t *>(tab_mask + MAX_E);
+    int32_t * tab_slot = tab_unit + MAX_E;                 // [3][E] when PRE
+    static_assert(!PRE || (3 * MAX_E + 3 * 64 * R) * 4 <= (4 + 1) * 16 * RX_PITCH * 4, "slot rows fit in LDS");
+    if (PRE && a.slot_tables) {
+#pragma unroll
+        for (int q = 0; q < SQ; ++q)
+            if (tid + 256 * q < 3 * E) tab_slot[tid + 256 * q] = slq[q];
+    }
     __shared__ unsigned long long s_bal[2];
     const int P = T * k;
     const int p = tid;
@@ -279,7 +299,7 @@ __global__ void __launch_bounds__(256) k_route(RouteKArgs a) {
         tab_unit[e] = u;
         if (a.slot_tables)
             for (int r = 0; r < 3; ++r)
-                a.uslot[4 * u + r] = a.slot_tables[(size_t)r * a.table_stride + (size_t)a.layer * E + e];
+                a.uslot[4 * u + r] = PRE ? tab_slot[r * E + e] : a.slot_tables[(size_t)r * a.table_stride + (size_t)a.layer * E + e];
     }
     __syncthreads();
     if (p < P) {
@@ -287,7 +307,7 @@ __global__ void __launch_bounds__(256) k_route(RouteKArgs a) {
         a.units[tab_unit[e]].pair[__popc(tmask & ((1u << t) - 1u))] = p;
         if (a.slot_tables)
             for (int r = 0; r < 3; ++r)
-                a.slots_ws[r * P + p] = a.slot_tables[(size_t)r * a.table_stride + (size_t)a.layer * E + e];
+                a.slots_ws[r * P + p] = PRE ? tab_slot[r * E + e] : a.slot_tables[(size_t)r * a.table_stride + (size_t)a.layer * E + e];
     }
     if (tid == 0) {
         if (a.shared) {

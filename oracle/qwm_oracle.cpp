@@ -1,7 +1,7 @@
 // qwm_oracle.cpp -- CPU restatement of the MoE expert path of QuestWend's
 // vendored ggml CPU backend (x86-64, AVX-512 build), used ONLY as test
 // infrastructure: tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
-// leg load it as the checker.  Nothing in questwend_amd/ links or calls it.
+// leg load it to check results.  Nothing in questwend_amd/ links or calls it.
 //
 // Every function cites the reference file:line whose behaviour it restates
 // (paths relative to the QuestWend tree; ggml = third_party/ggml/src).

@@ -1,7 +1,8 @@
 """Pins the oracle against committed vectors of the reference's own CPU kernels
 (tests/golden/ref_vectors.npz, written by tests/golden/make_golden.py from the
 ggml sources and core/gpu_lru_index.h compiled by oracle/Makefile).  Runs
-without the reference build: this is the oracle's pin on the GPU box."""
+without the reference build: this is the oracle's pin where the reference
+tree is absent."""
 import ctypes
 import os
 

@@ -18,9 +18,10 @@
 //     dequantized fp64 dot; softmax/top-k/combine against fp64 textbook forms.
 //   * The slot pool is checked against the reference GpuLruIndex header and the
 //     reference test's linear_scan known answers.
-//   * The tinyBLAS (T>=2 router) lane order is restated from sgemm.cpp but
-//     cannot be executed here (it needs ggml-cpu's thread pool): its bit-level
-//     order is "parity unpinned"; only its value (fp64 bound) is checked.
+//   * The f32 router mul_mat runs vec_dot_f32 per (row, column) at every
+//     column count, as the reference's ggml-cpu build does (GGML_LLAMAFILE is
+//     off there, ggml/CMakeLists.txt:113-114,197, so ggml-cpu.c:1300 is
+//     compiled out, and tiled/tiled.cpp:605-640 takes no f32 weights).
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
@@ -476,8 +477,8 @@ float vec_dot_q6_K_q8_K(int n, const block_q6_K * x, const block_q8_K * y) {
     return hsum8(acc);
 }
 
-// ggml-cpu/arch/x86/quants.c:1372-1402 (AVX2 branch); tinyBLAS_Q0_AVX
-// (llamafile/sgemm.cpp:1625-1660) accumulates in the same lane order.
+// ggml-cpu/arch/x86/quants.c:1372-1402 (AVX2 branch, taken by the AVX-512
+// build too).
 float vec_dot_q8_0_q8_0(int n, const block_q8_0 * x, const block_q8_0 * y) {
     const int nb = n / QK8_0;
     float acc[8] = {0};
@@ -517,20 +518,6 @@ float vec_dot_f32(int n, const float * x, const float * y) {
     }
     for (; i < n; ++i) sumf = fmaf(x[i], y[i], sumf);
     return sumf;
-}
-
-// llamafile/sgemm.cpp:559-700 (tinyBLAS<16, __m512>): one 16-lane fused
-// multiply-add accumulator per output over k/16 steps (partial last step),
-// then _mm512_reduce_add_ps.  Used by ggml-CPU for f32 mul_mat with >= 2
-// columns when the row count is a multiple of 4.
-float sgemm_dot_f32(int k, const float * a, const float * b) {
-    float acc[16] = {0};
-    int l = 0;
-    for (; l + 16 <= k; l += 16)
-        for (int t = 0; t < 16; ++t) acc[t] = fmaf(a[l + t], b[l + t], acc[t]);
-    if (l < k)
-        for (int t = 0; l + t < k; ++t) acc[t] = fmaf(a[l + t], b[l + t], acc[t]);
-    return reduce16(acc);
 }
 
 // ------------------------------------------------------------ SIMD math ----
@@ -679,17 +666,18 @@ void mul_mat_id(int type, const void * as, int64_t K, int64_t N, int64_t n_as,
         }
 }
 
-// Dense mul_mat (ggml-cpu.c:1255-1470): vec_dot per (row, column) for the
-// quantized types on this path; f32 weights use vec_dot for one column (or a
-// row count that is not a multiple of 4) and tinyBLAS otherwise.
+// Dense mul_mat (ggml-cpu.c:1165-1244 one_chunk, 1257-1470): vec_dot per
+// (row, column) for every type on this path, f32 included, at any column
+// count: the reference builds ggml-cpu without llamafile (the branch at
+// ggml-cpu.c:1300 is compiled out) and its tiled path takes only K-quant and
+// IQ weights (tiled/tiled.cpp:605-640).
 void mul_mat(int type, const void * w, int64_t K, int64_t N, const float * x, int64_t T, float * dst) {
     const size_t wrow = row_bytes(type, K);
     if (type == T_F32) {
-        const bool tiny = T >= 2 && (N % 4) == 0;
         for (int64_t t = 0; t < T; ++t)
             for (int64_t r = 0; r < N; ++r) {
                 const float * wr = (const float *)((const uint8_t *)w + (size_t)r * wrow);
-                dst[t * N + r] = tiny ? sgemm_dot_f32((int)K, wr, x + t * K) : vec_dot_f32((int)K, wr, x + t * K);
+                dst[t * N + r] = vec_dot_f32((int)K, wr, x + t * K);
             }
         return;
     }
@@ -731,7 +719,6 @@ QWO_API float qwo_vec_dot_q6_K_q8_K(int n, const void * x, const void * y) { ret
 QWO_API void qwo_dequantize_q6_K(const void * x, float * y, int64_t k) { dequantize_row_q6_K((const block_q6_K *)x, y, k); }
 QWO_API float qwo_vec_dot_q8_0_q8_0(int n, const void * x, const void * y) { return vec_dot_q8_0_q8_0(n, (const block_q8_0 *)x, (const block_q8_0 *)y); }
 QWO_API float qwo_vec_dot_f32(int n, const float * x, const float * y) { return vec_dot_f32(n, x, y); }
-QWO_API float qwo_sgemm_dot_f32(int k, const float * a, const float * b) { return sgemm_dot_f32(k, a, b); }
 QWO_API float qwo_v_expf(float x) { return v_expf(x); }
 QWO_API float qwo_v_silu(float x) { return v_silu(x); }
 QWO_API void qwo_swiglu(int n, float * y, const float * gate, const float * up) { vec_swiglu(n, y, gate, up); }

@@ -26,7 +26,6 @@ namespace qwm {
 struct RouteKArgs {
     const float * W; const float * x; const float * rm; const float * sgi;
     int E, H, T, k, norm; float scale;
-    int tiny;                                        // tinyBLAS order (T >= 2, E % 4 == 0)
     int n_row_wg;                                    // workgroups holding router rows
     float * logits; float * sh_logit;                // hand-off to the last workgroup
     int32_t * ids_ws; float * w_ws;                  // [T][k]
@@ -41,19 +40,18 @@ struct RouteKArgs {
     int32_t * uslot;                                 // resident mode: [unit][4] slots of each unit (gate, up, down)
 };
 
-constexpr int RX_PITCH = 132;           // LDS pitch of the transposed rows (floats; 128 steps + 4)
+// LDS of the last workgroup's expert union: first pair, token mask and unit
+// per expert, and the layer's three slot-table rows (E <= 512).
+constexpr int ROUTE_LDS_INTS = 3 * MAX_E + 3 * 512;
 
 // One kernel for the whole routing step, one router row per workgroup (the
 // whole row in one round trip of coalesced 16-byte loads; H <= 2048, a
 // multiple of 256).
-//  * Router rows.  T >= 2: llamafile tinyBLAS<16, __m512> order (sgemm.cpp:
-//    600-670): per (row, token) sixteen fma accumulators over 16-wide steps,
-//    then the 16-lane tree.  The row and x are transposed into LDS so that
-//    lane (t, l) reads its stride-16 elements as 128-bit words; a wave holds
-//    four tokens.  T == 1 (and the single shared-gate row, which ggml runs
-//    through vec_dot_f32): ggml_vec_dot_f32's AVX-512 order (ggml-cpu/vec.cpp:
-//    11-135), one token per wave: lane L = 16j + l accumulates over 64-wide
-//    steps, then (j0+j2, j1+j3, 0+1) and the 16-lane tree.
+//  * Router rows in ggml_vec_dot_f32's AVX-512 order (ggml-cpu/vec.cpp:
+//    11-135), which ggml-CPU runs per (row, token) at every token count
+//    (ggml-cpu.c:1165-1244; the reference builds it without llamafile): one
+//    token per wave, lane L = 16j + l accumulates over 64-wide steps, then
+//    (j0+j2, j1+j3, 0+1) and the 16-lane tree.  The shared-gate row likewise.
 //  * Q8_K of x (Q8_0 for Q8_0 pools), one 256-block per wave across the grid.
 //  * The last workgroup: per token (one wave each) soft_max (ggml-cpu/ops.cpp:
 //    5813-5920, vec.cpp:531 AVX-512: v_expf over 16-lane chunks, each chunk
@@ -65,7 +63,7 @@ constexpr int RX_PITCH = 132;           // LDS pitch of the transposed rows (flo
 // R: probabilities per lane in the selection (E <= 64 R).
 template <int R>
 __global__ void __launch_bounds__(256) k_route(RouteKArgs a) {
-    __shared__ __align__(16) float smem[(4 + 1) * 16 * RX_PITCH];   // x of four tokens + the row, transposed
+    __shared__ __align__(16) int32_t smem[ROUTE_LDS_INTS];
     __shared__ int32_t s_ids[MAX_PAIRS];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int E = a.E, H = a.H, T = a.T, k = a.k;
@@ -90,63 +88,7 @@ __global__ void __launch_bounds__(256) k_route(RouteKArgs a) {
     if (g < rows) {
         const bool sh_row = g == E;
         const float * w = sh_row ? a.sgi : a.W + (size_t)g * H;
-        if (a.tiny && !sh_row) {
-            float * xt = smem;                       // [4][16][RX_PITCH]
-            float * wt = smem + 4 * 16 * RX_PITCH;   // [16][RX_PITCH]
-            const int nq = H / 4;                    // float4 per row (<= 512)
-            // dst[h & 15][h >> 4] = src[h] for the float4 number q of a row
-            auto put = [&](float * dst, int q, const float4 v) {
-                const int h = 4 * q;
-                dst[((h + 0) & 15) * RX_PITCH + ((h + 0) >> 4)] = v.x;
-                dst[((h + 1) & 15) * RX_PITCH + ((h + 1) >> 4)] = v.y;
-                dst[((h + 2) & 15) * RX_PITCH + ((h + 2) >> 4)] = v.z;
-                dst[((h + 3) & 15) * RX_PITCH + ((h + 3) >> 4)] = v.w;
-            };
-            float4 wv[2];
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-                if (tid + 256 * i < nq) wv[i] = reinterpret_cast<const float4 *>(w)[tid + 256 * i];
-            for (int t0 = 0; t0 < T; t0 += 4) {
-                float4 xv[4][2];
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
-#pragma unroll
-                    for (int i = 0; i < 2; ++i)
-                        if (t0 + q < T && tid + 256 * i < nq)
-                            xv[q][i] = reinterpret_cast<const float4 *>(a.x + (size_t)(t0 + q) * H)[tid + 256 * i];
-                if (t0) __syncthreads();             // the previous group's readers are done with LDS
-#pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    if (tid + 256 * i < nq) {
-                        if (t0 == 0) put(wt, tid + 256 * i, wv[i]);
-#pragma unroll
-                        for (int q = 0; q < 4; ++q)
-                            if (t0 + q < T) put(xt + q * 16 * RX_PITCH, tid + 256 * i, xv[q][i]);
-                    }
-                }
-                __syncthreads();
-                const int l = lane & 15, t = t0 + (lane >> 4);
-                if (wave == 0 && t < T) {
-                    const float * xr = xt + (t - t0) * 16 * RX_PITCH + l * RX_PITCH;
-                    const float * wr = wt + l * RX_PITCH;
-                    float acc = 0.f;
-                    for (int st = 0; st < H / 16; st += 16) {
-#pragma unroll
-                        for (int u = 0; u < 16; u += 4) {
-                            const float4 x4 = *reinterpret_cast<const float4 *>(xr + st + u);
-                            const float4 w4 = *reinterpret_cast<const float4 *>(wr + st + u);
-                            acc = __builtin_fmaf(w4.x, x4.x, acc);
-                            acc = __builtin_fmaf(w4.y, x4.y, acc);
-                            acc = __builtin_fmaf(w4.z, x4.z, acc);
-                            acc = __builtin_fmaf(w4.w, x4.w, acc);
-                        }
-                    }
-                    acc = tree16_dpp(acc);
-                    if (l == 0) st_agent(a.logits + (size_t)t * E + g, a.rm ? acc + a.rm[(size_t)t * E + g] : acc);
-                }
-            }
-        } else {
-            // ggml_vec_dot_f32's AVX-512 order, one token per wave pass
+        {
             const int ns = H / 64;
             float wv[32];
 #pragma unroll
@@ -268,11 +210,11 @@ __global__ void __launch_bounds__(256) k_route(RouteKArgs a) {
     __syncthreads();
 
     // expert union through per-expert LDS tables: first pair, token mask, unit
-    int32_t * tab_first = reinterpret_cast<int32_t *>(smem);
+    int32_t * tab_first = smem;
     uint32_t * tab_mask = reinterpret_cast<uint32_t *>(tab_first + MAX_E);
     int32_t * tab_unit = reinterpret_cast<int32_t *>(tab_mask + MAX_E);
     int32_t * tab_slot = tab_unit + MAX_E;                 // [3][E] when PRE
-    static_assert(!PRE || (3 * MAX_E + 3 * 64 * R) * 4 <= (4 + 1) * 16 * RX_PITCH * 4, "slot rows fit in LDS");
+    static_assert(!PRE || 3 * MAX_E + 3 * 64 * R <= ROUTE_LDS_INTS, "slot rows fit in LDS");
     if (PRE && a.slot_tables) {
 #pragma unroll
         for (int q = 0; q < SQ; ++q)
@@ -809,7 +751,6 @@ int launch_route(const RouteArgs & a, const MoePlan & p, uint8_t * ws, int32_t *
     RouteKArgs r;
     r.W = a.W; r.x = a.x; r.rm = a.rm; r.sgi = a.sh_gate_inp;
     r.E = (int)a.E; r.H = (int)a.H; r.T = (int)a.T; r.k = (int)a.k; r.norm = a.norm; r.scale = a.scale;
-    r.tiny = (a.T >= 2 && a.E % 4 == 0) ? 1 : 0;
     r.n_row_wg = (int)a.E;
     r.logits = reinterpret_cast<float *>(ws + p.logits);
     float * sh = reinterpret_cast<float *>(ws + p.sh_gate);

@@ -18,13 +18,12 @@ constexpr int SNB = SH / QK_K;           // Q8_K blocks per token
 constexpr uint32_t SPIN_LIMIT = 1u << 21;
 constexpr int MAX_NDOWN_S = 2048;        // longest down-projection input (FFN width)
 constexpr int STEP_MAX_E = 512;          // experts per layer in the fused step
-constexpr int RX_P = 132;                // pitch of the transposed router rows in LDS (floats)
 constexpr int XSP = 96;                  // workspace dwords per exact-layout Q8_K block of x (3 whole lines)
 constexpr size_t cmax(size_t x, size_t y) { return x > y ? x : y; }
 
 struct StepArgs {
     const float * W_r; const float * x; const float * rm; const float * sgi;   // router [E][H], x [T][H]
-    int E, k, norm, tiny; float scale;
+    int E, k, norm; float scale;
     int N, N_sh, shared;
     const uint8_t * gate; const uint8_t * up; const uint8_t * down;
     size_t gate_slab, up_slab, down_slab;
@@ -101,7 +100,7 @@ QWM_DEV void grid_barrier(const StepArgs & a, int i, int G, uint32_t epoch) {
 // Router rows e = g, g + G, ... (row E: the shared-expert gate row) and the
 // Q8_K blocks of x (waves counted from the end of the grid).
 template <int NT>
-QWM_DEV void step_router(const StepArgs & a, int g, int G, uint8_t * smem) {
+QWM_DEV void step_router(const StepArgs & a, int g, int G) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int E = a.E;
     {
@@ -113,69 +112,11 @@ QWM_DEV void step_router(const StepArgs & a, int g, int G, uint8_t * smem) {
     }
     const int rows = E + (a.sgi ? 1 : 0);
     if (g >= rows) return;                       // uniform per workgroup; no barrier follows inside
-    float * xt = reinterpret_cast<float *>(smem);            // [4][16][RX_P]: x of four tokens, transposed
-    float * wt = xt + 4 * 16 * RX_P;                         // [16][RX_P]: one router row, transposed
-    // 16 x 128 transposes into LDS: dst[h & 15][h >> 4] = src[h]; thread tid
-    // owns float4 number tid and tid + 256 of a 2048-float row
-    auto put = [&](float * dst, const float4 (&v)[2]) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int h = 4 * (tid + 256 * i);
-            dst[((h + 0) & 15) * RX_P + ((h + 0) >> 4)] = v[i].x;
-            dst[((h + 1) & 15) * RX_P + ((h + 1) >> 4)] = v[i].y;
-            dst[((h + 2) & 15) * RX_P + ((h + 2) >> 4)] = v[i].z;
-            dst[((h + 3) & 15) * RX_P + ((h + 3) >> 4)] = v[i].w;
-        }
-    };
-    auto get = [&](float4 (&v)[2], const float * src) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i) v[i] = reinterpret_cast<const float4 *>(src)[tid + 256 * i];
-    };
-    if (a.tiny) {
-        // llamafile tinyBLAS<16> order (sgemm.cpp:600-670): lane (t, l) runs one
-        // fma chain over 16-wide steps, then the 16-lane tree.  Tokens in groups
-        // of four (x of one group staged in LDS with the first row, one round
-        // trip); one row at a time.
-        for (int t0 = 0; t0 < NT; t0 += 4) {
-            float4 xv[4][2], wv[2];
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-                if (t0 + q < NT) get(xv[q], a.x + (size_t)(t0 + q) * SH);
-            for (int e = g; e < E; e += G) {
-                get(wv, a.W_r + (size_t)e * SH);
-                __syncthreads();                 // the previous row's readers are done with LDS
-                if (e == g) {
-#pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        if (t0 + q < NT) put(xt + q * 16 * RX_P, xv[q]);
-                }
-                put(wt, wv);
-                __syncthreads();
-                const int l = lane & 15, t = t0 + (lane >> 4);
-                if (wave == 0 && t < NT) {
-                    const float * xr = xt + (t - t0) * 16 * RX_P + l * RX_P;
-                    const float * wr = wt + l * RX_P;
-                    float acc = 0.f;
-#pragma unroll 8
-                    for (int s = 0; s < SH / 16; s += 4) {
-                        const float4 x4 = *reinterpret_cast<const float4 *>(xr + s);
-                        const float4 w4 = *reinterpret_cast<const float4 *>(wr + s);
-                        acc = __builtin_fmaf(w4.x, x4.x, acc);
-                        acc = __builtin_fmaf(w4.y, x4.y, acc);
-                        acc = __builtin_fmaf(w4.z, x4.z, acc);
-                        acc = __builtin_fmaf(w4.w, x4.w, acc);
-                    }
-                    acc = tree16_dpp(acc);
-                    if (l == 0) st_agent(a.lg + (size_t)e * 32 + t, a.rm ? acc + a.rm[(size_t)t * E + e] : acc);
-                }
-            }
-            __syncthreads();
-        }
-    }
+    // ggml_vec_dot_f32's AVX-512 order (vec.cpp:11-135), which ggml-CPU runs
+    // per (row, token) at every token count (ggml-cpu.c:1165-1244; llamafile
+    // is not built), one token per wave pass
     for (int e = g; e < rows; e += G) {
         const bool sh_row = e == E;
-        if (a.tiny && !sh_row) continue;
-        // ggml_vec_dot_f32's AVX-512 order (vec.cpp:11-135), one token per wave pass
         const float * w = sh_row ? a.sgi : a.W_r + (size_t)e * SH;
         float wv[SH / 64];
 #pragma unroll
@@ -539,10 +480,9 @@ QWM_DEV void step_down(const StepArgs & a, int g, int G, const StepShared & S, u
 template <int NT, int NB_D>
 __global__ void __launch_bounds__(256) k_step(StepArgs a) {
     constexpr int MAXP = NT <= 1 ? 1 : NT <= 2 ? 2 : NT <= 4 ? 4 : 8;
-    constexpr size_t router_bytes = (size_t)5 * 16 * RX_P * 4;
     constexpr size_t down_bytes = (size_t)MAXP * (NB_D * XS * 4 + DN_TR * 4);
     constexpr size_t gateup_bytes = (size_t)MAXP * SNB * XS * 4;
-    constexpr size_t smem_bytes = cmax(cmax(cmax(router_bytes, down_bytes), gateup_bytes), VhSmem<NT>::bytes);
+    constexpr size_t smem_bytes = cmax(cmax(down_bytes, gateup_bytes), VhSmem<NT>::bytes);
     __shared__ __align__(16) uint8_t smem[smem_bytes];
     __shared__ StepShared S;
     __shared__ uint32_t s_epoch;
@@ -559,7 +499,7 @@ __global__ void __launch_bounds__(256) k_step(StepArgs a) {
         const int idx = threadIdx.x + 256 * q;
         sl[q] = idx < 3 * a.E ? a.slot_tables[(size_t)(idx / a.E) * a.table_stride + (size_t)a.layer * a.E + idx % a.E] : 0;
     }
-    step_router<NT>(a, g, G, smem);
+    step_router<NT>(a, g, G);
 #pragma unroll
     for (int q = 0; q < SLQ; ++q) S.slot_of[threadIdx.x + 256 * q] = sl[q];
     grid_barrier(a, 1, G, epoch);

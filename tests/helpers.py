@@ -37,7 +37,7 @@ def oracle():
             raise RuntimeError("oracle/liboracle.so missing: run __graft_entry__.build()")
         lib = ctypes.CDLL(ORACLE_SO)
         for name in ["qwo_vec_dot_q4_K_q8_K", "qwo_vec_dot_q8_0_q8_0", "qwo_vec_dot_q6_K_q8_K", "qwo_vec_dot_q5_K_q8_K", "qwo_vec_dot_f32",
-                     "qwo_sgemm_dot_f32", "qwo_v_expf", "qwo_v_silu", "qwo_fp16_to_fp32"]:
+                     "qwo_v_expf", "qwo_v_silu", "qwo_fp16_to_fp32"]:
             getattr(lib, name).restype = F32
         lib.qwo_v_expf.argtypes = [F32]
         lib.qwo_v_silu.argtypes = [F32]

@@ -86,22 +86,6 @@ def test_q4_K_dot_is_exact_blockwise(K):
     assert np.all(np.abs(got - exact) <= 1e-6 * scale + 1e-7)
 
 
-def test_sgemm_f32_order_value():
-    """tinyBLAS lane order (bit-level order unpinned): value within fp32
-    accumulation error of the fp64 dot."""
-    rng = np.random.default_rng(8)
-    for k in [16, 2048, 100, 1]:
-        a = rng.standard_normal(k).astype(np.float32)
-        b = rng.standard_normal(k).astype(np.float32)
-        got = oracle().qwo_sgemm_dot_f32(k, ptr(a), ptr(b))
-        exact = float(np.dot(a.astype(np.float64), b.astype(np.float64)))
-        assert abs(got - exact) <= 1e-6 * float(np.abs(a).dot(np.abs(b))) + 1e-30
-    # exactly representable sums: every order gives the exact answer
-    a = np.arange(64, dtype=np.float32)
-    b = np.ones(64, np.float32)
-    assert oracle().qwo_sgemm_dot_f32(64, ptr(a), ptr(b)) == 2016.0
-
-
 # ------------------------------------------------------------- routing --
 
 def route(Wr, x, k, norm=1, scale=1.0, rm=None):

@@ -114,6 +114,27 @@ def test_vec_dot_f32_bits(n):
         assert np.float32(a).view(np.uint32) == np.float32(b).view(np.uint32)
 
 
+@pytest.mark.parametrize("E,T", [(128, 2), (128, 4), (512, 3), (512, 8), (100, 5)])
+def test_router_logits_bits_every_token_count(E, T):
+    """Router mul_mat f32 at T >= 2: ggml-cpu computes vec_dot_f32 per (row,
+    column) (ggml-cpu.c:1165-1244; llamafile is compiled out of the
+    reference's build and tiled/ takes no f32 weights), so each logit equals
+    the reference's own vec_dot_f32 on that row and column, bit for bit."""
+    H = 2048
+    rng = np.random.default_rng(E * 10 + T)
+    Wr = (rng.standard_normal((E, H)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    k = 8
+    ids = np.zeros((T, k), np.int32)
+    w = np.zeros((T, k), np.float32)
+    logits = np.zeros((T, E), np.float32)
+    assert oracle().qwo_route(I64(E), I64(H), I64(T), ptr(Wr), ptr(x), None, k, 1, 1.0,
+                              ptr(ids), ptr(w), ptr(logits), None, None) == 0
+    want = np.array([[ref().qwr_vec_dot_f32(H, ptr(Wr[e]), ptr(x[t])) for e in range(E)] for t in range(T)],
+                    np.float32)
+    assert np.array_equal(bits(logits), bits(want))
+
+
 def test_simd_expf_silu_bits():
     rng = np.random.default_rng(29)
     xs = np.concatenate([rng.uniform(-110, 92, 4096), rng.standard_normal(4096) * 4,

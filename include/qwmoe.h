@@ -74,9 +74,12 @@ int qwm_workspace_init(void * workspace, size_t bytes, void * stream);
 
 /* GGML_OP_MUL_MAT_ID (ggml.c:3398-3440; CPU: ggml-cpu.c:1554-1734):
  *   dst[:, e, t] = as[:, :, ids[e, t]] . b[:, e % ne11(b), t]
- * as: Q4_K or Q8_0 [K, N, n_as]; b: f32 [K, ne11, T]; ids: i32 [n_ids, T];
- * dst: f32 [N, n_ids, T].  Supported: K % 256 == 0 and K <= 2048 (Q4_K and
- * Q8_0), T <= 8, n_ids * T <= 128. */
+ * as: Q4_K, Q5_K, Q6_K or Q8_0 [K, N, n_as]; b: f32 [K, ne11, T]; ids: i32
+ * [n_ids, T]; dst: f32 [N, n_ids, T].  Supported: K % 256 == 0 and
+ * K <= 2048; Q5_K data 16-byte aligned, Q6_K 4-byte aligned.
+ *   T <= 8: one GEMV launch, n_ids * T <= 128.
+ *   T > 8, Q4_K: the grouped int8-MFMA GEMM (prefill), n_ids * T <= 2^22.
+ *   T > 8, other types: GEMV launches over column chunks, n_ids <= 128. */
 size_t qwm_mul_mat_id_workspace_size(const qwm_tensor * as, const qwm_tensor * b, const qwm_tensor * ids);
 int qwm_mul_mat_id(const qwm_tensor * as, const qwm_tensor * b, const qwm_tensor * ids, qwm_tensor * dst,
                    void * workspace, size_t ws_bytes, void * stream);
@@ -86,8 +89,10 @@ int qwm_mul_mat_id(const qwm_tensor * as, const qwm_tensor * b, const qwm_tensor
 /* One MoE layer's weights: slot pools in ggml layout (gate/up [H, N, S],
  * down [N, H, S]), the f32 router [H, E], and an optional shared expert
  * (data == NULL when absent): gate/up [H, N_sh], down [N_sh, H], and the
- * optional f32 shared gate row [H, 1].  Pools and shared expert are all Q4_K
- * or all Q8_0; H and N are multiples of 256 up to 2048, N_sh = N. */
+ * optional f32 shared gate row [H, 1].  gate/up are Q4_K, Q5_K or Q8_0 and
+ * down the same type (or Q6_K beside Q4_K/Q5_K, as K-quant "_M" files have
+ * it); the shared expert's types match the pools'.  H and N are multiples of
+ * 256 up to 2048. */
 typedef struct qwm_moe_layer {
     qwm_tensor gate_pool, up_pool, down_pool;
     qwm_tensor router;

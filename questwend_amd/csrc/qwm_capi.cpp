@@ -118,13 +118,20 @@ int qwm_profile_stop(float * durations_ms, int32_t capacity) {
     if (!g_prof.open) return fail(QWM_ERR_STATE, "profile_stop: profiling was not started");
     g_prof.open = false;
     const int n = std::min(g_prof.used, capacity);
-    for (int i = 0; i < n; ++i) {
-        QWM_HIP_CHECK(hipEventSynchronize(g_prof.ev[2 * i + 1]));
+    int rc = QWM_OK;
+    for (int i = 0; i < n && rc == QWM_OK; ++i) {
         float ms = 0.f;
-        QWM_HIP_CHECK(hipEventElapsedTime(&ms, g_prof.ev[2 * i], g_prof.ev[2 * i + 1]));
-        if (durations_ms) durations_ms[i] = ms;
+        hipError_t e = hipEventSynchronize(g_prof.ev[2 * i + 1]);
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, g_prof.ev[2 * i], g_prof.ev[2 * i + 1]);
+        if (e != hipSuccess) rc = fail(QWM_ERR_HIP, std::string("profile_stop: ") + hipGetErrorString(e));
+        else if (durations_ms) durations_ms[i] = ms;
     }
-    return n;
+    // the events are released here, not left for process exit (where the HIP
+    // runtime and a profiler may already be tearing down)
+    for (hipEvent_t e : g_prof.ev) (void)hipEventDestroy(e);
+    g_prof.ev.clear();
+    g_prof.used = 0;
+    return rc == QWM_OK ? n : rc;
 }
 
 // ------------------------------------------------------------ mul_mat_id --
@@ -347,9 +354,15 @@ int qwm_moe_block_resident(const qwm_moe_layer * layer, int32_t layer_index, con
     if (rc != QWM_OK) return rc;
     if ((rc = check_act(x, p.H, "x")) != QWM_OK) return rc;
     if ((rc = check_act(out, p.H, "out")) != QWM_OK) return rc;
-    if (resid && ((rc = check_act(resid, p.H, "resid")) != QWM_OK)) return rc;
+    if (out->ne[1] != p.T) return fail(QWM_ERR_ARG, "moe_block: out must be [H, T]");
+    if (resid && ((rc = check_act(resid, p.H, "resid")) != QWM_OK || resid->ne[1] != p.T))
+        return rc != QWM_OK ? rc : fail(QWM_ERR_ARG, "moe_block: resid must be [H, T]");
     if (rm && (rm->type != T_F32 || rm->ne[0] != p.E || rm->ne[1] != p.T || !fully_contiguous(rm)))
         return fail(QWM_ERR_ARG, "moe_block: rm must be contiguous f32 [E, T]");
+    if (ids_out && (ids_out->type != T_I32 || ids_out->ne[0] != p.k || ids_out->ne[1] != p.T || ids_out->nb[0] != 4))
+        return fail(QWM_ERR_ARG, "moe_block: ids_out must be i32 [k, T]");
+    if (w_out && (w_out->type != T_F32 || w_out->ne[0] != p.k || w_out->ne[1] != p.T || w_out->nb[0] != 4))
+        return fail(QWM_ERR_ARG, "moe_block: w_out must be f32 [k, T]");
     if (table_stride < (int64_t)(layer_index + 1) * p.E) return fail(QWM_ERR_ARG, "moe_block: slot table stride too small");
     if (!workspace || ws_bytes < p.total) return fail(QWM_ERR_WORKSPACE, "moe_block: workspace too small");
     uint8_t * ws = (uint8_t *)workspace;

@@ -18,6 +18,7 @@ constexpr int SNB = SH / QK_K;           // Q8_K blocks per token
 constexpr uint32_t SPIN_LIMIT = 1u << 21;
 constexpr int MAX_NDOWN_S = 2048;        // longest down-projection input (FFN width)
 constexpr int STEP_MAX_E = 512;          // experts per layer in the fused step
+constexpr size_t STEP_SELECT_LDS = (size_t)3 * STEP_MAX_E * 4;   // the selection's union tables
 constexpr int XSP = 96;                  // workspace dwords per exact-layout Q8_K block of x (3 whole lines)
 constexpr size_t cmax(size_t x, size_t y) { return x > y ? x : y; }
 
@@ -234,9 +235,10 @@ QWM_DEV void step_select(const StepArgs & a, int g, StepShared & S, uint8_t * sm
     }
     __syncthreads();
     // expert union through per-expert LDS tables: first pair, token mask, unit
+    // (STEP_SELECT_LDS bytes: three tables of STEP_MAX_E words, E <= STEP_MAX_E)
     int32_t * tab_first = reinterpret_cast<int32_t *>(smem);
-    uint32_t * tab_mask = reinterpret_cast<uint32_t *>(tab_first + MAX_E);
-    int32_t * tab_unit = reinterpret_cast<int32_t *>(tab_mask + MAX_E);
+    uint32_t * tab_mask = reinterpret_cast<uint32_t *>(tab_first + STEP_MAX_E);
+    int32_t * tab_unit = reinterpret_cast<int32_t *>(tab_mask + STEP_MAX_E);
     __shared__ unsigned long long s_bal[2];
     const int P = NT * k;
     const int p = tid;
@@ -482,7 +484,7 @@ __global__ void __launch_bounds__(256) k_step(StepArgs a) {
     constexpr int MAXP = NT <= 1 ? 1 : NT <= 2 ? 2 : NT <= 4 ? 4 : 8;
     constexpr size_t down_bytes = (size_t)MAXP * (NB_D * XS * 4 + DN_TR * 4);
     constexpr size_t gateup_bytes = (size_t)MAXP * SNB * XS * 4;
-    constexpr size_t smem_bytes = cmax(cmax(down_bytes, gateup_bytes), VhSmem<NT>::bytes);
+    constexpr size_t smem_bytes = cmax(cmax(cmax(STEP_SELECT_LDS, down_bytes), gateup_bytes), VhSmem<NT>::bytes);
     __shared__ __align__(16) uint8_t smem[smem_bytes];
     __shared__ StepShared S;
     __shared__ uint32_t s_epoch;

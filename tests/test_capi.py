@@ -74,6 +74,37 @@ def test_argument_validation_without_gpu():
     assert L.qwm_verify_workspace_size(qa.tensor(qa.TYPE_Q8_0, 2048, 151936), 4) > 0
 
 
+def test_block_resident_rejects_short_tensors_without_gpu():
+    """qwm_moe_block_resident checks out/resid columns and the ids/weights
+    outputs' type, shape and stride before any device work (a tensor with
+    too few columns would otherwise be written past its end)."""
+    L = qa.lib()
+    lay = qa.MoeLayer()
+    lay.router = qa.tensor(qa.TYPE_F32, 2048, 128, 1, 0x10000)
+    lay.gate_pool = qa.tensor(qa.TYPE_Q4_K, 2048, 768, 4, 0x10000)
+    lay.up_pool = qa.tensor(qa.TYPE_Q4_K, 2048, 768, 4, 0x10000)
+    lay.down_pool = qa.tensor(qa.TYPE_Q4_K, 768, 2048, 4, 0x10000)
+    lay.n_expert_used = 8
+    T = 4
+    fake = 0x20000
+    x = qa.tensor(qa.TYPE_F32, 2048, T, 1, fake)
+    ids = qa.tensor(qa.TYPE_I32, 8, T, 1, fake)
+    w = qa.tensor(qa.TYPE_F32, 8, T, 1, fake)
+
+    def call(out, resid=None, ids_out=None, w_out=None):
+        return L.qwm_moe_block_resident(lay, 0, ctypes.c_void_p(fake), 128, x, None, resid, out, ids_out, w_out,
+                                        ctypes.c_void_p(fake), 1, None)
+
+    good = qa.tensor(qa.TYPE_F32, 2048, T, 1, fake)
+    assert call(good) == qa.ERR_WORKSPACE                    # every argument accepted; the workspace is too small
+    assert call(qa.tensor(qa.TYPE_F32, 2048, T - 1, 1, fake)) == qa.ERR_ARG
+    assert call(good, resid=qa.tensor(qa.TYPE_F32, 2048, 1, 1, fake)) == qa.ERR_ARG
+    assert call(good, ids_out=qa.tensor(qa.TYPE_I32, 8, T - 1, 1, fake)) == qa.ERR_ARG
+    assert call(good, ids_out=qa.tensor(qa.TYPE_F32, 8, T, 1, fake)) == qa.ERR_ARG      # wrong type
+    assert call(good, w_out=qa.tensor(qa.TYPE_F32, 4, T, 1, fake)) == qa.ERR_ARG
+    assert call(good, ids_out=ids, w_out=w) == qa.ERR_WORKSPACE
+
+
 class GpuPool:
     """Decision-only libqwmoe pool (no host slabs, so no copies, no GPU)."""
 

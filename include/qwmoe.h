@@ -186,6 +186,22 @@ int qwm_verify_step(const qwm_moe_layer * layer, int32_t layer_index, const int3
                     const float * norm_w, float eps, const int32_t * drafts, int32_t * result,
                     void * workspace, size_t ws_bytes, void * stream);
 
+/* qwm_verify_step without a workspace argument.  No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * step's scratch is a static device array of QWM_NOALLOC_SCRATCH_BYTES that
+ * each GPU holds until the process ends; every supported shape of
+ * qwm_verify_step fits (a larger need returns QWM_ERR_UNSUPPORTED).  Each
+ * call clears the part it uses with a fill kernel before the step (so the
+ * call can be captured).  All calls on one GPU share that array: calls that
+ * overlap on one GPU (other streams, other threads) race.  The device address
+ * is looked up on the first call per device.  Allocates nothing. */
+#define QWM_NOALLOC_SCRATCH_BYTES (4u << 20)
+int qwm_verify_step_noalloc(const qwm_moe_layer * layer, int32_t layer_index, const int32_t * slot_tables,
+                            int64_t table_stride, const qwm_tensor * x, const qwm_tensor * rm, const qwm_tensor * resid,
+                            qwm_tensor * out, qwm_tensor * ids_out, qwm_tensor * w_out, const qwm_tensor * lm_head,
+                            const float * norm_w, float eps, const int32_t * drafts, int32_t * result, void * stream);
+
 /* ------------------------------------------------------- quantization --- */
 
 /* Model-file quantization on the device, as ggml_quantize_chunk does it

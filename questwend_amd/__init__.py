@@ -19,6 +19,7 @@ LIB_PATH = os.path.join(_HERE, "libqwmoe.so")
 
 TYPE_F32, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_I32 = 0, 8, 12, 13, 14, 26
 FETCH_MEMCPY, FETCH_GATHER = 0, 1
+NOALLOC_SCRATCH_BYTES = 4 << 20        # QWM_NOALLOC_SCRATCH_BYTES
 _TYPE_SIZE = {TYPE_F32: (4, 1), TYPE_I32: (4, 1), TYPE_Q8_0: (34, 32), TYPE_Q4_K: (144, 256), TYPE_Q5_K: (176, 256),
               TYPE_Q6_K: (210, 256)}
 
@@ -100,6 +101,8 @@ def lib():
         "qwm_verify_step_workspace_size": (_SZ, [ctypes.POINTER(MoeLayer), T, _I64]),
         "qwm_verify_step": (ctypes.c_int, [ctypes.POINTER(MoeLayer), _I32, _P, _I64, T, T, T, T, T, T, T,
                                            _P, ctypes.c_float, _P, _P, _P, _SZ, _P]),
+        "qwm_verify_step_noalloc": (ctypes.c_int, [ctypes.POINTER(MoeLayer), _I32, _P, _I64, T, T, T, T, T, T, T,
+                                                   _P, ctypes.c_float, _P, _P, _P]),
         "qwm_pool_create": (ctypes.c_int, [ctypes.POINTER(PoolDesc), _P, ctypes.POINTER(_P)]),
         "qwm_pool_destroy": (None, [_P]),
         "qwm_pool_ensure": (ctypes.c_int, [_P, _I32, _P, _I32, _P, _P, _P]),

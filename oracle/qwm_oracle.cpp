@@ -641,6 +641,18 @@ float dot_row(int type, int k, const void * w, const void * xq) {
     throw std::invalid_argument("unsupported weight type");
 }
 
+// Runs fn(i) for i in [0, n) over the host's threads when n is large.  Every
+// output element is computed by one call in its own fixed order, so the split
+// changes nothing but the wall time of large fixtures.
+void parallel_for(int64_t n, const std::function<void(int64_t)> & fn) {
+    const int64_t nt = std::max<int64_t>(1, std::min<int64_t>(n / 16, (int64_t)std::thread::hardware_concurrency()));
+    if (nt <= 1) { for (int64_t i = 0; i < n; ++i) fn(i); return; }
+    std::vector<std::thread> pool;
+    for (int64_t w = 0; w < nt; ++w)
+        pool.emplace_back([&, w]() { for (int64_t i = w; i < n; i += nt) fn(i); });
+    for (auto & th : pool) th.join();
+}
+
 // ggml-cpu.c:1554-1734: quantize every column of b to the weight's
 // vec_dot_type, then dst[:, e, t] = as[:, :, ids[e,t]] . b[:, e % ne11, t].
 // (The tiled path that ggml takes for experts with >= 8 routed columns sums
@@ -655,15 +667,15 @@ void mul_mat_id(int type, const void * as, int64_t K, int64_t N, int64_t n_as,
         for (int64_t i = 0; i < ne11; ++i)
             from_float(vt, b + (t * ne11 + i) * K, bq.data() + (size_t)(t * ne11 + i) * qrow, K);
     const size_t wrow = row_bytes(type, K);
-    for (int64_t t = 0; t < T; ++t)
-        for (int64_t e = 0; e < n_ids; ++e) {
-            const int32_t id = ids[t * n_ids + e];
-            if (id < 0 || id >= n_as) throw std::out_of_range("mul_mat_id: expert id out of range");
-            const uint8_t * slab = (const uint8_t *)as + (size_t)id * N * wrow;
-            const uint8_t * col = bq.data() + (size_t)(t * ne11 + e % ne11) * qrow;
-            float * out = dst + (t * n_ids + e) * N;
-            for (int64_t r = 0; r < N; ++r) out[r] = dot_row(type, (int)K, slab + (size_t)r * wrow, col);
-        }
+    for (int64_t i = 0; i < T * n_ids; ++i)
+        if (ids[i] < 0 || ids[i] >= n_as) throw std::out_of_range("mul_mat_id: expert id out of range");
+    parallel_for(T * n_ids, [&](int64_t i) {
+        const int64_t t = i / n_ids, e = i % n_ids;
+        const uint8_t * slab = (const uint8_t *)as + (size_t)ids[i] * N * wrow;
+        const uint8_t * col = bq.data() + (size_t)(t * ne11 + e % ne11) * qrow;
+        float * out = dst + i * N;
+        for (int64_t r = 0; r < N; ++r) out[r] = dot_row(type, (int)K, slab + (size_t)r * wrow, col);
+    });
 }
 
 // Dense mul_mat (ggml-cpu.c:1165-1244 one_chunk, 1257-1470): vec_dot per
@@ -685,9 +697,11 @@ void mul_mat(int type, const void * w, int64_t K, int64_t N, const float * x, in
     const size_t qrow = row_bytes(vt, K);
     std::vector<uint8_t> xq((size_t)T * qrow);
     for (int64_t t = 0; t < T; ++t) from_float(vt, x + t * K, xq.data() + (size_t)t * qrow, K);
-    for (int64_t t = 0; t < T; ++t)
-        for (int64_t r = 0; r < N; ++r)
-            dst[t * N + r] = dot_row(type, (int)K, (const uint8_t *)w + (size_t)r * wrow, xq.data() + (size_t)t * qrow);
+    parallel_for((N + 255) / 256, [&](int64_t c) {
+        for (int64_t r = 256 * c; r < std::min<int64_t>(N, 256 * (c + 1)); ++r)
+            for (int64_t t = 0; t < T; ++t)
+                dst[t * N + r] = dot_row(type, (int)K, (const uint8_t *)w + (size_t)r * wrow, xq.data() + (size_t)t * qrow);
+    });
 }
 
 }  // namespace

@@ -31,6 +31,11 @@ constexpr int XS = 76;       // LDS dwords per Q8_K block in the exact layout (6
 // One wave quantizes 256 floats to Q8_K (quantize_block_q8K's arithmetic)
 // into the exact layout at `dst` (XS dwords).  Lane l owns elements 4l..4l+3,
 // i.e. qs dword l = 16p + 8h + m.
+// quantize_q8K_x_reg: the same from the lane's four elements already in
+// registers (so a wave can request several blocks before quantizing any).
+template <bool AGENT = false>
+QWM_DEV void quantize_q8K_x_reg(const float4 v4, uint32_t * __restrict__ dst, int lane);
+
 template <bool SRC_AGENT = false, bool AGENT = false>
 QWM_DEV void quantize_block_q8K_x(const float * __restrict__ src, uint32_t * __restrict__ dst, int lane) {
     float4 v4;
@@ -42,6 +47,11 @@ QWM_DEV void quantize_block_q8K_x(const float * __restrict__ src, uint32_t * __r
     } else {
         v4 = reinterpret_cast<const float4 *>(src)[lane];
     }
+    quantize_q8K_x_reg<AGENT>(v4, dst, lane);
+}
+
+template <bool AGENT>
+QWM_DEV void quantize_q8K_x_reg(const float4 v4, uint32_t * __restrict__ dst, int lane) {
     const float v[4] = {v4.x, v4.y, v4.z, v4.w};
     float a = __builtin_fabsf(v[0]);
     int ii = 0;
@@ -94,10 +104,26 @@ QWM_DEV void load_xblk(XBlk & B, const uint8_t * blk, int m) {
     for (int p = 0; p < 4; ++p) B.q[p] = *reinterpret_cast<const uint32_t *>(blk + 16 + 32 * p + 4 * m);
 }
 
+// The integer products below run on the 24-bit multiplier (full rate; a
+// 32-bit v_mul_lo is quarter rate): every operand fits 24 signed bits, e.g.
+// |dot4| <= 4 * 63 * 128 (Q6_K), scales and mins <= 63 (Q4_K/Q5_K) or 128
+// (Q6_K), |q8s| <= 32 * 128, so the products and sums are the exact integers.
+
 // Row dots of one weight row (NB blocks in W) with n <= MAXP activation rows
-// at sx + i * NB * XS in LDS.  out[i] is valid in lane m == 0 of the group.
-template <int NB, int MAXP>
-QWM_DEV void q4k_dot8(float (&out)[MAXP], const XBlk (&W)[NB], const uint32_t * sx, int n, int m) {
+// at sx + off[i] in LDS (NB consecutive blocks of XS dwords each).  out[i] is
+// valid in lane m == 0 of the group.
+// FIXN > 0: exactly FIXN tokens (a compile-time count, so that no branch
+// splits the unrolled block loop and the scheduler can request later blocks'
+// activations early); 0: n at run time.
+template <int NB, int MAXP, int FIXN = 0>
+QWM_DEV void q4k_dot8_off(float (&out)[MAXP], const XBlk (&W)[NB], const uint32_t * sx, const int (&off)[MAXP], int n_,
+                          int m) {
+    // the token count and offsets are uniform: scalar loop control, and each
+    // token's activation rows at one scalar base (block offsets immediate)
+    const int n = FIXN > 0 ? FIXN : __builtin_amdgcn_readfirstlane(n_);
+    const uint32_t * xt[MAXP];
+#pragma unroll
+    for (int i = 0; i < MAXP; ++i) xt[i] = sx + __builtin_amdgcn_readfirstlane(off[i]);
     float acc[MAXP], accm[MAXP];
 #pragma unroll
     for (int i = 0; i < MAXP; ++i) { acc[i] = 0.f; accm[i] = 0.f; }
@@ -108,10 +134,13 @@ QWM_DEV void q4k_dot8(float (&out)[MAXP], const XBlk (&W)[NB], const uint32_t * 
         const XBlk & B = W[b];
         // scales and mins as ggml unpacks them (quants.c:2133-2138)
         const uint32_t u0 = B.h.y, u1 = B.h.z, u2 = B.h.w;
-        const uint32_t mn_hi = ((u2 >> 4) & k2) | (((u1 >> 6) & k3) << 4);
-        const uint32_t mn_lo = u1 & k1;
-        const uint32_t sc_hi = (u2 & k2) | (((u0 >> 6) & k3) << 4);
-        const uint32_t sc_lo = u0 & k1;
+        uint32_t mn_hi = ((u2 >> 4) & k2) | (((u1 >> 6) & k3) << 4);
+        uint32_t mn_lo = u1 & k1;
+        uint32_t sc_hi = (u2 & k2) | (((u0 >> 6) & k3) << 4);
+        uint32_t sc_lo = u0 & k1;
+        // opaque to the optimizer, so that each scale below is a byte select
+        // of these words inside the multiply (no separate bit-field extract)
+        asm("" : "+v"(sc_lo), "+v"(sc_hi), "+v"(mn_lo), "+v"(mn_hi));
         int sc[8];
 #pragma unroll
         for (int j = 0; j < 4; ++j) { sc[j] = (sc_lo >> (8 * j)) & 0xff; sc[4 + j] = (sc_hi >> (8 * j)) & 0xff; }
@@ -126,22 +155,21 @@ QWM_DEV void q4k_dot8(float (&out)[MAXP], const XBlk (&W)[NB], const uint32_t * 
 #pragma unroll
         for (int i = 0; i < MAXP; ++i) {
             if (i < n) {
-                const uint32_t * xb = sx + (i * NB + b) * XS;
+                const uint32_t * xb = xt[i] + b * XS;
                 const uint4 x0 = *reinterpret_cast<const uint4 *>(xb + 8 * m);
                 const uint4 x1 = *reinterpret_cast<const uint4 *>(xb + 8 * m + 4);
                 const float yd = __uint_as_float(xb[64]);
                 const int qa = (int)xb[65 + 2 * l], qb = (int)xb[66 + 2 * l];
-                int s = 0;
-                s += sc[0] * dot4(wl[0], x0.x, 0);
-                s += sc[1] * dot4(wh[0], x0.y, 0);
-                s += sc[2] * dot4(wl[1], x0.z, 0);
-                s += sc[3] * dot4(wh[1], x0.w, 0);
-                s += sc[4] * dot4(wl[2], x1.x, 0);
-                s += sc[5] * dot4(wh[2], x1.y, 0);
-                s += sc[6] * dot4(wl[3], x1.z, 0);
-                s += sc[7] * dot4(wh[3], x1.w, 0);
+                int s = __mul24(sc[0], dot4(wl[0], x0.x, 0));
+                s += __mul24(sc[1], dot4(wh[0], x0.y, 0));
+                s += __mul24(sc[2], dot4(wl[1], x0.z, 0));
+                s += __mul24(sc[3], dot4(wh[1], x0.w, 0));
+                s += __mul24(sc[4], dot4(wl[2], x1.x, 0));
+                s += __mul24(sc[5], dot4(wh[2], x1.y, 0));
+                s += __mul24(sc[6], dot4(wl[3], x1.z, 0));
+                s += __mul24(sc[7], dot4(wh[3], x1.w, 0));
                 acc[i] = __builtin_fmaf(yd * dw, (float)s, acc[i]);
-                const int prod = mnA * qa + mnB * qb;
+                const int prod = __mul24(mnA, qa) + __mul24(mnB, qb);
                 accm[i] = __builtin_fmaf(-yd * dmw, (float)prod, accm[i]);
             }
         }
@@ -160,6 +188,26 @@ QWM_DEV void q4k_dot8(float (&out)[MAXP], const XBlk (&W)[NB], const uint32_t * 
             out[i] = 0.f;
         }
     }
+}
+
+// q4k_dot8_off with the common token counts (1 and 2, most expert units of a
+// verify batch) as branch-free instances.
+template <int NB, int MAXP>
+QWM_DEV void q4k_dot8_auto(float (&out)[MAXP], const XBlk (&W)[NB], const uint32_t * sx, const int (&off)[MAXP], int n_,
+                           int m) {
+    const int n = __builtin_amdgcn_readfirstlane(n_);
+    if (n == 1) q4k_dot8_off<NB, MAXP, 1>(out, W, sx, off, 1, m);
+    else if (MAXP >= 2 && n == 2) q4k_dot8_off<NB, MAXP, (MAXP >= 2 ? 2 : 1)>(out, W, sx, off, 2, m);
+    else q4k_dot8_off<NB, MAXP>(out, W, sx, off, n, m);
+}
+
+// The same with the activation rows packed at sx + i * NB * XS.
+template <int NB, int MAXP>
+QWM_DEV void q4k_dot8(float (&out)[MAXP], const XBlk (&W)[NB], const uint32_t * sx, int n, int m) {
+    int off[MAXP];
+#pragma unroll
+    for (int i = 0; i < MAXP; ++i) off[i] = i * NB * XS;
+    q4k_dot8_auto<NB, MAXP>(out, W, sx, off, n, m);
 }
 
 }  // namespace qwm
@@ -287,21 +335,21 @@ QWM_DEV void q6k_dot8(float (&out)[MAXP], const uint8_t * row, const uint32_t * 
                 const uint4 x1 = *reinterpret_cast<const uint4 *>(xb + 8 * m + 4);
                 const float yd = __uint_as_float(xb[64]);
                 int isum = 0;
-                isum += scc[0] * dot4(q6[0], x0.x, 0);
-                isum += scc[1] * dot4(q6[1], x0.y, 0);
-                isum += scc[2] * dot4(q6[2], x0.z, 0);
-                isum += scc[3] * dot4(q6[3], x0.w, 0);
-                isum += scc[4] * dot4(q6[4], x1.x, 0);
-                isum += scc[5] * dot4(q6[5], x1.y, 0);
-                isum += scc[6] * dot4(q6[6], x1.z, 0);
-                isum += scc[7] * dot4(q6[7], x1.w, 0);
+                isum += __mul24(scc[0], dot4(q6[0], x0.x, 0));
+                isum += __mul24(scc[1], dot4(q6[1], x0.y, 0));
+                isum += __mul24(scc[2], dot4(q6[2], x0.z, 0));
+                isum += __mul24(scc[3], dot4(q6[3], x0.w, 0));
+                isum += __mul24(scc[4], dot4(q6[4], x1.x, 0));
+                isum += __mul24(scc[5], dot4(q6[5], x1.y, 0));
+                isum += __mul24(scc[6], dot4(q6[6], x1.z, 0));
+                isum += __mul24(scc[7], dot4(q6[7], x1.w, 0));
                 int bA = 0, bB = 0;
 #pragma unroll
                 for (int mm = 0; mm < 4; ++mm) {
                     bA = dot4(xb[8 * mm + m], 0x01010101u, bA);
                     bB = dot4(xb[8 * (mm + 4) + m], 0x01010101u, bB);
                 }
-                isum -= 32 * (bA * sA + bB * sB);
+                isum -= 32 * (__mul24(bA, sA) + __mul24(bB, sB));
                 acc[i] = __builtin_fmaf(yd * dw, (float)isum, acc[i]);
             }
         }
@@ -367,18 +415,18 @@ QWM_DEV void q5k_dot8(float (&out)[MAXP], const uint8_t * row, const uint32_t * 
                 const uint4 x1 = *reinterpret_cast<const uint4 *>(xb + 8 * m + 4);
                 const float yd = __uint_as_float(xb[64]);
                 int s = 0;
-                s += sc[0] * dot4(wl[0], x0.x, 0);
-                s += sc[1] * dot4(wh[0], x0.y, 0);
-                s += sc[2] * dot4(wl[1], x0.z, 0);
-                s += sc[3] * dot4(wh[1], x0.w, 0);
-                s += sc[4] * dot4(wl[2], x1.x, 0);
-                s += sc[5] * dot4(wh[2], x1.y, 0);
-                s += sc[6] * dot4(wl[3], x1.z, 0);
-                s += sc[7] * dot4(wh[3], x1.w, 0);
+                s += __mul24(sc[0], dot4(wl[0], x0.x, 0));
+                s += __mul24(sc[1], dot4(wh[0], x0.y, 0));
+                s += __mul24(sc[2], dot4(wl[1], x0.z, 0));
+                s += __mul24(sc[3], dot4(wh[1], x0.w, 0));
+                s += __mul24(sc[4], dot4(wl[2], x1.x, 0));
+                s += __mul24(sc[5], dot4(wh[2], x1.y, 0));
+                s += __mul24(sc[6], dot4(wl[3], x1.z, 0));
+                s += __mul24(sc[7], dot4(wh[3], x1.w, 0));
                 acc[i] = __builtin_fmaf(yd * dw, (float)s, acc[i]);
                 int ms = 0;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) ms += mn[j] * (int)xb[65 + j];
+                for (int j = 0; j < 8; ++j) ms += __mul24(mn[j], (int)xb[65 + j]);
                 summs[i] = __builtin_fmaf(-yd * dmw, (float)ms, summs[i]);
             }
         }

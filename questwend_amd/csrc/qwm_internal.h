@@ -100,7 +100,7 @@ int launch_prefill(const MmidArgs & a, uint8_t * ws, hipStream_t s);
 struct StepPlan {
     MoePlan moe;
     int64_t V;
-    size_t v_counter, v_pv, v_pi, lg, xq_x, bar, flags, gu_done, tiles_done, total;
+    size_t v_counter, v_pv, v_pi, lg, xq_x, bar, gu_done, tiles_done, total;
 };
 bool step_plan(const qwm_moe_layer * L, const qwm_tensor * lm_head, int64_t T, StepPlan & p, std::string & why);
 struct StepCall {

@@ -246,7 +246,7 @@ __global__ void __launch_bounds__(256) k_pf_gemm(PfArgs a) {
             const int c = 4 * kq + r;
             int mins = 0;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) mins += mn[j] * (int)s_q8s[c][b * 8 + j];
+            for (int j = 0; j < 8; ++j) mins += __mul24(mn[j], (int)s_q8s[c][b * 8 + j]);
             const float dx = s_d[b][c];
             facc[r] = __builtin_fmaf(dx * dw, (float)acc[r], facc[r]);
             facc_m[r] = __builtin_fmaf(-dx * dmw, (float)mins, facc_m[r]);

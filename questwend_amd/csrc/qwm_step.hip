@@ -8,7 +8,8 @@
 // exactly the co-resident workgroups (sized by the occupancy query) walks the
 // phases:
 //
-//   P0  router rows (CPU summation order), Q8_K of x            -> barrier
+//   P0  router rows (CPU summation order) and Q8_K of x, counted per
+//       workgroup                                                -> count
 //   P1  every workgroup repeats the selection for all tokens from the logits
 //       (softmax, top-k, weights, expert union, slots) in registers and LDS:
 //       no hand-off and no serial tail
@@ -23,18 +24,18 @@
 //
 // Data that crosses workgroups inside the launch is written with agent-scope
 // stores (write-through, coherent across the XCDs' L2s) into buffers that no
-// workgroup reads before the barrier or ticket that publishes them.  Every
+// workgroup reads before the counter or ticket that publishes them.  Every
 // 128-byte line of such a buffer has a single writing workgroup (the router
-// logits, the Q8_K scales and the combine tiles are padded or aligned for
-// that), so a consumer's ordinary L2-cached load can only find that writer's
-// fresh line or none; the one multi-writer buffer (SwiGLU activations) is read
-// with agent-scope loads.  The grid barrier after P0: group arrival counters,
-// and a flag line per workgroup that the last arriver sets, so no line is
-// polled by more than one workgroup.  P2 -> P3 and P3 -> P4 are completion
-// counters instead (per unit, and for the combined tiles), so no workgroup
-// waits for work it does not read.  Every wait is bounded (a timeout sets an
-// error word and the result reports a = -1 instead of hanging); the last
-// workgroup of the launch re-arms the counters.
+// logits and the combine tiles are padded or aligned for that), so a
+// consumer's ordinary L2-cached load can only find that writer's fresh line
+// or none; the one multi-writer buffer (SwiGLU activations) is read with
+// agent-scope loads.  Every hand-off is a completion counter: P0 -> P1 counts
+// the workgroups holding router rows or x blocks (the others do not take
+// part, so a workgroup that starts late delays nobody), P2 -> P3 counts per unit and
+// P3 -> P4 the combined tiles, so no workgroup waits for work it does not
+// read.  Every wait is bounded (a timeout sets an error word and the result
+// reports a = -1 instead of hanging); the last workgroup of the launch
+// re-arms the counters.
 #include "qwm_step_kernel.h"
 
 // ======================================================================
@@ -66,8 +67,7 @@ bool step_plan(const qwm_moe_layer * L, const qwm_tensor * lm_head, int64_t T, S
     p.v_pi = take(sizeof(int32_t) * MAX_STEP_WG * T);
     p.lg = take(sizeof(float) * 32 * (p.moe.E + 1));
     p.xq_x = take(sizeof(uint32_t) * XSP * T * SNB);
-    p.bar = take(512 + 128 * BAR_GROUPS);     // top counter, epoch, error word, group counters at 512
-    p.flags = take(sizeof(uint32_t) * 32 * MAX_STEP_WG);
+    p.bar = take(512);                        // P0 workgroup count at 0, error word at 256
     p.gu_done = take(128 * (MAX_PAIRS + 1));
     p.tiles_done = take(128);
     p.total = o;
@@ -91,13 +91,11 @@ int launch_step(const StepCall & c, const StepPlan & p, uint8_t * ws, hipStream_
     a.resid = c.resid; a.out = c.out;
     a.ids_out = c.ids_out; a.ids_ld = c.ids_ld; a.w_out = c.w_out; a.w_ld = c.w_ld;
     a.lg = reinterpret_cast<float *>(ws + p.lg);
-    a.xq_x = reinterpret_cast<uint32_t *>(ws + p.xq_x);
     a.act = reinterpret_cast<float *>(ws + m.act); a.act_sh = reinterpret_cast<float *>(ws + m.act_sh);
     a.ex = reinterpret_cast<float *>(ws + m.ex); a.ex_sh = reinterpret_cast<float *>(ws + m.ex_sh);
-    a.bar = reinterpret_cast<uint32_t *>(ws + p.bar);
-    a.epoch = reinterpret_cast<uint32_t *>(ws + p.bar + 128);
+    a.xq_x = reinterpret_cast<uint32_t *>(ws + p.xq_x);
+    a.rows_done = reinterpret_cast<int32_t *>(ws + p.bar);
     a.err = reinterpret_cast<int32_t *>(ws + p.bar + 256);
-    a.flags = reinterpret_cast<uint32_t *>(ws + p.flags);
     a.tile_counters = reinterpret_cast<int32_t *>(ws + m.tile_counters);
     a.gu_done = reinterpret_cast<int32_t *>(ws + p.gu_done);
     a.tiles_done = reinterpret_cast<int32_t *>(ws + p.tiles_done);

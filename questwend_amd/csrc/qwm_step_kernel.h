@@ -33,9 +33,9 @@ struct StepArgs {
     const float * resid; float * out;                                           // [T][H]
     int32_t * ids_out; int64_t ids_ld; float * w_out; int64_t w_ld;
     float * lg;                                                                 // [E + 1][32]: logits of row e (row E: shared gate)
-    uint32_t * xq_x;                                                            // Q8_K of x, exact-dot layout, XSP per block
     float * act; float * act_sh; float * ex; float * ex_sh;
-    uint32_t * bar; uint32_t * epoch; uint32_t * flags;                         // flags: one 32-word line per workgroup
+    int32_t * rows_done;                                                        // P0 workgroups finished
+    uint32_t * xq_x;                                                            // Q8_K of x, exact layout, XSP dwords per block
     int32_t * tile_counters; int32_t * err;
     int d6;                                                                     // down slabs are Q6_K
     int32_t * gu_done;                                                          // per unit, one 32-word line each
@@ -54,65 +54,36 @@ struct StepShared {
     int32_t slot_of[3 * STEP_MAX_E];   // this layer's slot tables, [role][expert]
 };
 
-// Grid barrier number `i` (1, 2, 3) of launch `epoch`.  Arrivals count in
-// BAR_GROUPS group counters (workgroup g in group g % BAR_GROUPS, one line
-// each); the last arrival of a group re-arms its counter and counts the group
-// at the top counter.  The last group's last workgroup re-arms the top counter
-// and then sets every workgroup's flag line to epoch * 4 + i; the others poll
-// their own line.
-constexpr int BAR_GROUPS = 16;
-
-QWM_DEV void grid_barrier(const StepArgs & a, int i, int G, uint32_t epoch) {
-    __shared__ int s_rel;
-    __builtin_amdgcn_s_waitcnt(0);               // this wave's agent-scope writes have completed
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const int grp = blockIdx.x % BAR_GROUPS;
-        const int groups = G < BAR_GROUPS ? G : BAR_GROUPS;
-        const uint32_t in_grp = (uint32_t)((G - 1 - grp) / BAR_GROUPS + 1);
-        uint32_t * gc = a.bar + 128 + 32 * grp;
-        bool rel = false;
-        if (__hip_atomic_fetch_add(gc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == in_grp - 1) {
-            st_agent(gc, 0u);
-            __builtin_amdgcn_s_waitcnt(0);           // re-armed before the group counts as arrived
-            rel = __hip_atomic_fetch_add(a.bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)groups - 1;
-        }
-        s_rel = rel;
-    }
-    __syncthreads();
-    const uint32_t v = epoch * 4u + (uint32_t)i;
-    if (s_rel) {
-        if (threadIdx.x == 0) st_agent(a.bar, 0u);
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        for (int q = threadIdx.x; q < G * 32; q += 256) st_agent(a.flags + q, v);   // whole lines
-    } else if (threadIdx.x == 0) {
-        const uint32_t * f = a.flags + (size_t)blockIdx.x * 32;
-        uint32_t spins = 0;
-        while (ld_agent(f) != v) {
-            __builtin_amdgcn_s_sleep(1);
-            if (++spins > SPIN_LIMIT) { st_agent(a.err, 1); break; }
-        }
-    }
-    __syncthreads();
-}
-
 // ---------------------------------------------------------------- P0 ----
-// Router rows e = g, g + G, ... (row E: the shared-expert gate row) and the
-// Q8_K blocks of x (waves counted from the end of the grid).
+// Router rows e = g, g + G, ... (row E: the shared-expert gate row), and the
+// Q8_K of x: NT * SNB / 4 quantizer workgroups, one 256-block per wave, into
+// the workspace (the workgroups after the router rows when the grid has them,
+// else the first router workgroups).  Every workgroup with a share counts
+// once in rows_done when its writes are out; step_p0_parts() is the total.
+template <int NT>
+QWM_DEV int step_p0_first_quantizer(int rows, int G) {
+    return rows + NT * SNB / 4 <= G ? rows : 0;
+}
+template <int NT>
+QWM_DEV int step_p0_parts(int rows, int G) {
+    const int q0 = step_p0_first_quantizer<NT>(rows, G);
+    return (rows < G ? rows : G) + (q0 ? NT * SNB / 4 : 0);
+}
 template <int NT>
 QWM_DEV void step_router(const StepArgs & a, int g, int G) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int E = a.E;
-    {
-        const int gw = (G - 1 - g) * 4 + wave;
-        for (int jb = gw; jb < NT * SNB; jb += 4 * G) {
-            const int t = jb / SNB, b = jb % SNB;
-            quantize_block_q8K_x<false, true>(a.x + (size_t)t * SH + b * QK_K, a.xq_x + (size_t)(t * SNB + b) * XSP, lane);
-        }
-    }
     const int rows = E + (a.sgi ? 1 : 0);
-    if (g >= rows) return;                       // uniform per workgroup; no barrier follows inside
+    const int q0 = step_p0_first_quantizer<NT>(rows, G);
+    const bool quantizer = g >= q0 && g < q0 + NT * SNB / 4;
+    if (quantizer) {
+        const int jb = (g - q0) * 4 + wave;                   // < NT * SNB
+        quantize_block_q8K_x<false, true>(a.x + (size_t)(jb / SNB) * SH + (jb % SNB) * QK_K, a.xq_x + (size_t)jb * XSP, lane);
+    }
+    if (g >= rows) {                             // uniform per workgroup
+        if (quantizer) signal_count(a.rows_done);
+        return;
+    }
     // ggml_vec_dot_f32's AVX-512 order (vec.cpp:11-135), which ggml-CPU runs
     // per (row, token) at every token count (ggml-cpu.c:1165-1244; llamafile
     // is not built), one token per wave pass
@@ -136,6 +107,7 @@ QWM_DEV void step_router(const StepArgs & a, int g, int G) {
             if (lane == 0) st_agent(a.lg + (size_t)e * 32 + t, (a.rm && !sh_row) ? acc + a.rm[(size_t)t * E + e] : acc);
         }
     }
+    signal_count(a.rows_done);
 }
 
 // ---------------------------------------------------------------- P1 ----
@@ -289,14 +261,13 @@ QWM_DEV void step_select(const StepArgs & a, int g, StepShared & S, uint8_t * sm
 constexpr int GU_ROWS = 32;
 
 template <int MAXP>
-QWM_DEV void step_gateup(const StepArgs & a, int g, int G, const StepShared & S, uint8_t * smem) {
+QWM_DEV void step_gateup(const StepArgs & a, int g, int G, const StepShared & S, const uint32_t * s_xq) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int m = lane & 7, rsub = lane >> 3;
-    uint32_t * s_x = reinterpret_cast<uint32_t *>(smem);          // [MAXP][SNB][XS]
     const int nb_r = (a.N + GU_ROWS - 1) / GU_ROWS, nb_s = a.shared ? (a.N_sh + GU_ROWS - 1) / GU_ROWS : 0;
     const int items = S.nu * nb_r + nb_s;
     constexpr size_t row_bytes = (size_t)SNB * 144;
-    constexpr int Q4 = SNB * XS / 4;                               // uint4 per token in LDS
+    (void)tid;
     for (int item = g; item < items; item += G) {
         const bool shared = item >= S.nu * nb_r;
         const int u = shared ? S.nu : item / nb_r;
@@ -314,16 +285,15 @@ QWM_DEV void step_gateup(const StepArgs & a, int g, int G, const StepShared & S,
             load_xblk(Gw[b], gbase + (size_t)rc * row_bytes + b * 144, m);
             load_xblk(Uw[b], ubase + (size_t)rc * row_bytes + b * 144, m);
         }
-        for (int q = tid; q < n * Q4; q += 256) {
-            const int i = q / Q4, o = q % Q4, b = o / (XS / 4), w4 = o % (XS / 4);
-            const int tok = shared ? U_.pair[i] : U_.pair[i] / a.k;
-            reinterpret_cast<uint4 *>(s_x)[q] =
-                reinterpret_cast<const uint4 *>(a.xq_x + (size_t)(tok * SNB + b) * XSP)[w4];
+        int off[MAXP];                                             // the unit's tokens in s_xq
+#pragma unroll
+        for (int i = 0; i < MAXP; ++i) {
+            const int pi = i < n ? U_.pair[i] : 0;
+            off[i] = (shared ? pi : pi / a.k) * (SNB * XS);
         }
-        __syncthreads();
         float gs[MAXP], us[MAXP];
-        q4k_dot8<SNB, MAXP>(gs, Gw, s_x, n, m);
-        q4k_dot8<SNB, MAXP>(us, Uw, s_x, n, m);
+        q4k_dot8_auto<SNB, MAXP>(gs, Gw, s_xq, off, n, m);
+        q4k_dot8_auto<SNB, MAXP>(us, Uw, s_xq, off, n, m);
         if (m == 0 && r < rows) {
 #pragma unroll
             for (int i = 0; i < MAXP; ++i)
@@ -333,7 +303,7 @@ QWM_DEV void step_gateup(const StepArgs & a, int g, int G, const StepShared & S,
                     else st_agent(a.act + (size_t)U_.pair[i] * rows + r, v);
                 }
         }
-        signal_count(a.gu_done + 32 * u);        // also orders s_x's reuse by the next item
+        signal_count(a.gu_done + 32 * u);
     }
 }
 
@@ -483,15 +453,11 @@ template <int NT, int NB_D>
 __global__ void __launch_bounds__(256) k_step(StepArgs a) {
     constexpr int MAXP = NT <= 1 ? 1 : NT <= 2 ? 2 : NT <= 4 ? 4 : 8;
     constexpr size_t down_bytes = (size_t)MAXP * (NB_D * XS * 4 + DN_TR * 4);
-    constexpr size_t gateup_bytes = (size_t)MAXP * SNB * XS * 4;
-    constexpr size_t smem_bytes = cmax(cmax(cmax(STEP_SELECT_LDS, down_bytes), gateup_bytes), VhSmem<NT>::bytes);
+    constexpr size_t smem_bytes = cmax(cmax(STEP_SELECT_LDS, down_bytes), VhSmem<NT>::bytes);
     __shared__ __align__(16) uint8_t smem[smem_bytes];
+    __shared__ __align__(16) uint32_t s_xq[NT * SNB * XS];     // Q8_K of every token's x, exact layout [t][b]
     __shared__ StepShared S;
-    __shared__ uint32_t s_epoch;
     const int g = blockIdx.x, G = gridDim.x;
-    if (threadIdx.x == 0) s_epoch = ld_agent(a.epoch);   // constant until the last workgroup of this launch
-    __syncthreads();
-    const uint32_t epoch = s_epoch;
 
     // the layer's slot tables, requested first and kept in LDS for the selection
     constexpr int SLQ = 3 * STEP_MAX_E / 256;
@@ -504,22 +470,35 @@ __global__ void __launch_bounds__(256) k_step(StepArgs a) {
     step_router<NT>(a, g, G);
 #pragma unroll
     for (int q = 0; q < SLQ; ++q) S.slot_of[threadIdx.x + 256 * q] = sl[q];
-    grid_barrier(a, 1, G, epoch);
+    wait_count(a.rows_done, step_p0_parts<NT>(a.E + (a.sgi ? 1 : 0), G), a.err, SPIN_LIMIT);   // ends with a workgroup barrier
+    // Q8_K of x into LDS for the gate/up GEMVs: requested now, stored after
+    // the selection, whose round trip and arithmetic hide the loads
+    constexpr int XW = (NT * SNB * XS + 255) / 256;            // dwords per thread
+    uint32_t xw[XW];
+#pragma unroll
+    for (int i = 0; i < XW; ++i) {
+        const int q = threadIdx.x + 256 * i;
+        xw[i] = q < NT * SNB * XS ? a.xq_x[(size_t)(q / XS) * XSP + q % XS] : 0u;
+    }
     if (a.E <= 128) step_select<NT, 2>(a, g, S, smem);
     else step_select<NT, STEP_MAX_E / 64>(a, g, S, smem);
-    step_gateup<MAXP>(a, g, G, S, smem);
+#pragma unroll
+    for (int i = 0; i < XW; ++i) {
+        const int q = threadIdx.x + 256 * i;
+        if (q < NT * SNB * XS) s_xq[q] = xw[i];
+    }
+    __syncthreads();
+    step_gateup<MAXP>(a, g, G, S, s_xq);
     step_down<NT, NB_D, MAXP>(a, g, G, S, smem);
     __syncthreads();
     constexpr int PF = NT <= 4 ? 2 : 1;
     if (verify_body<NT, SH / 512, PF, VH_BEFORE_WAIT>(a.v, g, G, smem, a.tiles_done, SH / DN_TR, a.err, SPIN_LIMIT)) {
-        // every workgroup has read the epoch, passed the barrier and all waits:
-        // re-arm the completion counters, then the epoch
+        // every workgroup has passed all its waits: re-arm the completion counters
         for (int q = threadIdx.x; q < MAX_PAIRS + 1; q += 256) st_agent(a.gu_done + 32 * q, 0);
-        if (threadIdx.x == 0) st_agent(a.tiles_done, 0);
+        if (threadIdx.x == 0) { st_agent(a.tiles_done, 0); st_agent(a.rows_done, 0); }
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         if (threadIdx.x == 0) {
-            st_agent(a.epoch, epoch + 1u);
             if (ld_agent(a.err)) {
                 a.v.result[NT] = -1;
                 a.v.result[NT + 1] = -1;

@@ -100,14 +100,17 @@ typedef struct qwm_moe_layer {
     int32_t n_expert_used;      /* k */
     int32_t norm_weights;       /* hparams.expert_weights_norm */
     float   weights_scale;      /* hparams.expert_weights_scale (0 or 1: none) */
+    int32_t gating_func;        /* hparams.expert_gating_func: 2 = sigmoid; 0 or 1 = soft_max */
+    qwm_tensor exp_probs_b;     /* optional f32 [E] ranking bias (blk.N.exp_probs_b.bias); data NULL: none */
 } qwm_moe_layer;
 
 /* Router (core/runtime.cpp:2693-2734 after the router mul_mat 3785-3798):
- *   logits = router . x (+ rm);  probs = soft_max(logits);
- *   ids = top-k(probs) [k, T];   w = probs[ids] (/ clamp(sum, 6.1035e-5) if norm)
+ *   logits = router . x (+ rm);  probs = soft_max(logits) (gating_func 2: sigmoid);
+ *   rank = probs (+ exp_probs_b, then + rm again);
+ *   ids = top-k(rank) [k, T];    w = probs[ids] (/ clamp(sum, 6.1035e-5) if norm)
  * x: f32 [H, T]; rm: optional f32 [E, T] added to the logits; ids_out: i32
  * [k, T]; w_out: f32 [k, T].  The top-k keeps the lower expert index on exact
- * probability ties (std::sort leaves their order unspecified).  T <= 8.
+ * rank ties (std::sort leaves their order unspecified).  T <= 8.
  * Activation tensors (x, out, resid) must be 16-byte aligned. */
 size_t qwm_moe_workspace_size(const qwm_moe_layer * layer, int64_t T);
 int qwm_moe_route(const qwm_moe_layer * layer, const qwm_tensor * x, const qwm_tensor * rm,

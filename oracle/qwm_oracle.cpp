@@ -753,27 +753,42 @@ QWO_API int qwo_mul_mat(int type, const void * w, int64_t K, int64_t N, const fl
 
 // core/runtime.cpp:2693-2734 (route_experts) after the router mul_mat
 // (build_router 3785-3798 / build_segB router 4515-4519):
-//   logits = W_r . x (+ rm);  probs = soft_max(logits);  sel = top-k(probs);
-//   w = probs[sel];  if norm: w /= clamp(sum(w), 6.103515625e-5, inf);
-//   if scale not in {0, 1}: w *= scale.
+//   logits = W_r . x (+ rm);
+//   probs = soft_max(logits), or sigmoid(logits) when gating_func == 2
+//     (hparams.gating_sigmoid(), core/model.h:160; ggml-cpu unary-ops.cpp:31-33:
+//     1 / (1 + expf(-x)) with the C library's expf);
+//   rank = probs; with exp_probs_b: rank = probs + bias, then + rm again;
+//   sel = argsort_top_k(rank);  w = probs[sel];
+//   if norm: w /= clamp(sum(w), 6.103515625e-5, inf); if scale not in {0, 1}: w *= scale.
 // Outputs: ids [T][k] (token-major, k order), weights [T][k]; optional
-// logits/probs [T][E] and the rank margin (probs[k-1] - probs[k]) per token.
-QWO_API int qwo_route(int64_t E, int64_t H, int64_t T, const float * Wr, const float * x, const float * rm,
-                      int k, int norm, float scale, int32_t * ids, float * weights,
-                      float * logits_out, float * probs_out, float * margin_out) {
+// logits/probs [T][E] and the rank margin (rank[k-1] - rank[k]) per token.
+QWO_API int qwo_route_ex(int64_t E, int64_t H, int64_t T, const float * Wr, const float * x, const float * rm,
+                         const float * bias, int gating_func, int k, int norm, float scale, int32_t * ids,
+                         float * weights, float * logits_out, float * probs_out, float * margin_out) {
     try {
-        std::vector<float> logits((size_t)(E * T)), probs((size_t)(E * T));
+        if (k < 1 || k > E || k > 512) return -1;
+        std::vector<float> logits((size_t)(E * T)), probs((size_t)(E * T)), rank((size_t)E);
         mul_mat(T_F32, Wr, H, E, x, T, logits.data());
         for (int64_t t = 0; t < T; ++t) {
             float * lt = logits.data() + t * E;
             if (rm) for (int64_t e = 0; e < E; ++e) lt[e] = lt[e] + rm[t * E + e];
             float * pt = probs.data() + t * E;
-            soft_max_row((int)E, lt, pt);
+            if (gating_func == 2)
+                for (int64_t e = 0; e < E; ++e) pt[e] = 1.0f / (1.0f + expf(-lt[e]));
+            else
+                soft_max_row((int)E, lt, pt);
+            for (int64_t e = 0; e < E; ++e) {
+                rank[e] = pt[e];
+                if (bias) {
+                    rank[e] = rank[e] + bias[e];
+                    if (rm) rank[e] = rank[e] + rm[t * E + e];
+                }
+            }
             std::vector<int32_t> idx((size_t)E);
-            argsort_desc((int)E, pt, idx.data());
+            argsort_desc((int)E, rank.data(), idx.data());
             float w[512];
             for (int j = 0; j < k; ++j) { ids[t * k + j] = idx[j]; w[j] = pt[idx[j]]; }
-            if (margin_out) margin_out[t] = (k < E) ? pt[idx[k - 1]] - pt[idx[k]] : INFINITY;
+            if (margin_out) margin_out[t] = (k < E) ? rank[idx[k - 1]] - rank[idx[k]] : INFINITY;
             if (norm) {
                 double s = 0.0;
                 for (int j = 0; j < k; ++j) s += (double)w[j];
@@ -790,6 +805,15 @@ QWO_API int qwo_route(int64_t E, int64_t H, int64_t T, const float * Wr, const f
         return 0;
     } catch (...) { return -1; }
 }
+QWO_API int qwo_route(int64_t E, int64_t H, int64_t T, const float * Wr, const float * x, const float * rm,
+                      int k, int norm, float scale, int32_t * ids, float * weights,
+                      float * logits_out, float * probs_out, float * margin_out) {
+    return qwo_route_ex(E, H, T, Wr, x, rm, nullptr, 1, k, norm, scale, ids, weights, logits_out, probs_out, margin_out);
+}
+
+// The C library's expf and the sigmoid built on it (ggml-cpu unary-ops.cpp:31-33).
+QWO_API float qwo_expf(float x) { return expf(x); }
+QWO_API float qwo_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
 
 // One MoE FFN block over the slot pools: core/runtime.cpp:3801-3830
 // (build_moe_cached, T=1) and 4534-4572 (build_segB, T>1).

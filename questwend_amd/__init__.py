@@ -48,7 +48,7 @@ class MoeLayer(ctypes.Structure):
     _fields_ = [("gate_pool", QwmTensor), ("up_pool", QwmTensor), ("down_pool", QwmTensor),
                 ("router", QwmTensor), ("sh_gate", QwmTensor), ("sh_up", QwmTensor), ("sh_down", QwmTensor),
                 ("sh_gate_inp", QwmTensor), ("n_expert_used", ctypes.c_int32), ("norm_weights", ctypes.c_int32),
-                ("weights_scale", ctypes.c_float)]
+                ("weights_scale", ctypes.c_float), ("gating_func", ctypes.c_int32), ("exp_probs_b", QwmTensor)]
 
 
 class PoolDesc(ctypes.Structure):

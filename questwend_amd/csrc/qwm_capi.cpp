@@ -253,7 +253,13 @@ static int check_layer(const qwm_moe_layer * L, int64_t T, MoePlan & p) {
         if (L->sh_gate_inp.data && (L->sh_gate_inp.type != T_F32 || L->sh_gate_inp.ne[0] != L->router.ne[0]))
             return fail(QWM_ERR_ARG, "moe: shared gate row must be f32 [H]");
     }
+    // core/model.cpp:751-756: expert_gating_func is 1 (soft_max) or 2 (sigmoid); 0 is taken as the default
+    if (L->gating_func != 0 && L->gating_func != 1 && L->gating_func != 2)
+        return fail(QWM_ERR_UNSUPPORTED, "moe: gating_func must be 1 (soft_max) or 2 (sigmoid)");
     if (!moe_plan(L, T, p, why)) return fail(QWM_ERR_UNSUPPORTED, "moe: " + why);
+    if (L->exp_probs_b.data && (L->exp_probs_b.type != T_F32 || L->exp_probs_b.ne[0] != p.E ||
+                                L->exp_probs_b.ne[1] != 1 || L->exp_probs_b.nb[0] != 4))
+        return fail(QWM_ERR_ARG, "moe: exp_probs_b must be f32 [E]");
     return QWM_OK;
 }
 
@@ -278,6 +284,8 @@ static int do_route(const qwm_moe_layer * L, const MoePlan & p, const qwm_tensor
     a.rm = rm ? (const float *)rm->data : nullptr;
     a.sh_gate_inp = (L->sh_gate.data && L->sh_gate_inp.data) ? (const float *)L->sh_gate_inp.data : nullptr;
     a.E = p.E; a.H = p.H; a.T = p.T; a.k = p.k; a.norm = L->norm_weights; a.scale = L->weights_scale;
+    a.sigm = L->gating_func == 2 ? 1 : 0;
+    a.bias = L->exp_probs_b.data ? (const float *)L->exp_probs_b.data : nullptr;
     a.slot_tables = tables; a.table_stride = stride; a.layer = layer_index;
     a.wtype = L->gate_pool.type;
     return launch_route(a, p, ws, ids_out, ids_ld, w_out, w_ld, s);

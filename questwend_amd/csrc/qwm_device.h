@@ -10,6 +10,8 @@
 #include <hip/hip_fp16.h>
 #include <stdint.h>
 
+#include "qwm_expf.h"
+
 #define QWM_DEV __device__ __forceinline__
 
 namespace qwm {

@@ -61,7 +61,8 @@ bool verify_plan(const qwm_tensor * lm_head, int64_t T, VerifyPlan & p, std::str
 struct RouteArgs {
     const float * W; const float * x; const float * rm;   // router [E][H], x [T][H], rm [T][E] or null
     const float * sh_gate_inp;                           // [H] or null
-    int64_t E, H, T, k; int norm; float scale;
+    int64_t E, H, T, k; int norm, sigm; float scale;
+    const float * bias;                                  // exp_probs_b [E] or null
     const int32_t * slot_tables; int64_t table_stride; int32_t layer;  // resident remap or null
     int32_t wtype;                                       // pool type: the activation format of x
 };

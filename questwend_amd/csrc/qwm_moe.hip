@@ -16,6 +16,7 @@
 #include "qwm_q4k.h"
 #include "qwm_q80.h"
 #include "qwm_exact.h"
+#include "qwm_select.h"
 
 namespace qwm {
 
@@ -25,7 +26,8 @@ namespace qwm {
 
 struct RouteKArgs {
     const float * W; const float * x; const float * rm; const float * sgi;
-    int E, H, T, k, norm; float scale;
+    int E, H, T, k, norm, sigm; float scale;
+    const float * bias;                              // exp_probs_b [E] or null
     int n_row_wg;                                    // workgroups holding router rows
     float * logits; float * sh_logit;                // hand-off to the last workgroup
     int32_t * ids_ws; float * w_ws;                  // [T][k]
@@ -53,13 +55,10 @@ constexpr int ROUTE_LDS_INTS = 3 * MAX_E + 3 * 512;
 //    token per wave, lane L = 16j + l accumulates over 64-wide steps, then
 //    (j0+j2, j1+j3, 0+1) and the 16-lane tree.  The shared-gate row likewise.
 //  * Q8_K of x (Q8_0 for Q8_0 pools), one 256-block per wave across the grid.
-//  * The last workgroup: per token (one wave each) soft_max (ggml-cpu/ops.cpp:
-//    5813-5920, vec.cpp:531 AVX-512: v_expf over 16-lane chunks, each chunk
-//    summed with the 16-lane tree into a double), top-k as k rounds of a wave
-//    maximum with ballots for the tie order (larger probability, then lower
-//    expert index), the weight sum in selection order (double), clamp
-//    6.103515625e-5, division and scale; then the expert union in
-//    first-occurrence order and, in resident mode, the slot ids.
+//  * The last workgroup: per token (one wave each) the selection of
+//    select_token (qwm_select.h: soft_max or sigmoid, the optional ranking
+//    bias, top-k, weights); then the expert union in first-occurrence order
+//    and, in resident mode, the slot ids.
 // R: probabilities per lane in the selection (E <= 64 R).
 template <int R>
 __global__ void __launch_bounds__(256) k_route(RouteKArgs a) {
@@ -131,73 +130,18 @@ __global__ void __launch_bounds__(256) k_route(RouteKArgs a) {
         }
     }
     const int nr = (E + 63) / 64;
-    const int nfull = E & ~15;
+    const SelectCfg sel{E, k, a.norm, a.sigm, a.scale, a.bias};
     for (int t = wave; t < T; t += 4) {
         const float * lt = a.logits + (size_t)t * E;
         float v[R];
-        float m = -__builtin_inff();
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            v[r] = -__builtin_inff();
-            const int i = 64 * r + lane;
-            if (r < nr && i < E) v[r] = ld_agent(lt + i);
-            m = fmaxf(m, v[r]);
-        }
-        m = wave_max(m);
-        double sum = 0.0;
-        float tailv = 0.f;
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            if (r < nr) {
-                const int i = 64 * r + lane;
-                float ev = 0.f;
-                if (i < nfull) ev = v_expf(v[r] - m);
-                else if (i < E) ev = expf(v[r] - m);          // scalar tail: libm expf on the CPU
-                const float cs = tree16_dpp(i < nfull ? ev : 0.f);
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    if (64 * r + 16 * q < nfull) sum += (double)readlane_f(cs, 16 * q);
-                if (r == (nfull >> 6)) tailv = ev;
-                v[r] = ev;
-            }
-        }
-        for (int i = nfull; i < E; ++i) sum += (double)readlane_f(tailv, i & 63);
-        const float sc = (float)(1.0 / sum);
-        // top-k: k rounds of the wave maximum; a tie goes to the lower index
-        // (the first r, then the first lane, holding the maximum).  Lane j
-        // keeps the j-th selection; the weight sum runs in selection order.
-        float cur[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const int i = 64 * r + lane;
-            cur[r] = (r < nr && i < E) ? v[r] * sc : -1.f;             // probabilities are >= 0
+            v[r] = (r < nr && i < E) ? ld_agent(lt + i) : -__builtin_inff();
         }
-        float myw = 0.f;
-        int myid = 0;
-        double wsum = 0.0;
-        for (int j = 0; j < k; ++j) {
-            float mx = cur[0];
-#pragma unroll
-            for (int r = 1; r < R; ++r) mx = fmaxf(mx, cur[r]);
-            mx = wave_max(mx);
-            int id = -1;
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const unsigned long long bal = __ballot(cur[r] == mx);
-                if (id < 0 && bal) id = 64 * r + (int)__builtin_ctzll(bal);
-            }
-            if (lane == j) { myw = mx; myid = id; }
-            wsum += (double)mx;
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-                if (64 * r + lane == id) cur[r] = -1.f;
-        }
-        if (a.norm) {
-            float ws = (float)wsum;
-            ws = fmaxf(fminf(ws, __builtin_inff()), 6.103515625e-5f);
-            myw = myw / ws;
-        }
-        if (a.scale != 0.0f && a.scale != 1.0f) myw = myw * a.scale;
+        int myid;
+        float myw;
+        select_token<R>(v, sel, a.rm ? a.rm + (size_t)t * E : nullptr, lane, myid, myw);
         if (lane < k) {
             s_ids[t * k + lane] = myid;
             a.ids_ws[t * k + lane] = myid;
@@ -205,7 +149,7 @@ __global__ void __launch_bounds__(256) k_route(RouteKArgs a) {
             if (a.ids_out) a.ids_out[(size_t)t * a.ids_ld + lane] = myid;
             if (a.w_out) a.w_out[(size_t)t * a.w_ld + lane] = myw;
         }
-        if (lane == 0 && a.sh_gate) a.sh_gate[t] = 1.f / (1.f + expf(-ld_agent(a.sh_logit + t)));   // unary-ops.cpp:31
+        if (lane == 0 && a.sh_gate) a.sh_gate[t] = libm_sigmoid(ld_agent(a.sh_logit + t));   // unary-ops.cpp:31
     }
     __syncthreads();
 
@@ -364,7 +308,7 @@ __global__ void __launch_bounds__(256) k_gateup_x(GateUpArgs a) {
 #pragma unroll
         for (int i = 0; i < MAXP; ++i)
             if (i < n) {
-                const float v = (r < rows - (rows & 15)) ? v_silu(g[i]) * up[i] : g[i] / (1.0f + expf(-g[i])) * up[i];
+                const float v = (r < rows - (rows & 15)) ? v_silu(g[i]) * up[i] : g[i] / (1.0f + libm_expf(-g[i])) * up[i];
                 if (shared) a.act_sh[(size_t)U.pair[i] * rows + r] = v;
                 else a.act[(size_t)U.pair[i] * rows + r] = v;
             }
@@ -409,7 +353,7 @@ __global__ void __launch_bounds__(256) k_gateup_x5(GateUpArgs a) {
 #pragma unroll
         for (int i = 0; i < MAXP; ++i)
             if (i < n) {
-                const float v = (r < rows - (rows & 15)) ? v_silu(g[i]) * up[i] : g[i] / (1.0f + expf(-g[i])) * up[i];
+                const float v = (r < rows - (rows & 15)) ? v_silu(g[i]) * up[i] : g[i] / (1.0f + libm_expf(-g[i])) * up[i];
                 if (shared) a.act_sh[(size_t)U.pair[i] * rows + r] = v;
                 else a.act[(size_t)U.pair[i] * rows + r] = v;
             }
@@ -455,7 +399,7 @@ __global__ void __launch_bounds__(256) k_gateup_x80(GateUpArgs a) {
 #pragma unroll
         for (int i = 0; i < MAXP; ++i)
             if (i < n) {
-                const float v = (r < rows - (rows & 15)) ? v_silu(g[i]) * up[i] : g[i] / (1.0f + expf(-g[i])) * up[i];
+                const float v = (r < rows - (rows & 15)) ? v_silu(g[i]) * up[i] : g[i] / (1.0f + libm_expf(-g[i])) * up[i];
                 if (shared) a.act_sh[(size_t)U.pair[i] * rows + r] = v;
                 else a.act[(size_t)U.pair[i] * rows + r] = v;
             }
@@ -751,6 +695,7 @@ int launch_route(const RouteArgs & a, const MoePlan & p, uint8_t * ws, int32_t *
     RouteKArgs r;
     r.W = a.W; r.x = a.x; r.rm = a.rm; r.sgi = a.sh_gate_inp;
     r.E = (int)a.E; r.H = (int)a.H; r.T = (int)a.T; r.k = (int)a.k; r.norm = a.norm; r.scale = a.scale;
+    r.sigm = a.sigm; r.bias = a.bias;
     r.n_row_wg = (int)a.E;
     r.logits = reinterpret_cast<float *>(ws + p.logits);
     float * sh = reinterpret_cast<float *>(ws + p.sh_gate);

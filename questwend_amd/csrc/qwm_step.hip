@@ -81,6 +81,8 @@ int launch_step(const StepCall & c, const StepPlan & p, uint8_t * ws, hipStream_
     a.W_r = (const float *)L->router.data; a.x = c.x; a.rm = c.rm;
     a.sgi = (L->sh_gate.data && L->sh_gate_inp.data) ? (const float *)L->sh_gate_inp.data : nullptr;
     a.E = (int)m.E; a.k = (int)m.k; a.norm = L->norm_weights; a.scale = L->weights_scale;
+    a.sigm = L->gating_func == 2 ? 1 : 0;
+    a.bias = L->exp_probs_b.data ? (const float *)L->exp_probs_b.data : nullptr;
     a.N = (int)m.N; a.N_sh = (int)m.N_sh; a.shared = m.shared ? 1 : 0;
     a.gate = (const uint8_t *)L->gate_pool.data; a.up = (const uint8_t *)L->up_pool.data;
     a.down = (const uint8_t *)L->down_pool.data;

@@ -10,6 +10,7 @@
 #include "qwm_q4k.h"
 #include "qwm_vhead.h"
 #include "qwm_exact.h"
+#include "qwm_select.h"
 
 namespace qwm {
 
@@ -24,7 +25,8 @@ constexpr size_t cmax(size_t x, size_t y) { return x > y ? x : y; }
 
 struct StepArgs {
     const float * W_r; const float * x; const float * rm; const float * sgi;   // router [E][H], x [T][H]
-    int E, k, norm; float scale;
+    int E, k, norm, sigm; float scale;
+    const float * bias;                                                         // exp_probs_b [E] or null
     int N, N_sh, shared;
     const uint8_t * gate; const uint8_t * up; const uint8_t * down;
     size_t gate_slab, up_slab, down_slab;
@@ -112,89 +114,28 @@ QWM_DEV void step_router(const StepArgs & a, int g, int G) {
 
 // ---------------------------------------------------------------- P1 ----
 // The selection of route_experts (runtime.cpp:2693-2734) for every token, in
-// every workgroup: soft_max (ops.cpp:5813-5920, vec.cpp:531: v_expf over
-// 16-lane chunks, each chunk's 16-lane tree added to a double sum in order,
-// scaled by 1/sum), top-k (larger probability, then lower index), weight
-// normalization (double sum, clamp 6.103515625e-5, division), scale; then
-// the expert union in first-occurrence order and each unit's slots.
-//
-// One wave per token; top-k as k rounds of a wave maximum with ballots for
-// the tie order, the weight normalization one lane per selected expert.
-// R: probabilities per lane (E <= 64 * R).
+// every workgroup, one wave per token (select_token, qwm_select.h: soft_max
+// or sigmoid, the optional ranking bias, top-k, weights); then the expert
+// union in first-occurrence order and each unit's slots.
+// R: logits per lane (E <= 64 * R).
 template <int NT, int R>
 QWM_DEV void step_select(const StepArgs & a, int g, StepShared & S, uint8_t * smem) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int E = a.E, k = a.k;
     const int nr = (E + 63) / 64;
-    const int nfull = E & ~15;
     const unsigned long long below = (1ull << lane) - 1ull;
+    const SelectCfg sel{E, k, a.norm, a.sigm, a.scale, a.bias};
     for (int t = wave; t < NT; t += 4) {
         const float shl = a.sgi ? a.lg[(size_t)E * 32 + t] : 0.f;      // shared-expert gate logit
         float v[R];
-        float m = -__builtin_inff();
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            v[r] = -__builtin_inff();
-            const int i = 64 * r + lane;
-            if (r < nr && i < E) v[r] = a.lg[(size_t)i * 32 + t];
-            m = fmaxf(m, v[r]);
-        }
-        m = wave_max(m);
-        double sum = 0.0;
-        float tailv = 0.f;
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            if (r < nr) {
-                const int i = 64 * r + lane;
-                float ev = 0.f;
-                if (i < nfull) ev = v_expf(v[r] - m);
-                else if (i < E) ev = expf(v[r] - m);          // scalar tail: libm expf on the CPU
-                const float cs = tree16_dpp(i < nfull ? ev : 0.f);
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    if (64 * r + 16 * q < nfull) sum += (double)readlane_f(cs, 16 * q);
-                if (r == (nfull >> 6)) tailv = ev;
-                v[r] = ev;
-            }
-        }
-        for (int i = nfull; i < E; ++i) sum += (double)readlane_f(tailv, i & 63);
-        const float sc = (float)(1.0 / sum);
-        // top-k: k rounds of the wave maximum; a tie goes to the lower index
-        // (the first r, then the first lane, holding the maximum).  Lane j
-        // keeps the j-th selection; the weight sum runs in selection order.
-        float cur[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const int i = 64 * r + lane;
-            v[r] = v[r] * sc;
-            cur[r] = (r < nr && i < E) ? v[r] : -1.f;                  // probabilities are >= 0
+            v[r] = (r < nr && i < E) ? a.lg[(size_t)i * 32 + t] : -__builtin_inff();
         }
-        float myw = 0.f;
-        int myid = 0;
-        double wsum = 0.0;
-        for (int j = 0; j < k; ++j) {
-            float m = cur[0];
-#pragma unroll
-            for (int r = 1; r < R; ++r) m = fmaxf(m, cur[r]);
-            m = wave_max(m);
-            int id = -1;
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const unsigned long long bal = __ballot(cur[r] == m);
-                if (id < 0 && bal) id = 64 * r + (int)__builtin_ctzll(bal);
-            }
-            if (lane == j) { myw = m; myid = id; }
-            wsum += (double)m;
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-                if (64 * r + lane == id) cur[r] = -1.f;
-        }
-        if (a.norm) {
-            float ws = (float)wsum;
-            ws = fmaxf(fminf(ws, __builtin_inff()), 6.103515625e-5f);
-            myw = myw / ws;
-        }
-        if (a.scale != 0.0f && a.scale != 1.0f) myw = myw * a.scale;
+        int myid;
+        float myw;
+        select_token<R>(v, sel, a.rm ? a.rm + (size_t)t * E : nullptr, lane, myid, myw);
         if (lane < k) {
             S.ids[t * k + lane] = myid;
             S.w[t * k + lane] = myw;
@@ -203,7 +144,7 @@ QWM_DEV void step_select(const StepArgs & a, int g, StepShared & S, uint8_t * sm
                 if (a.w_out) a.w_out[(size_t)t * a.w_ld + lane] = myw;
             }
         }
-        if (lane == 0) S.shg[t] = a.sgi ? 1.f / (1.f + expf(-shl)) : 1.f;   // unary-ops.cpp:31
+        if (lane == 0) S.shg[t] = a.sgi ? libm_sigmoid(shl) : 1.f;   // unary-ops.cpp:31
     }
     __syncthreads();
     // expert union through per-expert LDS tables: first pair, token mask, unit
@@ -298,7 +239,7 @@ QWM_DEV void step_gateup(const StepArgs & a, int g, int G, const StepShared & S,
 #pragma unroll
             for (int i = 0; i < MAXP; ++i)
                 if (i < n) {
-                    const float v = (r < rows - (rows & 15)) ? v_silu(gs[i]) * us[i] : gs[i] / (1.0f + expf(-gs[i])) * us[i];
+                    const float v = (r < rows - (rows & 15)) ? v_silu(gs[i]) * us[i] : gs[i] / (1.0f + libm_expf(-gs[i])) * us[i];
                     if (shared) st_agent(a.act_sh + (size_t)U_.pair[i] * rows + r, v);
                     else st_agent(a.act + (size_t)U_.pair[i] * rows + r, v);
                 }

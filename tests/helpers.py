@@ -60,6 +60,12 @@ def oracle():
         lib.qwo_pool_clear_counts.argtypes = [P]
         lib.qwo_pool_load_profile.argtypes = [P, ctypes.c_char_p, P]
         lib.qwo_route.argtypes = [I64, I64, I64, P, P, P, ctypes.c_int, ctypes.c_int, F32, P, P, P, P, P]
+        lib.qwo_route_ex.argtypes = [I64, I64, I64, P, P, P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int, F32,
+                                     P, P, P, P, P]
+        lib.qwo_expf.argtypes = [F32]
+        lib.qwo_expf.restype = F32
+        lib.qwo_sigmoid.argtypes = [F32]
+        lib.qwo_sigmoid.restype = F32
         lib.qwo_mul_mat_id.argtypes = [ctypes.c_int, P, I64, I64, I64, P, I64, I64, P, I64, P]
         lib.qwo_mul_mat.argtypes = [ctypes.c_int, P, I64, I64, P, I64, P]
         lib.qwo_rms_norm.argtypes = [I64, P, F32, P, P]

@@ -26,11 +26,13 @@ class QwoMoeArgs(ctypes.Structure):
 
 class MoeCase:
     def __init__(self, seed, H=2048, N=768, E=128, k=8, S=16, shared=False, N_sh=512, sh_gate=True, wtype="q4_K",
-                 down="same"):
+                 down="same", gating=1, bias=0.0):
         """wtype: "q4_K" or "q8_0" expert slabs (the model-file quantizers), or
         "q5_K" (random valid blocks);
         down="q6_K": random Q6_K down slabs (routed and shared) beside Q4_K
-        gate/up, as Q4_K_M model files store some layers."""
+        gate/up, as Q4_K_M model files store some layers;
+        gating: 1 soft_max, 2 sigmoid routing; bias > 0: an exp_probs_b
+        ranking bias drawn N(0, bias^2)."""
         rng = np.random.default_rng(seed)
         assert wtype in ("q4_K", "q8_0", "q5_K") and down in ("same", "q6_K")
         self.wtype = wtype
@@ -44,6 +46,8 @@ class MoeCase:
         self.H, self.N, self.E, self.k, self.S = H, N, E, k, S
         self.shared, self.N_sh, self.has_sh_gate = shared, N_sh, sh_gate
         self.router = (rng.standard_normal((E, H)) * 0.02).astype(np.float32)
+        self.gating = gating
+        self.bias = (rng.standard_normal(E) * bias).astype(np.float32) if bias > 0 else None
         self.gate_q = quantize((rng.standard_normal((S, N, H)) * 0.02).astype(np.float32))
         self.up_q = quantize((rng.standard_normal((S, N, H)) * 0.02).astype(np.float32))
         self.down_q = quantize((rng.standard_normal((S, H, N)) * 0.02).astype(np.float32))
@@ -67,9 +71,10 @@ class MoeCase:
         w = np.zeros((T, self.k), np.float32)
         mg = np.zeros(T, np.float32)
         lg = np.zeros((T, self.E), np.float32)
-        assert oracle().qwo_route(I64(self.E), I64(self.H), I64(T), ptr(self.router), ptr(x),
-                                  ptr(rm) if rm is not None else None, self.k, 1, F32(1.0),
-                                  ptr(ids), ptr(w), ptr(lg), None, ptr(mg)) == 0
+        assert oracle().qwo_route_ex(I64(self.E), I64(self.H), I64(T), ptr(self.router), ptr(x),
+                                     ptr(rm) if rm is not None else None,
+                                     ptr(self.bias) if self.bias is not None else None, self.gating, self.k, 1,
+                                     F32(1.0), ptr(ids), ptr(w), ptr(lg), None, ptr(mg)) == 0
         return ids, w, mg, lg
 
     def block(self, x, slots, weights):
@@ -116,6 +121,10 @@ class MoeCase:
         L.n_expert_used = self.k
         L.norm_weights = 1
         L.weights_scale = 1.0
+        L.gating_func = self.gating
+        if self.bias is not None:
+            self.d_bias = dev(self.bias)
+            L.exp_probs_b = qa.tensor(qa.TYPE_F32, self.E, 1, 1, self.d_bias)
         self.layer = L
         return L
 

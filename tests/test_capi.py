@@ -105,6 +105,28 @@ def test_block_resident_rejects_short_tensors_without_gpu():
     assert call(good, ids_out=ids, w_out=w) == qa.ERR_WORKSPACE
 
 
+def test_gating_and_bias_checks_without_gpu():
+    L = qa.lib()
+    lay = qa.MoeLayer()
+    lay.router = qa.tensor(qa.TYPE_F32, 2048, 128, 1, 0x10000)
+    lay.gate_pool = qa.tensor(qa.TYPE_Q4_K, 2048, 768, 4, 0x10000)
+    lay.up_pool = qa.tensor(qa.TYPE_Q4_K, 2048, 768, 4, 0x10000)
+    lay.down_pool = qa.tensor(qa.TYPE_Q4_K, 768, 2048, 4, 0x10000)
+    lay.n_expert_used = 8
+    for g in (0, 1, 2):
+        lay.gating_func = g
+        assert L.qwm_moe_workspace_size(lay, 4) > 0
+    lay.gating_func = 3                                    # core/model.cpp:754-756 refuses it too
+    assert L.qwm_moe_workspace_size(lay, 4) == 0
+    lay.gating_func = 2
+    lay.exp_probs_b = qa.tensor(qa.TYPE_F32, 128, 1, 1, 0x20000)
+    assert L.qwm_moe_workspace_size(lay, 4) > 0
+    lay.exp_probs_b = qa.tensor(qa.TYPE_F32, 64, 1, 1, 0x20000)    # not [E]
+    assert L.qwm_moe_workspace_size(lay, 4) == 0
+    lay.exp_probs_b = qa.tensor(qa.TYPE_I32, 128, 1, 1, 0x20000)
+    assert L.qwm_moe_workspace_size(lay, 4) == 0
+
+
 class GpuPool:
     """Decision-only libqwmoe pool (no host slabs, so no copies, no GPU)."""
 

@@ -59,6 +59,8 @@ def slot_tables(case, ids):
     dict(T=2, E=512, k=10, N=512, shared=True, sh_gate=False),
     dict(T=4, E=128, k=8, N=768, down="q6_K"),                  # Q6_K down slabs (Q4_K_M last layers)
     dict(T=3, E=512, k=10, N=512, shared=True, down="q6_K"),
+    dict(T=4, E=512, k=10, N=512, shared=True, gating=2, bias=0.05),   # sigmoid routing + exp_probs_b
+    dict(T=2, E=128, k=8, N=768, bias=0.004),                           # soft_max + exp_probs_b
 ])
 def test_fused_step(dev, lm_head, cfg):
     T = cfg.pop("T")
@@ -114,10 +116,7 @@ def test_fused_step(dev, lm_head, cfg):
         assert r_b[T] >= 0, "device-side barrier timeout"
         assert np.array_equal(ids_b, ids) and np.array_equal(bits(w_b), bits(w))
         assert rel_err(out_b, out_ref) < TOL
-        if cfg.get("shared"):
-            assert rel_err(out_b, out_ref) < 1e-6          # shared gate: device expf vs libm
-        else:
-            assert np.array_equal(bits(out_b), bits(out_ref)), "block output not bit-exact"
+        assert np.array_equal(bits(out_b), bits(out_ref)), "block output not bit-exact"
         assert np.array_equal(bits(out_b), bits(out_a)), "fused step and per-op path differ"
         assert np.array_equal(r_b, r_a)
         clear = margins > 1e-3

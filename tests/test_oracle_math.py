@@ -126,6 +126,70 @@ def test_route_against_fp64(E, k, T):
         assert np.allclose(w[t], ref_w, rtol=2e-6)
 
 
+def route_ex(Wr, x, k, gating, bias=None, rm=None, norm=1):
+    E, H = Wr.shape
+    T = x.shape[0]
+    ids = np.zeros((T, k), np.int32)
+    w = np.zeros((T, k), np.float32)
+    pr = np.zeros((T, E), np.float32)
+    lg = np.zeros((T, E), np.float32)
+    assert oracle().qwo_route_ex(I64(E), I64(H), I64(T), ptr(Wr), ptr(x), ptr(rm) if rm is not None else None,
+                                 ptr(bias) if bias is not None else None, gating, k, norm, F32(1.0),
+                                 ptr(ids), ptr(w), ptr(lg), ptr(pr), None) == 0
+    return ids, w, lg, pr
+
+
+def test_route_sigmoid_and_bias_known_answer():
+    """Sigmoid gating with an exp_probs_b bias, by hand (runtime.cpp:2701-2728):
+    the bias reorders the ranking but the weights stay the selected experts'
+    own sigmoid probabilities, renormalized.  E = 4, top-2, identity router."""
+    Wr = np.eye(4, 256, dtype=np.float32)
+    x = np.zeros((1, 256), np.float32)
+    x[0, :4] = [2.0, 1.0, 0.0, -1.0]
+    bias = np.array([0.0, 0.0, 0.5, 0.0], np.float32)
+    ids, w, _, pr = route_ex(Wr, x, 2, gating=2, bias=bias)
+    s = 1.0 / (1.0 + np.exp(-np.array([2.0, 1.0, 0.0, -1.0])))
+    # ranks: 0.881, 0.731, 0.5 + 0.5 = 1.0, 0.269 -> experts 2 then 0
+    assert list(ids[0]) == [2, 0]
+    assert np.allclose(pr[0], s, rtol=1e-6)
+    assert np.allclose(w[0], np.array([s[2], s[0]]) / (s[2] + s[0]), rtol=1e-6)
+    # without the bias: experts 0 then 1
+    ids, w, _, _ = route_ex(Wr, x, 2, gating=2)
+    assert list(ids[0]) == [0, 1]
+    assert np.allclose(w[0], np.array([s[0], s[1]]) / (s[0] + s[1]), rtol=1e-6)
+    # the mask is applied again after the bias: a masked expert never wins
+    rm = np.zeros((1, 4), np.float32)
+    rm[0, 2] = -np.inf
+    ids, _, _, _ = route_ex(Wr, x, 2, gating=2, bias=bias, rm=rm)
+    assert 2 not in list(ids[0])
+    # soft_max gating with the same bias: probabilities e^l / sum, rank + bias
+    ids, w, _, pr = route_ex(Wr, x, 2, gating=1, bias=np.array([0.0, 0.0, 0.9, 0.0], np.float32))
+    e = np.exp(np.array([2.0, 1.0, 0.0, -1.0]) - 2.0)
+    p = e / e.sum()
+    assert np.allclose(pr[0], p, rtol=1e-6)
+    assert list(ids[0]) == [2, 0]                     # 0.087 + 0.9 > 0.644 > 0.237
+    assert np.allclose(w[0], np.array([p[2], p[0]]) / (p[2] + p[0]), rtol=1e-6)
+
+
+@pytest.mark.parametrize("E,k,T", [(128, 8, 4), (512, 10, 2)])
+def test_route_sigmoid_bias_against_fp64(E, k, T):
+    rng = np.random.default_rng(E + k)
+    H = 2048
+    Wr = (rng.standard_normal((E, H)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    bias = (rng.standard_normal(E) * 0.05).astype(np.float32)
+    ids, w, lg, pr = route_ex(Wr, x, k, gating=2, bias=bias)
+    l64 = x.astype(np.float64) @ Wr.astype(np.float64).T
+    p64 = 1.0 / (1.0 + np.exp(-l64))
+    assert np.allclose(pr, p64, rtol=2e-6)
+    rank = p64 + bias
+    for t in range(T):
+        order = np.argsort(-rank[t], kind="stable")
+        if rank[t][order[k - 1]] - rank[t][order[k]] > 1e-5:
+            assert sorted(ids[t]) == sorted(order[:k])
+        assert np.allclose(w[t], p64[t][ids[t]] / p64[t][ids[t]].sum(), rtol=2e-6)
+
+
 def test_route_mask_scale_and_no_norm():
     rng = np.random.default_rng(4)
     E, H, k = 128, 256, 8

@@ -152,6 +152,25 @@ size_t qwm_moe_decode_workspace_size(const qwm_moe_layer * layers, int32_t n_lay
 int qwm_moe_decode(const qwm_moe_layer * layers, int32_t n_layers, const int32_t * slot_tables, int64_t table_stride,
                    qwm_tensor * x, void * workspace, size_t ws_bytes, void * stream);
 
+/* qwm_moe_decode with the record of the optimistic single-graph decode
+ * (decode_cached_fast: the selection kept per layer, runtime.cpp:2759-2766;
+ * residency verified after the run, 6155-6166, and the selected experts
+ * touched, 6170-6176):
+ *   ids_all: device i32 [k, T, n_layers] or NULL: every layer's selected
+ *     experts (the runtime's sel_all);
+ *   resident_bits: device u32 [n_layers][ceil(E / 32)] or NULL: bit e of
+ *     layer l set when expert e of layer l is resident in all three role
+ *     pools (qwm_pool_resident_bits);
+ *   miss_flag: device i32, cleared by the call and set to 1 when a selected
+ *     expert's bit is clear.  Such a layer read the slot-0 sentinel of its
+ *     slot table, so x is then invalid: the reference restores its state and
+ *     runs the token through the cached path (decode_cached); with the flag
+ *     clear, the caller touches the selected experts (qwm_pool_touch).
+ * Graph-capturable like qwm_moe_decode (the flag is cleared by a kernel). */
+int qwm_moe_decode_sel(const qwm_moe_layer * layers, int32_t n_layers, const int32_t * slot_tables,
+                       int64_t table_stride, qwm_tensor * x, int32_t * ids_all, const uint32_t * resident_bits,
+                       int32_t * miss_flag, void * workspace, size_t ws_bytes, void * stream);
+
 /* -------------------------------------------------- verify + acceptance --- */
 
 /* Verify head + greedy acceptance (runtime.cpp:5014-5046 and 3648-3652):
@@ -283,6 +302,15 @@ int qwm_pool_get_stats(const qwm_pool * pool, qwm_pool_stats * out);
 int qwm_pool_slot_of_row(const qwm_pool * pool, int32_t role, int32_t layer, int32_t * out);
 /* Per-slot key (layer * n_expert + expert, -1 free) and clock of one role. */
 int qwm_pool_slots(const qwm_pool * pool, int32_t role, int32_t * keys, uint64_t * clocks);
+/* ExpertCache::resident for all three roles (expert_cache.cpp:1442-1446), as
+ * a bitmap: bit e of bits[e / 32] set when expert e of `layer` is resident
+ * in the gate, up and down pools; host u32 [ceil(n_expert / 32)]. */
+int qwm_pool_resident_bits(const qwm_pool * pool, int32_t layer, uint32_t * bits);
+/* ExpertCache::touch (expert_cache.cpp:1453-1463) of GATE, UP, DOWN for each
+ * of ids[0..n) in order (runtime.cpp:6170-6176): a resident key counts one
+ * access, its slot takes clock + 1 and the hit counter grows; a key that is
+ * not resident is left alone. */
+int qwm_pool_touch(qwm_pool * pool, int32_t layer, const int32_t * ids, int32_t n);
 
 /* One layer of the cached decode path (decode_cached, runtime.cpp:5292-5341)
  * in one call: qwm_moe_route, the routed ids read back to the host

@@ -1207,6 +1207,27 @@ QWO_API uint64_t qwo_pool_clock(const qwo_pool * p) { return p->clock; }
 QWO_API void qwo_pool_slot_of_row(const qwo_pool * p, int role, int layer, int32_t * out) {
     std::memcpy(out, p->role[role].slot_of.data() + (size_t)layer * p->n_expert, (size_t)p->n_expert * 4);
 }
+// ExpertCache::resident (expert_cache.cpp:1442-1446) and ::touch (1453-1463):
+// a resident key counts one access, its slot takes clock + 1, the hit counter
+// grows; the decode fast path touches GATE, UP, DOWN per selected expert
+// (runtime.cpp:6170-6176).
+QWO_API int qwo_pool_resident(const qwo_pool * p, int role, int layer, int expert) {
+    return p->role[role].key2slot.count(layer * p->n_expert + expert) ? 1 : 0;
+}
+QWO_API void qwo_pool_touch(qwo_pool * p, int layer, const int32_t * ids, int n) {
+    for (int i = 0; i < n; ++i) {
+        const int key = layer * p->n_expert + ids[i];
+        for (int r = 0; r < 3; ++r) {
+            auto & R = p->role[r];
+            auto it = R.key2slot.find(key);
+            if (it == R.key2slot.end()) continue;
+            R.count[key]++;
+            p->clock += 1;
+            R.clk[(size_t)it->second] = p->clock;
+            p->hits++;
+        }
+    }
+}
 QWO_API void qwo_pool_slots(const qwo_pool * p, int role, int32_t * slot2key, uint64_t * clk) {
     const auto & R = p->role[role];
     for (int s = 0; s < R.n_slots; ++s) { slot2key[s] = R.slot2key[(size_t)s]; clk[s] = R.clk[(size_t)s]; }

@@ -96,6 +96,9 @@ def lib():
                                                   _P, _SZ, _P]),
         "qwm_moe_decode_workspace_size": (_SZ, [ctypes.POINTER(MoeLayer), _I32, _I64]),
         "qwm_moe_decode": (ctypes.c_int, [ctypes.POINTER(MoeLayer), _I32, _P, _I64, T, _P, _SZ, _P]),
+        "qwm_moe_decode_sel": (ctypes.c_int, [ctypes.POINTER(MoeLayer), _I32, _P, _I64, T, _P, _P, _P, _P, _SZ, _P]),
+        "qwm_pool_resident_bits": (ctypes.c_int, [_P, _I32, _P]),
+        "qwm_pool_touch": (ctypes.c_int, [_P, _I32, _P, _I32]),
         "qwm_verify_workspace_size": (_SZ, [T, _I64]),
         "qwm_verify_accept": (ctypes.c_int, [T, T, _P, ctypes.c_float, _P, _P, _P, _SZ, _P]),
         "qwm_verify_step_workspace_size": (_SZ, [ctypes.POINTER(MoeLayer), T, _I64]),

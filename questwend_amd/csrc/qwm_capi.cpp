@@ -278,8 +278,10 @@ size_t qwm_moe_workspace_size(const qwm_moe_layer * layer, int64_t T) {
 
 static int do_route(const qwm_moe_layer * L, const MoePlan & p, const qwm_tensor * x, const qwm_tensor * rm,
                     const int32_t * tables, int64_t stride, int32_t layer_index, int32_t * ids_out, int64_t ids_ld,
-                    float * w_out, int64_t w_ld, uint8_t * ws, hipStream_t s) {
+                    float * w_out, int64_t w_ld, uint8_t * ws, hipStream_t s, const uint32_t * res_bits = nullptr,
+                    int32_t * res_flag = nullptr) {
     RouteArgs a;
+    a.res_bits = res_bits; a.res_flag = res_flag;
     a.W = (const float *)L->router.data; a.x = (const float *)x->data;
     a.rm = rm ? (const float *)rm->data : nullptr;
     a.sh_gate_inp = (L->sh_gate.data && L->sh_gate_inp.data) ? (const float *)L->sh_gate_inp.data : nullptr;
@@ -351,10 +353,10 @@ int qwm_moe_experts(const qwm_moe_layer * layer, const qwm_tensor * x, const qwm
                       (hipStream_t)stream);
 }
 
-int qwm_moe_block_resident(const qwm_moe_layer * layer, int32_t layer_index, const int32_t * slot_tables,
-                           int64_t table_stride, const qwm_tensor * x, const qwm_tensor * rm,
-                           const qwm_tensor * resid, qwm_tensor * out, qwm_tensor * ids_out, qwm_tensor * w_out,
-                           void * workspace, size_t ws_bytes, void * stream) {
+static int block_resident(const qwm_moe_layer * layer, int32_t layer_index, const int32_t * slot_tables,
+                          int64_t table_stride, const qwm_tensor * x, const qwm_tensor * rm, const qwm_tensor * resid,
+                          qwm_tensor * out, qwm_tensor * ids_out, qwm_tensor * w_out, void * workspace,
+                          size_t ws_bytes, void * stream, const uint32_t * res_bits, int32_t * res_flag) {
     if (!x) return fail(QWM_ERR_ARG, "moe_block: x is NULL");
     if (!slot_tables) return fail(QWM_ERR_ARG, "moe_block: slot tables are NULL");
     MoePlan p;
@@ -377,13 +379,22 @@ int qwm_moe_block_resident(const qwm_moe_layer * layer, int32_t layer_index, con
     hipStream_t s = (hipStream_t)stream;
     rc = do_route(layer, p, x, rm, slot_tables, table_stride, layer_index,
                   ids_out ? (int32_t *)ids_out->data : nullptr, ids_out ? (int64_t)(ids_out->nb[1] / 4) : 0,
-                  w_out ? (float *)w_out->data : nullptr, w_out ? (int64_t)(w_out->nb[1] / 4) : 0, ws, s);
+                  w_out ? (float *)w_out->data : nullptr, w_out ? (int64_t)(w_out->nb[1] / 4) : 0, ws, s,
+                  res_bits, res_flag);
     if (rc != QWM_OK) return rc;
     const int64_t P = p.T * p.k;
     const int32_t * slots = (const int32_t *)(ws + p.slots);
     return do_experts(layer, p, slots, slots + P, slots + 2 * P, (const float *)(ws + p.w),
                       resid ? (const float *)resid->data : nullptr, (float *)out->data, ws, s,
                       (const int32_t *)(ws + p.uslot));
+}
+
+int qwm_moe_block_resident(const qwm_moe_layer * layer, int32_t layer_index, const int32_t * slot_tables,
+                           int64_t table_stride, const qwm_tensor * x, const qwm_tensor * rm,
+                           const qwm_tensor * resid, qwm_tensor * out, qwm_tensor * ids_out, qwm_tensor * w_out,
+                           void * workspace, size_t ws_bytes, void * stream) {
+    return block_resident(layer, layer_index, slot_tables, table_stride, x, rm, resid, out, ids_out, w_out, workspace,
+                          ws_bytes, stream, nullptr, nullptr);
 }
 
 // ------------------------------------------------------------ layer loop --
@@ -462,7 +473,15 @@ size_t qwm_moe_decode_workspace_size(const qwm_moe_layer * layers, int32_t n_lay
 
 int qwm_moe_decode(const qwm_moe_layer * layers, int32_t n_layers, const int32_t * slot_tables, int64_t table_stride,
                    qwm_tensor * x, void * workspace, size_t ws_bytes, void * stream) {
+    return qwm_moe_decode_sel(layers, n_layers, slot_tables, table_stride, x, nullptr, nullptr, nullptr, workspace,
+                              ws_bytes, stream);
+}
+
+int qwm_moe_decode_sel(const qwm_moe_layer * layers, int32_t n_layers, const int32_t * slot_tables,
+                       int64_t table_stride, qwm_tensor * x, int32_t * ids_all, const uint32_t * resident_bits,
+                       int32_t * miss_flag, void * workspace, size_t ws_bytes, void * stream) {
     if (!x) return fail(QWM_ERR_ARG, "moe_decode: x is NULL");
+    if (resident_bits && !miss_flag) return fail(QWM_ERR_ARG, "moe_decode: resident_bits needs miss_flag");
     if (!slot_tables) return fail(QWM_ERR_ARG, "moe_decode: slot tables are NULL");
     MoePlan p;
     int rc = check_layers(layers, n_layers, x->ne[1], p);
@@ -475,11 +494,16 @@ int qwm_moe_decode(const qwm_moe_layer * layers, int32_t n_layers, const int32_t
     qwm_tensor buf = *x;
     buf.data = ws + align_up(p.total, 256);
     hipStream_t s = (hipStream_t)stream;
+    if (miss_flag && (rc = launch_fill_zero(miss_flag, 4, s)) != QWM_OK) return rc;
+    const int64_t words = (p.E + 31) / 32;
     for (int32_t l = 0; l < n_layers; ++l) {
         qwm_tensor * src = (l & 1) ? &buf : x;
         qwm_tensor * dst = (l & 1) ? x : &buf;
-        rc = qwm_moe_block_resident(&layers[l], l, slot_tables, table_stride, src, nullptr, src, dst, nullptr, nullptr,
-                                    ws, p.total, s);
+        qwm_tensor ids_l;
+        if (ids_all) qwm_tensor_init(&ids_l, QWM_TYPE_I32, p.k, p.T, 1, ids_all + (size_t)l * p.k * p.T);
+        rc = block_resident(&layers[l], l, slot_tables, table_stride, src, nullptr, src, dst, ids_all ? &ids_l : nullptr,
+                            nullptr, ws, p.total, s, resident_bits ? resident_bits + (size_t)l * words : nullptr,
+                            miss_flag);
         if (rc != QWM_OK) return rc;
     }
     if (n_layers & 1)

@@ -65,6 +65,8 @@ struct RouteArgs {
     const float * bias;                                  // exp_probs_b [E] or null
     const int32_t * slot_tables; int64_t table_stride; int32_t layer;  // resident remap or null
     int32_t wtype;                                       // pool type: the activation format of x
+    const uint32_t * res_bits = nullptr;                 // residency bits of the layer's experts, or null
+    int32_t * res_flag = nullptr;                        // set to 1 when a selected expert's bit is clear
 };
 int launch_route(const RouteArgs & a, const MoePlan & p, uint8_t * ws, int32_t * ids_out, int64_t ids_ld,
                  float * w_out, int64_t w_ld, hipStream_t s);

@@ -32,6 +32,7 @@ struct RouteKArgs {
     float * logits; float * sh_logit;                // hand-off to the last workgroup
     int32_t * ids_ws; float * w_ws;                  // [T][k]
     int32_t * ids_out; int64_t ids_ld; float * w_out; int64_t w_ld;  // optional user copies
+    const uint32_t * res_bits; int32_t * res_flag;   // residency bitmap of the layer's experts; miss flag (or null)
     float * sh_gate;                                 // [T] or null
     int8_t * xq_qs; float * xq_d; int32_t * xq_bs;   // Q8_K of x
     int q80; float * xq_d0;                         // Q8_0 pools: x as Q8_0 (qs in xq_qs, scales per 32)
@@ -142,6 +143,9 @@ __global__ void __launch_bounds__(256) k_route(RouteKArgs a) {
         int myid;
         float myw;
         select_token<R>(v, sel, a.rm ? a.rm + (size_t)t * E : nullptr, lane, myid, myw);
+        // the optimistic path's residency check (runtime.cpp:6155-6166): a
+        // selected expert without its bit ran on the slot-0 sentinel
+        if (a.res_bits && lane < k && !((a.res_bits[myid >> 5] >> (myid & 31)) & 1u)) st_agent(a.res_flag, 1);
         if (lane < k) {
             s_ids[t * k + lane] = myid;
             a.ids_ws[t * k + lane] = myid;
@@ -703,6 +707,7 @@ int launch_route(const RouteArgs & a, const MoePlan & p, uint8_t * ws, int32_t *
     r.ids_ws = reinterpret_cast<int32_t *>(ws + p.ids);
     r.w_ws = reinterpret_cast<float *>(ws + p.w);
     r.ids_out = ids_out; r.ids_ld = ids_ld; r.w_out = w_out; r.w_ld = w_ld;
+    r.res_bits = a.res_bits; r.res_flag = a.res_flag;
     r.sh_gate = a.sh_gate_inp ? sh : nullptr;
     r.xq_qs = reinterpret_cast<int8_t *>(ws + p.xq_qs);
     r.xq_d = reinterpret_cast<float *>(ws + p.xq_d);

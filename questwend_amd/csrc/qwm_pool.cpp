@@ -593,6 +593,37 @@ int qwm_pool_slot_of_row(const qwm_pool * p, int32_t role, int32_t layer, int32_
     return QWM_OK;
 }
 
+int qwm_pool_resident_bits(const qwm_pool * p, int32_t layer, uint32_t * bits) {
+    if (!p || !bits || layer < 0 || layer >= p->n_layer) return fail(QWM_ERR_ARG, "pool_resident_bits: bad argument");
+    const int32_t words = (p->n_expert + 31) / 32;
+    for (int32_t w = 0; w < words; ++w) bits[w] = 0u;
+    for (int32_t e = 0; e < p->n_expert; ++e) {
+        const int32_t key = layer * p->n_expert + e;
+        bool all = true;
+        for (int r = 0; r < 3 && all; ++r) all = p->role[r].key2slot.count(key) != 0;
+        if (all) bits[e >> 5] |= 1u << (e & 31);
+    }
+    return QWM_OK;
+}
+
+int qwm_pool_touch(qwm_pool * p, int32_t layer, const int32_t * ids, int32_t n) {
+    if (!p || (!ids && n) || layer < 0 || layer >= p->n_layer) return fail(QWM_ERR_ARG, "pool_touch: bad argument");
+    for (int32_t i = 0; i < n; ++i)
+        if (ids[i] < 0 || ids[i] >= p->n_expert) return fail(QWM_ERR_ARG, "pool_touch: expert id out of range");
+    for (int32_t i = 0; i < n; ++i) {
+        const int32_t key = layer * p->n_expert + ids[i];
+        for (int r = 0; r < 3; ++r) {
+            auto & R = p->role[r];
+            auto it = R.key2slot.find(key);
+            if (it == R.key2slot.end()) continue;
+            R.count[key]++;
+            p->touch(R, it->second);
+            p->hits++;
+        }
+    }
+    return QWM_OK;
+}
+
 int qwm_pool_slots(const qwm_pool * p, int32_t role, int32_t * keys, uint64_t * clocks) {
     if (!p || role < 0 || role > 2) return fail(QWM_ERR_ARG, "pool_slots: bad argument");
     const auto & R = p->role[role];

@@ -55,6 +55,8 @@ def oracle():
         lib.qwo_pool_clock.restype = ctypes.c_uint64
         lib.qwo_pool_slot_of_row.argtypes = [P, ctypes.c_int, ctypes.c_int, P]
         lib.qwo_pool_slots.argtypes = [P, ctypes.c_int, P, P]
+        lib.qwo_pool_resident.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        lib.qwo_pool_touch.argtypes = [P, ctypes.c_int, P, ctypes.c_int]
         lib.qwo_pool_save_profile.argtypes = [P, ctypes.c_char_p, ctypes.c_int]
         lib.qwo_pool_rebalance.argtypes = [P, ctypes.c_int, I64, P]
         lib.qwo_pool_clear_counts.argtypes = [P]

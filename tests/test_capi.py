@@ -219,6 +219,69 @@ def test_pool_matches_oracle_on_zipf_traces(indexed, protect):
             assert np.array_equal(row_g, row_o)
 
 
+@pytest.mark.parametrize("indexed", [0, 1])
+def test_pool_touch_and_residency_match_oracle(indexed):
+    """The fast path's bookkeeping (runtime.cpp:6155-6176): residency bitmaps
+    equal ExpertCache::resident for all three roles, and touches of the
+    selected experts (GATE, UP, DOWN per expert, non-resident ones left
+    alone) leave the pool in the oracle's state, interleaved with ensure
+    calls on a Zipf trace."""
+    rng = np.random.default_rng(31 + indexed)
+    n_layer, n_expert, slots = 3, 96, [40, 33, 47]
+    g = GpuPool(n_layer, n_expert, slots, 0, indexed)
+    o = OraclePool(n_layer, n_expert, slots, 0)
+    pop = 1.0 / np.arange(1, n_expert + 1) ** 1.1
+    pop /= pop.sum()
+    words = (n_expert + 31) // 32
+    for step in range(300):
+        layer = int(rng.integers(0, n_layer))
+        ids = rng.choice(n_expert, 8, replace=False, p=pop).astype(np.int32)
+        if step % 3:
+            rg, _ = g.ensure(layer, ids)
+            ro, _ = o.ensure(layer, ids)
+            assert rg == ro == 0
+        else:
+            qa.check(qa.lib().qwm_pool_touch(g.h, layer, ptr(ids), ids.size))
+            oracle().qwo_pool_touch(o.h, layer, ptr(ids), ids.size)
+        bits = np.zeros(words, np.uint32)
+        qa.check(qa.lib().qwm_pool_resident_bits(g.h, layer, ptr(bits)))
+        want = [all(oracle().qwo_pool_resident(o.h, r, layer, e) for r in range(3)) for e in range(n_expert)]
+        got = [bool((bits[e >> 5] >> (e & 31)) & 1) for e in range(n_expert)]
+        assert got == want
+    for r in range(3):
+        kg, cg = g.state(r)
+        ko, co = o.state(r)
+        assert np.array_equal(kg, ko) and np.array_equal(cg, co)
+    st = qa.PoolStats()
+    qa.check(qa.lib().qwm_pool_get_stats(g.h, ctypes.byref(st)))
+    hmo = np.zeros(3, np.uint64)
+    oracle().qwo_pool_stats(o.h, ptr(hmo))
+    assert (st.hits, st.misses, st.evictions) == tuple(int(v) for v in hmo)
+
+
+def test_pool_touch_known_answer():
+    """One layer, 4 experts, 2 slots per role: ensure [0, 1], then touch
+    [1, 3]: expert 1 gets clock + 1 (gate), + 2 (up), + 3 (down); expert 3 is
+    not resident and is left alone."""
+    g = GpuPool(1, 4, [2, 2, 2])
+    rc, _ = g.ensure(0, np.array([0, 1], np.int32))
+    assert rc == 0
+    st = qa.PoolStats()
+    qa.check(qa.lib().qwm_pool_get_stats(g.h, ctypes.byref(st)))
+    c0, h0 = st.clock, st.hits
+    ids = np.array([1, 3], np.int32)
+    qa.check(qa.lib().qwm_pool_touch(g.h, 0, ptr(ids), 2))
+    for r in range(3):
+        keys, clk = g.state(r)
+        assert clk[list(keys).index(1)] == c0 + 1 + r
+    qa.check(qa.lib().qwm_pool_get_stats(g.h, ctypes.byref(st)))
+    assert st.clock == c0 + 3 and st.hits == h0 + 3
+    bits = np.zeros(1, np.uint32)
+    qa.check(qa.lib().qwm_pool_resident_bits(g.h, 0, ptr(bits)))
+    assert bits[0] == 0b0011
+    assert qa.lib().qwm_pool_touch(g.h, 0, ptr(np.array([4], np.int32)), 1) == qa.ERR_ARG
+
+
 def test_pool_exhaustion_is_reported_and_consistent():
     g = GpuPool(1, 16, [2, 2, 2], protect=1)
     assert g.ensure(0, [0, 1])[0] == 0

@@ -124,3 +124,69 @@ def test_decode_graph_replay(dev, T, n_layers):
         torch.cuda.synchronize()
         got = gx.cpu().numpy()
         assert np.array_equal(got.view(np.uint32), exp.view(np.uint32)), f"replay {rep} differs from the eager loop"
+
+
+@pytest.mark.parametrize("T", [1, 2])
+def test_decode_sel_record_and_miss_flag(dev, T):
+    """qwm_moe_decode_sel keeps every layer's selected experts (the fast
+    path's sel_all, runtime.cpp:2759-2766) and raises the miss flag exactly
+    when a selected expert's residency bit is clear (6155-6166): all bits set
+    -> flag 0, ids equal to the oracle's layer by layer and x bit-exact; the
+    bit of one expert that layer 1 selects cleared -> flag 1; the bit of an
+    expert no layer selects cleared -> flag 0."""
+    H, N, E, k, n_layers = 512, 256, 40, 4, 3
+    cases = [MoeCase(seed=500 + l, H=H, N=N, E=E, k=k, S=E) for l in range(n_layers)]
+    rng = np.random.default_rng(23 + T)
+    perms = [rng.permutation(E).astype(np.int32) for _ in range(n_layers)]
+    tables = np.zeros((3, n_layers * E), np.int32)
+    for l in range(n_layers):
+        tables[:, l * E:(l + 1) * E] = perms[l]
+    layers = (qa.MoeLayer * n_layers)()
+    for l, c in enumerate(cases):
+        layers[l] = c.upload(torch)
+    x0 = rng.standard_normal((T, H)).astype(np.float32)
+    x = x0.copy()
+    ids_ref = []
+    for l, c in enumerate(cases):
+        ids, w, _, _ = c.route(x)
+        ids_ref.append(ids)
+        x = c.block(x, perms[l][ids], w) + x
+    L = qa.lib()
+    dtab = torch.from_numpy(tables).cuda()
+    ws = workspace(L.qwm_moe_decode_workspace_size(layers, n_layers, T))
+    words = (E + 31) // 32
+    used = set(int(e) for i in ids_ref for e in i.ravel())
+    unused = [e for e in range(E) if e not in used]
+    assert unused
+
+    def run(bits):
+        dx = torch.from_numpy(x0).cuda()
+        dids = torch.full((n_layers, T, k), -7, dtype=torch.int32, device="cuda")
+        dbits = torch.from_numpy(bits.view(np.int32)).cuda()
+        flag = torch.full((1,), 5, dtype=torch.int32, device="cuda")
+        qa.check(L.qwm_moe_decode_sel(layers, n_layers, dtab.data_ptr(), n_layers * E,
+                                      qa.tensor(qa.TYPE_F32, H, T, 1, dx), dids.data_ptr(), dbits.data_ptr(),
+                                      flag.data_ptr(), ws.data_ptr(), ws.numel(), None))
+        torch.cuda.synchronize()
+        return dx.cpu().numpy(), dids.cpu().numpy(), int(flag.cpu().numpy()[0])
+
+    full = np.zeros((n_layers, words), np.uint32)
+    for l in range(n_layers):
+        for e in range(E):
+            full[l, e >> 5] |= np.uint32(1 << (e & 31))
+    got, gids, flag = run(full)
+    print(f"decode_sel T={T}: flag {flag}", flush=True)
+    assert flag == 0
+    for l in range(n_layers):
+        assert np.array_equal(gids[l], ids_ref[l]), f"layer {l}: recorded ids differ"
+    assert np.array_equal(got.view(np.uint32), x.view(np.uint32))
+    miss = full.copy()
+    e1 = int(ids_ref[1][0, 0])
+    miss[1, e1 >> 5] &= np.uint32(~(1 << (e1 & 31)) & 0xFFFFFFFF)
+    _, gids, flag = run(miss)
+    assert flag == 1 and np.array_equal(gids[1], ids_ref[1])
+    other = full.copy()
+    eu = unused[0]
+    other[2, eu >> 5] &= np.uint32(~(1 << (eu & 31)) & 0xFFFFFFFF)
+    _, _, flag = run(other)
+    assert flag == 0

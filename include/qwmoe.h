@@ -327,6 +327,51 @@ int qwm_moe_cached_step(const qwm_moe_layer * layer, qwm_pool * pool, int32_t la
                         const qwm_tensor * rm, const qwm_tensor * resid, qwm_tensor * out, int32_t * ids_host,
                         void * workspace, size_t ws_bytes, void * stream);
 
+/* ExpertCache::capacity (expert_cache.cpp:478-491): the fewest slots the
+ * layer may hold in any role before recycling its own (its quota, at least
+ * n_used, while quotas are on; else the pool size).  quota_of (493-501): the
+ * layer's quota (the pool size where none was computed).  set_quotas /
+ * quotas_active: ExpertCache::set_quotas / quotas_active (expert_cache.h:
+ * 154-162).  Return values >= 0, or a QWM_ERR_* code. */
+int qwm_pool_capacity(const qwm_pool * pool, int32_t layer);
+int qwm_pool_quota_of(const qwm_pool * pool, int32_t layer);
+int qwm_pool_quotas_active(const qwm_pool * pool);
+int qwm_pool_set_quotas(qwm_pool * pool, int32_t on);
+/* decode_cached_batch's plan_slices (runtime.cpp:4639-4687) for the routed
+ * ids sel (host i32 [T * n_used], token-major) of one layer: quotas switched
+ * on when the batch's expert union fits quota_of(layer) - 8 and off
+ * otherwise (left so: save qwm_pool_quotas_active() before a batch and
+ * restore it after, as the reference's QuotaScope does); then slices
+ * (t0, len) of consecutive tokens, cut where the slice's union would pass
+ * max(n_used, capacity(layer) - 8) or its length max_slice (0: 1024, the
+ * QWEN_SEGB_SLICE default).  slices: host i32 [2 * T]; *union_out (may be
+ * NULL) receives the batch's union size. */
+int qwm_pool_plan_slices(qwm_pool * pool, int32_t layer, const int32_t * sel, int32_t T, int32_t n_used,
+                         int32_t max_slice, int32_t * slices, int32_t * n_slices, int32_t * union_out);
+
+/* A batch of 1..QWM_BATCH_MAX_T tokens through one MoE layer on the slot pool
+ * (decode_cached_batch's router, plan_slices / ensure_slice and seg B,
+ * runtime.cpp:4509-4572, 4639-4698):
+ *   the router for every token (qwm_moe_route's numerics, eight tokens per
+ *   launch); the routed ids read back (synchronizes `stream`); the slices
+ *   planned on the pool (qwm_pool_plan_slices, which sets the quota mode);
+ *   per slice: qwm_pool_ensure (after the previous slice's kernels finish,
+ *   so that no victim is still being read), the slot ids uploaded,
+ *   qwm_pool_wait, then up/gate MUL_MAT_ID, SwiGLU, down MUL_MAT_ID, the
+ *   weighted sum in k order (ggml_mul then a left-to-right ggml_add chain),
+ *   the shared expert times its sigmoid gate, and resid (may be NULL).
+ * x, resid, out: f32 [H, T] (out must not overlap x); rm: optional f32
+ * [E, T].  ids_host (host i32 [k * T]), slices_host (host i32 [2 * T]) and
+ * n_slices may be NULL.  The layer's pools are the pool's device tensors.
+ * Slices of more than 8 tokens run the grouped MUL_MAT_ID GEMM (Q4_K) or GEMV
+ * launches over column chunks (other types).  Not capturable. */
+#define QWM_BATCH_MAX_T 4096
+size_t qwm_moe_cached_batch_workspace_size(const qwm_moe_layer * layer, int64_t T, int32_t max_slice);
+int qwm_moe_cached_batch(const qwm_moe_layer * layer, qwm_pool * pool, int32_t layer_index, const qwm_tensor * x,
+                         const qwm_tensor * rm, const qwm_tensor * resid, qwm_tensor * out, int32_t max_slice,
+                         int32_t * ids_host, int32_t * slices_host, int32_t * n_slices, void * workspace,
+                         size_t ws_bytes, void * stream);
+
 /* Cache profiles (ExpertCache::save_profile / load_prefetch,
  * expert_cache.cpp:1485-1538), in the reference's text format:
  * "QWENEXPCACHE 1", "n_layer n_expert", then "role layer expert count" per

@@ -968,6 +968,7 @@ struct qwo_pool {
     } role[3];
     std::vector<uint8_t> active;
     bool quota_on = false;
+    int n_used = 0;
 };
 
 // pick_victim (expert_cache.cpp:1129-1170, activation scores off): the lowest
@@ -1030,6 +1031,7 @@ QWO_API qwo_pool * qwo_pool_new(int n_layer, int n_expert, const int32_t * n_slo
         R.clk.assign((size_t)R.n_slots, 0);
         R.slot_of.assign((size_t)n_layer * n_expert, 0);
         R.occ.assign((size_t)n_layer, 0);
+        R.quota.assign((size_t)n_layer, -1);
     }
     if (p->protect) p->active.assign((size_t)n_layer * n_expert, 0);
     return p;
@@ -1181,6 +1183,7 @@ QWO_API int qwo_pool_rebalance(qwo_pool * p, int n_used, int64_t fill_budget, in
     }
     for (auto & R : p->role) R.quota = quota;
     p->quota_on = true;
+    p->n_used = n_used;
     if (quota_out) for (int l = 0; l < L; ++l) quota_out[l] = quota[(size_t)l];
     std::vector<int> seen((size_t)L, 0);
     int filled = 0;
@@ -1228,6 +1231,65 @@ QWO_API void qwo_pool_touch(qwo_pool * p, int layer, const int32_t * ids, int n)
         }
     }
 }
+// ExpertCache::capacity (expert_cache.cpp:478-491) and ::quota_of (493-501).
+QWO_API int qwo_pool_capacity(const qwo_pool * p, int layer) {
+    int m = INT32_MAX;
+    for (const auto & R : p->role) {
+        const int q = R.quota[(size_t)layer];
+        m = std::min(m, p->quota_on && q >= 0 ? std::max(q, p->n_used) : R.n_slots);
+    }
+    return m;
+}
+QWO_API int qwo_pool_quota_of(const qwo_pool * p, int layer) {
+    int m = INT32_MAX;
+    for (const auto & R : p->role) m = std::min(m, R.quota[(size_t)layer] >= 0 ? R.quota[(size_t)layer] : R.n_slots);
+    return m;
+}
+QWO_API void qwo_pool_set_quotas(qwo_pool * p, int on) { p->quota_on = on != 0; }
+QWO_API int qwo_pool_quotas_active(const qwo_pool * p) { return p->quota_on ? 1 : 0; }
+
+// decode_cached_batch's plan_slices (core/runtime.cpp:4639-4687): pass 1 the
+// layer's union over the batch, quotas on iff it fits quota_of - 8; pass 2
+// token slices whose union stays within max(n_used, capacity - 8) and whose
+// length stays within max_slice (0: 1024).  slices: (t0, len) pairs.
+QWO_API int qwo_pool_plan_slices(qwo_pool * p, int layer, const int32_t * sel, int T, int n_used, int max_slice,
+                                 int32_t * slices, int32_t * union_out) {
+    const int E = p->n_expert;
+    if (max_slice == 0) max_slice = 1024;
+    std::vector<uint8_t> seen((size_t)E, 0);
+    int uni = 0;
+    for (int t = 0; t < T; ++t)
+        for (int j = 0; j < n_used; ++j) {
+            const int e = sel[(size_t)t * n_used + j];
+            if (!seen[(size_t)e]) { seen[(size_t)e] = 1; ++uni; }
+        }
+    p->quota_on = uni <= qwo_pool_quota_of(p, layer) - 8;
+    const int cap = std::max(n_used, qwo_pool_capacity(p, layer) - 8);
+    std::fill(seen.begin(), seen.end(), 0);
+    int ns = 0, distinct = 0, t0 = 0;
+    for (int t = 0; t < T; ++t) {
+        int nnew = 0;
+        for (int j = 0; j < n_used; ++j) {
+            const int e = sel[(size_t)t * n_used + j];
+            if (!seen[(size_t)e]) { seen[(size_t)e] = 1; ++nnew; }
+        }
+        if ((distinct + nnew > cap || t - t0 >= max_slice) && t > t0) {
+            slices[2 * ns] = t0; slices[2 * ns + 1] = t - t0; ++ns;
+            std::fill(seen.begin(), seen.end(), 0);
+            distinct = 0; nnew = 0;
+            for (int j = 0; j < n_used; ++j) {
+                const int e = sel[(size_t)t * n_used + j];
+                if (!seen[(size_t)e]) { seen[(size_t)e] = 1; ++nnew; }
+            }
+            t0 = t;
+        }
+        distinct += nnew;
+    }
+    slices[2 * ns] = t0; slices[2 * ns + 1] = T - t0; ++ns;
+    if (union_out) *union_out = uni;
+    return ns;
+}
+
 QWO_API void qwo_pool_slots(const qwo_pool * p, int role, int32_t * slot2key, uint64_t * clk) {
     const auto & R = p->role[role];
     for (int s = 0; s < R.n_slots; ++s) { slot2key[s] = R.slot2key[(size_t)s]; clk[s] = R.clk[(size_t)s]; }

@@ -99,6 +99,14 @@ def lib():
         "qwm_moe_decode_sel": (ctypes.c_int, [ctypes.POINTER(MoeLayer), _I32, _P, _I64, T, _P, _P, _P, _P, _SZ, _P]),
         "qwm_pool_resident_bits": (ctypes.c_int, [_P, _I32, _P]),
         "qwm_pool_touch": (ctypes.c_int, [_P, _I32, _P, _I32]),
+        "qwm_pool_capacity": (ctypes.c_int, [_P, _I32]),
+        "qwm_pool_quota_of": (ctypes.c_int, [_P, _I32]),
+        "qwm_pool_quotas_active": (ctypes.c_int, [_P]),
+        "qwm_pool_set_quotas": (ctypes.c_int, [_P, _I32]),
+        "qwm_pool_plan_slices": (ctypes.c_int, [_P, _I32, _P, _I32, _I32, _I32, _P, _P, _P]),
+        "qwm_moe_cached_batch_workspace_size": (_SZ, [ctypes.POINTER(MoeLayer), _I64, _I32]),
+        "qwm_moe_cached_batch": (ctypes.c_int, [ctypes.POINTER(MoeLayer), _P, _I32, T, T, T, T, _I32, _P, _P, _P, _P,
+                                                _SZ, _P]),
         "qwm_verify_workspace_size": (_SZ, [T, _I64]),
         "qwm_verify_accept": (ctypes.c_int, [T, T, _P, ctypes.c_float, _P, _P, _P, _SZ, _P]),
         "qwm_verify_step_workspace_size": (_SZ, [ctypes.POINTER(MoeLayer), T, _I64]),

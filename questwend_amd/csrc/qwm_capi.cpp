@@ -465,6 +465,201 @@ int qwm_moe_cached_step(const qwm_moe_layer * layer, qwm_pool * pool, int32_t la
     return qwm_moe_experts(layer, x, &t_sl[0], &t_sl[1], &t_sl[2], &t_w, resid, out, ws, p.total, stream);
 }
 
+// ------------------------------------------------------ batched layer --
+// decode_cached_batch's per-layer path for a batch of tokens (runtime.cpp:
+// 4509-4572 with plan_slices / ensure_slice, 4639-4698): the router over the
+// batch in groups of MAX_T tokens, the ids read back, the slices planned on
+// the pool, then per slice ensure + slot upload + the expert MUL_MAT_IDs,
+// SwiGLU, the k-ordered weighted sum, the shared expert and the residual.
+static bool overlaps(const qwm_tensor * a, const qwm_tensor * b);
+
+struct BatchPlan {
+    MoePlan route;                   // one router group (<= MAX_T tokens)
+    int64_t T = 0, S = 0;            // batch length, longest slice
+    size_t route_ws = 0, ids = 0, w = 0, slots = 0, zeros = 0, shg = 0;
+    size_t gate = 0, up = 0, act = 0, ex = 0, sh_g = 0, sh_u = 0, sh_act = 0, sh_out = 0, mmid = 0, mmid_bytes = 0;
+    size_t total = 0;
+};
+
+static size_t mmid_need(const qwm_tensor & as, int64_t K, int64_t ne11, int64_t n_ids, int64_t T) {
+    qwm_tensor b, ids;
+    qwm_tensor_init(&b, QWM_TYPE_F32, K, ne11, T, (void *)64);
+    qwm_tensor_init(&ids, QWM_TYPE_I32, n_ids, T, 1, (void *)64);
+    return qwm_mul_mat_id_workspace_size(&as, &b, &ids);
+}
+
+static int batch_plan(const qwm_moe_layer * L, int64_t T, int32_t max_slice, BatchPlan & b) {
+    if (T < 1 || T > QWM_BATCH_MAX_T) return fail(QWM_ERR_UNSUPPORTED, "moe_batch: 1 <= T <= 4096");
+    if (max_slice < 0) return fail(QWM_ERR_ARG, "moe_batch: max_slice must be >= 0");
+    int rc = check_layer(L, std::min<int64_t>(T, MAX_T), b.route);
+    if (rc != QWM_OK) return rc;
+    const MoePlan & p = b.route;
+    b.T = T;
+    b.S = std::min<int64_t>(T, max_slice ? max_slice : 1024);
+    const int64_t S = b.S, k = p.k, H = p.H, N = p.N, Nsh = p.N_sh;
+    // the MUL_MAT_ID workspaces at the longest slice and at the GEMV width
+    size_t mm = 0;
+    for (int64_t t : {S, std::min<int64_t>(S, MAX_T)}) {
+        const size_t need[3] = {mmid_need(L->gate_pool, H, 1, k, t), mmid_need(L->up_pool, H, 1, k, t),
+                                mmid_need(L->down_pool, N, k, k, t)};
+        for (size_t v : need) {
+            if (!v) return fail(QWM_ERR_UNSUPPORTED, std::string("moe_batch: expert MUL_MAT_ID: ") + qwm_last_error());
+            mm = std::max(mm, v);
+        }
+        if (p.shared) {
+            qwm_tensor g = L->sh_gate, u = L->sh_up, d = L->sh_down;
+            g.ne[2] = u.ne[2] = d.ne[2] = 1;
+            const size_t sh[3] = {mmid_need(g, H, 1, 1, t), mmid_need(u, H, 1, 1, t), mmid_need(d, Nsh, 1, 1, t)};
+            for (size_t v : sh) {
+                if (!v) return fail(QWM_ERR_UNSUPPORTED, std::string("moe_batch: shared expert: ") + qwm_last_error());
+                mm = std::max(mm, v);
+            }
+        }
+    }
+    size_t o = 0;
+    auto take = [&](size_t bytes) { size_t at = o; o = align_up(o + bytes, 256); return at; };
+    b.route_ws = take(p.total);
+    b.ids = take(4 * (size_t)(k * T));
+    b.w = take(4 * (size_t)(k * T));
+    b.slots = take(12 * (size_t)(k * T));
+    b.zeros = take(4 * (size_t)S);
+    b.shg = take(4 * (size_t)T);
+    b.gate = take(4 * (size_t)(N * k * S));
+    b.up = take(4 * (size_t)(N * k * S));
+    b.act = take(4 * (size_t)(N * k * S));
+    b.ex = take(4 * (size_t)(H * k * S));
+    if (p.shared) {
+        b.sh_g = take(4 * (size_t)(Nsh * S));
+        b.sh_u = take(4 * (size_t)(Nsh * S));
+        b.sh_act = take(4 * (size_t)(Nsh * S));
+        b.sh_out = take(4 * (size_t)(H * S));
+    }
+    b.mmid = take(mm);
+    b.mmid_bytes = mm;
+    b.total = o;
+    return QWM_OK;
+}
+
+size_t qwm_moe_cached_batch_workspace_size(const qwm_moe_layer * layer, int64_t T, int32_t max_slice) {
+    BatchPlan b;
+    return batch_plan(layer, T, max_slice, b) == QWM_OK ? b.total : 0;
+}
+
+int qwm_moe_cached_batch(const qwm_moe_layer * layer, qwm_pool * pool, int32_t layer_index, const qwm_tensor * x,
+                         const qwm_tensor * rm, const qwm_tensor * resid, qwm_tensor * out, int32_t max_slice,
+                         int32_t * ids_host, int32_t * slices_host, int32_t * n_slices, void * workspace,
+                         size_t ws_bytes, void * stream) {
+    if (!pool || !x || !out) return fail(QWM_ERR_ARG, "moe_batch: NULL argument");
+    BatchPlan b;
+    int rc = batch_plan(layer, x->ne[1], max_slice, b);
+    if (rc != QWM_OK) return rc;
+    const MoePlan & p = b.route;
+    const int64_t T = b.T, k = p.k, H = p.H, N = p.N, E = p.E;
+    if ((rc = check_act(x, H, "x")) != QWM_OK) return rc;
+    if ((rc = check_act(out, H, "out")) != QWM_OK) return rc;
+    if (out->ne[1] != T) return fail(QWM_ERR_ARG, "moe_batch: out must be [H, T]");
+    if (resid && ((rc = check_act(resid, H, "resid")) != QWM_OK || resid->ne[1] != T))
+        return rc != QWM_OK ? rc : fail(QWM_ERR_ARG, "moe_batch: resid must be [H, T]");
+    if (overlaps(out, x)) return fail(QWM_ERR_ARG, "moe_batch: out must not overlap x");
+    if (rm && (rm->type != T_F32 || rm->ne[0] != E || rm->ne[1] != T || !fully_contiguous(rm)))
+        return fail(QWM_ERR_ARG, "moe_batch: rm must be contiguous f32 [E, T]");
+    if (layer_index < 0 || layer_index >= pool_n_layer(pool) || pool_n_expert(pool) != E)
+        return fail(QWM_ERR_ARG, "moe_batch: layer index or expert count disagrees with the pool");
+    if (!workspace || ws_bytes < b.total) return fail(QWM_ERR_WORKSPACE, "moe_batch: workspace too small");
+    uint8_t * ws = (uint8_t *)workspace;
+    hipStream_t s = (hipStream_t)stream;
+    int32_t * d_ids = (int32_t *)(ws + b.ids);
+    float * d_w = (float *)(ws + b.w);
+    int32_t * d_sl = (int32_t *)(ws + b.slots);
+    float * d_shg = (float *)(ws + b.shg);
+    const float * xd = (const float *)x->data;
+
+    // the router, MAX_T tokens at a time (the route workspace is cleared
+    // whenever the group's shape changes: its counters sit at shape-dependent
+    // places)
+    int64_t prev_n = -1;
+    for (int64_t t0 = 0; t0 < T; t0 += MAX_T) {
+        const int64_t n = std::min<int64_t>(MAX_T, T - t0);
+        MoePlan pg;
+        if ((rc = check_layer(layer, n, pg)) != QWM_OK) return rc;
+        if (n != prev_n && (rc = launch_fill_zero(ws + b.route_ws, pg.total & ~(size_t)3, s)) != QWM_OK) return rc;
+        prev_n = n;
+        qwm_tensor xg, rg;
+        qwm_tensor_init(&xg, QWM_TYPE_F32, H, n, 1, (void *)(xd + t0 * H));
+        if (rm) qwm_tensor_init(&rg, QWM_TYPE_F32, E, n, 1, (float *)rm->data + t0 * E);
+        if ((rc = do_route(layer, pg, &xg, rm ? &rg : nullptr, nullptr, 0, 0, d_ids + t0 * k, k, d_w + t0 * k, k,
+                           ws + b.route_ws, s)) != QWM_OK)
+            return rc;
+    }
+    const bool sh_gate = p.shared && layer->sh_gate_inp.data;
+    if (sh_gate && (rc = launch_sh_gate((const float *)layer->sh_gate_inp.data, xd, d_shg, (int)H, (int)T, s)) != QWM_OK)
+        return rc;
+    if (p.shared && (rc = launch_fill_zero(ws + b.zeros, 4 * (size_t)b.S, s)) != QWM_OK) return rc;
+
+    // the routed ids on the host (synchronizes the stream, as the
+    // reference's read of `selected` does)
+    std::vector<int32_t> ids((size_t)(k * T)), sl((size_t)(3 * k * T)), slices((size_t)(2 * T));
+    QWM_HIP_CHECK(hipMemcpyAsync(ids.data(), d_ids, 4 * ids.size(), hipMemcpyDeviceToHost, s));
+    QWM_HIP_CHECK(hipStreamSynchronize(s));
+    if (ids_host) std::copy(ids.begin(), ids.end(), ids_host);
+    int32_t ns = 0;
+    if ((rc = qwm_pool_plan_slices(pool, layer_index, ids.data(), (int32_t)T, (int32_t)k, max_slice, slices.data(), &ns,
+                                   nullptr)) != QWM_OK)
+        return rc;
+    if (slices_host) std::copy(slices.begin(), slices.begin() + 2 * ns, slices_host);
+    if (n_slices) *n_slices = ns;
+
+    auto mmid = [&](const qwm_tensor & as, const float * bdata, int64_t K, int64_t ne11, const int32_t * idd,
+                    int64_t n_ids, int64_t len, float * dst, int64_t Nout) {
+        qwm_tensor bt, it, dt;
+        qwm_tensor_init(&bt, QWM_TYPE_F32, K, ne11, len, (void *)bdata);
+        qwm_tensor_init(&it, QWM_TYPE_I32, n_ids, len, 1, (void *)idd);
+        qwm_tensor_init(&dt, QWM_TYPE_F32, Nout, n_ids, len, dst);
+        return qwm_mul_mat_id(&as, &bt, &it, &dt, ws + b.mmid, b.mmid_bytes, s);
+    };
+    float * gbuf = (float *)(ws + b.gate);
+    float * ubuf = (float *)(ws + b.up);
+    float * abuf = (float *)(ws + b.act);
+    float * ebuf = (float *)(ws + b.ex);
+    for (int32_t si = 0; si < ns; ++si) {
+        const int64_t t0 = slices[2 * si], len = slices[2 * si + 1];
+        // ensure_slice (runtime.cpp:4690-4698); before it, the previous
+        // slice's kernels must be done with the slots ensure may recycle
+        if (si > 0) QWM_HIP_CHECK(hipStreamSynchronize(s));
+        const size_t off = (size_t)(t0 * k), cnt = (size_t)(len * k);
+        int32_t * sg = sl.data() + off, * su = sl.data() + k * T + off, * sd = sl.data() + 2 * k * T + off;
+        if ((rc = qwm_pool_ensure(pool, layer_index, ids.data() + off, (int32_t)cnt, sg, su, sd)) != QWM_OK) return rc;
+        int32_t * dsg = d_sl + off, * dsu = d_sl + k * T + off, * dsd = d_sl + 2 * k * T + off;
+        QWM_HIP_CHECK(hipMemcpyAsync(dsg, sg, 4 * cnt, hipMemcpyHostToDevice, s));
+        QWM_HIP_CHECK(hipMemcpyAsync(dsu, su, 4 * cnt, hipMemcpyHostToDevice, s));
+        QWM_HIP_CHECK(hipMemcpyAsync(dsd, sd, 4 * cnt, hipMemcpyHostToDevice, s));
+        if ((rc = qwm_pool_wait(pool, stream)) != QWM_OK) return rc;
+        const float * xs = xd + t0 * H;
+        if ((rc = mmid(layer->up_pool, xs, H, 1, dsu, k, len, ubuf, N)) != QWM_OK) return rc;
+        if ((rc = mmid(layer->gate_pool, xs, H, 1, dsg, k, len, gbuf, N)) != QWM_OK) return rc;
+        if ((rc = launch_swiglu_rows(gbuf, ubuf, abuf, (int)N, k * len, s)) != QWM_OK) return rc;
+        if ((rc = mmid(layer->down_pool, abuf, N, k, dsd, k, len, ebuf, H)) != QWM_OK) return rc;
+        const float * shout = nullptr;
+        if (p.shared) {
+            qwm_tensor g = layer->sh_gate, u = layer->sh_up, d = layer->sh_down;
+            g.ne[2] = u.ne[2] = d.ne[2] = 1;
+            const int32_t * z = (const int32_t *)(ws + b.zeros);
+            float * shg_b = (float *)(ws + b.sh_g), * shu_b = (float *)(ws + b.sh_u);
+            float * sha_b = (float *)(ws + b.sh_act), * sho_b = (float *)(ws + b.sh_out);
+            if ((rc = mmid(g, xs, H, 1, z, 1, len, shg_b, p.N_sh)) != QWM_OK) return rc;
+            if ((rc = mmid(u, xs, H, 1, z, 1, len, shu_b, p.N_sh)) != QWM_OK) return rc;
+            if ((rc = launch_swiglu_rows(shg_b, shu_b, sha_b, (int)p.N_sh, len, s)) != QWM_OK) return rc;
+            if ((rc = mmid(d, sha_b, p.N_sh, 1, z, 1, len, sho_b, H)) != QWM_OK) return rc;
+            shout = sho_b;
+        }
+        if ((rc = launch_combine_batch(ebuf, d_w + t0 * k, shout, sh_gate ? d_shg + t0 : nullptr,
+                                       resid ? (const float *)resid->data + t0 * H : nullptr,
+                                       (float *)out->data + t0 * H, (int)H, (int)k, len, s)) != QWM_OK)
+            return rc;
+    }
+    return QWM_OK;
+}
+
 size_t qwm_moe_decode_workspace_size(const qwm_moe_layer * layers, int32_t n_layers, int64_t T) {
     MoePlan p;
     if (check_layers(layers, n_layers, T, p) != QWM_OK) return 0;

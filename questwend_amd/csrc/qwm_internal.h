@@ -120,6 +120,12 @@ int launch_verify(const uint8_t * lm_head, const float * x, const float * norm_w
 
 int launch_fill_zero(void * p, size_t bytes, hipStream_t s);
 
+// ---- batched MoE layer tail (qwm_batch.hip) ----
+int launch_swiglu_rows(const float * g, const float * u, float * act, int n, int64_t rows, hipStream_t s);
+int launch_combine_batch(const float * ex, const float * w, const float * sh, const float * shg, const float * resid,
+                         float * out, int H, int k, int64_t T, hipStream_t s);
+int launch_sh_gate(const float * gw, const float * x, float * shg, int H, int T, hipStream_t s);
+
 // ---- slab gather (qwm_fetch.hip) ----
 constexpr int GATHER_MAX = 224;   // misses per launch (kernel arguments stay under 2 KiB)
 struct GatherItem {

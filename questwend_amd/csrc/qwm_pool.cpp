@@ -173,6 +173,7 @@ struct qwm_pool {
     int n_layer = 0, n_expert = 0;
     bool protect = false, indexed = false;
     bool quota_on = false;                          // per-layer quotas steer the victims (after a rebalance)
+    int32_t n_used = 0;                             // the model's n_expert_used, from the last rebalance
     uint64_t clock = 0;
     uint64_t hits = 0, misses = 0, evictions = 0, fetch_bytes = 0, fetches = 0;
     Role role[3];
@@ -506,6 +507,7 @@ int qwm_pool_create(const qwm_pool_desc * d, void * copy_stream, qwm_pool ** out
         R.clk.assign((size_t)R.n_slots, 0);
         R.slot_of.assign((size_t)d->n_layer * d->n_expert, 0);
         R.occ.assign((size_t)d->n_layer, 0);
+        R.quota.assign((size_t)d->n_layer, -1);     // no quota until a rebalance computes them
         if (p->indexed)
             for (int32_t s = 0; s < R.n_slots; ++s) R.free_slots.insert(s);
     }
@@ -621,6 +623,90 @@ int qwm_pool_touch(qwm_pool * p, int32_t layer, const int32_t * ids, int32_t n) 
             p->hits++;
         }
     }
+    return QWM_OK;
+}
+
+// ExpertCache::capacity (expert_cache.cpp:478-491): the fewest slots the
+// layer may hold in any role before it recycles its own -- its quota (at
+// least n_used) while quotas are on and computed, else the pool size.
+int qwm_pool_capacity(const qwm_pool * p, int32_t layer) {
+    if (!p || layer < 0 || layer >= p->n_layer) return fail(QWM_ERR_ARG, "pool_capacity: bad argument");
+    int32_t m = INT32_MAX;
+    for (const auto & R : p->role) {
+        const int32_t q = R.quota[(size_t)layer];
+        m = std::min(m, p->quota_on && q >= 0 ? std::max(q, p->n_used) : R.n_slots);
+    }
+    return m;
+}
+
+// ExpertCache::quota_of (expert_cache.cpp:493-501): the layer's quota (min
+// over the roles), or the pool size where none was computed.
+int qwm_pool_quota_of(const qwm_pool * p, int32_t layer) {
+    if (!p || layer < 0 || layer >= p->n_layer) return fail(QWM_ERR_ARG, "pool_quota_of: bad argument");
+    int32_t m = INT32_MAX;
+    for (const auto & R : p->role) {
+        const int32_t q = R.quota[(size_t)layer];
+        m = std::min(m, q >= 0 ? q : R.n_slots);
+    }
+    return m;
+}
+
+int qwm_pool_quotas_active(const qwm_pool * p) {
+    if (!p) return fail(QWM_ERR_ARG, "pool_quotas_active: NULL pool");
+    return p->quota_on ? 1 : 0;
+}
+
+// ExpertCache::set_quotas (expert_cache.h:162).  The indexed mode's shortcut
+// is off while quotas steer the victims.
+int qwm_pool_set_quotas(qwm_pool * p, int32_t on) {
+    if (!p) return fail(QWM_ERR_ARG, "pool_set_quotas: NULL pool");
+    p->quota_on = on != 0;
+    return QWM_OK;
+}
+
+// plan_slices (runtime.cpp:4639-4687): the layer's expert union over the
+// batch; quotas on when the union fits the layer's quota - 8, off otherwise;
+// then slices of consecutive tokens, cut before a token whose new experts
+// would take the slice's union past max(n_used, capacity - 8) or whose slice
+// reached max_slice tokens (QWEN_SEGB_SLICE, 1024 by default).
+int qwm_pool_plan_slices(qwm_pool * p, int32_t layer, const int32_t * sel, int32_t T, int32_t n_used,
+                         int32_t max_slice, int32_t * slices, int32_t * n_slices, int32_t * union_out) {
+    if (!p || !sel || !slices || !n_slices || T < 1 || n_used < 1 || max_slice < 0 || layer < 0 ||
+        layer >= p->n_layer)
+        return fail(QWM_ERR_ARG, "pool_plan_slices: bad argument");
+    const int32_t E = p->n_expert;
+    for (int64_t i = 0; i < (int64_t)T * n_used; ++i)
+        if (sel[i] < 0 || sel[i] >= E) return fail(QWM_ERR_ARG, "pool_plan_slices: expert id out of range");
+    if (max_slice == 0) max_slice = 1024;
+    std::vector<uint8_t> seen((size_t)E, 0);
+    int32_t uni = 0;
+    for (int64_t i = 0; i < (int64_t)T * n_used; ++i)
+        if (!seen[(size_t)sel[i]]) { seen[(size_t)sel[i]] = 1; ++uni; }
+    p->quota_on = uni <= qwm_pool_quota_of(p, layer) - 8;
+    const int32_t cap = std::max(n_used, qwm_pool_capacity(p, layer) - 8);
+    std::fill(seen.begin(), seen.end(), 0);
+    int32_t ns = 0, distinct = 0, t0 = 0;
+    for (int32_t t = 0; t < T; ++t) {
+        int32_t nnew = 0;
+        for (int32_t j = 0; j < n_used; ++j) {
+            const int32_t e = sel[(size_t)t * n_used + j];
+            if (!seen[(size_t)e]) { seen[(size_t)e] = 1; ++nnew; }
+        }
+        if ((distinct + nnew > cap || t - t0 >= max_slice) && t > t0) {
+            slices[2 * ns] = t0; slices[2 * ns + 1] = t - t0; ++ns;
+            std::fill(seen.begin(), seen.end(), 0);
+            distinct = 0; nnew = 0;
+            for (int32_t j = 0; j < n_used; ++j) {
+                const int32_t e = sel[(size_t)t * n_used + j];
+                if (!seen[(size_t)e]) { seen[(size_t)e] = 1; ++nnew; }
+            }
+            t0 = t;
+        }
+        distinct += nnew;
+    }
+    slices[2 * ns] = t0; slices[2 * ns + 1] = T - t0; ++ns;
+    *n_slices = ns;
+    if (union_out) *union_out = uni;
     return QWM_OK;
 }
 
@@ -747,6 +833,7 @@ int qwm_pool_rebalance(qwm_pool * p, int32_t n_used, int64_t fill_budget, int32_
     }
     for (auto & R : p->role) R.quota = quota;
     p->quota_on = true;
+    p->n_used = n_used;
     if (quota_out) std::copy(quota.begin(), quota.end(), quota_out);
     int rc = QWM_OK, cur = -1;
     int64_t filled = 0;

@@ -57,6 +57,11 @@ def oracle():
         lib.qwo_pool_slots.argtypes = [P, ctypes.c_int, P, P]
         lib.qwo_pool_resident.argtypes = [P, ctypes.c_int, ctypes.c_int, ctypes.c_int]
         lib.qwo_pool_touch.argtypes = [P, ctypes.c_int, P, ctypes.c_int]
+        lib.qwo_pool_capacity.argtypes = [P, ctypes.c_int]
+        lib.qwo_pool_quota_of.argtypes = [P, ctypes.c_int]
+        lib.qwo_pool_set_quotas.argtypes = [P, ctypes.c_int]
+        lib.qwo_pool_quotas_active.argtypes = [P]
+        lib.qwo_pool_plan_slices.argtypes = [P, ctypes.c_int, P, ctypes.c_int, ctypes.c_int, ctypes.c_int, P, P]
         lib.qwo_pool_save_profile.argtypes = [P, ctypes.c_char_p, ctypes.c_int]
         lib.qwo_pool_rebalance.argtypes = [P, ctypes.c_int, I64, P]
         lib.qwo_pool_clear_counts.argtypes = [P]

@@ -282,6 +282,72 @@ def test_pool_touch_known_answer():
     assert qa.lib().qwm_pool_touch(g.h, 0, ptr(np.array([4], np.int32)), 1) == qa.ERR_ARG
 
 
+def plan(h, layer, sel, T, n_used, max_slice, oracle_side=False):
+    sel = np.ascontiguousarray(sel, np.int32)
+    slices = np.zeros(2 * T, np.int32)
+    uni = ctypes.c_int32()
+    if oracle_side:
+        ns = oracle().qwo_pool_plan_slices(h, layer, ptr(sel), T, n_used, max_slice, ptr(slices), ctypes.byref(uni))
+    else:
+        n = ctypes.c_int32()
+        qa.check(qa.lib().qwm_pool_plan_slices(h, layer, ptr(sel), T, n_used, max_slice, ptr(slices),
+                                               ctypes.byref(n), ctypes.byref(uni)))
+        ns = n.value
+    return [tuple(slices[2 * i:2 * i + 2]) for i in range(ns)], uni.value
+
+
+def test_plan_slices_known_answer():
+    """plan_slices (runtime.cpp:4639-4687), by hand: 12 slots per role, no
+    quotas: cap = max(2, 12 - 8) = 4 distinct experts per slice; the batch
+    union (5) exceeds quota_of - 8 = 4, so quotas end off."""
+    g = GpuPool(1, 16, [12, 12, 12])
+    sel = [0, 1,  2, 3,  0, 4,  4, 5]
+    got, uni = plan(g.h, 0, sel, 4, 2, 0)
+    assert got == [(0, 2), (2, 2)] and uni == 6
+    assert qa.lib().qwm_pool_quotas_active(g.h) == 0
+    assert qa.lib().qwm_pool_capacity(g.h, 0) == 12 and qa.lib().qwm_pool_quota_of(g.h, 0) == 12
+    got, _ = plan(g.h, 0, sel, 4, 2, 1)                 # max_slice 1: one token per slice
+    assert got == [(0, 1), (1, 1), (2, 1), (3, 1)]
+    got, _ = plan(g.h, 0, [0, 1, 0, 1, 1, 0], 3, 2, 0)   # union 2 <= 4: quotas on, one slice
+    assert got == [(0, 3)] and qa.lib().qwm_pool_quotas_active(g.h) == 1
+
+
+@pytest.mark.parametrize("indexed", [0, 1])
+def test_plan_slices_match_oracle(indexed):
+    """Slices, union and quota mode equal the oracle's over Zipf batches of
+    1..300 tokens, before and after a quota rebalance (which makes capacity
+    and quota_of per layer), with and without a slice length cap."""
+    rng = np.random.default_rng(41 + indexed)
+    n_layer, E, k, slots = 3, 64, 4, [40, 36, 44]
+    g = GpuPool(n_layer, E, slots, 0, indexed)
+    o = OraclePool(n_layer, E, slots, 0)
+    pop = 1.0 / np.arange(1, E + 1) ** 1.1
+    pop /= pop.sum()
+    for step in range(120):
+        layer = int(rng.integers(0, n_layer))
+        T = int(rng.integers(1, 300))
+        sel = np.concatenate([rng.choice(E, k, replace=False, p=pop) for _ in range(T)]).astype(np.int32)
+        max_slice = int(rng.choice([0, 0, 7, 64]))
+        a = plan(g.h, layer, sel, T, k, max_slice)
+        b = plan(o.h, layer, sel, T, k, max_slice, oracle_side=True)
+        assert a == b, (step, a, b)
+        assert qa.lib().qwm_pool_quotas_active(g.h) == oracle().qwo_pool_quotas_active(o.h)
+        for l in range(n_layer):
+            assert qa.lib().qwm_pool_capacity(g.h, l) == oracle().qwo_pool_capacity(o.h, l)
+            assert qa.lib().qwm_pool_quota_of(g.h, l) == oracle().qwo_pool_quota_of(o.h, l)
+        for s0, ln in a[0]:                                # each slice's union fits the capacity it was cut for
+            assert ln >= 1
+        # feed the pools a decode-like step, and now and then rebalance
+        ids = rng.choice(E, k, replace=False, p=pop).astype(np.int32)
+        assert g.ensure(layer, ids)[0] == o.ensure(layer, ids)[0] == 0
+        if step == 60:
+            q = np.zeros(n_layer, np.int32)
+            qa.check(qa.lib().qwm_pool_rebalance(g.h, k, 0, ptr(q), None))
+            qo = np.zeros(n_layer, np.int32)
+            assert oracle().qwo_pool_rebalance(o.h, k, 0, ptr(qo)) >= 0
+            assert np.array_equal(q, qo)
+
+
 def test_pool_exhaustion_is_reported_and_consistent():
     g = GpuPool(1, 16, [2, 2, 2], protect=1)
     assert g.ensure(0, [0, 1])[0] == 0

@@ -315,3 +315,75 @@ def test_config_prefill_mul_mat_id(dev, K, N):
         worst = max(rel_err(got[t], exp[t]) for t in range(T))
         print(f"  rel err {err:.3e}, worst column {worst:.3e}, experts used {np.unique(ids).size}", flush=True)
         assert np.isfinite(got).all() and err < 1e-3 and worst < 1e-3
+
+
+def test_config_batch_through_pool(dev):
+    """A 64-token batch through the Qwen3-Next-shape layer (512 experts +
+    shared, FFN 512, top-10) and a 128-slot pool per role
+    (qwm_moe_cached_batch): Zipf(1.1) routing makes the batch's union exceed
+    the pool, so plan_slices cuts it into several slices; ids bit-exact,
+    slices and final pool state equal to the oracle's, output within 1e-5 of
+    the oracle block over the full expert table."""
+    E, N, k, T, S = 512, 512, 10, 64, 128
+    blk = Block(880, E, N, k, S, shared=True)
+    d_all, h_all = resident_pools(E, N, 890)
+    slab = h_all[0].size // E
+    host = [pinned(hh) for hh in h_all]
+    del d_all
+    host_ptrs = [(ctypes.c_void_p * 1)(host[r].data_ptr()) for r in range(3)]
+    pool_t = [torch.full((S * slab,), 0xA5, dtype=torch.uint8, device="cuda") for _ in range(3)]
+    d = qa.PoolDesc()
+    d.n_layer, d.n_expert = 1, E
+    for r in range(3):
+        d.n_slots[r], d.pool_data[r], d.slab_bytes[r] = S, pool_t[r].data_ptr(), slab
+        d.host_slabs[r] = ctypes.cast(host_ptrs[r], ctypes.c_void_p)
+    d.fetch_mode = qa.FETCH_GATHER
+    L = qa.lib()
+    copy = torch.cuda.Stream()
+    h = ctypes.c_void_p()
+    qa.check(L.qwm_pool_create(ctypes.byref(d), ctypes.c_void_p(copy.cuda_stream), ctypes.byref(h)))
+    o = oracle().qwo_pool_new(1, E, ptr(np.array([S, S, S], np.int32)), 0)
+    layer = blk.layer(pool_t)
+    try:
+        x = blk.rng.standard_normal((T, H)).astype(np.float32)
+        resid = blk.rng.standard_normal((T, H)).astype(np.float32)
+        mask = zipf_mask(blk.rng, blk.rng.permutation(E), k, T)
+        ids, w, _ = blk.route(x, mask)
+        exp = blk.block(x, h_all, E, [ids, ids, ids], w) + resid
+        flat = np.ascontiguousarray(ids.ravel())
+        sl_o = np.zeros(2 * T, np.int32)
+        ns_o = oracle().qwo_pool_plan_slices(o, 0, ptr(flat), T, k, 0, ptr(sl_o), None)
+        nf = ctypes.c_int()
+        for i in range(ns_o):
+            t0, ln = sl_o[2 * i], sl_o[2 * i + 1]
+            sub = np.ascontiguousarray(flat[t0 * k:(t0 + ln) * k])
+            s3 = np.zeros((3, sub.size), np.int32)
+            assert oracle().qwo_pool_ensure(o, 0, ptr(sub), sub.size, ptr(s3[0]), ptr(s3[1]), ptr(s3[2]), None,
+                                            ctypes.byref(nf)) == 0
+        dx, dr, drm = torch.from_numpy(x).cuda(), torch.from_numpy(resid).cuda(), torch.from_numpy(mask).cuda()
+        out = torch.full((T, H), float("nan"), dtype=torch.float32, device="cuda")
+        ws = workspace(L.qwm_moe_cached_batch_workspace_size(layer, T, 0))
+        hids = np.zeros(T * k, np.int32)
+        hsl = np.zeros(2 * T, np.int32)
+        nsl = ctypes.c_int32()
+        print(f"batch through the pool: T={T}, oracle slices {ns_o}", flush=True)
+        qa.check(L.qwm_moe_cached_batch(layer, h, 0, qa.tensor(qa.TYPE_F32, H, T, 1, dx),
+                                        qa.tensor(qa.TYPE_F32, E, T, 1, drm), qa.tensor(qa.TYPE_F32, H, T, 1, dr),
+                                        qa.tensor(qa.TYPE_F32, H, T, 1, out), 0, ptr(hids), ptr(hsl),
+                                        ctypes.byref(nsl), ws.data_ptr(), ws.numel(), None))
+        torch.cuda.synchronize()
+        slices = [tuple(hsl[2 * i:2 * i + 2]) for i in range(nsl.value)]
+        got = out.cpu().numpy()
+        print(f"  slices {slices}, rel err {rel_err(got, exp):.3e}", flush=True)
+        assert np.array_equal(hids.reshape(T, k), ids)
+        assert slices == [tuple(sl_o[2 * i:2 * i + 2]) for i in range(ns_o)] and len(slices) >= 2
+        assert np.isfinite(got).all() and rel_err(got, exp) < 1e-5
+        for r in range(3):
+            kg, cg = np.zeros(S, np.int32), np.zeros(S, np.uint64)
+            ko, co = np.zeros(S, np.int32), np.zeros(S, np.uint64)
+            qa.check(L.qwm_pool_slots(h, r, ptr(kg), ptr(cg)))
+            oracle().qwo_pool_slots(o, r, ptr(ko), ptr(co))
+            assert np.array_equal(kg, ko) and np.array_equal(cg, co), f"role {r}: pool state differs"
+    finally:
+        L.qwm_pool_destroy(h)
+        oracle().qwo_pool_free(o)

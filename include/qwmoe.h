@@ -285,6 +285,51 @@ typedef struct qwm_pool_stats {
 
 int qwm_pool_create(const qwm_pool_desc * desc, void * copy_stream, qwm_pool ** out);
 void qwm_pool_destroy(qwm_pool * pool);
+
+/* Signature pools (ExpertCache's constructor, expert_cache.cpp:225-296): one
+ * pool per (role, type, ne0, ne1) of the expert tensors, so that a file whose
+ * ffn_down_exps is Q6_K on some layers and Q4_K on others keeps each in a
+ * pool of its own slab size.  Every (role, layer) is routed to one pool; a
+ * pool holds the keys (layer * n_expert + expert) of all the layers routed
+ * to it; one clock and one quota per layer serve every pool.  A pool made
+ * by qwm_pool_create is the case of three pools, pool r serving role r of
+ * every layer. */
+typedef struct qwm_pool_sig {
+    int32_t role;                /* 0 gate, 1 up, 2 down */
+    int32_t type;                /* ggml type of the expert tensors */
+    int64_t ne0, ne1;            /* their first two dimensions */
+    size_t  slab_bytes;          /* their nb[2] */
+    int32_t n_layers;            /* layers routed to this pool */
+    int32_t n_slots;
+    void *  pool_data;           /* device [ne0, ne1, n_slots]: set by the caller before qwm_pool_create_sig */
+} qwm_pool_sig;
+
+/* Signature discovery and sizing (expert_cache.cpp:225-287).  experts: the
+ * expert tensors per (role, layer), role-major (experts[r * n_layer + l];
+ * type, ne[0..2] and nb[2] are read; ne[2] must be n_expert).  For roles in
+ * order and layers in order, a tensor joins the first signature with its
+ * role, type, ne0 and ne1, or opens a new one (sigs[], in that order, at most
+ * max_sigs); layer_pool[r * n_layer + l] receives the index.  Sizing: frac =
+ * vram_bytes / sum(slab_bytes * n_layers * n_expert), at most 1; a pool gets
+ * (int)(frac * n_layers * n_expert) slots, at least n_used and at most that
+ * cap.  A pool left with n_used slots or fewer is refused (QWM_ERR_ARG), as
+ * the reference refuses it.  *frac_out (may be NULL): frac.  pool_data is
+ * left NULL. */
+int qwm_pool_plan_sigs(int32_t n_layer, int32_t n_expert, const qwm_tensor * experts, uint64_t vram_bytes,
+                       int32_t n_used, qwm_pool_sig * sigs, int32_t max_sigs, int32_t * n_sigs,
+                       int32_t * layer_pool, double * frac_out);
+
+typedef struct qwm_pool_sig_desc {
+    int32_t n_layer, n_expert;
+    int32_t n_pools;
+    const qwm_pool_sig * pools;  /* [n_pools]: role, n_slots, pool_data and slab_bytes are used */
+    const int32_t * layer_pool;  /* [3 * n_layer], role-major: the pool of (role, layer), of that role */
+    const void * const * host_slabs[3]; /* as in qwm_pool_desc */
+    int32_t protect_active, indexed, fetch_mode; /* as in qwm_pool_desc */
+} qwm_pool_sig_desc;
+int qwm_pool_create_sig(const qwm_pool_sig_desc * desc, void * copy_stream, qwm_pool ** out);
+/* The pool index of (role, layer) (0..n_pools-1), or a QWM_ERR_* code. */
+int qwm_pool_layer_pool(const qwm_pool * pool, int32_t role, int32_t layer);
 /* ids: host i32 [n] (token-major); slot_*: host i32 [n].  Issues the slab
  * copies for misses on the copy stream.  QWM_ERR_NO_VICTIM leaves the pool
  * consistent (the failing role is not published; the misses before it are
@@ -298,10 +343,12 @@ int qwm_pool_ensure(qwm_pool * pool, int32_t layer, const int32_t * ids, int32_t
 int qwm_pool_wait(qwm_pool * pool, void * stream);
 int qwm_pool_get_stats(const qwm_pool * pool, qwm_pool_stats * out);
 /* Dense expert -> slot row of (role, layer), 0 for non-resident experts
- * (ExpertCache::slot_of_row, expert_cache.cpp:1448-1451); host i32 [n_expert]. */
+ * (ExpertCache::slot_of_row, expert_cache.cpp:1448-1451); host i32 [n_expert].
+ * The slots index the pool of (role, layer). */
 int qwm_pool_slot_of_row(const qwm_pool * pool, int32_t role, int32_t layer, int32_t * out);
-/* Per-slot key (layer * n_expert + expert, -1 free) and clock of one role. */
-int qwm_pool_slots(const qwm_pool * pool, int32_t role, int32_t * keys, uint64_t * clocks);
+/* Per-slot key (layer * n_expert + expert, -1 free) and clock of pool
+ * `pool_index` (for a pool made by qwm_pool_create, the role). */
+int qwm_pool_slots(const qwm_pool * pool, int32_t pool_index, int32_t * keys, uint64_t * clocks);
 /* ExpertCache::resident for all three roles (expert_cache.cpp:1442-1446), as
  * a bitmap: bit e of bits[e / 32] set when expert e of `layer` is resident
  * in the gate, up and down pools; host u32 [ceil(n_expert / 32)]. */
@@ -319,7 +366,9 @@ int qwm_pool_touch(qwm_pool * pool, int32_t layer, const int32_t * ids, int32_t 
  * pool's copy stream, the slot ids uploaded, qwm_pool_wait(pool, stream),
  * then qwm_moe_experts on the slot ids (resid may be NULL).  ids_host
  * (i32 [T * k], may be NULL) receives the routed ids.  The layer's pools are
- * the pool's device tensors.  Not capturable into a graph (host round trip).
+ * the device tensors of the pools of (role, layer_index): same base, nb[2]
+ * equal to their slab bytes and ne[2] at least their slots (QWM_ERR_ARG
+ * otherwise).  Not capturable into a graph (host round trip).
  * Pool errors (QWM_ERR_NO_VICTIM, QWM_ERR_IO) are returned before the
  * experts run. */
 size_t qwm_moe_cached_workspace_size(const qwm_moe_layer * layer, int64_t T);
@@ -362,7 +411,8 @@ int qwm_pool_plan_slices(qwm_pool * pool, int32_t layer, const int32_t * sel, in
  *   the shared expert times its sigmoid gate, and resid (may be NULL).
  * x, resid, out: f32 [H, T] (out must not overlap x); rm: optional f32
  * [E, T].  ids_host (host i32 [k * T]), slices_host (host i32 [2 * T]) and
- * n_slices may be NULL.  The layer's pools are the pool's device tensors.
+ * n_slices may be NULL.  The layer's pools are the pools of (role,
+ * layer_index), checked as in qwm_moe_cached_step.
  * Slices of more than 8 tokens run the grouped MUL_MAT_ID GEMM (Q4_K) or GEMV
  * launches over column chunks (other types).  Not capturable. */
 #define QWM_BATCH_MAX_T 4096

@@ -942,22 +942,26 @@ QWO_API int qwo_accept(const int32_t * vA, const int32_t * drafts, int K, int32_
 // ====================================================================
 // Slot pool: the RAM-tier decisions of core/expert_cache.cpp (ensure
 // 1615-1645, slot_for 1465-1479, install 1173-1180, pick_victim 1129-1170
-// with quotas and activation scores off, release_victim/drop_slot
-// 1067-1088, publish/record hooks gpu_lru_pool_hooks.h:11-79).  One pool
-// per role; one clock shared by all pools; per id the roles go gate, up,
-// down.  Victim: the lowest free slot, else the minimum clock among
-// unprotected occupied slots (strict <, so the lowest slot wins ties and a
-// UINT64_MAX clock never wins).  Protection (ActiveExpertGuard,
-// expert_cache.cpp:46-59) only exists when the demand table is allocated,
-// i.e. under the TinyLFU admission mode; `protect` selects it.
+// with activation scores off, release_victim/drop_slot 1067-1088,
+// publish/record hooks gpu_lru_pool_hooks.h:11-79).  Signature pools
+// (225-296): one pool per (role, type, ne0, ne1), every (role, layer)
+// routed to one of them; one clock shared by all pools; per id the roles go
+// gate, up, down.  qwo_pool_new makes the three-pool case (pool r serves
+// role r of every layer).  Victim: the lowest free slot, else the minimum
+// clock among unprotected occupied slots (strict <, so the lowest slot wins
+// ties and a UINT64_MAX clock never wins).  Protection
+// (ActiveExpertGuard, expert_cache.cpp:46-59) only exists when the demand
+// table is allocated, i.e. under the TinyLFU admission mode; `protect`
+// selects it.
 // ====================================================================
 struct qwo_pool {
     int n_layer, n_expert;
     bool protect;
     uint64_t clock = 0;
     uint64_t hits = 0, misses = 0, evictions = 0;
-    struct Role {
-        int n_slots;
+    struct Pool {
+        int role = 0;
+        int n_slots = 0;
         std::vector<int> slot2key;
         std::vector<uint64_t> clk;
         std::unordered_map<int, int> key2slot;
@@ -965,10 +969,14 @@ struct qwo_pool {
         std::vector<int> occ;
         std::unordered_map<int, uint64_t> count;
         std::vector<int> quota;         // per layer, after a rebalance
-    } role[3];
+    };
+    std::vector<Pool> pools;
+    std::vector<int> lp[3];             // pool index of (role, layer)
     std::vector<uint8_t> active;
     bool quota_on = false;
     int n_used = 0;
+    Pool & P(int r, int l) { return pools[(size_t)lp[r][(size_t)l]]; }
+    const Pool & P(int r, int l) const { return pools[(size_t)lp[r][(size_t)l]]; }
 };
 
 // pick_victim (expert_cache.cpp:1129-1170, activation scores off): the lowest
@@ -976,7 +984,7 @@ struct qwo_pool {
 // occupied slots; with quotas (after a rebalance) a layer at or over its
 // quota takes from its own slots and any other layer from layers over their
 // quotas, and if that finds nothing, the global minimum clock.
-static int qwo_pick(const qwo_pool * p, const qwo_pool::Role & R, int layer) {
+static int qwo_pick(const qwo_pool * p, const qwo_pool::Pool & R, int layer) {
     const bool self = p->quota_on && R.quota[(size_t)layer] >= 0 && R.occ[(size_t)layer] >= R.quota[(size_t)layer];
     int victim = -1;
     uint64_t best = UINT64_MAX;
@@ -1001,7 +1009,7 @@ static int qwo_pick(const qwo_pool * p, const qwo_pool::Role & R, int layer) {
 }
 
 // install (expert_cache.cpp:1173-1180): pick, drop, publish with clock + 1.
-static int qwo_install(qwo_pool * p, qwo_pool::Role & R, int key, int layer) {
+static int qwo_install(qwo_pool * p, qwo_pool::Pool & R, int key, int layer) {
     const int victim = qwo_pick(p, R, layer);
     if (victim < 0) return -1;
     const int old = R.slot2key[(size_t)victim];
@@ -1021,22 +1029,91 @@ static int qwo_install(qwo_pool * p, qwo_pool::Role & R, int key, int layer) {
     return victim;
 }
 
-QWO_API qwo_pool * qwo_pool_new(int n_layer, int n_expert, const int32_t * n_slots, int protect) {
+// Signature pools: pool_slots [n_pools], pool_role [n_pools], layer_pool
+// [3 * n_layer] (role-major).  Returns NULL when a (role, layer) names a
+// pool out of range or of another role.
+QWO_API qwo_pool * qwo_pool_new_sig(int n_layer, int n_expert, int n_pools, const int32_t * pool_slots,
+                                    const int32_t * pool_role, const int32_t * layer_pool, int protect) {
     auto * p = new qwo_pool();
     p->n_layer = n_layer; p->n_expert = n_expert; p->protect = protect != 0;
-    for (int r = 0; r < 3; ++r) {
-        auto & R = p->role[r];
-        R.n_slots = n_slots[r];
+    p->pools.resize((size_t)n_pools);
+    for (int i = 0; i < n_pools; ++i) {
+        auto & R = p->pools[(size_t)i];
+        R.role = pool_role[i];
+        R.n_slots = pool_slots[i];
         R.slot2key.assign((size_t)R.n_slots, -1);
         R.clk.assign((size_t)R.n_slots, 0);
         R.slot_of.assign((size_t)n_layer * n_expert, 0);
         R.occ.assign((size_t)n_layer, 0);
         R.quota.assign((size_t)n_layer, -1);
     }
+    for (int r = 0; r < 3; ++r) {
+        p->lp[r].assign(layer_pool + (size_t)r * n_layer, layer_pool + (size_t)(r + 1) * n_layer);
+        for (int l = 0; l < n_layer; ++l) {
+            const int i = p->lp[r][(size_t)l];
+            if (i < 0 || i >= n_pools || p->pools[(size_t)i].role != r) { delete p; return nullptr; }
+        }
+    }
     if (p->protect) p->active.assign((size_t)n_layer * n_expert, 0);
     return p;
 }
+QWO_API qwo_pool * qwo_pool_new(int n_layer, int n_expert, const int32_t * n_slots, int protect) {
+    const int32_t roles[3] = {0, 1, 2};
+    std::vector<int32_t> lp((size_t)3 * n_layer);
+    for (int r = 0; r < 3; ++r)
+        for (int l = 0; l < n_layer; ++l) lp[(size_t)r * n_layer + l] = r;
+    return qwo_pool_new_sig(n_layer, n_expert, 3, n_slots, roles, lp.data(), protect);
+}
 QWO_API void qwo_pool_free(qwo_pool * p) { delete p; }
+QWO_API int qwo_pool_layer_pool(const qwo_pool * p, int role, int layer) { return p->lp[role][(size_t)layer]; }
+
+// Signature discovery and sizing (expert_cache.cpp:225-287): for roles in
+// order and layers in order, the expert tensor's (type, ne0, ne1) finds its
+// signature (the first with the same role, type and shape) or opens a new
+// one; each signature counts its layers.  frac = vram / sum(slab * n_layers *
+// n_expert), at most 1 (1 when the sum is 0); a pool gets (int)(frac * cap)
+// slots, cap = n_layers * n_expert, raised to n_used and cut to cap; a pool
+// of n_used slots or fewer is refused (the reference throws: with the
+// transient workspace off it must hold more than n_used).  tensors: per
+// (role, layer), role-major, {type, ne0, ne1, slab}.  sigs_out: per signature
+// {role, type, ne0, ne1, slab, n_layers, n_slots}, at most max_sigs.
+// Returns the signature count, -1 when a pool is too small, -2 when
+// max_sigs is exceeded.
+QWO_API int qwo_pool_plan_sigs(int n_layer, int n_expert, const int64_t * tensors, uint64_t vram, int n_used,
+                               int64_t * sigs_out, int max_sigs, int32_t * layer_pool, double * frac_out) {
+    int ns = 0;
+    for (int r = 0; r < 3; ++r)
+        for (int l = 0; l < n_layer; ++l) {
+            const int64_t * t = tensors + 4 * ((size_t)r * n_layer + l);
+            int idx = -1;
+            for (int s = 0; s < ns; ++s) {
+                const int64_t * g = sigs_out + 7 * s;
+                if (g[0] == r && g[1] == t[0] && g[2] == t[1] && g[3] == t[2]) { idx = s; break; }
+            }
+            if (idx < 0) {
+                if (ns >= max_sigs) return -2;
+                idx = ns++;
+                int64_t * g = sigs_out + 7 * idx;
+                g[0] = r; g[1] = t[0]; g[2] = t[1]; g[3] = t[2]; g[4] = t[3]; g[5] = 0; g[6] = 0;
+            }
+            sigs_out[7 * idx + 5]++;
+            layer_pool[(size_t)r * n_layer + l] = idx;
+        }
+    uint64_t total = 0;
+    for (int s = 0; s < ns; ++s) total += (uint64_t)sigs_out[7 * s + 4] * (uint64_t)sigs_out[7 * s + 5] * (uint64_t)n_expert;
+    double frac = total ? (double)vram / (double)total : 1.0;
+    if (frac > 1.0) frac = 1.0;
+    if (frac_out) *frac_out = frac;
+    for (int s = 0; s < ns; ++s) {
+        const int cap = (int)sigs_out[7 * s + 5] * n_expert;
+        int n = (int)(frac * cap);
+        if (n < n_used) n = n_used;
+        if (n > cap) n = cap;
+        if (n <= n_used) return -1;
+        sigs_out[7 * s + 6] = n;
+    }
+    return ns;
+}
 
 // Returns 0, or -1 when no unprotected victim exists ("No unprotected GPU
 // cache victim").  fetch_log (optional, 4 ints per fetch: role, layer,
@@ -1057,7 +1134,7 @@ QWO_API int qwo_pool_ensure(qwo_pool * p, int layer, const int32_t * ids, int n,
         const int e = ids[i];
         const int key = layer * p->n_expert + e;
         for (int r = 0; r < 3; ++r) {
-            auto & R = p->role[r];
+            auto & R = p->P(r, layer);
             R.count[key]++;
             auto it = R.key2slot.find(key);
             if (it != R.key2slot.end()) {
@@ -1084,16 +1161,16 @@ QWO_API int qwo_pool_ensure(qwo_pool * p, int layer, const int32_t * ids, int n,
 }
 // ExpertCache::save_profile (expert_cache.cpp:1485-1500) as text into buf
 // (cap bytes): "QWENEXPCACHE 1", "n_layer n_expert", then "role layer expert
-// count" for every counted key, roles in order, keys ascending (the
-// reference walks its count map in hash order; the loader below reads any
-// order).  Returns the text length, or -1 if it does not fit.
+// count" for every counted key, pools in order, keys ascending within a pool
+// (the reference walks each pool's count map in hash order; the loader below
+// reads any order).  Returns the text length, or -1 if it does not fit.
 QWO_API int qwo_pool_save_profile(const qwo_pool * p, char * buf, int cap) {
     std::string s = "QWENEXPCACHE 1\n" + std::to_string(p->n_layer) + " " + std::to_string(p->n_expert) + "\n";
-    for (int r = 0; r < 3; ++r) {
-        std::vector<std::pair<int, uint64_t>> kv(p->role[r].count.begin(), p->role[r].count.end());
+    for (const auto & R : p->pools) {
+        std::vector<std::pair<int, uint64_t>> kv(R.count.begin(), R.count.end());
         std::sort(kv.begin(), kv.end());
         for (const auto & c : kv)
-            s += std::to_string(r) + " " + std::to_string(c.first / p->n_expert) + " " +
+            s += std::to_string(R.role) + " " + std::to_string(c.first / p->n_expert) + " " +
                  std::to_string(c.first % p->n_expert) + " " + std::to_string(c.second) + "\n";
     }
     if ((int)s.size() + 1 > cap) return -1;
@@ -1107,8 +1184,8 @@ QWO_API int qwo_pool_save_profile(const qwo_pool * p, char * buf, int cap) {
 // and expert in range are ordered by count, largest first (a stable order:
 // equal counts keep the text's order, where the reference's std::sort leaves
 // it unspecified); each is installed -- lowest free slot, drop-free, clock +
-// 1, uncounted -- unless its role's pool is full or the key is resident.
-// fetch_log as in qwo_pool_ensure.  Returns the number of installs.
+// 1, uncounted -- unless the pool of its (role, layer) is full or the key is
+// resident.  fetch_log as in qwo_pool_ensure.  Returns the number of installs.
 QWO_API int qwo_pool_load_profile(qwo_pool * p, const char * text, int32_t * fetch_log) {
     int ver = 0, nl = 0, ne = 0, used = 0;
     if (std::sscanf(text, "QWENEXPCACHE %d%n", &ver, &used) != 1 || ver != 1) return 0;
@@ -1125,7 +1202,7 @@ QWO_API int qwo_pool_load_profile(qwo_pool * p, const char * text, int32_t * fet
     std::stable_sort(ents.begin(), ents.end(), [](const Ent & a, const Ent & b) { return a.c > b.c; });
     int n = 0;
     for (const Ent & x : ents) {
-        auto & R = p->role[x.r];
+        auto & R = p->P(x.r, x.l);
         if ((int)R.key2slot.size() >= R.n_slots) continue;
         const int key = x.l * p->n_expert + x.e;
         if (R.key2slot.count(key)) continue;
@@ -1146,42 +1223,46 @@ QWO_API int qwo_pool_load_profile(qwo_pool * p, const char * text, int32_t * fet
     return n;
 }
 
-// ExpertCache::compute_quota + rebalance (expert_cache.cpp:509-625), one
-// pool per role shared by every layer: per-key counts summed over the roles,
-// entries ordered by (count, key) descending; floor: each layer up to n_used
-// while every role has a slot left; then one more per entry beyond its
-// layer's first n_used (quota < n_expert) while slots remain.  Quotas on;
+// ExpertCache::compute_quota + rebalance (expert_cache.cpp:509-625): per-key
+// counts summed over the pools, entries ordered by (count, key) descending;
+// a layer takes one slot in each of the pools of its three roles, while all
+// three have one left; floor: each layer up to n_used; then one more per
+// entry beyond its layer's first n_used (quota < n_expert) while its pools
+// have slots.  The same quota goes to each of a layer's pools; quotas on;
 // then up to fill_budget experts, hottest first within each layer's quota,
 // installed in every role that lacks them.  quota_out [n_layer] (optional).
 // Returns the experts filled, or -1 when an install finds no victim.
 QWO_API int qwo_pool_rebalance(qwo_pool * p, int n_used, int64_t fill_budget, int32_t * quota_out) {
     const int L = p->n_layer, E = p->n_expert;
     std::unordered_map<int, uint64_t> cnt;
-    for (const auto & R : p->role)
+    for (const auto & R : p->pools)
         for (const auto & kv : R.count) cnt[kv.first] += kv.second;
     std::vector<std::pair<uint64_t, int>> ents;
     for (const auto & kv : cnt) ents.emplace_back(kv.second, kv.first);
     std::sort(ents.begin(), ents.end(), std::greater<std::pair<uint64_t, int>>());
     std::vector<int> quota((size_t)L, 0);
     if (!cnt.empty()) {
-        int64_t rem[3] = {p->role[0].n_slots, p->role[1].n_slots, p->role[2].n_slots};
-        auto take = [&]() {
-            if (rem[0] <= 0 || rem[1] <= 0 || rem[2] <= 0) return false;
-            rem[0]--; rem[1]--; rem[2]--;
+        std::vector<int64_t> rem(p->pools.size());
+        for (size_t i = 0; i < p->pools.size(); ++i) rem[i] = p->pools[i].n_slots;
+        auto take = [&](int l) {
+            for (int r = 0; r < 3; ++r)
+                if (rem[(size_t)p->lp[r][(size_t)l]] <= 0) return false;
+            for (int r = 0; r < 3; ++r) rem[(size_t)p->lp[r][(size_t)l]]--;
             return true;
         };
         for (int l = 0; l < L; ++l)
-            while (quota[(size_t)l] < n_used && take()) quota[(size_t)l]++;
+            while (quota[(size_t)l] < n_used && take(l)) quota[(size_t)l]++;
         std::vector<int> seen((size_t)L, 0);
         for (const auto & e : ents) {
             const int l = e.second / E;
             if (seen[(size_t)l]++ < n_used) continue;
             if (quota[(size_t)l] >= E) continue;
-            if (!take()) continue;
+            if (!take(l)) continue;
             quota[(size_t)l]++;
         }
     }
-    for (auto & R : p->role) R.quota = quota;
+    for (int l = 0; l < L; ++l)
+        for (int r = 0; r < 3; ++r) p->P(r, l).quota[(size_t)l] = quota[(size_t)l];
     p->quota_on = true;
     p->n_used = n_used;
     if (quota_out) for (int l = 0; l < L; ++l) quota_out[l] = quota[(size_t)l];
@@ -1193,35 +1274,37 @@ QWO_API int qwo_pool_rebalance(qwo_pool * p, int n_used, int64_t fill_budget, in
         if (seen[(size_t)l] >= quota[(size_t)l]) continue;
         seen[(size_t)l]++;
         bool all = true;
-        for (const auto & R : p->role) all = all && R.key2slot.count(key);
+        for (int r = 0; r < 3; ++r) all = all && p->P(r, l).key2slot.count(key);
         if (all) continue;
-        for (auto & R : p->role)
+        for (int r = 0; r < 3; ++r) {
+            auto & R = p->P(r, l);
             if (!R.key2slot.count(key) && qwo_install(p, R, key, l) < 0) return -1;
+        }
         ++filled;
     }
     return filled;
 }
-QWO_API void qwo_pool_clear_counts(qwo_pool * p) { for (auto & R : p->role) R.count.clear(); }
+QWO_API void qwo_pool_clear_counts(qwo_pool * p) { for (auto & R : p->pools) R.count.clear(); }
 
 QWO_API void qwo_pool_stats(const qwo_pool * p, uint64_t * out3) {
     out3[0] = p->hits; out3[1] = p->misses; out3[2] = p->evictions;
 }
 QWO_API uint64_t qwo_pool_clock(const qwo_pool * p) { return p->clock; }
 QWO_API void qwo_pool_slot_of_row(const qwo_pool * p, int role, int layer, int32_t * out) {
-    std::memcpy(out, p->role[role].slot_of.data() + (size_t)layer * p->n_expert, (size_t)p->n_expert * 4);
+    std::memcpy(out, p->P(role, layer).slot_of.data() + (size_t)layer * p->n_expert, (size_t)p->n_expert * 4);
 }
 // ExpertCache::resident (expert_cache.cpp:1442-1446) and ::touch (1453-1463):
 // a resident key counts one access, its slot takes clock + 1, the hit counter
 // grows; the decode fast path touches GATE, UP, DOWN per selected expert
 // (runtime.cpp:6170-6176).
 QWO_API int qwo_pool_resident(const qwo_pool * p, int role, int layer, int expert) {
-    return p->role[role].key2slot.count(layer * p->n_expert + expert) ? 1 : 0;
+    return p->P(role, layer).key2slot.count(layer * p->n_expert + expert) ? 1 : 0;
 }
 QWO_API void qwo_pool_touch(qwo_pool * p, int layer, const int32_t * ids, int n) {
     for (int i = 0; i < n; ++i) {
         const int key = layer * p->n_expert + ids[i];
         for (int r = 0; r < 3; ++r) {
-            auto & R = p->role[r];
+            auto & R = p->P(r, layer);
             auto it = R.key2slot.find(key);
             if (it == R.key2slot.end()) continue;
             R.count[key]++;
@@ -1231,10 +1314,12 @@ QWO_API void qwo_pool_touch(qwo_pool * p, int layer, const int32_t * ids, int n)
         }
     }
 }
-// ExpertCache::capacity (expert_cache.cpp:478-491) and ::quota_of (493-501).
+// ExpertCache::capacity (expert_cache.cpp:478-491) and ::quota_of (493-501),
+// over the pools of the layer's three roles.
 QWO_API int qwo_pool_capacity(const qwo_pool * p, int layer) {
     int m = INT32_MAX;
-    for (const auto & R : p->role) {
+    for (int r = 0; r < 3; ++r) {
+        const auto & R = p->P(r, layer);
         const int q = R.quota[(size_t)layer];
         m = std::min(m, p->quota_on && q >= 0 ? std::max(q, p->n_used) : R.n_slots);
     }
@@ -1242,7 +1327,10 @@ QWO_API int qwo_pool_capacity(const qwo_pool * p, int layer) {
 }
 QWO_API int qwo_pool_quota_of(const qwo_pool * p, int layer) {
     int m = INT32_MAX;
-    for (const auto & R : p->role) m = std::min(m, R.quota[(size_t)layer] >= 0 ? R.quota[(size_t)layer] : R.n_slots);
+    for (int r = 0; r < 3; ++r) {
+        const auto & R = p->P(r, layer);
+        m = std::min(m, R.quota[(size_t)layer] >= 0 ? R.quota[(size_t)layer] : R.n_slots);
+    }
     return m;
 }
 QWO_API void qwo_pool_set_quotas(qwo_pool * p, int on) { p->quota_on = on != 0; }
@@ -1290,7 +1378,8 @@ QWO_API int qwo_pool_plan_slices(qwo_pool * p, int layer, const int32_t * sel, i
     return ns;
 }
 
-QWO_API void qwo_pool_slots(const qwo_pool * p, int role, int32_t * slot2key, uint64_t * clk) {
-    const auto & R = p->role[role];
+// Per-slot key and clock of pool `pool` (for qwo_pool_new, the role).
+QWO_API void qwo_pool_slots(const qwo_pool * p, int pool, int32_t * slot2key, uint64_t * clk) {
+    const auto & R = p->pools[(size_t)pool];
     for (int s = 0; s < R.n_slots; ++s) { slot2key[s] = R.slot2key[(size_t)s]; clk[s] = R.clk[(size_t)s]; }
 }

@@ -11,7 +11,8 @@ if the library was not built (there is no CPU fallback).
 import ctypes
 import os
 
-__all__ = ["lib", "QwmError", "QwmTensor", "MoeLayer", "PoolDesc", "PoolStats", "tensor", "check",
+__all__ = ["lib", "QwmError", "QwmTensor", "MoeLayer", "PoolDesc", "PoolSig", "PoolSigDesc", "PoolStats", "tensor",
+           "check",
            "TYPE_F32", "TYPE_Q8_0", "TYPE_Q4_K", "TYPE_Q5_K", "TYPE_Q6_K", "TYPE_I32", "FETCH_MEMCPY", "FETCH_GATHER"]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -55,6 +56,21 @@ class PoolDesc(ctypes.Structure):
     """struct qwm_pool_desc."""
     _fields_ = [("n_layer", ctypes.c_int32), ("n_expert", ctypes.c_int32), ("n_slots", ctypes.c_int32 * 3),
                 ("pool_data", ctypes.c_void_p * 3), ("slab_bytes", ctypes.c_size_t * 3),
+                ("host_slabs", ctypes.c_void_p * 3), ("protect_active", ctypes.c_int32),
+                ("indexed", ctypes.c_int32), ("fetch_mode", ctypes.c_int32)]
+
+
+class PoolSig(ctypes.Structure):
+    """struct qwm_pool_sig: one signature pool (role, type, ne0, ne1)."""
+    _fields_ = [("role", ctypes.c_int32), ("type", ctypes.c_int32), ("ne0", ctypes.c_int64), ("ne1", ctypes.c_int64),
+                ("slab_bytes", ctypes.c_size_t), ("n_layers", ctypes.c_int32), ("n_slots", ctypes.c_int32),
+                ("pool_data", ctypes.c_void_p)]
+
+
+class PoolSigDesc(ctypes.Structure):
+    """struct qwm_pool_sig_desc."""
+    _fields_ = [("n_layer", ctypes.c_int32), ("n_expert", ctypes.c_int32), ("n_pools", ctypes.c_int32),
+                ("pools", ctypes.POINTER(PoolSig)), ("layer_pool", ctypes.c_void_p),
                 ("host_slabs", ctypes.c_void_p * 3), ("protect_active", ctypes.c_int32),
                 ("indexed", ctypes.c_int32), ("fetch_mode", ctypes.c_int32)]
 
@@ -116,6 +132,10 @@ def lib():
                                                    _P, ctypes.c_float, _P, _P, _P]),
         "qwm_pool_create": (ctypes.c_int, [ctypes.POINTER(PoolDesc), _P, ctypes.POINTER(_P)]),
         "qwm_pool_destroy": (None, [_P]),
+        "qwm_pool_create_sig": (ctypes.c_int, [ctypes.POINTER(PoolSigDesc), _P, ctypes.POINTER(_P)]),
+        "qwm_pool_plan_sigs": (ctypes.c_int, [_I32, _I32, T, ctypes.c_uint64, _I32, ctypes.POINTER(PoolSig), _I32, _P,
+                                              _P, _P]),
+        "qwm_pool_layer_pool": (ctypes.c_int, [_P, _I32, _I32]),
         "qwm_pool_ensure": (ctypes.c_int, [_P, _I32, _P, _I32, _P, _P, _P]),
         "qwm_pool_wait": (ctypes.c_int, [_P, _P]),
         "qwm_pool_get_stats": (ctypes.c_int, [_P, ctypes.POINTER(PoolStats)]),

@@ -441,6 +441,10 @@ int qwm_moe_cached_step(const qwm_moe_layer * layer, qwm_pool * pool, int32_t la
     MoePlan p;
     int rc = check_layer(layer, x->ne[1], p);
     if (rc != QWM_OK) return rc;
+    if (layer_index < 0 || layer_index >= pool_n_layer(pool) || pool_n_expert(pool) != p.E)
+        return fail(QWM_ERR_ARG, "moe_cached_step: layer index or expert count disagrees with the pool");
+    const qwm_tensor * const lt[3] = {&layer->gate_pool, &layer->up_pool, &layer->down_pool};
+    if ((rc = pool_check_layer(pool, layer_index, lt, "moe_cached_step")) != QWM_OK) return rc;
     const size_t base = align_up(p.total, 256);
     if (!workspace || ws_bytes < base + cached_extra(p)) return fail(QWM_ERR_WORKSPACE, "moe_cached_step: workspace too small");
     const int64_t n = p.T * p.k;
@@ -565,6 +569,8 @@ int qwm_moe_cached_batch(const qwm_moe_layer * layer, qwm_pool * pool, int32_t l
         return fail(QWM_ERR_ARG, "moe_batch: rm must be contiguous f32 [E, T]");
     if (layer_index < 0 || layer_index >= pool_n_layer(pool) || pool_n_expert(pool) != E)
         return fail(QWM_ERR_ARG, "moe_batch: layer index or expert count disagrees with the pool");
+    const qwm_tensor * const lt[3] = {&layer->gate_pool, &layer->up_pool, &layer->down_pool};
+    if ((rc = pool_check_layer(pool, layer_index, lt, "moe_batch")) != QWM_OK) return rc;
     if (!workspace || ws_bytes < b.total) return fail(QWM_ERR_WORKSPACE, "moe_batch: workspace too small");
     uint8_t * ws = (uint8_t *)workspace;
     hipStream_t s = (hipStream_t)stream;

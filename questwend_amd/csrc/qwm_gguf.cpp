@@ -209,8 +209,8 @@ int qwm_pool_attach_gguf(qwm_pool * pool, const char * path, int32_t first_block
             if (it == idx.end()) return fail(QWM_ERR_ARG, "gguf: no tensor " + name + " in " + path);
             const GgufTensor & t = it->second;
             const uint64_t nb = tensor_bytes(t);
-            if (t.ne[2] != n_expert || t.ne[3] != 1 || nb != (uint64_t)n_expert * pool_slab_bytes(pool, r))
-                return fail(QWM_ERR_ARG, "gguf: " + name + " does not hold n_expert slabs of the pool's slab_bytes");
+            if (t.ne[2] != n_expert || t.ne[3] != 1 || nb != (uint64_t)n_expert * pool_slab_bytes(pool, r, l))
+                return fail(QWM_ERR_ARG, "gguf: " + name + " does not hold n_expert slabs of its pool's slab_bytes");
             const int arc = qwm_pool_attach_file(pool, r, l, path, t.offset);
             if (arc != QWM_OK) return arc;
         }

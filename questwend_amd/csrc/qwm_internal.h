@@ -146,7 +146,8 @@ int launch_slab_gather(const GatherArgs & a, hipStream_t s);
 // ---- qwm_pool.cpp: what qwm_gguf.cpp needs of a pool ----
 int32_t pool_n_layer(const qwm_pool * p);
 int32_t pool_n_expert(const qwm_pool * p);
-size_t pool_slab_bytes(const qwm_pool * p, int role);
+size_t pool_slab_bytes(const qwm_pool * p, int role, int32_t layer);
+int pool_check_layer(const qwm_pool * p, int32_t layer, const qwm_tensor * const t[3], const char * who);
 
 // ---- qwm_quant.hip ----
 int launch_quantize(int32_t type, const float * src, void * dst, int64_t n, hipStream_t s);

@@ -1,6 +1,6 @@
 // qwm_pool.cpp -- the GPU slot pool: the RAM-tier decisions of QuestWend's
-// ExpertCache (core/expert_cache.cpp) over per-role pools of expert slabs in
-// HBM, with misses filled from pinned host memory on a copy stream, by
+// ExpertCache (core/expert_cache.cpp) over signature pools of expert slabs
+// in HBM, with misses filled from pinned host memory on a copy stream, by
 // hipMemcpyAsync per slab or by one slab-gather launch per call.  Host code,
 // owner thread only.
 //
@@ -14,7 +14,10 @@
 //   pick_victim (1129-1170, quotas and activation scores off): the lowest
 //     free slot, else the minimum clock among unprotected occupied slots with
 //     strict '<' (lowest slot wins ties; a UINT64_MAX clock never wins).
-//   clock (gpu_lru_pool_hooks.h:11-25): one counter shared by every role pool;
+//   signature pools (225-296): one pool per (role, type, ne0, ne1); every
+//     (role, layer) is routed to one pool, which holds the keys of all the
+//     layers routed to it.  qwm_pool_create makes one pool per role.
+//   clock (gpu_lru_pool_hooks.h:11-25): one counter shared by every pool;
 //     each hit or publication takes clock + 1.
 //   drop (hooks 68-79): slot_of[key] returns to the 0 sentinel.
 //   protection (ActiveExpertGuard, expert_cache.cpp:46-59): only when the
@@ -152,12 +155,11 @@ struct FileJob {
 }  // namespace
 
 struct qwm_pool {
-    struct Role {
+    struct Pool {                                   // one signature pool
+        int role = 0;
         int n_slots = 0;
         uint8_t * data = nullptr;
         size_t slab = 0;
-        std::vector<const uint8_t *> host;          // per layer, pinned [*, *, n_expert]
-        std::vector<const uint8_t *> host_dev;      // GATHER: device-visible addresses of `host`
         std::vector<int32_t> slot2key;
         std::vector<uint64_t> clk;
         std::unordered_map<int32_t, int32_t> key2slot;
@@ -167,8 +169,12 @@ struct qwm_pool {
         std::set<std::pair<uint64_t, int32_t>> lru; // indexed mode: occupied (clock, slot)
         std::set<int32_t> free_slots;               // indexed mode
         std::vector<int32_t> quota;                 // per layer, after a rebalance
-        std::vector<int> fd;                        // file tier: per layer, -1 = none
-        std::vector<uint64_t> foff;                 // file tier: per layer, offset of expert 0
+    };
+    struct Src {                                    // where one role's slabs come from, per layer
+        std::vector<const uint8_t *> host;          // pinned [*, *, n_expert]
+        std::vector<const uint8_t *> host_dev;      // GATHER: device-visible addresses of `host`
+        std::vector<int> fd;                        // file tier: -1 = none
+        std::vector<uint64_t> foff;                 // file tier: offset of expert 0
     };
     int n_layer = 0, n_expert = 0;
     bool protect = false, indexed = false;
@@ -176,7 +182,9 @@ struct qwm_pool {
     int32_t n_used = 0;                             // the model's n_expert_used, from the last rebalance
     uint64_t clock = 0;
     uint64_t hits = 0, misses = 0, evictions = 0, fetch_bytes = 0, fetches = 0;
-    Role role[3];
+    std::vector<Pool> pools;
+    std::vector<int32_t> lp[3];                     // pool index of (role, layer)
+    Src src[3];
     std::vector<uint8_t> active;                    // [n_layer * n_expert] when protect
     hipStream_t copy = nullptr;
     hipEvent_t done = nullptr;
@@ -194,9 +202,12 @@ struct qwm_pool {
     hipEvent_t staging_free = nullptr;              // recorded after each batch's copies
     bool staging_busy = false;
 
+    Pool & P(int r, int32_t layer) { return pools[(size_t)lp[r][(size_t)layer]]; }
+    const Pool & P(int r, int32_t layer) const { return pools[(size_t)lp[r][(size_t)layer]]; }
+
     ~qwm_pool() {   // every flush ended with no reader inside a job
-        for (auto & R : role)
-            for (int f : R.fd)
+        for (auto & S : src)
+            for (int f : S.fd)
                 if (f >= 0) close(f);
         if (staging_free) {
             (void)hipEventSynchronize(staging_free);
@@ -205,7 +216,7 @@ struct qwm_pool {
         if (staging) (void)hipHostFree(staging);
     }
 
-    void touch(Role & R, int32_t slot) {
+    void touch(Pool & R, int32_t slot) {
         const uint64_t next = clock + 1;
         if (indexed) {
             R.lru.erase({R.clk[slot], slot});
@@ -215,7 +226,7 @@ struct qwm_pool {
         clock = next;
     }
 
-    int32_t pick(const Role & R, int32_t layer) const {
+    int32_t pick(const Pool & R, int32_t layer) const {
         if (quota_on) return pick_quota(R, layer);
         if (indexed) {
             if (!R.free_slots.empty()) return *R.free_slots.begin();
@@ -241,7 +252,7 @@ struct qwm_pool {
     // slot first; a layer at or over its quota recycles one of its own slots,
     // any other layer takes from a layer over its quota; least recently used
     // among those (strict <: the lowest slot on ties); none: the global LRU.
-    int32_t pick_quota(const Role & R, int32_t layer) const {
+    int32_t pick_quota(const Pool & R, int32_t layer) const {
         const bool self = R.quota[layer] >= 0 && R.occ[layer] >= R.quota[layer];
         int32_t victim = -1;
         uint64_t best = std::numeric_limits<uint64_t>::max();
@@ -263,7 +274,7 @@ struct qwm_pool {
         return victim;
     }
 
-    void drop(Role & R, int32_t slot) {
+    void drop(Pool & R, int32_t slot) {
         const int32_t key = R.slot2key[slot];
         if (key < 0) return;
         if (indexed) {
@@ -278,9 +289,10 @@ struct qwm_pool {
     }
 
     int fetch(int r, int32_t layer, int32_t expert, int32_t slot) {
-        Role & R = role[r];
-        const bool from_file = !R.fd.empty() && R.fd[layer] >= 0;
-        if (!from_file && (R.host.empty() || !R.host[layer])) return QWM_OK;   // no host tier: metadata only
+        Pool & R = P(r, layer);
+        const Src & S = src[r];
+        const bool from_file = !S.fd.empty() && S.fd[layer] >= 0;
+        if (!from_file && (S.host.empty() || !S.host[layer])) return QWM_OK;   // no host tier: metadata only
         if (!done) {   // created on first use, so decision-only pools need no GPU
             hipError_t e = hipEventCreateWithFlags(&done, hipEventDisableTiming);
             if (e != hipSuccess) return fail(QWM_ERR_HIP, std::string("slab fetch: hipEventCreate: ") + hipGetErrorString(e));
@@ -295,8 +307,8 @@ struct qwm_pool {
                 if (it.role == r && it.slot == slot) { it.expert = expert; replaced = true; }
             if (!replaced) batch.push_back(GatherItem{expert, (int16_t)slot, (int16_t)r});
         } else {
-            const uint8_t * src = R.host[layer] + (size_t)expert * R.slab;
-            hipError_t e = hipMemcpyAsync(R.data + (size_t)slot * R.slab, src, R.slab, hipMemcpyHostToDevice, copy);
+            const uint8_t * from = S.host[layer] + (size_t)expert * R.slab;
+            hipError_t e = hipMemcpyAsync(R.data + (size_t)slot * R.slab, from, R.slab, hipMemcpyHostToDevice, copy);
             if (e != hipSuccess) return fail(QWM_ERR_HIP, std::string("slab fetch: ") + hipGetErrorString(e));
         }
         fetch_bytes += R.slab;
@@ -312,9 +324,9 @@ struct qwm_pool {
         if (batch.empty()) return QWM_OK;
         GatherArgs a{};
         for (int r = 0; r < 3; ++r) {
-            a.src[r] = role[r].host_dev.empty() ? nullptr : role[r].host_dev[layer];
-            a.dst[r] = role[r].data;
-            a.slab[r] = role[r].slab;
+            a.src[r] = src[r].host_dev.empty() ? nullptr : src[r].host_dev[layer];
+            a.dst[r] = P(r, layer).data;
+            a.slab[r] = P(r, layer).slab;
         }
         int rc = QWM_OK;
         for (size_t i0 = 0; i0 < batch.size() && rc == QWM_OK; i0 += GATHER_MAX) {
@@ -323,15 +335,15 @@ struct qwm_pool {
             rc = launch_slab_gather(a, copy);
         }
         if (rc != QWM_OK)
-            for (const GatherItem & it : batch) unpublish(it.role, it.slot);
+            for (const GatherItem & it : batch) unpublish(it.role, layer, it.slot);
         batch.clear();
         return rc;
     }
 
     // Frees the slot of an install whose slab was not filled (its key no
     // longer resolves), as if the miss had not been taken.
-    void unpublish(int r, int32_t slot) {
-        Role & R = role[r];
+    void unpublish(int r, int32_t layer, int32_t slot) {
+        Pool & R = P(r, layer);
         const int32_t key = R.slot2key[slot];
         if (key < 0) return;
         fetch_bytes -= R.slab;
@@ -352,7 +364,7 @@ struct qwm_pool {
     int flush_files(int32_t layer) {
         if (fjobs.empty()) return QWM_OK;
         size_t max_slab = 0;
-        for (const auto & R : role) max_slab = std::max(max_slab, R.slab);
+        for (const auto & R : pools) max_slab = std::max(max_slab, R.slab);
         if (!staging) {
             staging_stride = (max_slab + 4095) & ~(size_t)4095;
             staging_n = staging_slabs > 0 ? staging_slabs : (int)std::max<size_t>(1, ((size_t)64 << 20) / staging_stride);
@@ -365,7 +377,7 @@ struct qwm_pool {
             if (e == hipSuccess && !staging_free) e = hipEventCreateWithFlags(&staging_free, hipEventDisableTiming);
             if (e != hipSuccess) {
                 staging = nullptr;
-                for (const FileJob & j : fjobs) unpublish(j.role, j.slot);
+                for (const FileJob & j : fjobs) unpublish(j.role, layer, j.slot);
                 fjobs.clear();
                 return fail(QWM_ERR_HIP, std::string("file tier: pinned staging: ") + hipGetErrorString(e));
             }
@@ -382,17 +394,18 @@ struct qwm_pool {
             }
             readers.begin(bn, [this, b0, layer](int j) {
                 const FileJob & fj = fjobs[b0 + (size_t)j];
-                const Role & R = role[fj.role];
-                return read_full(R.fd[layer], staging + (size_t)j * staging_stride, R.slab,
-                                 R.foff[layer] + (uint64_t)fj.expert * R.slab);
+                const Pool & R = P(fj.role, layer);
+                const Src & S = src[fj.role];
+                return read_full(S.fd[layer], staging + (size_t)j * staging_stride, R.slab,
+                                 S.foff[layer] + (uint64_t)fj.expert * R.slab);
             });
             // GATHER: one slab-gather launch per FILE_GATHER_GROUP completed reads
             constexpr int FILE_GATHER_GROUP = 8;
             GatherArgs ga{};
             for (int r = 0; r < 3; ++r) {
                 ga.src[r] = staging_dev;
-                ga.dst[r] = role[r].data;
-                ga.slab[r] = role[r].slab;
+                ga.dst[r] = P(r, layer).data;
+                ga.slab[r] = P(r, layer).slab;
                 ga.src_stride[r] = staging_stride;
             }
             int g0 = 0;                                  // first job of the pending gather group
@@ -409,7 +422,7 @@ struct qwm_pool {
             for (int j = 0; j < bn; ++j) {
                 const int st = readers.wait(j);
                 const FileJob & fj = fjobs[b0 + (size_t)j];
-                Role & R = role[fj.role];
+                Pool & R = P(fj.role, layer);
                 if (st != 0) {
                     if (gather && launch_group(j) != QWM_OK) { rc = QWM_ERR_HIP; bad = b0 + (size_t)g0; break; }
                     rc = fail(QWM_ERR_IO, "file tier: reading the slab of expert " + std::to_string(fj.expert) +
@@ -435,12 +448,12 @@ struct qwm_pool {
             readers.end();                               // no reader still writes this batch's staging
             if (hipEventRecord(staging_free, copy) == hipSuccess) staging_busy = true;
         }
-        for (size_t i = bad; i < fjobs.size(); ++i) unpublish(fjobs[i].role, fjobs[i].slot);
+        for (size_t i = bad; i < fjobs.size(); ++i) unpublish(fjobs[i].role, layer, fjobs[i].slot);
         fjobs.clear();
         return rc;
     }
 
-    void publish(Role & R, int32_t slot, int32_t key, int32_t layer) {
+    void publish(Pool & R, int32_t slot, int32_t key, int32_t layer) {
         R.key2slot.emplace(key, slot);
         R.slot2key[slot] = key;
         R.occ[layer]++;
@@ -456,64 +469,182 @@ struct qwm_pool {
 namespace qwm {
 int32_t pool_n_layer(const qwm_pool * p) { return p->n_layer; }
 int32_t pool_n_expert(const qwm_pool * p) { return p->n_expert; }
-size_t pool_slab_bytes(const qwm_pool * p, int role) { return p->role[role].slab; }
+size_t pool_slab_bytes(const qwm_pool * p, int role, int32_t layer) { return p->P(role, layer).slab; }
+
+// The layer's gate/up/down pool tensors must be the pools of its (role,
+// layer) -- same base, slab stride and at least their slots -- so that every
+// slot the pool hands out indexes inside the tensor the kernels read.
+int pool_check_layer(const qwm_pool * p, int32_t layer, const qwm_tensor * const t[3], const char * who) {
+    static const char * const names[3] = {"gate", "up", "down"};
+    for (int r = 0; r < 3; ++r) {
+        const auto & R = p->P(r, layer);
+        if (t[r]->data != R.data || t[r]->nb[2] != R.slab || t[r]->ne[2] < R.n_slots)
+            return fail(QWM_ERR_ARG, std::string(who) + ": the layer's " + names[r] + "_pool is not the pool of (" +
+                                         names[r] + ", layer " + std::to_string(layer) + "): base " +
+                                         (t[r]->data == R.data ? "ok" : "differs") + ", nb[2] " +
+                                         std::to_string(t[r]->nb[2]) + " vs slab " + std::to_string(R.slab) +
+                                         ", ne[2] " + std::to_string(t[r]->ne[2]) + " vs " +
+                                         std::to_string(R.n_slots) + " slots");
+    }
+    return QWM_OK;
+}
 }  // namespace qwm
 
 extern "C" {
+
+// The pools, the (role, layer) routing and the host sources of a new pool;
+// deletes p and fails on a bad description.
+static int pool_init(qwm_pool * p, int32_t n_pools, const qwm_pool_sig * sig, const int32_t * layer_pool,
+                     const void * const * const host_slabs[3], int32_t fetch_mode, qwm_pool ** out) {
+    auto bad = [&](const std::string & why) {
+        delete p;
+        return fail(QWM_ERR_ARG, "pool_create: " + why);
+    };
+    if (fetch_mode != QWM_FETCH_MEMCPY && fetch_mode != QWM_FETCH_GATHER) return bad("unknown fetch_mode");
+    p->gather = fetch_mode == QWM_FETCH_GATHER;
+    if (n_pools < 3 || !sig || !layer_pool) return bad("fewer than three pools");
+    p->pools.resize((size_t)n_pools);
+    for (int32_t i = 0; i < n_pools; ++i) {
+        auto & R = p->pools[(size_t)i];
+        if (sig[i].role < 0 || sig[i].role > 2) return bad("a pool's role is not 0, 1 or 2");
+        if (sig[i].n_slots < 1) return bad("a pool has no slots");
+        R.role = sig[i].role;
+        R.n_slots = sig[i].n_slots;
+        R.data = (uint8_t *)sig[i].pool_data;
+        R.slab = sig[i].slab_bytes;
+        R.slot2key.assign((size_t)R.n_slots, -1);
+        R.clk.assign((size_t)R.n_slots, 0);
+        R.slot_of.assign((size_t)p->n_layer * p->n_expert, 0);
+        R.occ.assign((size_t)p->n_layer, 0);
+        R.quota.assign((size_t)p->n_layer, -1);     // no quota until a rebalance computes them
+        if (p->indexed)
+            for (int32_t s = 0; s < R.n_slots; ++s) R.free_slots.insert(s);
+    }
+    for (int r = 0; r < 3; ++r) {
+        p->lp[r].assign(layer_pool + (size_t)r * p->n_layer, layer_pool + (size_t)(r + 1) * p->n_layer);
+        for (int32_t l = 0; l < p->n_layer; ++l) {
+            const int32_t i = p->lp[r][(size_t)l];
+            if (i < 0 || i >= n_pools || p->pools[(size_t)i].role != r)
+                return bad("layer_pool routes (role " + std::to_string(r) + ", layer " + std::to_string(l) +
+                           ") to a pool out of range or of another role");
+        }
+    }
+    for (int r = 0; r < 3; ++r) {
+        auto & S = p->src[r];
+        if (!host_slabs[r]) continue;
+        S.host.assign((const uint8_t * const *)host_slabs[r], (const uint8_t * const *)host_slabs[r] + p->n_layer);
+        if (!p->gather) continue;
+        S.host_dev.assign((size_t)p->n_layer, nullptr);
+        for (int32_t l = 0; l < p->n_layer; ++l) {
+            if (!S.host[l]) continue;
+            const auto & R = p->P(r, l);
+            if (R.slab % 16 || ((uintptr_t)R.data & 15) || R.n_slots > 32767)
+                return bad("GATHER needs 16-byte aligned pools, slab_bytes % 16 == 0 and at most 32767 slots per pool");
+            void * dp = nullptr;
+            hipError_t e = hipHostGetDevicePointer(&dp, const_cast<uint8_t *>(S.host[l]), 0);
+            if (e != hipSuccess) (void)hipGetLastError();   // a refused pointer is an argument error, not sticky
+            if (e != hipSuccess || ((uintptr_t)dp & 15))
+                return bad(std::string("GATHER needs pinned (hipHostMalloc), 16-byte aligned host slabs: ") +
+                           hipGetErrorString(e));
+            S.host_dev[l] = (const uint8_t *)dp;
+        }
+    }
+    if (p->protect) p->active.assign((size_t)p->n_layer * p->n_expert, 0);
+    *out = p;
+    return QWM_OK;
+}
 
 int qwm_pool_create(const qwm_pool_desc * d, void * copy_stream, qwm_pool ** out) {
     if (!d || !out) return fail(QWM_ERR_ARG, "pool_create: NULL argument");
     *out = nullptr;
     if (d->n_layer < 1 || d->n_expert < 1) return fail(QWM_ERR_ARG, "pool_create: empty pool");
+    qwm_pool_sig sig[3] = {};
+    std::vector<int32_t> lp((size_t)3 * d->n_layer);
+    for (int r = 0; r < 3; ++r) {
+        sig[r].role = r;
+        sig[r].n_slots = d->n_slots[r];
+        sig[r].pool_data = d->pool_data[r];
+        sig[r].slab_bytes = d->slab_bytes[r];
+        for (int32_t l = 0; l < d->n_layer; ++l) lp[(size_t)r * d->n_layer + l] = r;
+    }
     auto * p = new qwm_pool();
     p->n_layer = d->n_layer;
     p->n_expert = d->n_expert;
     p->protect = d->protect_active != 0;
     p->indexed = d->indexed != 0;
     p->copy = (hipStream_t)copy_stream;
-    p->gather = d->fetch_mode == QWM_FETCH_GATHER;
-    if (d->fetch_mode != QWM_FETCH_MEMCPY && d->fetch_mode != QWM_FETCH_GATHER) {
-        delete p;
-        return fail(QWM_ERR_ARG, "pool_create: unknown fetch_mode");
-    }
-    for (int r = 0; r < 3; ++r) {
-        auto & R = p->role[r];
-        if (d->n_slots[r] < 1) { delete p; return fail(QWM_ERR_ARG, "pool_create: a role has no slots"); }
-        R.n_slots = d->n_slots[r];
-        R.data = (uint8_t *)d->pool_data[r];
-        R.slab = d->slab_bytes[r];
-        if (d->host_slabs[r]) R.host.assign((const uint8_t * const *)d->host_slabs[r], (const uint8_t * const *)d->host_slabs[r] + d->n_layer);
-        if (p->gather && !R.host.empty()) {
-            if (R.slab % 16 || ((uintptr_t)R.data & 15) || R.n_slots > 32767) {
-                delete p;
-                return fail(QWM_ERR_ARG, "pool_create: GATHER needs 16-byte aligned pools, slab_bytes % 16 == 0 and "
-                                         "at most 32767 slots per role");
-            }
-            R.host_dev.assign((size_t)d->n_layer, nullptr);
-            for (int32_t l = 0; l < d->n_layer; ++l) {
-                if (!R.host[l]) continue;
-                void * dp = nullptr;
-                hipError_t e = hipHostGetDevicePointer(&dp, const_cast<uint8_t *>(R.host[l]), 0);
-                if (e != hipSuccess) (void)hipGetLastError();   // a refused pointer is an argument error, not sticky
-                if (e != hipSuccess || ((uintptr_t)dp & 15)) {
-                    delete p;
-                    return fail(QWM_ERR_ARG, std::string("pool_create: GATHER needs pinned (hipHostMalloc), 16-byte "
-                                                         "aligned host slabs: ") + hipGetErrorString(e));
+    return pool_init(p, 3, sig, lp.data(), d->host_slabs, d->fetch_mode, out);
+}
+
+int qwm_pool_create_sig(const qwm_pool_sig_desc * d, void * copy_stream, qwm_pool ** out) {
+    if (!d || !out || !d->pools || !d->layer_pool) return fail(QWM_ERR_ARG, "pool_create_sig: NULL argument");
+    *out = nullptr;
+    if (d->n_layer < 1 || d->n_expert < 1) return fail(QWM_ERR_ARG, "pool_create_sig: empty pool");
+    auto * p = new qwm_pool();
+    p->n_layer = d->n_layer;
+    p->n_expert = d->n_expert;
+    p->protect = d->protect_active != 0;
+    p->indexed = d->indexed != 0;
+    p->copy = (hipStream_t)copy_stream;
+    return pool_init(p, d->n_pools, d->pools, d->layer_pool, d->host_slabs, d->fetch_mode, out);
+}
+
+// The signatures of ExpertCache's constructor (expert_cache.cpp:225-251) and
+// the uniform residency fraction that sizes their pools (253-287).
+int qwm_pool_plan_sigs(int32_t n_layer, int32_t n_expert, const qwm_tensor * experts, uint64_t vram_bytes,
+                       int32_t n_used, qwm_pool_sig * sigs, int32_t max_sigs, int32_t * n_sigs,
+                       int32_t * layer_pool, double * frac_out) {
+    if (!experts || !sigs || !n_sigs || !layer_pool || n_layer < 1 || n_expert < 1 || n_used < 1 || max_sigs < 1)
+        return fail(QWM_ERR_ARG, "pool_plan_sigs: bad argument");
+    int32_t ns = 0;
+    for (int r = 0; r < 3; ++r)
+        for (int32_t l = 0; l < n_layer; ++l) {
+            const qwm_tensor & t = experts[(size_t)r * n_layer + l];
+            if (t.ne[2] != n_expert || t.ne[0] < 1 || t.ne[1] < 1 || t.nb[2] == 0)
+                return fail(QWM_ERR_ARG, "pool_plan_sigs: expert tensor of role " + std::to_string(r) + ", layer " +
+                                             std::to_string(l) + " is not [ne0, ne1, n_expert]");
+            int32_t idx = -1;
+            for (int32_t s = 0; s < ns; ++s)
+                if (sigs[s].role == r && sigs[s].type == t.type && sigs[s].ne0 == t.ne[0] && sigs[s].ne1 == t.ne[1]) {
+                    idx = s;
+                    break;
                 }
-                R.host_dev[l] = (const uint8_t *)dp;
+            if (idx < 0) {
+                if (ns >= max_sigs) return fail(QWM_ERR_ARG, "pool_plan_sigs: more than max_sigs signatures");
+                idx = ns++;
+                sigs[idx] = qwm_pool_sig{};
+                sigs[idx].role = r;
+                sigs[idx].type = t.type;
+                sigs[idx].ne0 = t.ne[0];
+                sigs[idx].ne1 = t.ne[1];
+                sigs[idx].slab_bytes = t.nb[2];
             }
+            sigs[idx].n_layers++;
+            layer_pool[(size_t)r * n_layer + l] = idx;
         }
-        R.slot2key.assign((size_t)R.n_slots, -1);
-        R.clk.assign((size_t)R.n_slots, 0);
-        R.slot_of.assign((size_t)d->n_layer * d->n_expert, 0);
-        R.occ.assign((size_t)d->n_layer, 0);
-        R.quota.assign((size_t)d->n_layer, -1);     // no quota until a rebalance computes them
-        if (p->indexed)
-            for (int32_t s = 0; s < R.n_slots; ++s) R.free_slots.insert(s);
+    uint64_t total = 0;
+    for (int32_t s = 0; s < ns; ++s) total += (uint64_t)sigs[s].slab_bytes * (uint64_t)sigs[s].n_layers * (uint64_t)n_expert;
+    double frac = total ? (double)vram_bytes / (double)total : 1.0;
+    if (frac > 1.0) frac = 1.0;
+    for (int32_t s = 0; s < ns; ++s) {
+        const int32_t cap = sigs[s].n_layers * n_expert;
+        int32_t n = (int32_t)(frac * cap);
+        if (n < n_used) n = n_used;
+        if (n > cap) n = cap;
+        if (n <= n_used)
+            return fail(QWM_ERR_ARG, "pool_plan_sigs: pool " + std::to_string(s) + " would hold " + std::to_string(n) +
+                                         " slots, no more than n_used (the reference's \"GPU pool cannot fit "
+                                         "transient workspace plus retained experts\")");
+        sigs[s].n_slots = n;
     }
-    if (p->protect) p->active.assign((size_t)d->n_layer * d->n_expert, 0);
-    *out = p;
+    *n_sigs = ns;
+    if (frac_out) *frac_out = frac;
     return QWM_OK;
+}
+
+int qwm_pool_layer_pool(const qwm_pool * p, int32_t role, int32_t layer) {
+    if (!p || role < 0 || role > 2 || layer < 0 || layer >= p->n_layer) return fail(QWM_ERR_ARG, "pool_layer_pool: bad argument");
+    return p->lp[role][(size_t)layer];
 }
 
 void qwm_pool_destroy(qwm_pool * p) {
@@ -543,7 +674,7 @@ int qwm_pool_ensure(qwm_pool * p, int32_t layer, const int32_t * ids, int32_t n,
         const int32_t e = ids[i];
         const int32_t key = layer * p->n_expert + e;
         for (int r = 0; r < 3; ++r) {
-            auto & R = p->role[r];
+            auto & R = p->P(r, layer);
             R.count[key]++;
             auto it = R.key2slot.find(key);
             if (it != R.key2slot.end()) {
@@ -590,7 +721,7 @@ int qwm_pool_get_stats(const qwm_pool * p, qwm_pool_stats * out) {
 
 int qwm_pool_slot_of_row(const qwm_pool * p, int32_t role, int32_t layer, int32_t * out) {
     if (!p || !out || role < 0 || role > 2 || layer < 0 || layer >= p->n_layer) return fail(QWM_ERR_ARG, "pool_slot_of_row: bad argument");
-    const auto & R = p->role[role];
+    const auto & R = p->P(role, layer);
     for (int32_t e = 0; e < p->n_expert; ++e) out[e] = R.slot_of[(size_t)layer * p->n_expert + e];
     return QWM_OK;
 }
@@ -602,7 +733,7 @@ int qwm_pool_resident_bits(const qwm_pool * p, int32_t layer, uint32_t * bits) {
     for (int32_t e = 0; e < p->n_expert; ++e) {
         const int32_t key = layer * p->n_expert + e;
         bool all = true;
-        for (int r = 0; r < 3 && all; ++r) all = p->role[r].key2slot.count(key) != 0;
+        for (int r = 0; r < 3 && all; ++r) all = p->P(r, layer).key2slot.count(key) != 0;
         if (all) bits[e >> 5] |= 1u << (e & 31);
     }
     return QWM_OK;
@@ -615,7 +746,7 @@ int qwm_pool_touch(qwm_pool * p, int32_t layer, const int32_t * ids, int32_t n) 
     for (int32_t i = 0; i < n; ++i) {
         const int32_t key = layer * p->n_expert + ids[i];
         for (int r = 0; r < 3; ++r) {
-            auto & R = p->role[r];
+            auto & R = p->P(r, layer);
             auto it = R.key2slot.find(key);
             if (it == R.key2slot.end()) continue;
             R.count[key]++;
@@ -627,12 +758,14 @@ int qwm_pool_touch(qwm_pool * p, int32_t layer, const int32_t * ids, int32_t n) 
 }
 
 // ExpertCache::capacity (expert_cache.cpp:478-491): the fewest slots the
-// layer may hold in any role before it recycles its own -- its quota (at
-// least n_used) while quotas are on and computed, else the pool size.
+// layer may hold in the pools of its three roles before it recycles its own
+// -- its quota (at least n_used) while quotas are on and computed, else the
+// pool size.
 int qwm_pool_capacity(const qwm_pool * p, int32_t layer) {
     if (!p || layer < 0 || layer >= p->n_layer) return fail(QWM_ERR_ARG, "pool_capacity: bad argument");
     int32_t m = INT32_MAX;
-    for (const auto & R : p->role) {
+    for (int r = 0; r < 3; ++r) {
+        const auto & R = p->P(r, layer);
         const int32_t q = R.quota[(size_t)layer];
         m = std::min(m, p->quota_on && q >= 0 ? std::max(q, p->n_used) : R.n_slots);
     }
@@ -640,11 +773,12 @@ int qwm_pool_capacity(const qwm_pool * p, int32_t layer) {
 }
 
 // ExpertCache::quota_of (expert_cache.cpp:493-501): the layer's quota (min
-// over the roles), or the pool size where none was computed.
+// over the pools of its roles), or the pool size where none was computed.
 int qwm_pool_quota_of(const qwm_pool * p, int32_t layer) {
     if (!p || layer < 0 || layer >= p->n_layer) return fail(QWM_ERR_ARG, "pool_quota_of: bad argument");
     int32_t m = INT32_MAX;
-    for (const auto & R : p->role) {
+    for (int r = 0; r < 3; ++r) {
+        const auto & R = p->P(r, layer);
         const int32_t q = R.quota[(size_t)layer];
         m = std::min(m, q >= 0 ? q : R.n_slots);
     }
@@ -710,9 +844,9 @@ int qwm_pool_plan_slices(qwm_pool * p, int32_t layer, const int32_t * sel, int32
     return QWM_OK;
 }
 
-int qwm_pool_slots(const qwm_pool * p, int32_t role, int32_t * keys, uint64_t * clocks) {
-    if (!p || role < 0 || role > 2) return fail(QWM_ERR_ARG, "pool_slots: bad argument");
-    const auto & R = p->role[role];
+int qwm_pool_slots(const qwm_pool * p, int32_t pool, int32_t * keys, uint64_t * clocks) {
+    if (!p || pool < 0 || pool >= (int32_t)p->pools.size()) return fail(QWM_ERR_ARG, "pool_slots: bad argument");
+    const auto & R = p->pools[(size_t)pool];
     for (int32_t s = 0; s < R.n_slots; ++s) {
         if (keys) keys[s] = R.slot2key[s];
         if (clocks) clocks[s] = R.clk[s];
@@ -721,18 +855,20 @@ int qwm_pool_slots(const qwm_pool * p, int32_t role, int32_t * keys, uint64_t * 
 }
 
 // ExpertCache::save_profile (expert_cache.cpp:1485-1500): the same text
-// format; roles in order, keys ascending within a role.
+// format; pools in order (each line carries its pool's role), keys ascending
+// within a pool.
 int qwm_pool_save_profile(const qwm_pool * p, const char * path) {
     if (!p || !path) return fail(QWM_ERR_ARG, "pool_save_profile: NULL argument");
     FILE * f = std::fopen(path, "wb");
     if (!f) return fail(QWM_ERR_IO, std::string("pool_save_profile: ") + path + ": " + strerror(errno));
     bool ok = std::fprintf(f, "QWENEXPCACHE 1\n%d %d\n", p->n_layer, p->n_expert) > 0;
-    for (int r = 0; r < 3 && ok; ++r) {
-        std::vector<std::pair<int32_t, uint64_t>> kv(p->role[r].count.begin(), p->role[r].count.end());
+    for (const auto & R : p->pools) {
+        std::vector<std::pair<int32_t, uint64_t>> kv(R.count.begin(), R.count.end());
         std::sort(kv.begin(), kv.end());
         for (const auto & c : kv)
-            ok = ok && std::fprintf(f, "%d %d %d %llu\n", r, c.first / p->n_expert, c.first % p->n_expert,
+            ok = ok && std::fprintf(f, "%d %d %d %llu\n", R.role, c.first / p->n_expert, c.first % p->n_expert,
                                     (unsigned long long)c.second) > 0;
+        if (!ok) break;
     }
     ok = (std::fclose(f) == 0) && ok;
     if (!ok) return fail(QWM_ERR_IO, std::string("pool_save_profile: writing ") + path + " failed");
@@ -742,8 +878,8 @@ int qwm_pool_save_profile(const qwm_pool * p, const char * path) {
 // ExpertCache::load_prefetch (expert_cache.cpp:1502-1538): a missing or
 // incompatible profile is a cold start (nothing installed, QWM_OK).  The
 // in-range entries, largest count first (equal counts in file order), are
-// installed while their role's pool has a free slot and the key is not
-// resident; the slabs are fetched as ensure fetches misses.
+// installed while the pool of their (role, layer) has a free slot and the
+// key is not resident; the slabs are fetched as ensure fetches misses.
 int qwm_pool_load_profile(qwm_pool * p, const char * path, int64_t * n_installed) {
     if (!p || !path) return fail(QWM_ERR_ARG, "pool_load_profile: NULL argument");
     if (n_installed) *n_installed = 0;
@@ -771,7 +907,7 @@ int qwm_pool_load_profile(qwm_pool * p, const char * path, int64_t * n_installed
         return grc != QWM_OK ? grc : frc;
     };
     for (const Ent & x : ents) {
-        auto & R = p->role[x.r];
+        auto & R = p->P(x.r, x.l);
         if ((int)R.key2slot.size() >= R.n_slots) continue;
         const int32_t key = x.l * p->n_expert + x.e;
         if (R.key2slot.count(key)) continue;
@@ -792,10 +928,11 @@ int qwm_pool_load_profile(qwm_pool * p, const char * path, int64_t * n_installed
 }
 
 // ExpertCache::compute_quota and rebalance (expert_cache.cpp:509-625): one
-// quota per layer from the counts summed over the roles (entries by count,
-// then key, both descending): first every layer up to n_used experts while
-// every role's pool has slots left, then greedily one more expert per entry
-// beyond its layer's first n_used, while slots remain.  The quotas then steer
+// quota per layer from the counts summed over the pools (entries by count,
+// then key, both descending).  A layer's expert takes one slot in each of
+// the pools of its three roles, while all three have one left: first every
+// layer up to n_used experts, then greedily one more expert per entry beyond
+// its layer's first n_used.  Each of the layer's pools gets that quota.  The quotas then steer
 // every later victim (pick_quota), and the hottest experts within each
 // layer's quota are installed, all three roles together, up to fill_budget
 // experts.
@@ -804,7 +941,7 @@ int qwm_pool_rebalance(qwm_pool * p, int32_t n_used, int64_t fill_budget, int32_
     if (n_filled) *n_filled = 0;
     const int32_t L = p->n_layer, E = p->n_expert;
     std::unordered_map<int32_t, uint64_t> cnt;
-    for (const auto & R : p->role)
+    for (const auto & R : p->pools)
         for (const auto & kv : R.count) cnt[kv.first] += kv.second;
     std::vector<std::pair<uint64_t, int32_t>> ents;   // (count, key)
     ents.reserve(cnt.size());
@@ -812,26 +949,27 @@ int qwm_pool_rebalance(qwm_pool * p, int32_t n_used, int64_t fill_budget, int32_
     std::sort(ents.begin(), ents.end(), std::greater<std::pair<uint64_t, int32_t>>());
     std::vector<int32_t> quota((size_t)L, 0);
     if (!cnt.empty()) {
-        int64_t rem[3];
-        for (int r = 0; r < 3; ++r) rem[r] = p->role[r].n_slots;
-        auto take = [&]() {
+        std::vector<int64_t> rem(p->pools.size());
+        for (size_t i = 0; i < p->pools.size(); ++i) rem[i] = p->pools[i].n_slots;
+        auto take = [&](int32_t l) {
             for (int r = 0; r < 3; ++r)
-                if (rem[r] <= 0) return false;
-            for (int r = 0; r < 3; ++r) rem[r]--;
+                if (rem[(size_t)p->lp[r][(size_t)l]] <= 0) return false;
+            for (int r = 0; r < 3; ++r) rem[(size_t)p->lp[r][(size_t)l]]--;
             return true;
         };
         for (int32_t l = 0; l < L; ++l)
-            while (quota[l] < n_used && take()) quota[l]++;
+            while (quota[l] < n_used && take(l)) quota[l]++;
         std::vector<int32_t> seen((size_t)L, 0);
         for (const auto & e : ents) {
             const int32_t l = e.second / E;
             if (seen[l]++ < n_used) continue;
             if (quota[l] >= E) continue;
-            if (!take()) continue;
+            if (!take(l)) continue;
             quota[l]++;
         }
     }
-    for (auto & R : p->role) R.quota = quota;
+    for (int32_t l = 0; l < L; ++l)
+        for (int r = 0; r < 3; ++r) p->P(r, l).quota[(size_t)l] = quota[l];
     p->quota_on = true;
     p->n_used = n_used;
     if (quota_out) std::copy(quota.begin(), quota.end(), quota_out);
@@ -850,14 +988,14 @@ int qwm_pool_rebalance(qwm_pool * p, int32_t n_used, int64_t fill_budget, int32_
         if (seen[l] >= quota[l]) continue;
         seen[l]++;
         bool all = true;
-        for (const auto & R : p->role) all = all && R.key2slot.count(key);
+        for (int r = 0; r < 3; ++r) all = all && p->P(r, l).key2slot.count(key);
         if (all) continue;
         if (l != cur) {
             if ((rc = flush_layer(cur)) != QWM_OK) break;
             cur = l;
         }
         for (int r = 0; r < 3 && rc == QWM_OK; ++r) {
-            auto & R = p->role[r];
+            auto & R = p->P(r, l);
             if (R.key2slot.count(key)) continue;
             const int32_t victim = p->pick(R, l);
             if (victim < 0) { rc = fail(QWM_ERR_NO_VICTIM, "No unprotected GPU cache victim"); break; }
@@ -878,18 +1016,19 @@ int qwm_pool_rebalance(qwm_pool * p, int32_t n_used, int64_t fill_budget, int32_
 // ExpertCache::clear_counts (expert_cache.cpp:557-559).
 int qwm_pool_clear_counts(qwm_pool * p) {
     if (!p) return fail(QWM_ERR_ARG, "pool_clear_counts: NULL pool");
-    for (auto & R : p->role) R.count.clear();
+    for (auto & R : p->pools) R.count.clear();
     return QWM_OK;
 }
 
 int qwm_pool_attach_file(qwm_pool * p, int32_t role, int32_t layer, const char * path, uint64_t offset) {
     if (!p || !path || role < 0 || role > 2 || layer < 0 || layer >= p->n_layer)
         return fail(QWM_ERR_ARG, "pool_attach_file: bad argument");
-    auto & R = p->role[role];
-    if (!R.data) return fail(QWM_ERR_ARG, "pool_attach_file: the role has no device pool");
+    const auto & R = p->P(role, layer);
+    auto & S = p->src[role];
+    if (!R.data) return fail(QWM_ERR_ARG, "pool_attach_file: the (role, layer) has no device pool");
     if (p->gather && (R.slab % 16 || ((uintptr_t)R.data & 15) || R.n_slots > 32767))
         return fail(QWM_ERR_ARG, "pool_attach_file: GATHER needs 16-byte aligned pools, slab_bytes % 16 == 0 and at "
-                                 "most 32767 slots per role");
+                                 "most 32767 slots per pool");
     const int fd = open(path, O_RDONLY | O_CLOEXEC);
     if (fd < 0) return fail(QWM_ERR_IO, std::string("pool_attach_file: ") + path + ": " + strerror(errno));
     struct stat st;
@@ -898,13 +1037,13 @@ int qwm_pool_attach_file(qwm_pool * p, int32_t role, int32_t layer, const char *
         close(fd);
         return fail(QWM_ERR_ARG, std::string("pool_attach_file: ") + path + " is shorter than offset + n_expert * slab_bytes");
     }
-    if (R.fd.empty()) {
-        R.fd.assign((size_t)p->n_layer, -1);
-        R.foff.assign((size_t)p->n_layer, 0);
+    if (S.fd.empty()) {
+        S.fd.assign((size_t)p->n_layer, -1);
+        S.foff.assign((size_t)p->n_layer, 0);
     }
-    if (R.fd[layer] >= 0) close(R.fd[layer]);
-    R.fd[layer] = fd;
-    R.foff[layer] = offset;
+    if (S.fd[layer] >= 0) close(S.fd[layer]);
+    S.fd[layer] = fd;
+    S.foff[layer] = offset;
     return QWM_OK;
 }
 

@@ -49,6 +49,11 @@ def oracle():
         lib.qwo_pool_new.restype = P
         lib.qwo_pool_new.argtypes = [ctypes.c_int, ctypes.c_int, P, ctypes.c_int]
         lib.qwo_pool_free.argtypes = [P]
+        lib.qwo_pool_new_sig.restype = P
+        lib.qwo_pool_new_sig.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, P, P, P, ctypes.c_int]
+        lib.qwo_pool_layer_pool.argtypes = [P, ctypes.c_int, ctypes.c_int]
+        lib.qwo_pool_plan_sigs.argtypes = [ctypes.c_int, ctypes.c_int, P, ctypes.c_uint64, ctypes.c_int, P,
+                                           ctypes.c_int, P, P]
         lib.qwo_pool_ensure.argtypes = [P, ctypes.c_int, P, ctypes.c_int, P, P, P, P, P]
         lib.qwo_pool_stats.argtypes = [P, P]
         lib.qwo_pool_clock.argtypes = [P]

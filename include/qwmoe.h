@@ -10,9 +10,12 @@
  *    byte strides, `type` is a ggml_type value (ggml.h:390-420).  Data
  *    pointers are device pointers unless a comment says host.
  *  - Every entry point returns QWM_OK (0) or a negative QWM_ERR_* code and
- *    never throws; qwm_last_error() describes the last failure of the calling
- *    thread.  QWM_ERR_UNSUPPORTED means "shape/type not handled here": the
- *    caller keeps its own fallback, as ggml's supports_op contract expects.
+ *    never throws (each body runs behind an exception barrier); size queries
+ *    return 0 instead.  qwm_last_error() describes the last failure of the
+ *    calling thread.  The slot pool's calls take every allocation before
+ *    their first change to the pool, so a QWM_ERR_NOMEM leaves it as it was.
+ *    QWM_ERR_UNSUPPORTED means "shape/type not handled here": the caller
+ *    keeps its own fallback, as ggml's supports_op contract expects.
  *  - The library allocates no device memory on the hot path.  Scratch comes
  *    from a caller-owned workspace sized by qwm_*_workspace_size() and zeroed
  *    once with qwm_workspace_init() (it keeps self-resetting counters).
@@ -46,11 +49,15 @@ extern "C" {
 #define QWM_ERR_NO_VICTIM   (-5)
 #define QWM_ERR_STATE       (-6)
 #define QWM_ERR_IO          (-7)
+#define QWM_ERR_NOMEM       (-8)   /* host memory ran out (std::bad_alloc inside the library) */
+#define QWM_ERR_INTERNAL    (-9)   /* any other C++ exception inside the library */
 
 /* ggml_type values used on this path (ggml.h:390-420) */
 #define QWM_TYPE_F32   0
 #define QWM_TYPE_Q8_0  8
 #define QWM_TYPE_Q4_K 12
+#define QWM_TYPE_Q5_K 13
+#define QWM_TYPE_Q6_K 14
 #define QWM_TYPE_I32  26
 
 /* Mirrors the data-carrying part of struct ggml_tensor (ggml.h). */
@@ -134,7 +141,12 @@ int qwm_moe_experts(const qwm_moe_layer * layer, const qwm_tensor * x, const qwm
 /* Route + experts with the in-graph slot remap of the fast decode path
  * (runtime.cpp:2759-2787): slot = slot_of[role][layer * E + id] read on the
  * device from `slot_tables` (i32 [E * n_layer, 3], role-major: gate, up,
- * down).  No host round trip; the pools must hold every selected expert. */
+ * down).  No host round trip; the pools must hold every selected expert.
+ * Slot ids (here, in qwm_moe_experts' slot tensors and in the other
+ * resident paths) are not checked against the pools: the kernels clamp an
+ * id outside [0, S) into the pool, so a bad id computes with a wrong slab
+ * but never reads outside the pool tensor.  The cached paths take their ids
+ * from the pool, which are always in range. */
 int qwm_moe_block_resident(const qwm_moe_layer * layer, int32_t layer_index, const int32_t * slot_tables,
                            int64_t table_stride, const qwm_tensor * x, const qwm_tensor * rm,
                            const qwm_tensor * resid, qwm_tensor * out, qwm_tensor * ids_out, qwm_tensor * w_out,

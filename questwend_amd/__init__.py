@@ -25,6 +25,7 @@ _TYPE_SIZE = {TYPE_F32: (4, 1), TYPE_I32: (4, 1), TYPE_Q8_0: (34, 32), TYPE_Q4_K
               TYPE_Q6_K: (210, 256)}
 
 OK, ERR_UNSUPPORTED, ERR_ARG, ERR_WORKSPACE, ERR_HIP, ERR_NO_VICTIM, ERR_STATE, ERR_IO = 0, -1, -2, -3, -4, -5, -6, -7
+ERR_NOMEM, ERR_INTERNAL = -8, -9
 
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32

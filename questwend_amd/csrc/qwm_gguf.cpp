@@ -180,41 +180,45 @@ uint64_t tensor_bytes(const GgufTensor & t) {
 extern "C" {
 
 int qwm_gguf_find_tensor(const char * path, const char * name, qwm_gguf_tensor * out) {
-    if (!path || !name || !out) return fail(QWM_ERR_ARG, "gguf_find_tensor: NULL argument");
-    std::unordered_map<std::string, GgufTensor> idx;
-    const int rc = read_index(path, idx);
-    if (rc != QWM_OK) return rc;
-    auto it = idx.find(name);
-    if (it == idx.end()) return fail(QWM_ERR_ARG, std::string("gguf: no tensor ") + name + " in " + path);
-    const GgufTensor & t = it->second;
-    out->type = t.type;
-    out->n_dims = t.n_dims;
-    for (int d = 0; d < 4; ++d) out->ne[d] = t.ne[d];
-    out->offset = t.offset;
-    out->nbytes = tensor_bytes(t);
-    return QWM_OK;
+    return guard("qwm_gguf_find_tensor", [&]() -> int {
+        if (!path || !name || !out) return fail(QWM_ERR_ARG, "gguf_find_tensor: NULL argument");
+        std::unordered_map<std::string, GgufTensor> idx;
+        const int rc = read_index(path, idx);
+        if (rc != QWM_OK) return rc;
+        auto it = idx.find(name);
+        if (it == idx.end()) return fail(QWM_ERR_ARG, std::string("gguf: no tensor ") + name + " in " + path);
+        const GgufTensor & t = it->second;
+        out->type = t.type;
+        out->n_dims = t.n_dims;
+        for (int d = 0; d < 4; ++d) out->ne[d] = t.ne[d];
+        out->offset = t.offset;
+        out->nbytes = tensor_bytes(t);
+        return QWM_OK;
+    });
 }
 
 int qwm_pool_attach_gguf(qwm_pool * pool, const char * path, int32_t first_block) {
-    if (!pool || !path || first_block < 0) return fail(QWM_ERR_ARG, "pool_attach_gguf: bad argument");
-    std::unordered_map<std::string, GgufTensor> idx;
-    const int rc = read_index(path, idx);
-    if (rc != QWM_OK) return rc;
-    const int32_t n_layer = pool_n_layer(pool), n_expert = pool_n_expert(pool);
-    static const char * const roles[3] = {"gate", "up", "down"};   // expert_cache.cpp:88-93
-    for (int32_t l = 0; l < n_layer; ++l)
-        for (int r = 0; r < 3; ++r) {
-            const std::string name = "blk." + std::to_string(first_block + l) + ".ffn_" + roles[r] + "_exps.weight";
-            auto it = idx.find(name);
-            if (it == idx.end()) return fail(QWM_ERR_ARG, "gguf: no tensor " + name + " in " + path);
-            const GgufTensor & t = it->second;
-            const uint64_t nb = tensor_bytes(t);
-            if (t.ne[2] != n_expert || t.ne[3] != 1 || nb != (uint64_t)n_expert * pool_slab_bytes(pool, r, l))
-                return fail(QWM_ERR_ARG, "gguf: " + name + " does not hold n_expert slabs of its pool's slab_bytes");
-            const int arc = qwm_pool_attach_file(pool, r, l, path, t.offset);
-            if (arc != QWM_OK) return arc;
-        }
-    return QWM_OK;
+    return guard("qwm_pool_attach_gguf", [&]() -> int {
+        if (!pool || !path || first_block < 0) return fail(QWM_ERR_ARG, "pool_attach_gguf: bad argument");
+        std::unordered_map<std::string, GgufTensor> idx;
+        const int rc = read_index(path, idx);
+        if (rc != QWM_OK) return rc;
+        const int32_t n_layer = pool_n_layer(pool), n_expert = pool_n_expert(pool);
+        static const char * const roles[3] = {"gate", "up", "down"};   // expert_cache.cpp:88-93
+        for (int32_t l = 0; l < n_layer; ++l)
+            for (int r = 0; r < 3; ++r) {
+                const std::string name = "blk." + std::to_string(first_block + l) + ".ffn_" + roles[r] + "_exps.weight";
+                auto it = idx.find(name);
+                if (it == idx.end()) return fail(QWM_ERR_ARG, "gguf: no tensor " + name + " in " + path);
+                const GgufTensor & t = it->second;
+                const uint64_t nb = tensor_bytes(t);
+                if (t.ne[2] != n_expert || t.ne[3] != 1 || nb != (uint64_t)n_expert * pool_slab_bytes(pool, r, l))
+                    return fail(QWM_ERR_ARG, "gguf: " + name + " does not hold n_expert slabs of its pool's slab_bytes");
+                const int arc = qwm_pool_attach_file(pool, r, l, path, t.offset);
+                if (arc != QWM_OK) return arc;
+            }
+        return QWM_OK;
+    });
 }
 
 }  // extern "C"

@@ -14,14 +14,49 @@ namespace qwm {
 // ggml_type values (ggml.h:390-420)
 enum : int32_t { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_Q8_K = 15, T_I32 = 26 };
 
-void set_error(const std::string & msg);
-int fail(int code, const std::string & msg);
-#define QWM_HIP_CHECK(expr)                                                              \
-    do {                                                                                 \
-        hipError_t e_ = (expr);                                                          \
-        if (e_ != hipSuccess) return ::qwm::fail(QWM_ERR_HIP, std::string(#expr ": ") + \
-                                                 hipGetErrorString(e_));                 \
+// The calling thread's last error lives in a fixed buffer: recording one
+// never allocates, so an error path (out of memory included) cannot throw.
+void set_error(const char * msg) noexcept;
+const char * last_error() noexcept;
+int fail(int code, const char * msg) noexcept;
+int fail(int code, const std::string & msg) noexcept;
+int failf(int code, const char * fmt, ...) noexcept __attribute__((format(printf, 2, 3)));
+#define QWM_HIP_CHECK(expr)                                                          \
+    do {                                                                             \
+        hipError_t e_ = (expr);                                                      \
+        if (e_ != hipSuccess)                                                        \
+            return ::qwm::failf(QWM_ERR_HIP, "%s: %s", #expr, hipGetErrorString(e_)); \
     } while (0)
+
+// The exception barrier of the C ABI: every extern "C" entry point runs its
+// body through guard(), which turns std::bad_alloc into QWM_ERR_NOMEM and any
+// other exception into QWM_ERR_INTERNAL, so nothing unwinds into C callers.
+int fail_exception(const char * who) noexcept;   // call only inside a catch block
+template <class F>
+inline int guard(const char * who, F && f) noexcept {
+    try {
+        return f();
+    } catch (...) {
+        return fail_exception(who);
+    }
+}
+template <class F>
+inline size_t guard_size(const char * who, F && f) noexcept {   // 0 on an exception
+    try {
+        return f();
+    } catch (...) {
+        fail_exception(who);
+        return 0;
+    }
+}
+template <class F>
+inline void guard_void(const char * who, F && f) noexcept {
+    try {
+        f();
+    } catch (...) {
+        fail_exception(who);
+    }
+}
 
 constexpr int MAX_T = 8;        // tokens per GEMV batch (decode / verify)
 constexpr int MAX_TILES = 512;  // row tiles of the down projection (combine tickets)
@@ -76,6 +111,7 @@ struct ExpertArgs {
     int32_t down_type;      // down pools: wtype, or Q6_K beside Q4_K / Q5_K gate/up
     const uint8_t * gate; const uint8_t * up; const uint8_t * down;   // pool bases
     size_t gate_slab, up_slab, down_slab;                             // bytes per slot
+    int32_t n_slots_g, n_slots_u, n_slots_d;                          // slots per pool: ids are clamped into them
     const uint8_t * sh_gate; const uint8_t * sh_up; const uint8_t * sh_down;
     const int32_t * slot_g; const int32_t * slot_u; const int32_t * slot_d;  // [T][k]
     const int32_t * uslot;  // [unit][4] from the route's resident remap, or null

@@ -219,6 +219,7 @@ struct GateUpArgs {
     const uint8_t * sh_gate; const uint8_t * sh_up;
     const int32_t * slot_g; const int32_t * slot_u;
     const int32_t * uslot;                                        // [unit][4] or null: slots through the pairs
+    int S_g, S_u;                                                 // slots per pool
     const Unit * units; const int32_t * n_units; int unit_slots;  // routed unit grid rows
     const int8_t * xq_qs; const float * xq_d; const int32_t * xq_bs;
     const uint32_t * xq_x;                                        // Q8_K of x, exact-dot layout (Q4_K pools)
@@ -239,7 +240,7 @@ struct UnitView {
 template <int MAXP>
 QWM_DEV bool load_unit(UnitView<MAXP> & V, const Unit * units, const int32_t * n_units, const int32_t * uslot,
                        const int32_t * slot_a, const int32_t * slot_b, int u, bool shared, int T, int role_a,
-                       int role_b, int & nu) {
+                       int role_b, int S_a, int S_b, int & nu) {
     nu = *n_units;
     if (shared) {
         V.n = T;
@@ -257,6 +258,10 @@ QWM_DEV bool load_unit(UnitView<MAXP> & V, const Unit * units, const int32_t * n
     if (uslot) { sa = uslot[4 * u + role_a]; sb = uslot[4 * u + role_b]; }
     if (u >= nu) return false;
     if (!uslot) { sa = slot_a[pr[0]]; sb = slot_b ? slot_b[pr[0]] : 0; }
+    // caller slot ids out of [0, S) are clamped into the pool: wrong weights,
+    // but no read outside it
+    sa = min(max(sa, 0), S_a - 1);
+    sb = min(max(sb, 0), S_b - 1);
     V.n = n;
 #pragma unroll
     for (int i = 0; i < MAXP; ++i) V.pair[i] = pr[i];
@@ -279,7 +284,7 @@ __global__ void __launch_bounds__(256) k_gateup_x(GateUpArgs a) {
     const bool shared = u == a.unit_slots;
     UnitView<MAXP> U;
     int nu;
-    if (!load_unit<MAXP>(U, a.units, a.n_units, a.uslot, a.slot_g, a.slot_u, u, shared, a.T, 0, 1, nu)) return;
+    if (!load_unit<MAXP>(U, a.units, a.n_units, a.uslot, a.slot_g, a.slot_u, u, shared, a.T, 0, 1, a.S_g, a.S_u, nu)) return;
     const int n = U.n;
     const int rows = shared ? a.N_sh : a.N;
     const int r = blockIdx.x * GUX_ROWS + wave * 8 + rsub;
@@ -330,7 +335,7 @@ __global__ void __launch_bounds__(256) k_gateup_x5(GateUpArgs a) {
     const bool shared = u == a.unit_slots;
     UnitView<MAXP> U;
     int nu;
-    if (!load_unit<MAXP>(U, a.units, a.n_units, a.uslot, a.slot_g, a.slot_u, u, shared, a.T, 0, 1, nu)) return;
+    if (!load_unit<MAXP>(U, a.units, a.n_units, a.uslot, a.slot_g, a.slot_u, u, shared, a.T, 0, 1, a.S_g, a.S_u, nu)) return;
     const int n = U.n;
     const int rows = shared ? a.N_sh : a.N;
     const int r = blockIdx.x * GUX_ROWS + wave * 8 + rsub;
@@ -377,7 +382,7 @@ __global__ void __launch_bounds__(256) k_gateup_x80(GateUpArgs a) {
     const bool shared = u == a.unit_slots;
     UnitView<MAXP> U;
     int nu;
-    if (!load_unit<MAXP>(U, a.units, a.n_units, a.uslot, a.slot_g, a.slot_u, u, shared, a.T, 0, 1, nu)) return;
+    if (!load_unit<MAXP>(U, a.units, a.n_units, a.uslot, a.slot_g, a.slot_u, u, shared, a.T, 0, 1, a.S_g, a.S_u, nu)) return;
     const int n = U.n;
     const int rows = shared ? a.N_sh : a.N;
     const int r = blockIdx.x * GUX_ROWS + wave * 8 + rsub;
@@ -425,6 +430,7 @@ struct DownArgs {
     const uint8_t * down; size_t down_slab; const uint8_t * sh_down;
     const int32_t * slot_d;
     const int32_t * uslot;
+    int S_d;                                                      // slots in the down pool
     const Unit * units; const int32_t * n_units; int unit_slots; int shared;
     const float * act; const float * act_sh;
     float * ex; float * ex_sh;
@@ -477,7 +483,7 @@ __global__ void __launch_bounds__(256) k_down_q4k(DownArgs a) {
     const bool shared = u == a.unit_slots;
     UnitView<MAXP> U;
     int nu;
-    if (!load_unit<MAXP>(U, a.units, a.n_units, a.uslot, a.slot_d, nullptr, u, shared, a.T, 2, 2, nu)) return;
+    if (!load_unit<MAXP>(U, a.units, a.n_units, a.uslot, a.slot_d, nullptr, u, shared, a.T, 2, 2, a.S_d, a.S_d, nu)) return;
     const int n = U.n;
     const uint8_t * base = shared ? a.sh_down : a.down + (size_t)U.slot[0] * a.down_slab;
     const int row0 = blockIdx.x * TILE;
@@ -526,7 +532,7 @@ __global__ void __launch_bounds__(256) k_down_q6k(DownArgs a) {
     const bool shared = u == a.unit_slots;
     UnitView<MAXP> U;
     int nu;
-    if (!load_unit<MAXP>(U, a.units, a.n_units, a.uslot, a.slot_d, nullptr, u, shared, a.T, 2, 2, nu)) return;
+    if (!load_unit<MAXP>(U, a.units, a.n_units, a.uslot, a.slot_d, nullptr, u, shared, a.T, 2, 2, a.S_d, a.S_d, nu)) return;
     const int n = U.n;
     const uint8_t * base = shared ? a.sh_down : a.down + (size_t)U.slot[0] * a.down_slab;
     const int row0 = blockIdx.x * TILE;
@@ -570,7 +576,7 @@ __global__ void __launch_bounds__(256) k_down_q5k(DownArgs a) {
     const bool shared = u == a.unit_slots;
     UnitView<MAXP> U;
     int nu;
-    if (!load_unit<MAXP>(U, a.units, a.n_units, a.uslot, a.slot_d, nullptr, u, shared, a.T, 2, 2, nu)) return;
+    if (!load_unit<MAXP>(U, a.units, a.n_units, a.uslot, a.slot_d, nullptr, u, shared, a.T, 2, 2, a.S_d, a.S_d, nu)) return;
     const int n = U.n;
     const uint8_t * base = shared ? a.sh_down : a.down + (size_t)U.slot[0] * a.down_slab;
     const int row0 = blockIdx.x * TILE;
@@ -618,7 +624,7 @@ __global__ void __launch_bounds__(256) k_down_q80(DownArgs a) {
     const bool shared = u == a.unit_slots;
     UnitView<MAXP> U;
     int nu;
-    if (!load_unit<MAXP>(U, a.units, a.n_units, a.uslot, a.slot_d, nullptr, u, shared, a.T, 2, 2, nu)) return;
+    if (!load_unit<MAXP>(U, a.units, a.n_units, a.uslot, a.slot_d, nullptr, u, shared, a.T, 2, 2, a.S_d, a.S_d, nu)) return;
     const int n = U.n;
     const uint8_t * base = shared ? a.sh_down : a.down + (size_t)U.slot[0] * a.down_slab;
     const int row0 = blockIdx.x * TILE;
@@ -854,6 +860,7 @@ int launch_experts(const ExpertArgs & a, const MoePlan & p, uint8_t * ws, hipStr
     g.gate = a.gate; g.up = a.up; g.gate_slab = a.gate_slab; g.up_slab = a.up_slab;
     g.sh_gate = a.sh_gate; g.sh_up = a.sh_up;
     g.slot_g = a.slot_g; g.slot_u = a.slot_u; g.uslot = a.uslot;
+    g.S_g = a.n_slots_g; g.S_u = a.n_slots_u;
     g.units = units; g.n_units = n_units; g.unit_slots = unit_slots;
     g.xq_qs = reinterpret_cast<const int8_t *>(ws + p.xq_qs);
     g.xq_d = reinterpret_cast<const float *>(ws + (q80 ? p.xq_d0 : p.xq_d));
@@ -874,7 +881,7 @@ int launch_experts(const ExpertArgs & a, const MoePlan & p, uint8_t * ws, hipStr
 
     DownArgs d;
     d.down = a.down; d.down_slab = a.down_slab; d.sh_down = a.sh_down;
-    d.slot_d = a.slot_d; d.uslot = a.uslot;
+    d.slot_d = a.slot_d; d.uslot = a.uslot; d.S_d = a.n_slots_d;
     d.units = units; d.n_units = n_units; d.unit_slots = unit_slots;
     d.act = g.act; d.act_sh = g.act_sh;
     d.ex = reinterpret_cast<float *>(ws + p.ex);

@@ -52,19 +52,20 @@ extern "C" int qwm_verify_step_noalloc(const qwm_moe_layer * layer, int32_t laye
                                        const qwm_tensor * resid, qwm_tensor * out, qwm_tensor * ids_out,
                                        qwm_tensor * w_out, const qwm_tensor * lm_head, const float * norm_w, float eps,
                                        const int32_t * drafts, int32_t * result, void * stream) {
-    if (!x || !lm_head) return fail(QWM_ERR_ARG, "verify_step_noalloc: NULL argument");
-    const size_t need = qwm_verify_step_workspace_size(layer, lm_head, x->ne[1]);
-    if (!need)   // the shape is refused: the full call reports why, before any device work
-        return qwm_verify_step(layer, layer_index, slot_tables, table_stride, x, rm, resid, out, ids_out, w_out,
-                               lm_head, norm_w, eps, drafts, result, nullptr, 0, stream);
-    if (need > QWM_NOALLOC_SCRATCH_BYTES)
-        return fail(QWM_ERR_UNSUPPORTED, "verify_step_noalloc: the step needs " + std::to_string(need) +
-                                             " bytes of scratch; the static array holds " +
-                                             std::to_string((size_t)QWM_NOALLOC_SCRATCH_BYTES));
-    void * ptr = nullptr;
-    int rc = scratch_address(&ptr);
-    if (rc != QWM_OK) return rc;
-    if ((rc = launch_fill_zero(ptr, need & ~(size_t)3, (hipStream_t)stream)) != QWM_OK) return rc;
-    return qwm_verify_step(layer, layer_index, slot_tables, table_stride, x, rm, resid, out, ids_out, w_out, lm_head,
-                           norm_w, eps, drafts, result, ptr, need, stream);
+    return guard("qwm_verify_step_noalloc", [&]() -> int {
+        if (!x || !lm_head) return fail(QWM_ERR_ARG, "verify_step_noalloc: NULL argument");
+        const size_t need = qwm_verify_step_workspace_size(layer, lm_head, x->ne[1]);
+        if (!need)   // the shape is refused: the full call reports why, before any device work
+            return qwm_verify_step(layer, layer_index, slot_tables, table_stride, x, rm, resid, out, ids_out, w_out,
+                                   lm_head, norm_w, eps, drafts, result, nullptr, 0, stream);
+        if (need > QWM_NOALLOC_SCRATCH_BYTES)
+            return failf(QWM_ERR_UNSUPPORTED, "verify_step_noalloc: the step needs %zu bytes of scratch; the static "
+                                              "array holds %zu", need, (size_t)QWM_NOALLOC_SCRATCH_BYTES);
+        void * ptr = nullptr;
+        int rc = scratch_address(&ptr);
+        if (rc != QWM_OK) return rc;
+        if ((rc = launch_fill_zero(ptr, need & ~(size_t)3, (hipStream_t)stream)) != QWM_OK) return rc;
+        return qwm_verify_step(layer, layer_index, slot_tables, table_stride, x, rm, resid, out, ids_out, w_out, lm_head,
+                               norm_w, eps, drafts, result, ptr, need, stream);
+    });
 }

@@ -87,6 +87,8 @@ int launch_step(const StepCall & c, const StepPlan & p, uint8_t * ws, hipStream_
     a.gate = (const uint8_t *)L->gate_pool.data; a.up = (const uint8_t *)L->up_pool.data;
     a.down = (const uint8_t *)L->down_pool.data;
     a.gate_slab = L->gate_pool.nb[2]; a.up_slab = L->up_pool.nb[2]; a.down_slab = L->down_pool.nb[2];
+    a.n_slots[0] = (int)L->gate_pool.ne[2]; a.n_slots[1] = (int)L->up_pool.ne[2];
+    a.n_slots[2] = (int)L->down_pool.ne[2];
     a.sh_gate = (const uint8_t *)L->sh_gate.data; a.sh_up = (const uint8_t *)L->sh_up.data;
     a.sh_down = (const uint8_t *)L->sh_down.data;
     a.slot_tables = c.slot_tables; a.table_stride = c.table_stride; a.layer = c.layer;

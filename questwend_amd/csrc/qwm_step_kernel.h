@@ -30,6 +30,7 @@ struct StepArgs {
     int N, N_sh, shared;
     const uint8_t * gate; const uint8_t * up; const uint8_t * down;
     size_t gate_slab, up_slab, down_slab;
+    int n_slots[3];                                                             // slots per pool (gate, up, down)
     const uint8_t * sh_gate; const uint8_t * sh_up; const uint8_t * sh_down;
     const int32_t * slot_tables; int64_t table_stride; int layer;
     const float * resid; float * out;                                           // [T][H]
@@ -179,7 +180,8 @@ QWM_DEV void step_select(const StepArgs & a, int g, StepShared & S, uint8_t * sm
     }
     __syncthreads();
     for (int u = tid; u < nu; u += 256)
-        for (int r = 0; r < 3; ++r) S.uslot[u][r] = S.slot_of[r * E + S.units[u].expert];
+        for (int r = 0; r < 3; ++r)   // table entries out of [0, S) are clamped into the pool
+            S.uslot[u][r] = min(max(S.slot_of[r * E + S.units[u].expert], 0), a.n_slots[r] - 1);
     if (tid == 0) {
         if (a.shared) {
             S.units[nu].expert = -1;

@@ -123,3 +123,52 @@ def test_fused_step(dev, lm_head, cfg):
         assert np.array_equal(r_b[:T][clear], vA[clear])
         if clear.all():
             assert (r_b[T], r_b[T + 1]) == (a, xn)
+
+
+def test_out_of_range_slots_are_clamped(dev, lm_head):
+    """Slot tables with ids outside [0, S) -- -1, S + 3, -5 for the experts a
+    token selects -- run without reading outside the pools: the per-op
+    resident path and the fused step give bit for bit what the same tables
+    give with those ids clamped to 0, S - 1 and 0."""
+    T = 2
+    Wq, dW = lm_head
+    case = MoeCase(seed=4242, E=128, k=8, N=768, S=T * 8)
+    case.upload(torch)
+    L = qa.lib()
+    layer = case.layer
+    lm_t = qa.tensor(qa.TYPE_Q8_0, 2048, V, 1, dW)
+    ws_step = workspace(L.qwm_verify_step_workspace_size(layer, lm_t, T))
+    ws_moe = workspace(L.qwm_moe_workspace_size(layer, T))
+    norm_w = np.ones(2048, np.float32)
+    dn = torch.from_numpy(norm_w).cuda()
+    x = case.rng.standard_normal((T, case.H)).astype(np.float32)
+    ids, _, _, _ = case.route(x)
+    table, _ = slot_tables(case, ids)
+    e0, e1 = int(ids[0, 0]), int(ids[1, 1])
+    bad = table.copy()
+    bad[0 * case.E + e0], bad[1 * case.E + e0], bad[2 * case.E + e1] = -1, case.S + 3, -5
+    clamped = table.copy()
+    clamped[0 * case.E + e0], clamped[1 * case.E + e0], clamped[2 * case.E + e1] = 0, case.S - 1, 0
+    dx = torch.from_numpy(x).cuda()
+    ddr = torch.zeros(T - 1, dtype=torch.int32, device="cuda")
+    xt = qa.tensor(qa.TYPE_F32, case.H, T, 1, dx)
+    res = {}
+    for name, tab in (("bad", bad), ("clamped", clamped)):
+        dtab = torch.from_numpy(tab).cuda()
+        for path in ("ops", "step"):
+            out = torch.zeros((T, case.H), device="cuda")
+            r = torch.zeros(T + 2, dtype=torch.int32, device="cuda")
+            ot = qa.tensor(qa.TYPE_F32, case.H, T, 1, out)
+            print(f"clamp test: table {name}, path {path}", flush=True)
+            if path == "ops":
+                qa.check(L.qwm_moe_block_resident(layer, 0, dtab.data_ptr(), case.E, xt, None, xt, ot, None, None,
+                                                  ws_moe.data_ptr(), ws_moe.numel(), None))
+            else:
+                qa.check(L.qwm_verify_step(layer, 0, dtab.data_ptr(), case.E, xt, None, xt, ot, None, None, lm_t,
+                                           dn.data_ptr(), 1e-6, ddr.data_ptr(), r.data_ptr(), ws_step.data_ptr(),
+                                           ws_step.numel(), None))
+            torch.cuda.synchronize()
+            res[name, path] = out.cpu().numpy()
+    for path in ("ops", "step"):
+        assert np.isfinite(res["bad", path]).all()
+        assert np.array_equal(bits(res["bad", path]), bits(res["clamped", path])), path

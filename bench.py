@@ -316,6 +316,25 @@ def bench_decode(args, torch, qa, n_layers=48):
         decode(torch.cuda.current_stream().cuda_stream)
     ms_graph = timed(graph.replay)
     ms = min(ms_direct, ms_graph)
+    # the same 48 layers through the per-op kernels (qwm_moe_block_resident per
+    # layer: route, gate/up, down launches), replayed from a HIP graph on the
+    # same box, as the comparison for the persistent launches
+    wsb = torch.empty(L.qwm_moe_workspace_size(layers[0], T1), dtype=torch.uint8, device=dev)
+    qa.check(L.qwm_workspace_init(wsb.data_ptr(), wsb.numel(), stream))
+    xb = torch.empty((T1, H), device=dev)
+    tb = qa.tensor(qa.TYPE_F32, H, T1, 1, xb)
+
+    def per_op(st):
+        for l in range(n_layers):
+            src, dst = (xt, tb) if l % 2 == 0 else (tb, xt)
+            qa.check(L.qwm_moe_block_resident(layers[l], l, tables.data_ptr(), n_layers * E, src, None, src, dst,
+                                              None, None, wsb.data_ptr(), wsb.numel(), st))
+    g_op = torch.cuda.CUDAGraph()
+    xw.copy_(xs[0])
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g_op):
+        per_op(torch.cuda.current_stream().cuda_stream)
+    ms_per_op = timed(g_op.replay)
     step_bytes = n_layers * (K_USED * 3 * SLAB + E * H * 4 + 2 * T1 * H * 4)
     gbs = step_bytes / (ms * 1e-3) / 1e9
     cpu = None
@@ -387,8 +406,9 @@ def bench_decode(args, torch, qa, n_layers=48):
         "data": "synthetic",
         "config": {"workload": "1-token decode through 48 stacked Qwen3-30B-A3B-shape MoE blocks (H 2048, 128 experts "
                                "resident per layer, FFN 768, top-8, Q4_K; attention omitted), new N(0,1) input per step",
-                   "graph": ms_graph <= ms_direct, "ms_direct": ms_direct, "ms_graph": ms_graph},
-        "roofline": {"bound": "hbm", "kernel": "whole step (48 x route + gate/up + down)", "achieved": gbs,
+                   "graph": ms_graph <= ms_direct, "ms_direct": ms_direct, "ms_graph": ms_graph,
+                   "ms_per_op_kernels_graph": ms_per_op},
+        "roofline": {"bound": "hbm", "kernel": "whole step (3 persistent k_decode launches of 16 layers)", "achieved": gbs,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS, "traffic": None,
                      "bytes_per_launch": step_bytes},
         "cpu_baseline": cpu,

@@ -156,6 +156,7 @@ def lib():
         "qwm_quantize": (ctypes.c_int, [_I32, _P, _P, _I64, _P]),
         "qwm_profile_start": (ctypes.c_int, [ctypes.c_char_p, _I32]),
         "qwm_profile_stop": (ctypes.c_int, [_P, _I32]),
+        "qwm_set_spin_limit": (ctypes.c_int, [ctypes.c_uint32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

@@ -116,6 +116,11 @@ int qwm_profile_start(const char * kernel, int32_t max_launches) {
     });
 }
 
+int qwm_set_spin_limit(uint32_t sleeps) {
+    set_spin_limit(sleeps);
+    return QWM_OK;
+}
+
 int qwm_profile_stop(float * durations_ms, int32_t capacity) {
     return guard("qwm_profile_stop", [&]() -> int {
         if (!g_prof.open) return fail(QWM_ERR_STATE, "profile_stop: profiling was not started");
@@ -699,7 +704,10 @@ size_t qwm_moe_decode_workspace_size(const qwm_moe_layer * layers, int32_t n_lay
     return guard_size("qwm_moe_decode_workspace_size", [&]() -> size_t {
         MoePlan p;
         if (check_layers(layers, n_layers, T, p) != QWM_OK) return 0;
-        return align_up(p.total, 256) + align_up(sizeof(float) * (size_t)(T * p.H), 256);
+        const size_t loop = align_up(p.total, 256) + align_up(sizeof(float) * (size_t)(T * p.H), 256);
+        DecodePlan dp;
+        std::string why;
+        return decode_plan(layers, n_layers, T, dp, why) ? std::max(loop, dp.total) : loop;
     });
 }
 
@@ -723,9 +731,19 @@ int qwm_moe_decode_sel(const qwm_moe_layer * layers, int32_t n_layers, const int
         if (rc != QWM_OK) return rc;
         if ((rc = check_act(x, p.H, "x")) != QWM_OK) return rc;
         if (table_stride < (int64_t)n_layers * p.E) return fail(QWM_ERR_ARG, "moe_decode: slot table stride too small");
-        const size_t need = align_up(p.total, 256) + align_up(sizeof(float) * (size_t)(p.T * p.H), 256);
+        DecodePlan dp;
+        std::string why;
+        const bool persistent = decode_plan(layers, n_layers, p.T, dp, why);
+        const size_t loop = align_up(p.total, 256) + align_up(sizeof(float) * (size_t)(p.T * p.H), 256);
+        const size_t need = persistent ? std::max(loop, dp.total) : loop;
         if (!workspace || ws_bytes < need) return fail(QWM_ERR_WORKSPACE, "moe_decode: workspace too small");
         uint8_t * ws = (uint8_t *)workspace;
+        if (persistent) {   // one launch per group of layers (qwm_decode.hip)
+            if (miss_flag && (rc = launch_fill_zero(miss_flag, 4, (hipStream_t)stream)) != QWM_OK) return rc;
+            DecodeCall c{layers, n_layers, slot_tables, table_stride, (float *)x->data, ids_all, resident_bits,
+                         miss_flag};
+            return launch_decode(c, dp, ws, (hipStream_t)stream);
+        }
         qwm_tensor buf = *x;
         buf.data = ws + align_up(p.total, 256);
         hipStream_t s = (hipStream_t)stream;

@@ -21,6 +21,7 @@ const char * last_error() noexcept;
 int fail(int code, const char * msg) noexcept;
 int fail(int code, const std::string & msg) noexcept;
 int failf(int code, const char * fmt, ...) noexcept __attribute__((format(printf, 2, 3)));
+void set_spin_limit(uint32_t n);   // qwm_step.hip
 #define QWM_HIP_CHECK(expr)                                                          \
     do {                                                                             \
         hipError_t e_ = (expr);                                                      \
@@ -120,6 +121,24 @@ struct ExpertArgs {
     float * out;            // [T][H]
 };
 int launch_experts(const ExpertArgs & a, const MoePlan & p, uint8_t * ws, hipStream_t s);
+
+// the persistent decode loop (qwm_decode.hip): layers of one launch keep
+// their own logits, Q8_K of x, x, expert outputs and counters
+struct DecodePlan {
+    MoePlan moe;                                              // act, act_sh, tile tickets
+    uint32_t lg_stride, xq_stride, x_stride, ex_stride, exs_stride;   // dwords per layer
+    size_t lg, xq, xs, ex, ex_sh, rows_done, gu_done, tiles_done, err, done;
+    size_t total;
+};
+struct DecodeCall {
+    const qwm_moe_layer * layers; int32_t n_layers;
+    const int32_t * slot_tables; int64_t table_stride;
+    float * x;                                                // [T][H], in and out
+    int32_t * ids_all;                                        // [layer][T][k] or null
+    const uint32_t * res_bits; int32_t * res_flag;            // or null
+};
+bool decode_plan(const qwm_moe_layer * layers, int32_t n_layers, int64_t T, DecodePlan & p, std::string & why);
+int launch_decode(const DecodeCall & c, const DecodePlan & p, uint8_t * ws, hipStream_t s);
 
 // generic GGML_OP_MUL_MAT_ID (qwm_moe.hip)
 struct MmidArgs {

@@ -74,6 +74,10 @@ bool step_plan(const qwm_moe_layer * L, const qwm_tensor * lm_head, int64_t T, S
     return true;
 }
 
+static uint32_t g_spin_limit = SPIN_LIMIT;
+uint32_t spin_limit() { return __atomic_load_n(&g_spin_limit, __ATOMIC_RELAXED); }
+void set_spin_limit(uint32_t n) { __atomic_store_n(&g_spin_limit, n, __ATOMIC_RELAXED); }
+
 int launch_step(const StepCall & c, const StepPlan & p, uint8_t * ws, hipStream_t s) {
     const qwm_moe_layer * L = c.L;
     const MoePlan & m = p.moe;
@@ -103,6 +107,7 @@ int launch_step(const StepCall & c, const StepPlan & p, uint8_t * ws, hipStream_
     a.tile_counters = reinterpret_cast<int32_t *>(ws + m.tile_counters);
     a.gu_done = reinterpret_cast<int32_t *>(ws + p.gu_done);
     a.tiles_done = reinterpret_cast<int32_t *>(ws + p.tiles_done);
+    a.spin = spin_limit();
     VerifyArgs & v = a.v;
     v.W = c.lm_head; v.H = SH; v.V = (int)p.V;
     v.x = c.out; v.norm_w = c.norm_w; v.eps = c.eps;

@@ -16,7 +16,7 @@ namespace qwm {
 
 constexpr int SH = 2048;                 // hidden size of the fused step
 constexpr int SNB = SH / QK_K;           // Q8_K blocks per token
-constexpr uint32_t SPIN_LIMIT = 1u << 21;
+constexpr uint32_t SPIN_LIMIT = 1u << 21;   // default bound of every wait (qwm_set_spin_limit changes it)
 constexpr int MAX_NDOWN_S = 2048;        // longest down-projection input (FFN width)
 constexpr int STEP_MAX_E = 512;          // experts per layer in the fused step
 constexpr size_t STEP_SELECT_LDS = (size_t)3 * STEP_MAX_E * 4;   // the selection's union tables
@@ -43,6 +43,7 @@ struct StepArgs {
     int d6;                                                                     // down slabs are Q6_K
     int32_t * gu_done;                                                          // per unit, one 32-word line each
     int32_t * tiles_done;                                                       // combined down tiles
+    uint32_t spin;                                                              // bound of every wait, in sleeps
     VerifyArgs v;                                                               // v.x = out
 };
 
@@ -118,8 +119,10 @@ QWM_DEV void step_router(const StepArgs & a, int g, int G) {
 // every workgroup, one wave per token (select_token, qwm_select.h: soft_max
 // or sigmoid, the optional ranking bias, top-k, weights); then the expert
 // union in first-occurrence order and each unit's slots.
-// R: logits per lane (E <= 64 * R).
-template <int NT, int R>
+// R: logits per lane (E <= 64 * R).  LG_DENSE: the logits lie at lg[e * NT +
+// t] (several writers per line, so they are read with agent-scope loads)
+// instead of one 128-byte line per row (lg[e * 32 + t]).
+template <int NT, int R, bool LG_DENSE = false>
 QWM_DEV void step_select(const StepArgs & a, int g, StepShared & S, uint8_t * smem) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int E = a.E, k = a.k;
@@ -127,12 +130,13 @@ QWM_DEV void step_select(const StepArgs & a, int g, StepShared & S, uint8_t * sm
     const unsigned long long below = (1ull << lane) - 1ull;
     const SelectCfg sel{E, k, a.norm, a.sigm, a.scale, a.bias};
     for (int t = wave; t < NT; t += 4) {
-        const float shl = a.sgi ? a.lg[(size_t)E * 32 + t] : 0.f;      // shared-expert gate logit
+        const float shl = !a.sgi ? 0.f : LG_DENSE ? ld_agent(a.lg + (size_t)E * NT + t) : a.lg[(size_t)E * 32 + t];
         float v[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const int i = 64 * r + lane;
-            v[r] = (r < nr && i < E) ? a.lg[(size_t)i * 32 + t] : -__builtin_inff();
+            v[r] = (r < nr && i < E) ? (LG_DENSE ? ld_agent(a.lg + (size_t)i * NT + t) : a.lg[(size_t)i * 32 + t])
+                                     : -__builtin_inff();
         }
         int myid;
         float myw;
@@ -293,7 +297,7 @@ QWM_DEV void step_down_t(const StepArgs & a, int g, int G, const StepShared & S,
             for (int p = 0; p < PF; ++p)
 #pragma unroll
                 for (int b = 0; b < NB; ++b) load_xblk(Wb[p][b], rp + (size_t)(4 * RPS * p) * row_bytes + b * 144, c8);
-        wait_count(a.gu_done + 32 * u, shared ? nb_s : nb_r, a.err, SPIN_LIMIT);   // the unit's activations are out
+        wait_count(a.gu_done + 32 * u, shared ? nb_s : nb_r, a.err, a.spin);   // the unit's activations are out
         for (int jb = wave; jb < n * NB; jb += 4) {
             const int i = jb / NB, b = jb % NB;
             const float * src = shared ? a.act_sh + (size_t)U_.pair[i] * (NB * QK_K)
@@ -413,7 +417,7 @@ __global__ void __launch_bounds__(256) k_step(StepArgs a) {
     step_router<NT>(a, g, G);
 #pragma unroll
     for (int q = 0; q < SLQ; ++q) S.slot_of[threadIdx.x + 256 * q] = sl[q];
-    wait_count(a.rows_done, step_p0_parts<NT>(a.E + (a.sgi ? 1 : 0), G), a.err, SPIN_LIMIT);   // ends with a workgroup barrier
+    wait_count(a.rows_done, step_p0_parts<NT>(a.E + (a.sgi ? 1 : 0), G), a.err, a.spin);   // ends with a workgroup barrier
     // Q8_K of x into LDS for the gate/up GEMVs: requested now, stored after
     // the selection, whose round trip and arithmetic hide the loads
     constexpr int XW = (NT * SNB * XS + 255) / 256;            // dwords per thread
@@ -435,9 +439,13 @@ __global__ void __launch_bounds__(256) k_step(StepArgs a) {
     step_down<NT, NB_D, MAXP>(a, g, G, S, smem);
     __syncthreads();
     constexpr int PF = NT <= 4 ? 2 : 1;
-    if (verify_body<NT, SH / 512, PF, VH_BEFORE_WAIT>(a.v, g, G, smem, a.tiles_done, SH / DN_TR, a.err, SPIN_LIMIT)) {
-        // every workgroup has passed all its waits: re-arm the completion counters
+    if (verify_body<NT, SH / 512, PF, VH_BEFORE_WAIT>(a.v, g, G, smem, a.tiles_done, SH / DN_TR, a.err, a.spin)) {
+        // every workgroup has passed all its waits: re-arm the completion
+        // counters, and the tile tickets too (they re-arm themselves when
+        // exactly U units arrive, but after a wait gave up the workgroups
+        // may have selected from partial logits and disagree on U)
         for (int q = threadIdx.x; q < MAX_PAIRS + 1; q += 256) st_agent(a.gu_done + 32 * q, 0);
+        if (threadIdx.x < SH / DN_TR) st_agent(a.tile_counters + threadIdx.x, 0);
         if (threadIdx.x == 0) { st_agent(a.tiles_done, 0); st_agent(a.rows_done, 0); }
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
@@ -500,6 +508,9 @@ static int launch_step_nt(StepArgs & a, int nb_d, hipStream_t s) {
         default: return launch_step_t<NT, 8>(a, s);
     }
 }
+
+// the bound of the fused launches' waits (qwm_set_spin_limit)
+uint32_t spin_limit();
 
 // qwm_step_hi.hip: launch_step_nt<T> for T = 6, 7; qwm_step_t8.hip: T = 8
 int launch_step_hi(StepArgs & a, int T, int nb_d, hipStream_t s);

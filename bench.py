@@ -418,11 +418,12 @@ def bench_decode(args, torch, qa, n_layers=48):
 def bench_prefill(args, torch, qa, T_pf=512, E_pf=512, k_pf=10, N_pf=512):
     """A 512-token prefill chunk through one Qwen3-Next-shape MoE layer's
     expert GEMMs (hidden 2048, 512 experts, FFN 512, top-10, Q4_K from
-    N(0, 0.02)): up = mul_mat_id(up, x, ids), gate = mul_mat_id(gate, x, ids),
-    down = mul_mat_id(down, act, ids) with act = silu(gate) * up between
-    them.  ids are each token's top-10 of random router logits.  The timed
-    step is the three GGML_OP_MUL_MAT_ID calls (qwm_mul_mat_id, columns
-    grouped by expert on int8 MFMA)."""
+    N(0, 0.02)): act = swiglu(mul_mat_id(gate, x, ids), mul_mat_id(up, x, ids)),
+    down = mul_mat_id(down, act, ids).  ids are each token's top-10 of random
+    router logits.  The timed step is qwm_mul_mat_id_swiglu (one grouped
+    int8-MFMA pass over gate and up that writes act) and qwm_mul_mat_id for
+    down; the same step through three separate qwm_mul_mat_id calls and a
+    torch SwiGLU is timed beside it for comparison."""
     L = qa.lib()
     dev = torch.device("cuda:0")
     torch.manual_seed(args.seed)
@@ -447,7 +448,8 @@ def bench_prefill(args, torch, qa, T_pf=512, E_pf=512, k_pf=10, N_pf=512):
     t_x = qa.tensor(qa.TYPE_F32, H, 1, T_pf, x)
     t_ids = qa.tensor(qa.TYPE_I32, k_pf, T_pf, 1, ids)
     t_act = qa.tensor(qa.TYPE_F32, N_pf, k_pf, T_pf, act)
-    need = max(L.qwm_mul_mat_id_workspace_size(t_g, t_x, t_ids), L.qwm_mul_mat_id_workspace_size(t_d, t_act, t_ids))
+    need = max(L.qwm_mul_mat_id_swiglu_workspace_size(t_g, t_u, t_x, t_ids),
+               L.qwm_mul_mat_id_workspace_size(t_g, t_x, t_ids), L.qwm_mul_mat_id_workspace_size(t_d, t_act, t_ids))
     ws = torch.empty(need, dtype=torch.uint8, device=dev)
     qa.check(L.qwm_workspace_init(ws.data_ptr(), ws.numel(), stream))
 
@@ -457,25 +459,38 @@ def bench_prefill(args, torch, qa, T_pf=512, E_pf=512, k_pf=10, N_pf=512):
 
     def step():
         st = torch.cuda.current_stream().cuda_stream
+        qa.check(L.qwm_mul_mat_id_swiglu(t_g, t_u, t_x, t_ids, t_act, ws.data_ptr(), ws.numel(), st))
+        gemm(t_d, t_act, down, st)
+
+    def step_separate():
+        st = torch.cuda.current_stream().cuda_stream
         gemm(t_u, t_x, up, st)
         gemm(t_g, t_x, gate, st)
         torch.mul(torch.nn.functional.silu(gate), up, out=act)
         gemm(t_d, t_act, down, st)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    qa.check(L.qwm_profile_start(b"prefill_gemm", 3 * args.steps))
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(args.steps):
-        step()
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / args.steps
-    g_ms = np.zeros(3 * args.steps, np.float32)
-    n_g = L.qwm_profile_stop(g_ms.ctypes.data, 3 * args.steps)
-    g_ms = g_ms[:n_g].reshape(-1, 3) if n_g == 3 * args.steps else None
+    def timed(fn, launches):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        qa.check(L.qwm_profile_start(b"prefill_gemm*", launches * args.steps))
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        g = np.zeros(launches * args.steps, np.float32)
+        n = L.qwm_profile_stop(g.ctypes.data, launches * args.steps)
+        return e0.elapsed_time(e1) / args.steps, (g[:n].reshape(-1, launches) if n == launches * args.steps else None)
+
+    ms_sep, g_sep = timed(step_separate, 3)
+    down_sep = down.clone()
+    ms, g_ms = timed(step, 2)
+    act_fused = act.clone()
+    torch.mul(torch.nn.functional.silu(gate), up, out=act)     # the separate path's act, same x and ids
+    act_diff = float((act_fused - act).abs().max())
+    down_diff = float((down - down_sep).abs().max())
     cpu = None
     if not args.no_cpu:
         lib = ref_cpu_lib()
@@ -508,18 +523,27 @@ def bench_prefill(args, torch, qa, T_pf=512, E_pf=512, k_pf=10, N_pf=512):
     w_bytes = 3 * used * slab
     flops = 2.0 * T_pf * k_pf * (2 * N_pf * H + H * N_pf)
     gemm_ms = float(g_ms.sum(1).mean()) if g_ms is not None else ms
-    gbs = (w_bytes + 4 * T_pf * H + 3 * 4 * T_pf * k_pf * N_pf + 4 * T_pf * k_pf * H) / (gemm_ms * 1e-3) / 1e9
+    # the fused gate/up launch: both matrices' used slabs, x read, act written
+    gu_bytes = 2 * used * slab + 4 * T_pf * H + 4 * T_pf * k_pf * N_pf
+    gu_ms = float(g_ms[:, 0].mean()) if g_ms is not None else ms
+    gbs = gu_bytes / (gu_ms * 1e-3) / 1e9
+    step_gbs = (w_bytes + 4 * T_pf * H + 2 * 4 * T_pf * k_pf * N_pf + 4 * T_pf * k_pf * H) / (gemm_ms * 1e-3) / 1e9
     print(json.dumps({
         "metric": "MoE prefill tokens/s (expert GEMMs of one Qwen3-Next-shape layer), 1xMI355X",
         "value": T_pf / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
         "data": "synthetic",
         "config": {"workload": "512-token prefill chunk, one Qwen3-Next-shape MoE layer (H 2048, 512 experts, FFN 512, "
-                               "top-10, Q4_K): gate/up/down MUL_MAT_ID as expert-grouped int8 MFMA GEMMs",
+                               "top-10, Q4_K): gate+up+SwiGLU in one expert-grouped int8 MFMA pass, then down",
                    "experts_used": used, "gemm_ms_per_step": gemm_ms,
-                   "gemm_ms_each": g_ms.mean(0).tolist() if g_ms is not None else None},
-        "roofline": {"bound": "hbm", "kernel": "k_pf_gemm (3 launches per step)", "achieved": gbs, "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS, "traffic": None, "bytes_per_launch": w_bytes / 3},
+                   "gemm_ms_each": g_ms.mean(0).tolist() if g_ms is not None else None,
+                   "gemm_GBps_step": step_gbs,
+                   "separate": {"ms_per_step": ms_sep, "tokens_per_s": T_pf / (ms_sep * 1e-3),
+                                "gemm_ms_each": g_sep.mean(0).tolist() if g_sep is not None else None,
+                                "act_max_abs_diff_vs_torch_silu": act_diff, "down_max_abs_diff": down_diff}},
+        "roofline": {"bound": "hbm", "kernel": "k_pf_gemm<8, gate/up> (1 of 2 launches per step)", "achieved": gbs,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS, "traffic": None,
+                     "bytes_per_launch": gu_bytes},
         "mfma": {"tops": flops / (gemm_ms * 1e-3) / 1e12, "peak_int8_tops": 5000.0,
                  "frac": flops / (gemm_ms * 1e-3) / 5e15},
         "cpu_baseline": cpu,

@@ -91,6 +91,21 @@ size_t qwm_mul_mat_id_workspace_size(const qwm_tensor * as, const qwm_tensor * b
 int qwm_mul_mat_id(const qwm_tensor * as, const qwm_tensor * b, const qwm_tensor * ids, qwm_tensor * dst,
                    void * workspace, size_t ws_bytes, void * stream);
 
+/* The expert FFN's first half in one call: act = ggml_swiglu_split(
+ * MUL_MAT_ID(gate, b, ids), MUL_MAT_ID(up, b, ids)), the two MUL_MAT_ID nodes
+ * and the GGML_GLU_OP_SWIGLU node of build_segB (core/runtime.cpp:4539-4541;
+ * ops.cpp:3331-3385).  gate and up: same type, shape and strides, each as
+ * qwm_mul_mat_id's `as`; act: contiguous f32 [N, n_ids, T].  For T > 8 and
+ * Q4_K one grouped-GEMM pass streams the gate and up rows of each tile side
+ * by side and writes act (no gate/up intermediates in HBM; the activations
+ * are quantized once).  Otherwise two qwm_mul_mat_id calls into the workspace
+ * and an element-wise pass.  Either way act equals, bit for bit, SwiGLU
+ * applied to what two qwm_mul_mat_id calls return. */
+size_t qwm_mul_mat_id_swiglu_workspace_size(const qwm_tensor * gate, const qwm_tensor * up, const qwm_tensor * b,
+                                            const qwm_tensor * ids);
+int qwm_mul_mat_id_swiglu(const qwm_tensor * gate, const qwm_tensor * up, const qwm_tensor * b, const qwm_tensor * ids,
+                          qwm_tensor * act, void * workspace, size_t ws_bytes, void * stream);
+
 /* --------------------------------------------------- the MoE FFN block --- */
 
 /* One MoE layer's weights: slot pools in ggml layout (gate/up [H, N, S],
@@ -249,7 +264,10 @@ int qwm_quantize(int32_t type, const float * src, void * dst, int64_t n, void * 
 /* Brackets each of the next `max_launches` launches of one kernel with a
  * hipEvent pair on the stream it runs on.  Kernel names: "route",
  * "gate_up", "down" (with the combine), "lm_head", "step" (the fused verify
- * step), "mul_mat_id_prep", "mul_mat_id".  Owner thread only. */
+ * step), "decode" (the persistent decode), "mul_mat_id_prep", "mul_mat_id",
+ * "prefill_prep", "prefill_gemm" (the prefill GEMM), "prefill_gemm_gu" (its
+ * gate/up/SwiGLU form).  A name ending in '*' matches every kernel name that
+ * starts with the text before it.  Owner thread only. */
 int qwm_profile_start(const char * kernel, int32_t max_launches);
 /* Waits for the recorded events, writes each launch's duration in ms and
  * returns how many launches were timed (stops the profiling). */

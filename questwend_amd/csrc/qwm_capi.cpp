@@ -56,12 +56,19 @@ struct Profile {
 };
 static Profile g_prof;
 
+// the profiled name, or with a trailing '*' every name it prefixes
+static bool prof_match(const char * kernel) {
+    const std::string & k = g_prof.kernel;
+    if (!k.empty() && k.back() == '*') return std::strncmp(kernel, k.data(), k.size() - 1) == 0;
+    return k == kernel;
+}
+
 void prof_begin(const char * kernel, hipStream_t s) {
-    if (!g_prof.open || g_prof.kernel != kernel || 2 * g_prof.used + 1 >= (int)g_prof.ev.size()) return;
+    if (!g_prof.open || !prof_match(kernel) || 2 * g_prof.used + 1 >= (int)g_prof.ev.size()) return;
     (void)hipEventRecord(g_prof.ev[2 * g_prof.used], s);
 }
 void prof_end(const char * kernel, hipStream_t s) {
-    if (!g_prof.open || g_prof.kernel != kernel || 2 * g_prof.used + 1 >= (int)g_prof.ev.size()) return;
+    if (!g_prof.open || !prof_match(kernel) || 2 * g_prof.used + 1 >= (int)g_prof.ev.size()) return;
     (void)hipEventRecord(g_prof.ev[2 * g_prof.used + 1], s);
     g_prof.used++;
 }
@@ -226,6 +233,70 @@ int qwm_mul_mat_id(const qwm_tensor * as, const qwm_tensor * b, const qwm_tensor
             if ((rc = launch_mmid(c, (uint8_t *)workspace, (hipStream_t)stream)) != QWM_OK) return rc;
         }
         return QWM_OK;
+    });
+}
+
+// gate and up of one expert FFN: both the same quantized [K, N, n_as] layout
+// (the same slab stride too), act a contiguous f32 [N, n_ids, T].
+static int check_swiglu(const qwm_tensor * gate, const qwm_tensor * up, const qwm_tensor * b, const qwm_tensor * ids,
+                        const qwm_tensor * act) {
+    int rc = check_mmid(gate, b, ids, act);
+    if (rc != QWM_OK) return rc;
+    if ((rc = check_mmid(up, b, ids, nullptr)) != QWM_OK) return rc;
+    if (up->type != gate->type) return fail(QWM_ERR_ARG, "mul_mat_id_swiglu: gate and up differ in type");
+    for (int i = 0; i < 4; ++i)
+        if (up->ne[i] != gate->ne[i] || up->nb[i] != gate->nb[i])
+            return fail(QWM_ERR_ARG, "mul_mat_id_swiglu: gate and up differ in shape or strides");
+    if (act && !fully_contiguous(act)) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id_swiglu: act must be contiguous");
+    return QWM_OK;
+}
+
+static bool swiglu_fused(const qwm_tensor * gate, const qwm_tensor * b) { return b->ne[2] > MAX_T && gate->type == T_Q4_K; }
+
+// the separate path's layout: g and u [N, n_ids, T] f32, then the MUL_MAT_ID workspace
+static size_t swiglu_split_bytes(const qwm_tensor * gate, const qwm_tensor * b, const qwm_tensor * ids) {
+    return align_up(sizeof(float) * (size_t)gate->ne[1] * ids->ne[0] * b->ne[2], 256);
+}
+
+size_t qwm_mul_mat_id_swiglu_workspace_size(const qwm_tensor * gate, const qwm_tensor * up, const qwm_tensor * b,
+                                            const qwm_tensor * ids) {
+    return guard_size("qwm_mul_mat_id_swiglu_workspace_size", [&]() -> size_t {
+        if (check_swiglu(gate, up, b, ids, nullptr) != QWM_OK) return 0;
+        if (swiglu_fused(gate, b))
+            return prefill_workspace(gate->ne[0], gate->ne[1], gate->ne[2], b->ne[2], b->ne[1], ids->ne[0]);
+        return 2 * swiglu_split_bytes(gate, b, ids) + qwm_mul_mat_id_workspace_size(gate, b, ids);
+    });
+}
+
+int qwm_mul_mat_id_swiglu(const qwm_tensor * gate, const qwm_tensor * up, const qwm_tensor * b, const qwm_tensor * ids,
+                          qwm_tensor * act, void * workspace, size_t ws_bytes, void * stream) {
+    return guard("qwm_mul_mat_id_swiglu", [&]() -> int {
+        int rc = check_swiglu(gate, up, b, ids, act);
+        if (rc != QWM_OK) return rc;
+        if (!act) return fail(QWM_ERR_ARG, "mul_mat_id_swiglu: act is NULL");
+        const size_t need = qwm_mul_mat_id_swiglu_workspace_size(gate, up, b, ids);
+        if (!workspace || ws_bytes < need) return fail(QWM_ERR_WORKSPACE, "mul_mat_id_swiglu: workspace too small");
+        hipStream_t s = (hipStream_t)stream;
+        if (swiglu_fused(gate, b)) {
+            MmidArgs a;
+            a.wtype = gate->type; a.as = (const uint8_t *)gate->data; a.slab = gate->nb[2];
+            a.K = gate->ne[0]; a.N = gate->ne[1]; a.n_as = gate->ne[2];
+            a.b = (const float *)b->data; a.ne11 = b->ne[1]; a.T = b->ne[2];
+            a.ids = (const int32_t *)ids->data; a.n_ids = ids->ne[0];
+            a.b_nb1 = b->nb[1]; a.b_nb2 = b->nb[2]; a.ids_nb1 = ids->nb[1];
+            a.dst_nb1 = act->nb[1]; a.dst_nb2 = act->nb[2];
+            a.dst = (float *)act->data;
+            return launch_prefill(a, (uint8_t *)workspace, s, (const uint8_t *)up->data);
+        }
+        // two MUL_MAT_ID calls into the workspace, then the element-wise SwiGLU
+        const size_t gb = swiglu_split_bytes(gate, b, ids);
+        uint8_t * w = (uint8_t *)workspace;
+        qwm_tensor g = *act, u = *act;
+        g.data = w; u.data = w + gb;
+        if ((rc = qwm_mul_mat_id(gate, b, ids, &g, w + 2 * gb, ws_bytes - 2 * gb, stream)) != QWM_OK) return rc;
+        if ((rc = qwm_mul_mat_id(up, b, ids, &u, w + 2 * gb, ws_bytes - 2 * gb, stream)) != QWM_OK) return rc;
+        return launch_swiglu_rows((const float *)g.data, (const float *)u.data, (float *)act->data, (int)gate->ne[1],
+                                  ids->ne[0] * b->ne[2], s);
     });
 }
 
@@ -656,6 +727,10 @@ int qwm_moe_cached_batch(const qwm_moe_layer * layer, qwm_pool * pool, int32_t l
             qwm_tensor_init(&dt, QWM_TYPE_F32, Nout, n_ids, len, dst);
             return qwm_mul_mat_id(&as, &bt, &it, &dt, ws + b.mmid, b.mmid_bytes, s);
         };
+        // the fused gate/up pass needs the prefill GEMM's type and one layout for both pools
+        bool fuse_gate_up = layer->gate_pool.type == T_Q4_K && layer->up_pool.type == T_Q4_K;
+        for (int i = 0; i < 4 && fuse_gate_up; ++i)
+            fuse_gate_up = layer->gate_pool.ne[i] == layer->up_pool.ne[i] && layer->gate_pool.nb[i] == layer->up_pool.nb[i];
         float * gbuf = (float *)(ws + b.gate);
         float * ubuf = (float *)(ws + b.up);
         float * abuf = (float *)(ws + b.act);
@@ -674,9 +749,21 @@ int qwm_moe_cached_batch(const qwm_moe_layer * layer, qwm_pool * pool, int32_t l
             QWM_HIP_CHECK(hipMemcpyAsync(dsd, sd, 4 * cnt, hipMemcpyHostToDevice, s));
             if ((rc = qwm_pool_wait(pool, stream)) != QWM_OK) return rc;
             const float * xs = xd + t0 * H;
-            if ((rc = mmid(layer->up_pool, xs, H, 1, dsu, k, len, ubuf, N)) != QWM_OK) return rc;
-            if ((rc = mmid(layer->gate_pool, xs, H, 1, dsg, k, len, gbuf, N)) != QWM_OK) return rc;
-            if ((rc = launch_swiglu_rows(gbuf, ubuf, abuf, (int)N, k * len, s)) != QWM_OK) return rc;
+            if (fuse_gate_up && len > MAX_T && std::memcmp(sg, su, 4 * cnt) == 0) {
+                // gate and up rows under the same slots: one grouped pass writes act (equal, bit
+                // for bit, to the two calls and SwiGLU below; same workspace as one prefill call)
+                qwm_tensor bt, it, at;
+                qwm_tensor_init(&bt, QWM_TYPE_F32, H, 1, len, (void *)xs);
+                qwm_tensor_init(&it, QWM_TYPE_I32, k, len, 1, (void *)dsg);
+                qwm_tensor_init(&at, QWM_TYPE_F32, N, k, len, abuf);
+                if ((rc = qwm_mul_mat_id_swiglu(&layer->gate_pool, &layer->up_pool, &bt, &it, &at, ws + b.mmid,
+                                                b.mmid_bytes, s)) != QWM_OK)
+                    return rc;
+            } else {
+                if ((rc = mmid(layer->up_pool, xs, H, 1, dsu, k, len, ubuf, N)) != QWM_OK) return rc;
+                if ((rc = mmid(layer->gate_pool, xs, H, 1, dsg, k, len, gbuf, N)) != QWM_OK) return rc;
+                if ((rc = launch_swiglu_rows(gbuf, ubuf, abuf, (int)N, k * len, s)) != QWM_OK) return rc;
+            }
             if ((rc = mmid(layer->down_pool, abuf, N, k, dsd, k, len, ebuf, H)) != QWM_OK) return rc;
             const float * shout = nullptr;
             if (p.shared) {

@@ -152,7 +152,8 @@ int launch_mmid(const MmidArgs & a, uint8_t * ws, hipStream_t s);
 // prefill-sized batches (T > MAX_T), qwm_prefill.hip
 size_t prefill_workspace(int64_t K, int64_t N, int64_t n_as, int64_t T, int64_t ne11, int64_t n_ids);
 bool prefill_supported(int64_t K, int64_t N, int64_t n_as, std::string & why);
-int launch_prefill(const MmidArgs & a, uint8_t * ws, hipStream_t s);
+// up != nullptr: the gate/up/SwiGLU pass (a.as = gate, dst = act), Q4_K only
+int launch_prefill(const MmidArgs & a, uint8_t * ws, hipStream_t s, const uint8_t * up = nullptr);
 
 // ---- the fused verify step (qwm_step.hip) ----
 struct StepPlan {

@@ -22,16 +22,18 @@ namespace qwm {
 
 constexpr int PF_TOK = 16;     // columns per tile
 constexpr int PF_ROWS = 64;    // weight rows per tile
-constexpr int PF_RT = 4;       // row tiles per work item (the columns stay in LDS across them)
 constexpr int PF_MAXK = 2048;  // longest K held in LDS
 constexpr int PF_MAX_AS = 4096;
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));   // 16-byte pieces (plain vector loads and stores)
 
 struct PfArgs {
     const float * b; size_t b_nb1, b_nb2;     // bytes
     const int32_t * ids; size_t ids_nb1;      // bytes
     const uint8_t * as; size_t slab, row_bytes;
+    const uint8_t * as2;                      // GU: the up matrix (same type, shape and slabs as `as`)
     int K, N, ne11, T, n_ids, n_as;
     int8_t * qs; float * d; int32_t * bs;     // Q8_K rows of b: [T * ne11]
     int32_t * cnt_copy; int32_t * off; int32_t * fill; int32_t * item_off;
@@ -61,14 +63,13 @@ __global__ void __launch_bounds__(256) k_pf_prep(PfArgs a) {
 }
 
 // One workgroup: the expert histogram (in LDS, from this call's pairs), group
-// offsets (its exclusive scan) and the tile table (tiles of expert e are items
+// offsets (its exclusive scan) and the column-tile table (the 16-column tiles of expert e are
 // item_off[e] .. item_off[e + 1] - 1).  Nothing carries over between calls,
 // so calls of any shape may share a workspace.
 __global__ void __launch_bounds__(1024) k_pf_scan(PfArgs a) {
     __shared__ int32_t s_c[PF_MAX_AS], s_i[PF_MAX_AS];
     __shared__ int32_t s_wsum[2][16];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int rt = (a.N / PF_ROWS + PF_RT - 1) / PF_RT;    // row chunks per column tile
     for (int e = tid; e < a.n_as; e += 1024) s_c[e] = 0;
     __syncthreads();
     const int P = a.T * a.n_ids;
@@ -76,7 +77,7 @@ __global__ void __launch_bounds__(1024) k_pf_scan(PfArgs a) {
     __syncthreads();
     for (int e = tid; e < a.n_as; e += 1024) {
         const int c = s_c[e];
-        s_i[e] = (c + PF_TOK - 1) / PF_TOK * rt;
+        s_i[e] = (c + PF_TOK - 1) / PF_TOK;
         a.cnt_copy[e] = c;
         a.fill[e] = 0;
     }
@@ -110,10 +111,8 @@ __global__ void __launch_bounds__(1024) k_pf_scan(PfArgs a) {
         if (e < a.n_as) {
             a.off[e] = cb;
             a.item_off[e] = ib;
-            for (int it = 0; it < i4[q]; ++it) {
-                const int ct = it / rt;
-                a.items[ib + it] = make_int4(e, cb + ct * PF_TOK, min(PF_TOK, c4[q] - ct * PF_TOK), (it % rt) * PF_RT);
-            }
+            for (int ct = 0; ct < i4[q]; ++ct)
+                a.items[ib + ct] = make_int4(e, cb + ct * PF_TOK, min(PF_TOK, c4[q] - ct * PF_TOK), 0);
         }
         cb += c4[q];
         ib += i4[q];
@@ -132,153 +131,243 @@ __global__ void __launch_bounds__(256) k_pf_scatter(PfArgs a) {
     }
 }
 
-// The grouped GEMM.  Item it = (expert, 16-column tile, up to PF_RT row tiles
-// of 64): the columns are staged in LDS once, the row tiles run in turn.
-template <int NB>
-__global__ void __launch_bounds__(256) k_pf_gemm(PfArgs a) {
-    constexpr int K = NB * QK_K;
-    // rows padded by 16 bytes: an operand read (16 columns x 4 k-slices x 8 B)
-    // then covers all 64 banks once per half wave instead of one bank group
-    constexpr int QP = K + 16;
-    __shared__ __align__(16) int8_t s_q[PF_TOK][QP];
-    __shared__ float s_d[NB][PF_TOK];
-    __shared__ __align__(16) int16_t s_q8s[PF_TOK][NB * 8 + 2];   // sums of the 32 Q8_K values of each sub-block
-    __shared__ int32_t s_pair[PF_TOK];
-    const int it = blockIdx.x;
-    if (it >= *a.total) return;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int4 desc = a.items[it];
-    const int e = desc.x, c0 = desc.y, nc = desc.z;
-    const int rt0 = desc.w, rt1 = min(rt0 + PF_RT, a.N / PF_ROWS);
-    const int rl = lane & 15, kq = lane >> 4;           // B side: row rl, k-slice kq; outputs: columns 4 kq .. +3
-    int row = rt0 * PF_ROWS + wave * 16 + rl;
-    const uint8_t * wrow = a.as + (size_t)e * a.slab + (size_t)row * a.row_bytes;
-    // weights of block b: header (16 B) and the lane's 8 bytes of each 32-byte qs group;
-    // the first PF blocks are requested before the columns (they do not depend on them)
-    constexpr int PF = NB < 4 ? NB : 4;
-    uint4 hd_r[PF];
-    uint2 qq_r[PF][4];
-    auto load_w = [&](int b, uint4 & hd, uint2 (&qq)[4]) {
-        const uint8_t * blk = wrow + (size_t)b * 144;
-        hd = *reinterpret_cast<const uint4 *>(blk);
-#pragma unroll
-        for (int jp = 0; jp < 4; ++jp) qq[jp] = *reinterpret_cast<const uint2 *>(blk + 16 + 32 * jp + 8 * kq);
-    };
-#pragma unroll
-    for (int p = 0; p < PF; ++p) load_w(p, hd_r[p], qq_r[p]);      // PF <= NB: blocks of the first row tile
-    // the tile's columns: Q8_K rows of b into LDS (zeros past nc)
-    if (tid < PF_TOK) s_pair[tid] = tid < nc ? a.perm[c0 + tid] : -1;
-    __syncthreads();
-    for (int v = tid; v < PF_TOK * (K / 16); v += 256) {
-        const int c = v / (K / 16), o = v % (K / 16);
-        const int p = s_pair[c];
-        uint4 w = make_uint4(0, 0, 0, 0);
-        if (p >= 0) {
-            const int row = (p / a.n_ids) * a.ne11 + (p % a.n_ids) % a.ne11;
-            w = reinterpret_cast<const uint4 *>(a.qs + (size_t)row * K)[o];
-        }
-        reinterpret_cast<uint4 *>(&s_q[c][0])[o] = w;
-    }
-    for (int v = tid; v < PF_TOK * NB * 8; v += 256) {
-        const int c = v / (NB * 8), j = v % (NB * 8);
-        const int p = s_pair[c];
-        int16_t s = 0;
-        float dd = 0.f;
-        if (p >= 0) {
-            const int row = (p / a.n_ids) * a.ne11 + (p % a.n_ids) % a.ne11;
-            const int32_t * bs = a.bs + (size_t)row * (K / 16);
-            s = (int16_t)(bs[2 * j] + bs[2 * j + 1]);
-            if ((j & 7) == 0) dd = a.d[(size_t)row * NB + j / 8];
-        }
-        s_q8s[c][j] = s;
-        if ((j & 7) == 0) s_d[j / 8][c] = dd;
-    }
-    __syncthreads();
+// The grouped GEMM.  Units are (16-column tile of one expert, row tile of 64
+// weight rows); a workgroup owns 64 rows x 16 columns at a time, 16 rows per
+// wave, and runs a contiguous range of units (see the loop head).
+// GU: the same tile of the up matrix (a.as2) streams beside the gate rows
+// (a.as), and each output is ggml_swiglu_split's silu(gate) * up (the
+// vectorized silu on the rows' 16-wide chunks, libm expf on the tail, as
+// k_swiglu_rows): the dots are those of two separate calls bit for bit.
+// Three workgroups per CU (LDS 47 KB each at K 2048; 168 VGPRs), two where that
+// budget spills (gate/up with 1, 6 or 7 blocks per row).
+template <int NB, bool GU>
+constexpr int pf_occupancy() { return (GU && (NB == 1 || NB >= 6 && NB != 8)) ? 2 : 3; }
 
-    // the ring over the (row tile, block) sequence: groups of PF steps, slots
-    // static inside a group; the bound is a runtime count, so the groups stay
-    // a loop and only one group's values are live at a time.  Step s is block
-    // s % NB of row tile rt0 + s / NB.
-    const int nbr = a.K / QK_K;
-    const int nsteps = (rt1 - rt0) * nbr;
-    auto load_s = [&](int st, uint4 & hd, uint2 (&qq)[4]) {
-        const uint8_t * blk = wrow + (size_t)(st / nbr) * PF_ROWS * a.row_bytes + (size_t)(st % nbr) * 144;
-        hd = *reinterpret_cast<const uint4 *>(blk);
+template <int NB, bool GU>
+__global__ void __launch_bounds__(256, (pf_occupancy<NB, GU>())) k_pf_gemm(PfArgs a) {
+    constexpr int K = NB * QK_K;
+    // rows padded by 8 bytes: the operand reads (16 columns x 4 k-slices x 8 B)
+    // are then free of bank conflicts (measured on gfx950: none with 8, some with
+    // 16 or 32, many with no padding); the rows are 8-byte aligned
+    constexpr int QP = K + 8;
+    constexpr int NS = GU ? 2 : 1;                      // weight streams
+    __shared__ __align__(16) int8_t s_q[PF_TOK][QP];   // the columns' Q8_K values
+    __shared__ float s_d[NB][PF_TOK];
+    // the sums of the 32 Q8_K values of each sub-block, [sub-block][column]: integers below 2^12 in
+    // magnitude, held as floats for the mins' f32 MFMA (A[column][sub-block] at lane column + 16 k)
+    __shared__ __align__(16) float s_bsf[NB * 8][PF_TOK];
+    __shared__ __align__(16) uint8_t s_w[4][16 * 144];   // each wave's staging of one step's weights
+    __shared__ int32_t s_pair[PF_TOK];                  // each column's Q8_K row of b, -1: none
+    __shared__ int64_t s_out[PF_TOK];                   // byte offset of each column's output row in dst, -1: none
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // Persistent: the grid is the resident workgroup count W, and workgroup w takes
+    // the units u in [w U / W, (w + 1) U / W) of the U = column tiles x row tiles
+    // (column-tile-major), so every workgroup streams within one unit of the same
+    // weight bytes.  A run of units inside one column tile is a segment: its
+    // columns are staged once and its row tiles stream in turn.
+    const int RT = a.N / PF_ROWS;
+    const int U = *a.total * RT;
+    const int u_end = (int)((int64_t)(blockIdx.x + 1) * U / gridDim.x);
+    for (int u = (int)((int64_t)blockIdx.x * U / gridDim.x); u < u_end;) {
+        const int4 desc = a.items[u / RT];
+        const int e = desc.x, c0 = desc.y, nc = desc.z;
+        const int rt0 = u % RT, rt1 = min(RT, rt0 + (u_end - u));
+        u += rt1 - rt0;
+        __syncthreads();                                     // the previous segment's column tables are read
+        const int rl = lane & 15, kq = lane >> 4;           // B side: row rl, k-slice kq; outputs: columns 4 kq .. +3
+        int row = rt0 * PF_ROWS + wave * 16 + rl;           // the lane's output row
+        // A step's weights (the wave's 16 rows x one block, 2304 bytes) are loaded as
+        // whole 16-byte pieces: piece p = lane + 64 i (i < 3, p < 144) is piece p % 9
+        // of row p / 9's block, so one load covers about 7 rows' blocks in full (the
+        // 8-byte slices each lane needs for the MFMA would touch 16 lines for 32 bytes
+        // per load, which holds the stream near half the HBM rate).  Piece p goes to
+        // byte 16 p of the wave's LDS buffer, which then holds the 16 blocks in block
+        // layout.  The first PF steps are requested before the columns are staged.
+        // wave-uniform bases (scalar registers) and 32-bit lane offsets: a segment stays
+        // inside one expert's slab, below 2 GiB (checked at launch)
+        const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+        const uint8_t * wbase[NS];
+        wbase[0] = a.as + (size_t)e * a.slab + (size_t)(rt0 * PF_ROWS + wave_u * 16) * a.row_bytes;
+        if constexpr (GU) wbase[1] = a.as2 + (size_t)e * a.slab + (size_t)(rt0 * PF_ROWS + wave_u * 16) * a.row_bytes;
+        uint32_t poff[3];
 #pragma unroll
-        for (int jp = 0; jp < 4; ++jp) qq[jp] = *reinterpret_cast<const uint2 *>(blk + 16 + 32 * jp + 8 * kq);
-    };
-    float facc[4] = {0.f, 0.f, 0.f, 0.f}, facc_m[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 1
-    for (int b0 = 0; b0 < nsteps; b0 += PF)
-#pragma unroll
-    for (int pslot = 0; pslot < PF; ++pslot) {
-        const int st = b0 + pslot;
-        if (st >= nsteps) break;
-        const int b = st % nbr;
-        const uint4 hd = hd_r[pslot];
-        uint2 qq[4];
-#pragma unroll
-        for (int jp = 0; jp < 4; ++jp) qq[jp] = qq_r[pslot][jp];
-        if (st + PF < nsteps) load_s(st + PF, hd_r[pslot], qq_r[pslot]);
-        int sc[8], mn[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) q4k_scale_min_reg(j, hd.y, hd.z, hd.w, sc[j], mn[j]);
-        int acc[4] = {0, 0, 0, 0};
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const uint2 raw = qq[j >> 1];
-            const uint32_t m4 = 0x0F0F0F0Fu;
-            const uint32_t w0 = (j & 1) ? (raw.x >> 4) & m4 : raw.x & m4;
-            const uint32_t w1 = (j & 1) ? (raw.y >> 4) & m4 : raw.y & m4;
-            const long bw = (long)(((uint64_t)w1 << 32) | w0);
-            // A side: column rl's 8 activations of sub-block j (elements 32 j ..), k-slice kq
-            const int8_t * xs = &s_q[rl][b * QK_K + 32 * j + 8 * kq];
-            const uint2 xv = *reinterpret_cast<const uint2 *>(xs);
-            const long ax = (long)(((uint64_t)xv.y << 32) | xv.x);
-            v4i dj = {0, 0, 0, 0};
-            dj = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, bw, dj, 0, 0, 0);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[r] += sc[j] * dj[r];
+        for (int i = 0; i < 3; ++i) {
+            const int pc = min(lane + 64 * i, 143);           // lanes past piece 143 load it again (not staged)
+            poff[i] = (uint32_t)(pc / 9) * (uint32_t)a.row_bytes + (uint32_t)(pc % 9) * 16u;
         }
-        const float dw = fp16_to_f32((uint16_t)(hd.x & 0xffff)), dmw = fp16_to_f32((uint16_t)(hd.x >> 16));
+        // ring depth: steps in flight per stream, a divisor of NB (every group of PF steps is
+        // then whole); 3 waves per SIMD leave room for one step of each stream beside the other
+        // (deeper rings spill at that budget)
+        constexpr int PF = (GU || NB <= 2) ? 1 : (NB % 2 == 0 ? 2 : 1);
+        u32x4 wr0[NS][PF], wr1[NS][PF], wr2[NS][PF];        // the ring: a step's three pieces per lane
+        // step st: block st % NB of row tile rt0 + st / NB
+        auto load_s = [&](const uint8_t * base, int st, u32x4 & w0, u32x4 & w1, u32x4 & w2) {
+            const uint32_t o = (uint32_t)(st / NB) * (uint32_t)(PF_ROWS * a.row_bytes) + (uint32_t)(st % NB) * 144u;
+            w0 = *reinterpret_cast<const u32x4 *>(base + (poff[0] + o));
+            w1 = *reinterpret_cast<const u32x4 *>(base + (poff[1] + o));
+            w2 = *reinterpret_cast<const u32x4 *>(base + (poff[2] + o));
+        };
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int c = 4 * kq + r;
-            int mins = 0;
+        for (int p = 0; p < PF; ++p)
 #pragma unroll
-            for (int j = 0; j < 8; ++j) mins += __mul24(mn[j], (int)s_q8s[c][b * 8 + j]);
-            const float dx = s_d[b][c];
-            facc[r] = __builtin_fmaf(dx * dw, (float)acc[r], facc[r]);
-            facc_m[r] = __builtin_fmaf(-dx * dmw, (float)mins, facc_m[r]);
+            for (int q = 0; q < NS; ++q) load_s(wbase[q], p, wr0[q][p], wr1[q][p], wr2[q][p]);   // PF <= NB: the first row tile
+        // the tile's columns: Q8_K rows of b into LDS (zeros past nc)
+        // (pair p = t n_ids + slot: column t of b, row slot % ne11 of it; output row (slot, t))
+        if (tid < PF_TOK) {
+            const int p = tid < nc ? a.perm[c0 + tid] : -1;
+            const int t = p / a.n_ids, sl = p % a.n_ids;
+            s_pair[tid] = p >= 0 ? t * a.ne11 + sl % a.ne11 : -1;      // the Q8_K row of b
+            s_out[tid] = p >= 0 ? (int64_t)t * (int64_t)a.dst_nb2 + (int64_t)sl * (int64_t)a.dst_nb1 : (int64_t)-1;
         }
-        if (b == nbr - 1) {                          // the row tile is done: its outputs, then the next tile
+        __syncthreads();
+#pragma unroll
+        for (int v = tid; v < PF_TOK * (K / 16); v += 256) {
+            const int c = v / (K / 16), o = v % (K / 16);
+            const int src = s_pair[c];
+            uint4 w = make_uint4(0, 0, 0, 0);
+            if (src >= 0) w = reinterpret_cast<const uint4 *>(a.qs + (size_t)src * K)[o];
+            uint2 * dq = reinterpret_cast<uint2 *>(&s_q[c][16 * o]);
+            dq[0] = make_uint2(w.x, w.y);
+            dq[1] = make_uint2(w.z, w.w);
+        }
+#pragma unroll
+        for (int v = tid; v < PF_TOK * NB * 8; v += 256) {
+            const int c = v / (NB * 8), j = v % (NB * 8);
+            const int src = s_pair[c];
+            int sm = 0;
+            float dd = 0.f;
+            if (src >= 0) {
+                const int2 bs = reinterpret_cast<const int2 *>(a.bs + (size_t)src * (K / 16))[j];
+                sm = bs.x + bs.y;
+                if ((j & 7) == 0) dd = a.d[(size_t)src * NB + j / 8];
+            }
+            s_bsf[j][c] = (float)sm;
+            if ((j & 7) == 0) s_d[j / 8][c] = dd;
+        }
+        __syncthreads();
+
+        // the ring over the (row tile, block) sequence: groups of PF steps, slots
+        // static inside a group; the bound is a runtime count, so the groups stay
+        // a loop and only one group's values are live at a time.  Step s is block
+        // s % NB of row tile rt0 + s / NB.
+        const int nsteps = (rt1 - rt0) * NB;
+        uint8_t * wbuf = s_w[wave];
+        // one block of one weight row against the tile's 16 columns.  The sub-block
+        // dots are exact int32 (one int8 MFMA each, issued back to back into their
+        // own accumulators) and the 6-bit scales multiply them in 24-bit integer
+        // multiplies (|dot| <= 32 * 15 * 128 < 2^23).  The mins term
+        // sum_j min_j * bsum_j (|product| < 2^18, every partial sum < 2^24) runs as
+        // two f32 MFMAs (16x16x4): each value and partial sum is an integer that
+        // fp32 holds exactly, so the result is the integer sum in any order.
+        auto block_dot = [&](int b, const uint4 hd, const uint2 (&qq)[4], float (&facc)[4], float (&facc_m)[4]) {
+            // mins: B[k][row] = the row's min of sub-block k (k = kq, then kq + 4), A[column][k] = bsum
+            const int sh = 8 * kq;
+            const uint32_t a1 = hd.z >> sh, q8 = (hd.w >> sh) & 0xff;
+            const float mn_lo = (float)(int)(a1 & 63);
+            const float mn_hi = (float)(int)((q8 >> 4) | ((a1 >> 6 & 3) << 4));
+            v4f mins = {0.f, 0.f, 0.f, 0.f};
+            mins = __builtin_amdgcn_mfma_f32_16x16x4f32(s_bsf[b * 8 + kq][rl], mn_lo, mins, 0, 0, 0);
+            mins = __builtin_amdgcn_mfma_f32_16x16x4f32(s_bsf[b * 8 + 4 + kq][rl], mn_hi, mins, 0, 0, 0);
+            int acc[4] = {0, 0, 0, 0};
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {                 // two groups of 4 sub-blocks
+                v4i dj[4];
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) {
+                    const int j = 4 * h + jj;
+                    const uint2 raw = qq[j >> 1];
+                    const uint32_t m4 = 0x0F0F0F0Fu;
+                    const uint32_t w0 = (j & 1) ? (raw.x >> 4) & m4 : raw.x & m4;
+                    const uint32_t w1 = (j & 1) ? (raw.y >> 4) & m4 : raw.y & m4;
+                    const long bw = (long)(((uint64_t)w1 << 32) | w0);
+                    // A side: column rl's 8 activations of sub-block j (elements 32 j ..), k-slice kq
+                    const uint2 xv = *reinterpret_cast<const uint2 *>(&s_q[rl][b * QK_K + 32 * j + 8 * kq]);
+                    const long ax = (long)(((uint64_t)xv.y << 32) | xv.x);
+                    const v4i z = {0, 0, 0, 0};
+                    dj[jj] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, bw, z, 0, 0, 0);
+                }
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) {
+                    int scj, mnj;
+                    q4k_scale_min_reg(4 * h + jj, hd.y, hd.z, hd.w, scj, mnj);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[r] = __mul24(scj, dj[jj][r]) + acc[r];
+                }
+            }
+            const float dw = fp16_to_f32((uint16_t)(hd.x & 0xffff)), dmw = fp16_to_f32((uint16_t)(hd.x >> 16));
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int c = 4 * kq + r;
-                const int p = s_pair[c];
-                if (p >= 0) {
-                    float * o = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(a.dst) + (p / a.n_ids) * a.dst_nb2 +
-                                                          (p % a.n_ids) * a.dst_nb1);
-                    o[row] = facc[r] + facc_m[r];
-                }
-                facc[r] = 0.f;
-                facc_m[r] = 0.f;
+                const float dx = s_d[b][4 * kq + r];
+                facc[r] = __builtin_fmaf(dx * dw, (float)acc[r], facc[r]);
+                facc_m[r] = __builtin_fmaf(-dx * dmw, mins[r], facc_m[r]);
             }
-            row += PF_ROWS;
+        };
+        float facc[NS][4], facc_m[NS][4];
+#pragma unroll
+        for (int q = 0; q < NS; ++q)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) { facc[q][r] = 0.f; facc_m[q][r] = 0.f; }
+#pragma unroll 1
+        for (int b0 = 0; b0 < nsteps; b0 += PF)
+#pragma unroll
+        for (int pslot = 0; pslot < PF; ++pslot) {
+            const int st = b0 + pslot;
+            if constexpr (NB % PF != 0) {
+                if (st >= nsteps) break;
+            }
+            const int b = st % NB;
+#pragma unroll
+            for (int q = 0; q < NS; ++q) {
+                // the slot's pieces into the wave's buffer, then the slot is refilled (always: the
+                // tail re-reads the last block) and the lane reads its row's block in MFMA layout.
+                // A wave's LDS operations run in order, so the buffer needs no barrier between
+                // steps or between the gate and up streams.
+                u32x4 * wb4 = reinterpret_cast<u32x4 *>(wbuf);
+                wb4[lane] = wr0[q][pslot];
+                wb4[lane + 64] = wr1[q][pslot];
+                if (lane < 16) wb4[lane + 128] = wr2[q][pslot];
+                load_s(wbase[q], min(st + PF, nsteps - 1), wr0[q][pslot], wr1[q][pslot], wr2[q][pslot]);
+                __builtin_amdgcn_wave_barrier();
+                const uint4 hd = *reinterpret_cast<const uint4 *>(wbuf + rl * 144);
+                uint2 qq[4];
+#pragma unroll
+                for (int jp = 0; jp < 4; ++jp) qq[jp] = *reinterpret_cast<const uint2 *>(wbuf + rl * 144 + 16 + 32 * jp + 8 * kq);
+                __builtin_amdgcn_wave_barrier();
+                block_dot(b, hd, qq, facc[q], facc_m[q]);
+            }
+            if (b == NB - 1) {                          // the row tile is done: its outputs, then the next tile
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int64_t off = s_out[4 * kq + r];
+                    if (off >= 0) {
+                        float * o = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(a.dst) + off);
+                        const float gv = facc[0][r] + facc_m[0][r];
+                        if constexpr (GU) {
+                            const float uv = facc[NS - 1][r] + facc_m[NS - 1][r];
+                            o[row] = (row < a.N - (a.N & 15)) ? v_silu(gv) * uv : gv / (1.0f + libm_expf(-gv)) * uv;
+                        } else {
+                            o[row] = gv;
+                        }
+                    }
+#pragma unroll
+                    for (int q = 0; q < NS; ++q) { facc[q][r] = 0.f; facc_m[q][r] = 0.f; }
+                }
+                row += PF_ROWS;
+            }
         }
     }
 }
 
 size_t prefill_workspace(int64_t K, int64_t N, int64_t n_as, int64_t T, int64_t ne11, int64_t n_ids) {
     const int64_t rows = T * ne11, P = T * n_ids;
-    const int64_t max_items = (P / PF_TOK + n_as) * ((N / PF_ROWS + PF_RT - 1) / PF_RT);
+    const int64_t max_tiles = P / PF_TOK + n_as;                     // column tiles
     size_t o = 0;
     auto take = [&](size_t bytes) { o = align_up(o + bytes, 256); };
     take((size_t)rows * K);
     take(sizeof(float) * rows * (K / QK_K));
     take(sizeof(int32_t) * rows * (K / 16));
     for (int i = 0; i < 4; ++i) take(sizeof(int32_t) * (n_as + 1));   // cnt_copy, off, fill, item_off
-    take(sizeof(int4) * max_items);
+    take(sizeof(int4) * max_tiles);
     take(sizeof(int32_t) * P);                                        // perm
     take(sizeof(int32_t) * P);                                        // eid
     take(256);                                                        // total, err
@@ -289,20 +378,40 @@ bool prefill_supported(int64_t K, int64_t N, int64_t n_as, std::string & why) {
     if (K % QK_K || K > PF_MAXK) { why = "prefill mul_mat_id: K must be a multiple of 256, <= 2048"; return false; }
     if (N % PF_ROWS) { why = "prefill mul_mat_id: N must be a multiple of 64"; return false; }
     if (n_as > PF_MAX_AS) { why = "prefill mul_mat_id: more than 4096 experts"; return false; }
+    if ((uint64_t)N * (uint64_t)(K / QK_K) * 144u >= (1ull << 31)) { why = "prefill mul_mat_id: expert slab of 2 GiB or more"; return false; }
     return true;
 }
 
-int launch_prefill(const MmidArgs & m, uint8_t * ws, hipStream_t s) {
+// The persistent GEMM's grid: the workgroups one launch keeps resident (the
+// occupancy query per kernel and device, done once).
+template <int NB, bool GU>
+static int launch_gemm(const PfArgs & a, hipStream_t s) {
+    static int grid[64] = {};
+    int dev = 0;
+    QWM_HIP_CHECK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) return fail(QWM_ERR_UNSUPPORTED, "prefill mul_mat_id: device index past 63");
+    if (!grid[dev]) {
+        int per_cu = 0, cus = 0;
+        QWM_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_pf_gemm<NB, GU>, 256, 0));
+        QWM_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+        grid[dev] = std::max(1, per_cu) * std::max(1, cus);
+    }
+    k_pf_gemm<NB, GU><<<dim3((unsigned)grid[dev]), 256, 0, s>>>(a);
+    return QWM_OK;
+}
+
+int launch_prefill(const MmidArgs & m, uint8_t * ws, hipStream_t s, const uint8_t * up) {
     if (m.wtype != T_Q4_K) return fail(QWM_ERR_UNSUPPORTED, "prefill mul_mat_id: Q4_K weights only");
     std::string why;
     if (!prefill_supported(m.K, m.N, m.n_as, why)) return fail(QWM_ERR_UNSUPPORTED, why);
     const int64_t rows = m.T * m.ne11, P = m.T * m.n_ids;
-    const int64_t max_items = (P / PF_TOK + m.n_as) * ((m.N / PF_ROWS + PF_RT - 1) / PF_RT);
+    const int64_t max_tiles = P / PF_TOK + m.n_as;
     size_t o = 0;
     auto take = [&](size_t bytes) { size_t at = o; o = align_up(o + bytes, 256); return at; };
     PfArgs a;
     a.b = m.b; a.b_nb1 = m.b_nb1; a.b_nb2 = m.b_nb2; a.ids = m.ids; a.ids_nb1 = m.ids_nb1;
     a.as = m.as; a.slab = m.slab; a.row_bytes = (size_t)(m.K / QK_K) * 144;
+    a.as2 = up;
     a.K = (int)m.K; a.N = (int)m.N; a.ne11 = (int)m.ne11; a.T = (int)m.T; a.n_ids = (int)m.n_ids; a.n_as = (int)m.n_as;
     a.qs = reinterpret_cast<int8_t *>(ws + take((size_t)rows * m.K));
     a.d = reinterpret_cast<float *>(ws + take(sizeof(float) * rows * (m.K / QK_K)));
@@ -311,7 +420,7 @@ int launch_prefill(const MmidArgs & m, uint8_t * ws, hipStream_t s) {
     a.off = reinterpret_cast<int32_t *>(ws + take(sizeof(int32_t) * (m.n_as + 1)));
     a.fill = reinterpret_cast<int32_t *>(ws + take(sizeof(int32_t) * (m.n_as + 1)));
     a.item_off = reinterpret_cast<int32_t *>(ws + take(sizeof(int32_t) * (m.n_as + 1)));
-    a.items = reinterpret_cast<int4 *>(ws + take(sizeof(int4) * max_items));
+    a.items = reinterpret_cast<int4 *>(ws + take(sizeof(int4) * max_tiles));
     a.perm = reinterpret_cast<int32_t *>(ws + take(sizeof(int32_t) * P));
     a.eid = reinterpret_cast<int32_t *>(ws + take(sizeof(int32_t) * P));
     a.total = reinterpret_cast<int32_t *>(ws + take(256));
@@ -322,19 +431,21 @@ int launch_prefill(const MmidArgs & m, uint8_t * ws, hipStream_t s) {
     QWM_TIMED("prefill_prep", s, k_pf_prep<<<prep_grid, 256, 0, s>>>(a));
     k_pf_scan<<<1, 1024, 0, s>>>(a);
     k_pf_scatter<<<(unsigned)std::max<int64_t>(1, std::min<int64_t>(1024, (P + 255) / 256)), 256, 0, s>>>(a);
-    const dim3 grid((unsigned)max_items);
-    prof_begin("prefill_gemm", s);
+    const char * label = up ? "prefill_gemm_gu" : "prefill_gemm";
+    prof_begin(label, s);
+    int rc = QWM_OK;
     switch (m.K / QK_K) {
-        case 1: k_pf_gemm<1><<<grid, 256, 0, s>>>(a); break;
-        case 2: k_pf_gemm<2><<<grid, 256, 0, s>>>(a); break;
-        case 3: k_pf_gemm<3><<<grid, 256, 0, s>>>(a); break;
-        case 4: k_pf_gemm<4><<<grid, 256, 0, s>>>(a); break;
-        case 5: k_pf_gemm<5><<<grid, 256, 0, s>>>(a); break;
-        case 6: k_pf_gemm<6><<<grid, 256, 0, s>>>(a); break;
-        case 7: k_pf_gemm<7><<<grid, 256, 0, s>>>(a); break;
-        default: k_pf_gemm<8><<<grid, 256, 0, s>>>(a); break;
+        case 1: rc = up ? launch_gemm<1, true>(a, s) : launch_gemm<1, false>(a, s); break;
+        case 2: rc = up ? launch_gemm<2, true>(a, s) : launch_gemm<2, false>(a, s); break;
+        case 3: rc = up ? launch_gemm<3, true>(a, s) : launch_gemm<3, false>(a, s); break;
+        case 4: rc = up ? launch_gemm<4, true>(a, s) : launch_gemm<4, false>(a, s); break;
+        case 5: rc = up ? launch_gemm<5, true>(a, s) : launch_gemm<5, false>(a, s); break;
+        case 6: rc = up ? launch_gemm<6, true>(a, s) : launch_gemm<6, false>(a, s); break;
+        case 7: rc = up ? launch_gemm<7, true>(a, s) : launch_gemm<7, false>(a, s); break;
+        default: rc = up ? launch_gemm<8, true>(a, s) : launch_gemm<8, false>(a, s); break;
     }
-    prof_end("prefill_gemm", s);
+    if (rc != QWM_OK) return rc;
+    prof_end(label, s);
     QWM_HIP_CHECK(hipGetLastError());
     return QWM_OK;
 }

@@ -59,6 +59,18 @@ def test_argument_validation_without_gpu():
         L.qwm_mul_mat_id_workspace_size(a64, b64, i64)
     i200 = qa.tensor(qa.TYPE_I32, 200, 64, 1)     # more ids per column than the pair table holds
     assert L.qwm_mul_mat_id_workspace_size(qa.tensor(qa.TYPE_Q8_0, 2048, 512, 256), b64, i200) == 0
+    # the gate/up/SwiGLU call: up must match gate in type and shape; act is [N, n_ids, T]
+    act64 = qa.tensor(qa.TYPE_F32, 512, 4, 64)
+    assert L.qwm_mul_mat_id_swiglu_workspace_size(a64, a64, b64, i64) == L.qwm_mul_mat_id_workspace_size(a64, b64, i64)
+    for up in (qa.tensor(qa.TYPE_Q4_K, 2048, 512, 4), qa.tensor(qa.TYPE_Q8_0, 2048, 512, 8)):
+        assert L.qwm_mul_mat_id_swiglu_workspace_size(a64, up, b64, i64) == 0
+        assert L.qwm_mul_mat_id_swiglu(a64, up, b64, i64, act64, None, 0, None) == qa.ERR_ARG
+    assert L.qwm_mul_mat_id_swiglu(a64, a64, b64, i64, qa.tensor(qa.TYPE_F32, 512, 4, 32), None, 0, None) == qa.ERR_ARG
+    assert L.qwm_mul_mat_id_swiglu(a64, a64, b64, i64, act64, None, 0, None) == qa.ERR_WORKSPACE
+    b4 = qa.tensor(qa.TYPE_F32, 2048, 1, 4)     # 4 columns: two GEMV calls and the SwiGLU pass, gate/up in the workspace
+    i4 = qa.tensor(qa.TYPE_I32, 4, 4, 1)
+    assert L.qwm_mul_mat_id_swiglu_workspace_size(a64, a64, b4, i4) == \
+        2 * 512 * 4 * 4 * 4 + L.qwm_mul_mat_id_workspace_size(a64, b4, i4)
     lay = qa.MoeLayer()
     lay.router = qa.tensor(qa.TYPE_F32, 2048, 128)
     lay.gate_pool = qa.tensor(qa.TYPE_Q4_K, 2048, 768, 4)

@@ -35,10 +35,13 @@ def workspace(nbytes):
     return ws
 
 
-@pytest.mark.parametrize("T,max_slice,shared,fetch", [(40, 0, True, qa.FETCH_GATHER), (40, 0, False, qa.FETCH_MEMCPY),
-                                                      (30, 6, True, qa.FETCH_GATHER), (5, 0, True, qa.FETCH_MEMCPY)])
-def test_cached_batch_matches_oracle(dev, T, max_slice, shared, fetch):
-    H, N, E, k, S = 512, 256, 64, 4, 20
+@pytest.mark.parametrize("T,max_slice,shared,fetch,S", [(40, 0, True, qa.FETCH_GATHER, 20), (40, 0, False, qa.FETCH_MEMCPY, 20),
+                                                        (30, 6, True, qa.FETCH_GATHER, 20), (5, 0, True, qa.FETCH_MEMCPY, 20),
+                                                        (40, 0, True, qa.FETCH_GATHER, 64)])
+def test_cached_batch_matches_oracle(dev, T, max_slice, shared, fetch, S):
+    """S = 64 slots hold every expert: one slice of 40 tokens, whose gate and up
+    slots agree, so it runs the fused gate/up/SwiGLU pass."""
+    H, N, E, k = 512, 256, 64, 4
     case = MoeCase(seed=71 + T, H=H, N=N, E=E, k=k, S=E, shared=shared, N_sh=N)
     rng = np.random.default_rng(T + max_slice)
     slab = case.gate_q.nbytes // E
@@ -87,13 +90,18 @@ def test_cached_batch_matches_oracle(dev, T, max_slice, shared, fetch):
             hids = np.zeros(T * k, np.int32)
             hsl = np.zeros(2 * T, np.int32)
             nsl = ctypes.c_int32()
-            print(f"cached batch T={T} max_slice={max_slice} shared={shared}: rep {rep}", flush=True)
+            print(f"cached batch T={T} max_slice={max_slice} shared={shared} S={S}: rep {rep}", flush=True)
+            qa.check(L.qwm_profile_start(b"prefill_gemm_gu", 64))
             qa.check(L.qwm_moe_cached_batch(lay, h, 0, qa.tensor(qa.TYPE_F32, H, T, 1, dx),
                                             qa.tensor(qa.TYPE_F32, E, T, 1, drm), qa.tensor(qa.TYPE_F32, H, T, 1, dr),
                                             qa.tensor(qa.TYPE_F32, H, T, 1, out), max_slice, ptr(hids), ptr(hsl),
                                             ctypes.byref(nsl), ws.data_ptr(), ws.numel(), None))
             torch.cuda.synchronize()
+            durs = np.zeros(64, np.float32)
+            n_fused = L.qwm_profile_stop(durs.ctypes.data, 64)
             slices = [tuple(hsl[2 * i:2 * i + 2]) for i in range(nsl.value)]
+            if S == E:
+                assert n_fused == sum(1 for _, ln in slices if ln > 8) >= 1, "the fused gate/up pass did not run"
             print(f"  slices {slices}", flush=True)
             assert np.array_equal(hids.reshape(T, k), ids), "routed ids differ"
             assert slices == [tuple(sl_o[2 * i:2 * i + 2]) for i in range(ns_o)], "slices differ from the oracle's"
@@ -114,7 +122,7 @@ def test_cached_batch_matches_oracle(dev, T, max_slice, shared, fetch):
                 for s_, key in enumerate(kg):
                     if key >= 0:
                         assert np.array_equal(dev_bytes[s_], src[key]), f"role {r} slot {s_}"
-        if T >= 40:
+        if T >= 40 and S < E:
             assert nsl.value >= 2, "the batch should need several slices"
     finally:
         L.qwm_pool_destroy(h)

@@ -1,6 +1,7 @@
 """The op-level binding that INTEGRATION.md shows a maintainer adding to a
-ggml backend (its first C++ block: to_qwm and qwm_try_mul_mat_id) compiles
-against the reference's own ggml.h and include/qwmoe.h, and the layouts it
+ggml backend (its first C++ block: to_qwm and qwm_try_mul_mat_id; and the
+gate/up/SwiGLU node fusion, qwm_try_gate_up_swiglu) compiles against the
+reference's own ggml.h and include/qwmoe.h, and the layouts it
 relies on hold there: the ggml_type values the C ABI names equal ggml's,
 GGML_MAX_DIMS is 4, and qwm_tensor's ne/nb arrays match ggml_tensor's.
 Skipped where the reference tree is absent."""
@@ -25,6 +26,7 @@ static_assert(sizeof(((ggml_tensor *)0)->ne[0]) == sizeof(int64_t) && sizeof(((g
               "element types of ne[] and nb[]");
 // the stub is used, so the snippet's functions are instantiated and checked
 bool use_snippet(ggml_tensor * node, void * ws, size_t n, hipStream_t s) { return qwm_try_mul_mat_id(node, ws, n, s); }
+int use_fusion(ggml_tensor ** nodes, int n, void * ws, size_t b, hipStream_t s) { return qwm_try_gate_up_swiglu(nodes, n, 0, ws, b, s); }
 """
 
 
@@ -32,7 +34,8 @@ def snippet():
     text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
     blocks = re.findall(r"```cpp\n(.*?)```", text, re.S)
     block = next(b for b in blocks if "qwm_try_mul_mat_id" in b and "to_qwm" in b)
-    return block
+    fusion = next(b for b in blocks if "qwm_try_gate_up_swiglu" in b)
+    return block + fusion
 
 
 @pytest.mark.skipif(not os.path.isdir(GGML_INC), reason="the reference tree is not present")

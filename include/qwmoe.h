@@ -101,6 +101,13 @@ int qwm_mul_mat_id(const qwm_tensor * as, const qwm_tensor * b, const qwm_tensor
  * are quantized once).  Otherwise two qwm_mul_mat_id calls into the workspace
  * and an element-wise pass.  Either way act equals, bit for bit, SwiGLU
  * applied to what two qwm_mul_mat_id calls return. */
+/* GGML_GLU_OP_SWIGLU in split form (ggml_swiglu_split, ggml.c:3082; CPU
+ * ggml_compute_forward_swiglu_f32, ops.cpp:3331-3385): act = silu(gate) * up
+ * per row of ne[0] elements, ggml_vec_swiglu_f32's vectorized silu on the
+ * 16-wide chunks and libm expf on the tail.  gate, up, act: contiguous f32 of
+ * one shape; act may alias gate or up.  No workspace. */
+int qwm_swiglu(const qwm_tensor * gate, const qwm_tensor * up, qwm_tensor * act, void * stream);
+
 size_t qwm_mul_mat_id_swiglu_workspace_size(const qwm_tensor * gate, const qwm_tensor * up, const qwm_tensor * b,
                                             const qwm_tensor * ids);
 int qwm_mul_mat_id_swiglu(const qwm_tensor * gate, const qwm_tensor * up, const qwm_tensor * b, const qwm_tensor * ids,

@@ -106,6 +106,7 @@ def lib():
         "qwm_workspace_init": (ctypes.c_int, [_P, _SZ, _P]),
         "qwm_mul_mat_id_workspace_size": (_SZ, [T, T, T]),
         "qwm_mul_mat_id": (ctypes.c_int, [T, T, T, T, _P, _SZ, _P]),
+        "qwm_swiglu": (ctypes.c_int, [T, T, T, _P]),
         "qwm_mul_mat_id_swiglu_workspace_size": (_SZ, [T, T, T, T]),
         "qwm_mul_mat_id_swiglu": (ctypes.c_int, [T, T, T, T, T, _P, _SZ, _P]),
         "qwm_moe_workspace_size": (_SZ, [ctypes.POINTER(MoeLayer), _I64]),

@@ -236,6 +236,23 @@ int qwm_mul_mat_id(const qwm_tensor * as, const qwm_tensor * b, const qwm_tensor
     });
 }
 
+int qwm_swiglu(const qwm_tensor * gate, const qwm_tensor * up, qwm_tensor * act, void * stream) {
+    return guard("qwm_swiglu", [&]() -> int {
+        if (!gate || !up || !act) return fail(QWM_ERR_ARG, "swiglu: NULL tensor");
+        const qwm_tensor * t3[3] = {gate, up, act};
+        for (const qwm_tensor * t : t3) {
+            if (t->type != T_F32) return fail(QWM_ERR_ARG, "swiglu: tensors must be f32");
+            if (!fully_contiguous(t)) return fail(QWM_ERR_UNSUPPORTED, "swiglu: tensors must be contiguous");
+            for (int i = 0; i < 4; ++i)
+                if (t->ne[i] != gate->ne[i]) return fail(QWM_ERR_ARG, "swiglu: gate, up and act differ in shape");
+        }
+        const int64_t n = gate->ne[0], rows = gate->ne[1] * gate->ne[2] * gate->ne[3];
+        if (n < 1 || n > INT32_MAX) return fail(QWM_ERR_UNSUPPORTED, "swiglu: row length out of range");
+        return launch_swiglu_rows((const float *)gate->data, (const float *)up->data, (float *)act->data, (int)n, rows,
+                                  (hipStream_t)stream);
+    });
+}
+
 // gate and up of one expert FFN: both the same quantized [K, N, n_as] layout
 // (the same slab stride too), act a contiguous f32 [N, n_ids, T].
 static int check_swiglu(const qwm_tensor * gate, const qwm_tensor * up, const qwm_tensor * b, const qwm_tensor * ids,

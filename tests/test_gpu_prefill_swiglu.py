@@ -138,3 +138,24 @@ def test_swiglu_qwen3_next_full_size(dev):
         np.testing.assert_array_equal(act.view(np.uint32), swiglu_rows(g, u).view(np.uint32))
         print(f"qwen3-next T={T}: fused == separate over {act.size} outputs")
 
+
+
+@pytest.mark.parametrize("N,rows", [(512, 37), (200, 9), (7, 3)])
+def test_swiglu_node_matches_oracle(dev, N, rows):
+    """qwm_swiglu (the GGML_GLU_OP_SWIGLU node alone): bit for bit against the
+    oracle's ggml_vec_swiglu_f32 per row, 16-wide chunks and the scalar tail
+    (N 200 and 7 have one), also with act written over gate."""
+    rng = np.random.default_rng(N + rows)
+    g = (rng.standard_normal((rows, N)) * 4).astype(np.float32)
+    u = rng.standard_normal((rows, N)).astype(np.float32)
+    exp = swiglu_rows(g, u)
+    L = qa.lib()
+    dg, du = torch.from_numpy(g).cuda(), torch.from_numpy(u).cuda()
+    act = torch.full((rows, N), float("nan"), dtype=torch.float32, device="cuda")
+    tg, tu = qa.tensor(qa.TYPE_F32, N, rows, 1, dg), qa.tensor(qa.TYPE_F32, N, rows, 1, du)
+    qa.check(L.qwm_swiglu(tg, tu, qa.tensor(qa.TYPE_F32, N, rows, 1, act), None))
+    qa.check(L.qwm_swiglu(tg, tu, tg, None))                       # in place over gate
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(act.cpu().numpy().view(np.uint32), exp.view(np.uint32))
+    np.testing.assert_array_equal(dg.cpu().numpy().view(np.uint32), exp.view(np.uint32))
+    assert L.qwm_swiglu(tg, qa.tensor(qa.TYPE_F32, N, rows + 1, 1, du), tg, None) == qa.ERR_ARG

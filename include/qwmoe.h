@@ -83,24 +83,16 @@ int qwm_workspace_init(void * workspace, size_t bytes, void * stream);
  *   dst[:, e, t] = as[:, :, ids[e, t]] . b[:, e % ne11(b), t]
  * as: Q4_K, Q5_K, Q6_K or Q8_0 [K, N, n_as]; b: f32 [K, ne11, T]; ids: i32
  * [n_ids, T]; dst: f32 [N, n_ids, T].  Supported: K % 256 == 0 and
- * K <= 2048; Q5_K data 16-byte aligned, Q6_K 4-byte aligned.
+ * K <= 2048; Q5_K data 16-byte aligned, Q6_K and Q8_0 4-byte aligned.
  *   T <= 8: one GEMV launch, n_ids * T <= 128.
- *   T > 8, Q4_K: the grouped int8-MFMA GEMM (prefill), n_ids * T <= 2^22.
- *   T > 8, other types: GEMV launches over column chunks, n_ids <= 128. */
+ *   T > 8, Q4_K or Q8_0 with N % 64 == 0 and 16-byte aligned data: the
+ *   grouped int8-MFMA GEMM (prefill), n_ids * T <= 2^22.
+ *   T > 8, otherwise: GEMV launches over column chunks, n_ids <= 128.
+ * The workspace size covers either T > 8 path. */
 size_t qwm_mul_mat_id_workspace_size(const qwm_tensor * as, const qwm_tensor * b, const qwm_tensor * ids);
 int qwm_mul_mat_id(const qwm_tensor * as, const qwm_tensor * b, const qwm_tensor * ids, qwm_tensor * dst,
                    void * workspace, size_t ws_bytes, void * stream);
 
-/* The expert FFN's first half in one call: act = ggml_swiglu_split(
- * MUL_MAT_ID(gate, b, ids), MUL_MAT_ID(up, b, ids)), the two MUL_MAT_ID nodes
- * and the GGML_GLU_OP_SWIGLU node of build_segB (core/runtime.cpp:4539-4541;
- * ops.cpp:3331-3385).  gate and up: same type, shape and strides, each as
- * qwm_mul_mat_id's `as`; act: contiguous f32 [N, n_ids, T].  For T > 8 and
- * Q4_K one grouped-GEMM pass streams the gate and up rows of each tile side
- * by side and writes act (no gate/up intermediates in HBM; the activations
- * are quantized once).  Otherwise two qwm_mul_mat_id calls into the workspace
- * and an element-wise pass.  Either way act equals, bit for bit, SwiGLU
- * applied to what two qwm_mul_mat_id calls return. */
 /* GGML_GLU_OP_SWIGLU in split form (ggml_swiglu_split, ggml.c:3082; CPU
  * ggml_compute_forward_swiglu_f32, ops.cpp:3331-3385): act = silu(gate) * up
  * per row of ne[0] elements, ggml_vec_swiglu_f32's vectorized silu on the
@@ -108,6 +100,17 @@ int qwm_mul_mat_id(const qwm_tensor * as, const qwm_tensor * b, const qwm_tensor
  * one shape; act may alias gate or up.  No workspace. */
 int qwm_swiglu(const qwm_tensor * gate, const qwm_tensor * up, qwm_tensor * act, void * stream);
 
+/* The expert FFN's first half in one call: act = ggml_swiglu_split(
+ * MUL_MAT_ID(gate, b, ids), MUL_MAT_ID(up, b, ids)), the two MUL_MAT_ID nodes
+ * and the GGML_GLU_OP_SWIGLU node of build_segB (core/runtime.cpp:4539-4541;
+ * ops.cpp:3331-3385).  gate and up: same type, shape and strides, each as
+ * qwm_mul_mat_id's `as`; act: contiguous f32 [N, n_ids, T].  Where
+ * qwm_mul_mat_id takes the grouped GEMM, one grouped pass streams the gate
+ * and up rows of each tile side by side and writes act (no gate/up
+ * intermediates in HBM; the activations are quantized once).  Otherwise two
+ * qwm_mul_mat_id calls into the workspace and an element-wise pass; the
+ * workspace size covers both.  Either way act equals, bit for bit, SwiGLU
+ * applied to what two qwm_mul_mat_id calls return. */
 size_t qwm_mul_mat_id_swiglu_workspace_size(const qwm_tensor * gate, const qwm_tensor * up, const qwm_tensor * b,
                                             const qwm_tensor * ids);
 int qwm_mul_mat_id_swiglu(const qwm_tensor * gate, const qwm_tensor * up, const qwm_tensor * b, const qwm_tensor * ids,

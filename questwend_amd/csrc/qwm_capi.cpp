@@ -152,6 +152,15 @@ int qwm_profile_stop(float * durations_ms, int32_t capacity) {
 
 // ------------------------------------------------------------ mul_mat_id --
 
+// The grouped GEMM takes more than MAX_T columns of Q4_K or Q8_0 weights in the
+// shapes it supports (N % 64, K <= 2048, 16-byte aligned data); `data` false
+// leaves the alignment out (a size query before the weights are placed).
+static bool prefill_shape(const qwm_tensor * as, const qwm_tensor * b, bool data = true) {
+    std::string why;
+    return b->ne[2] > MAX_T && prefill_supported(as->type, as->ne[0], as->ne[1], as->ne[2], data ? as->data : nullptr, why);
+}
+static bool prefill_path(const qwm_tensor * as, const qwm_tensor * b) { return prefill_shape(as, b, true); }
+
 static int check_mmid(const qwm_tensor * as, const qwm_tensor * b, const qwm_tensor * ids, const qwm_tensor * dst) {
     if (!as || !b || !ids) return fail(QWM_ERR_ARG, "mul_mat_id: NULL tensor");
     if (as->type != T_Q4_K && as->type != T_Q8_0 && as->type != T_Q6_K && as->type != T_Q5_K)
@@ -160,6 +169,8 @@ static int check_mmid(const qwm_tensor * as, const qwm_tensor * b, const qwm_ten
         return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: Q5_K weights need 16-byte aligned data");
     if (as->type == T_Q6_K && ((uintptr_t)as->data % 4))   // rows and slabs may start 2 bytes off: handled
         return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: Q6_K weights need 4-byte aligned data");
+    if (as->type == T_Q8_0 && ((uintptr_t)as->data % 4))   // the row dots read dwords from the row start
+        return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: Q8_0 weights need 4-byte aligned data");
     if (b->type != T_F32 || ids->type != T_I32) return fail(QWM_ERR_ARG, "mul_mat_id: b must be f32 and ids i32");
     // ggml.c:3418-3428
     if (as->ne[3] != 1 || b->ne[3] != 1 || ids->ne[2] != 1 || ids->ne[3] != 1)
@@ -170,11 +181,9 @@ static int check_mmid(const qwm_tensor * as, const qwm_tensor * b, const qwm_ten
     if (!fully_contiguous(as)) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: as must be contiguous");
     if (b->nb[0] != 4 || ids->nb[0] != 4) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: b/ids must have unit element stride");
     if ((b->nb[1] | b->nb[2]) % 16) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: b rows must be 16-byte aligned");
-    if (b->ne[2] > MAX_T && as->type == T_Q4_K) {   // prefill: the grouped GEMM (qwm_prefill.hip)
-        std::string why;
-        if (!prefill_supported(as->ne[0], as->ne[1], as->ne[2], why)) return fail(QWM_ERR_UNSUPPORTED, why);
+    if (prefill_path(as, b)) {                  // prefill: the grouped GEMM (qwm_prefill.hip)
         if (ids->ne[0] * ids->ne[1] > (1 << 22)) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: too many (expert, column) pairs");
-    } else if (b->ne[2] > MAX_T) {              // other types: the GEMV path over column chunks
+    } else if (b->ne[2] > MAX_T) {              // other types and shapes: the GEMV path over column chunks
         if (ids->ne[0] > MAX_PAIRS) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: too many ids per column");
     } else if (ids->ne[0] * ids->ne[1] > MAX_PAIRS) {
         return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: too many (expert, column) pairs");
@@ -196,9 +205,13 @@ static int64_t mmid_chunk(int64_t n_ids) { return std::max<int64_t>(1, std::min<
 size_t qwm_mul_mat_id_workspace_size(const qwm_tensor * as, const qwm_tensor * b, const qwm_tensor * ids) {
     return guard_size("qwm_mul_mat_id_workspace_size", [&]() -> size_t {
         if (check_mmid(as, b, ids, nullptr) != QWM_OK) return 0;
-        if (b->ne[2] > MAX_T && as->type == T_Q4_K)
-            return prefill_workspace(as->ne[0], as->ne[1], as->ne[2], b->ne[2], b->ne[1], ids->ne[0]);
-        return mmid_workspace(as->ne[0], std::min<int64_t>(b->ne[2], mmid_chunk(ids->ne[0])), b->ne[1], ids->ne[0]);
+        // either path's need: the grouped GEMM, or the GEMV chunks it falls back to for unaligned weights
+        size_t need = 0;
+        if (ids->ne[0] <= MAX_PAIRS)
+            need = mmid_workspace(as->ne[0], std::min<int64_t>(b->ne[2], mmid_chunk(ids->ne[0])), b->ne[1], ids->ne[0]);
+        if (prefill_shape(as, b, false))
+            need = std::max(need, prefill_workspace(as->ne[0], as->ne[1], as->ne[2], b->ne[2], b->ne[1], ids->ne[0]));
+        return need;
     });
 }
 
@@ -208,7 +221,7 @@ int qwm_mul_mat_id(const qwm_tensor * as, const qwm_tensor * b, const qwm_tensor
         int rc = check_mmid(as, b, ids, dst);
         if (rc != QWM_OK) return rc;
         if (!dst) return fail(QWM_ERR_ARG, "mul_mat_id: dst is NULL");
-        const bool prefill = b->ne[2] > MAX_T && as->type == T_Q4_K;
+        const bool prefill = prefill_path(as, b);
         const int64_t chunk = std::min<int64_t>(b->ne[2], mmid_chunk(ids->ne[0]));
         const size_t need = prefill ? prefill_workspace(as->ne[0], as->ne[1], as->ne[2], b->ne[2], b->ne[1], ids->ne[0])
                                     : mmid_workspace(as->ne[0], chunk, b->ne[1], ids->ne[0]);
@@ -268,20 +281,27 @@ static int check_swiglu(const qwm_tensor * gate, const qwm_tensor * up, const qw
     return QWM_OK;
 }
 
-static bool swiglu_fused(const qwm_tensor * gate, const qwm_tensor * b) { return b->ne[2] > MAX_T && gate->type == T_Q4_K; }
+static bool swiglu_fused(const qwm_tensor * gate, const qwm_tensor * up, const qwm_tensor * b) {
+    return prefill_path(gate, b) && prefill_path(up, b);
+}
 
 // the separate path's layout: g and u [N, n_ids, T] f32, then the MUL_MAT_ID workspace
 static size_t swiglu_split_bytes(const qwm_tensor * gate, const qwm_tensor * b, const qwm_tensor * ids) {
     return align_up(sizeof(float) * (size_t)gate->ne[1] * ids->ne[0] * b->ne[2], 256);
 }
 
+// workspace of one path: the grouped pass (fused) or the two calls and SwiGLU
+static size_t swiglu_need(const qwm_tensor * gate, const qwm_tensor * b, const qwm_tensor * ids, bool fused) {
+    if (fused) return prefill_workspace(gate->ne[0], gate->ne[1], gate->ne[2], b->ne[2], b->ne[1], ids->ne[0]);
+    return 2 * swiglu_split_bytes(gate, b, ids) + qwm_mul_mat_id_workspace_size(gate, b, ids);
+}
+
 size_t qwm_mul_mat_id_swiglu_workspace_size(const qwm_tensor * gate, const qwm_tensor * up, const qwm_tensor * b,
                                             const qwm_tensor * ids) {
     return guard_size("qwm_mul_mat_id_swiglu_workspace_size", [&]() -> size_t {
         if (check_swiglu(gate, up, b, ids, nullptr) != QWM_OK) return 0;
-        if (swiglu_fused(gate, b))
-            return prefill_workspace(gate->ne[0], gate->ne[1], gate->ne[2], b->ne[2], b->ne[1], ids->ne[0]);
-        return 2 * swiglu_split_bytes(gate, b, ids) + qwm_mul_mat_id_workspace_size(gate, b, ids);
+        // either path's need (the split path serves weights the grouped pass cannot take)
+        return std::max(swiglu_need(gate, b, ids, prefill_shape(gate, b, false)), swiglu_need(gate, b, ids, false));
     });
 }
 
@@ -291,10 +311,11 @@ int qwm_mul_mat_id_swiglu(const qwm_tensor * gate, const qwm_tensor * up, const 
         int rc = check_swiglu(gate, up, b, ids, act);
         if (rc != QWM_OK) return rc;
         if (!act) return fail(QWM_ERR_ARG, "mul_mat_id_swiglu: act is NULL");
-        const size_t need = qwm_mul_mat_id_swiglu_workspace_size(gate, up, b, ids);
+        const bool fused = swiglu_fused(gate, up, b);
+        const size_t need = swiglu_need(gate, b, ids, fused);
         if (!workspace || ws_bytes < need) return fail(QWM_ERR_WORKSPACE, "mul_mat_id_swiglu: workspace too small");
         hipStream_t s = (hipStream_t)stream;
-        if (swiglu_fused(gate, b)) {
+        if (fused) {
             MmidArgs a;
             a.wtype = gate->type; a.as = (const uint8_t *)gate->data; a.slab = gate->nb[2];
             a.K = gate->ne[0]; a.N = gate->ne[1]; a.n_as = gate->ne[2];
@@ -744,8 +765,8 @@ int qwm_moe_cached_batch(const qwm_moe_layer * layer, qwm_pool * pool, int32_t l
             qwm_tensor_init(&dt, QWM_TYPE_F32, Nout, n_ids, len, dst);
             return qwm_mul_mat_id(&as, &bt, &it, &dt, ws + b.mmid, b.mmid_bytes, s);
         };
-        // the fused gate/up pass needs the prefill GEMM's type and one layout for both pools
-        bool fuse_gate_up = layer->gate_pool.type == T_Q4_K && layer->up_pool.type == T_Q4_K;
+        // the fused gate/up pass: both pools in one layout that the grouped GEMM takes
+        bool fuse_gate_up = layer->gate_pool.type == layer->up_pool.type;
         for (int i = 0; i < 4 && fuse_gate_up; ++i)
             fuse_gate_up = layer->gate_pool.ne[i] == layer->up_pool.ne[i] && layer->gate_pool.nb[i] == layer->up_pool.nb[i];
         float * gbuf = (float *)(ws + b.gate);
@@ -766,7 +787,10 @@ int qwm_moe_cached_batch(const qwm_moe_layer * layer, qwm_pool * pool, int32_t l
             QWM_HIP_CHECK(hipMemcpyAsync(dsd, sd, 4 * cnt, hipMemcpyHostToDevice, s));
             if ((rc = qwm_pool_wait(pool, stream)) != QWM_OK) return rc;
             const float * xs = xd + t0 * H;
-            if (fuse_gate_up && len > MAX_T && std::memcmp(sg, su, 4 * cnt) == 0) {
+            qwm_tensor xb;
+            qwm_tensor_init(&xb, QWM_TYPE_F32, H, 1, len, (void *)xs);
+            if (fuse_gate_up && swiglu_fused(&layer->gate_pool, &layer->up_pool, &xb) &&
+                std::memcmp(sg, su, 4 * cnt) == 0) {
                 // gate and up rows under the same slots: one grouped pass writes act (equal, bit
                 // for bit, to the two calls and SwiGLU below; same workspace as one prefill call)
                 qwm_tensor bt, it, at;

@@ -151,8 +151,10 @@ size_t mmid_workspace(int64_t K, int64_t T, int64_t ne11, int64_t n_ids);
 int launch_mmid(const MmidArgs & a, uint8_t * ws, hipStream_t s);
 // prefill-sized batches (T > MAX_T), qwm_prefill.hip
 size_t prefill_workspace(int64_t K, int64_t N, int64_t n_as, int64_t T, int64_t ne11, int64_t n_ids);
-bool prefill_supported(int64_t K, int64_t N, int64_t n_as, std::string & why);
-// up != nullptr: the gate/up/SwiGLU pass (a.as = gate, dst = act), Q4_K only
+// the grouped GEMM's reach: Q4_K or Q8_0 weights, K % 256 == 0 and <= 2048, N % 64 == 0,
+// at most 4096 experts, slabs below 2 GiB, `as` 16-byte aligned (nullptr: not checked)
+bool prefill_supported(int32_t wtype, int64_t K, int64_t N, int64_t n_as, const void * as, std::string & why);
+// up != nullptr: the gate/up/SwiGLU pass (a.as = gate, dst = act)
 int launch_prefill(const MmidArgs & a, uint8_t * ws, hipStream_t s, const uint8_t * up = nullptr);
 
 // ---- the fused verify step (qwm_step.hip) ----

@@ -17,6 +17,7 @@
 
 #include "qwm_internal.h"
 #include "qwm_q4k.h"
+#include "qwm_q80.h"
 
 namespace qwm {
 
@@ -35,14 +36,18 @@ struct PfArgs {
     const uint8_t * as; size_t slab, row_bytes;
     const uint8_t * as2;                      // GU: the up matrix (same type, shape and slabs as `as`)
     int K, N, ne11, T, n_ids, n_as;
-    int8_t * qs; float * d; int32_t * bs;     // Q8_K rows of b: [T * ne11]
+    int q8;                                   // weights Q8_0 (b quantized to Q8_0), else Q4_K (b to Q8_K)
+    int8_t * qs; float * d; int32_t * bs;     // quantized rows of b [T * ne11]: values, scales (K/32 per
+                                              // row), Q8_K sums of 16 (Q4_K only)
     int32_t * cnt_copy; int32_t * off; int32_t * fill; int32_t * item_off;
     int4 * items;                             // per work item: expert, first column, columns, first row tile
     int32_t * perm; int32_t * eid; int32_t * total; int32_t * err;
     float * dst; size_t dst_nb1, dst_nb2;
 };
 
-// Q8_K of b's columns (one 256-block per wave) and each pair's expert.
+// b's columns quantized (one 256-block per wave): Q8_K for Q4_K weights
+// (quantize_row_q8_K), ggml's x86 Q8_0 quantizer for Q8_0 weights; and each
+// pair's expert.
 __global__ void __launch_bounds__(256) k_pf_prep(PfArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int rows = a.T * a.ne11, nb = a.K / QK_K;
@@ -50,8 +55,12 @@ __global__ void __launch_bounds__(256) k_pf_prep(PfArgs a) {
         const int row = jb / nb, b = jb % nb;
         const int t = row / a.ne11, i = row % a.ne11;
         const float * src = reinterpret_cast<const float *>(reinterpret_cast<const uint8_t *>(a.b) + t * a.b_nb2 + i * a.b_nb1);
-        quantize_block_q8K(src + b * QK_K, a.qs + (size_t)row * a.K + b * QK_K, a.d + (size_t)row * nb + b,
-                           a.bs + (size_t)row * (a.K / 16) + b * 16, lane);
+        if (a.q8)
+            quantize_q80_256(src + b * QK_K, a.qs + (size_t)row * a.K + b * QK_K, a.d + (size_t)row * (a.K / 32) + b * 8,
+                             lane);
+        else
+            quantize_block_q8K(src + b * QK_K, a.qs + (size_t)row * a.K + b * QK_K, a.d + (size_t)row * (a.K / 32) + b,
+                               a.bs + (size_t)row * (a.K / 16) + b * 16, lane);
     }
     const int P = a.T * a.n_ids;
     for (int p = blockIdx.x * blockDim.x + threadIdx.x; p < P; p += gridDim.x * blockDim.x) {
@@ -138,25 +147,32 @@ __global__ void __launch_bounds__(256) k_pf_scatter(PfArgs a) {
 // (a.as), and each output is ggml_swiglu_split's silu(gate) * up (the
 // vectorized silu on the rows' 16-wide chunks, libm expf on the tail, as
 // k_swiglu_rows): the dots are those of two separate calls bit for bit.
-// Three workgroups per CU (LDS 47 KB each at K 2048; 168 VGPRs), two where that
-// budget spills (gate/up with 1, 6 or 7 blocks per row).
-template <int NB, bool GU>
-constexpr int pf_occupancy() { return (GU && (NB == 1 || NB >= 6 && NB != 8)) ? 2 : 3; }
+// Q8: Q8_0 weights (34-byte blocks of 32: fp16 d and int8 values), each block's
+// exact int32 dot on one MFMA and d_w d_x sumi in fp32; the activations are
+// Q8_0 (ggml's vec_dot_type for Q8_0).
+// Three workgroups per CU for Q4_K (LDS 47 KB each at K 2048; 168 VGPRs), two
+// where that budget spills (gate/up with 1, 6 or 7 blocks per row) and for Q8_0
+// (64 KB of LDS at K 2048).
+template <int NB, bool GU, bool Q8>
+constexpr int pf_occupancy() { return (Q8 || (GU && (NB == 1 || NB >= 6 && NB != 8))) ? 2 : 3; }
 
-template <int NB, bool GU>
-__global__ void __launch_bounds__(256, (pf_occupancy<NB, GU>())) k_pf_gemm(PfArgs a) {
+template <int NB, bool GU, bool Q8>
+__global__ void __launch_bounds__(256, (pf_occupancy<NB, GU, Q8>())) k_pf_gemm(PfArgs a) {
     constexpr int K = NB * QK_K;
+    // a step is the wave's 16 rows x 256 weights: PPR 16-byte pieces per row (one
+    // 144-byte Q4_K block, or eight 34-byte Q8_0 blocks), SP pieces, NL loads per lane
+    constexpr int PPR = Q8 ? 17 : 9, SROW = 16 * PPR, SP = 16 * PPR, NL = (SP + 63) / 64;
     // rows padded by 8 bytes: the operand reads (16 columns x 4 k-slices x 8 B)
     // are then free of bank conflicts (measured on gfx950: none with 8, some with
     // 16 or 32, many with no padding); the rows are 8-byte aligned
     constexpr int QP = K + 8;
     constexpr int NS = GU ? 2 : 1;                      // weight streams
-    __shared__ __align__(16) int8_t s_q[PF_TOK][QP];   // the columns' Q8_K values
-    __shared__ float s_d[NB][PF_TOK];
+    __shared__ __align__(16) int8_t s_q[PF_TOK][QP];   // the columns' quantized values
+    __shared__ __align__(16) float s_d[Q8 ? NB * 8 : NB][PF_TOK];   // their scales (per 32 or per 256)
     // the sums of the 32 Q8_K values of each sub-block, [sub-block][column]: integers below 2^12 in
     // magnitude, held as floats for the mins' f32 MFMA (A[column][sub-block] at lane column + 16 k)
-    __shared__ __align__(16) float s_bsf[NB * 8][PF_TOK];
-    __shared__ __align__(16) uint8_t s_w[4][16 * 144];   // each wave's staging of one step's weights
+    __shared__ __align__(16) float s_bsf[Q8 ? 1 : NB * 8][PF_TOK];
+    __shared__ __align__(16) uint8_t s_w[4][16 * SROW];  // each wave's staging of one step's weights
     __shared__ int32_t s_pair[PF_TOK];                  // each column's Q8_K row of b, -1: none
     __shared__ int64_t s_out[PF_TOK];                   // byte offset of each column's output row in dst, -1: none
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -176,41 +192,40 @@ __global__ void __launch_bounds__(256, (pf_occupancy<NB, GU>())) k_pf_gemm(PfArg
         __syncthreads();                                     // the previous segment's column tables are read
         const int rl = lane & 15, kq = lane >> 4;           // B side: row rl, k-slice kq; outputs: columns 4 kq .. +3
         int row = rt0 * PF_ROWS + wave * 16 + rl;           // the lane's output row
-        // A step's weights (the wave's 16 rows x one block, 2304 bytes) are loaded as
-        // whole 16-byte pieces: piece p = lane + 64 i (i < 3, p < 144) is piece p % 9
-        // of row p / 9's block, so one load covers about 7 rows' blocks in full (the
+        // A step's weights (the wave's 16 rows x SROW bytes) are loaded as whole
+        // 16-byte pieces: piece p = lane + 64 i (i < NL, p < SP) is piece p % PPR of
+        // row p / PPR's step, so one load covers several rows' steps in full (the
         // 8-byte slices each lane needs for the MFMA would touch 16 lines for 32 bytes
         // per load, which holds the stream near half the HBM rate).  Piece p goes to
-        // byte 16 p of the wave's LDS buffer, which then holds the 16 blocks in block
-        // layout.  The first PF steps are requested before the columns are staged.
+        // byte 16 p of the wave's LDS buffer, which then holds the 16 rows' steps in
+        // block layout.  The first PF steps are requested before the columns are staged.
         // wave-uniform bases (scalar registers) and 32-bit lane offsets: a segment stays
         // inside one expert's slab, below 2 GiB (checked at launch)
         const int wave_u = __builtin_amdgcn_readfirstlane(wave);
         const uint8_t * wbase[NS];
         wbase[0] = a.as + (size_t)e * a.slab + (size_t)(rt0 * PF_ROWS + wave_u * 16) * a.row_bytes;
         if constexpr (GU) wbase[1] = a.as2 + (size_t)e * a.slab + (size_t)(rt0 * PF_ROWS + wave_u * 16) * a.row_bytes;
-        uint32_t poff[3];
+        uint32_t poff[NL];
 #pragma unroll
-        for (int i = 0; i < 3; ++i) {
-            const int pc = min(lane + 64 * i, 143);           // lanes past piece 143 load it again (not staged)
-            poff[i] = (uint32_t)(pc / 9) * (uint32_t)a.row_bytes + (uint32_t)(pc % 9) * 16u;
+        for (int i = 0; i < NL; ++i) {
+            const int pc = min(lane + 64 * i, SP - 1);        // lanes past the last piece load it again (not staged)
+            poff[i] = (uint32_t)(pc / PPR) * (uint32_t)a.row_bytes + (uint32_t)(pc % PPR) * 16u;
         }
         // ring depth: steps in flight per stream, a divisor of NB (every group of PF steps is
         // then whole); 3 waves per SIMD leave room for one step of each stream beside the other
         // (deeper rings spill at that budget)
         constexpr int PF = (GU || NB <= 2) ? 1 : (NB % 2 == 0 ? 2 : 1);
-        u32x4 wr0[NS][PF], wr1[NS][PF], wr2[NS][PF];        // the ring: a step's three pieces per lane
-        // step st: block st % NB of row tile rt0 + st / NB
-        auto load_s = [&](const uint8_t * base, int st, u32x4 & w0, u32x4 & w1, u32x4 & w2) {
-            const uint32_t o = (uint32_t)(st / NB) * (uint32_t)(PF_ROWS * a.row_bytes) + (uint32_t)(st % NB) * 144u;
-            w0 = *reinterpret_cast<const u32x4 *>(base + (poff[0] + o));
-            w1 = *reinterpret_cast<const u32x4 *>(base + (poff[1] + o));
-            w2 = *reinterpret_cast<const u32x4 *>(base + (poff[2] + o));
+        u32x4 wr[NL][NS][PF];                               // the ring: a step's pieces per lane
+        // step st: the st % NB-th 256 weights of row tile rt0 + st / NB
+        auto load_s = [&](int q, int p, int st) {
+            const uint32_t o = (uint32_t)(st / NB) * (uint32_t)(PF_ROWS * a.row_bytes) + (uint32_t)(st % NB) * (uint32_t)SROW;
+#pragma unroll
+            for (int i = 0; i < NL; ++i) wr[i][q][p] = *reinterpret_cast<const u32x4 *>(wbase[q] + (poff[i] + o));
         };
 #pragma unroll
         for (int p = 0; p < PF; ++p)
 #pragma unroll
-            for (int q = 0; q < NS; ++q) load_s(wbase[q], p, wr0[q][p], wr1[q][p], wr2[q][p]);   // PF <= NB: the first row tile
+            for (int q = 0; q < NS; ++q) load_s(q, p, p);     // PF <= NB: inside the first row tile
         // the tile's columns: Q8_K rows of b into LDS (zeros past nc)
         // (pair p = t n_ids + slot: column t of b, row slot % ne11 of it; output row (slot, t))
         if (tid < PF_TOK) {
@@ -234,15 +249,19 @@ __global__ void __launch_bounds__(256, (pf_occupancy<NB, GU>())) k_pf_gemm(PfArg
         for (int v = tid; v < PF_TOK * NB * 8; v += 256) {
             const int c = v / (NB * 8), j = v % (NB * 8);
             const int src = s_pair[c];
-            int sm = 0;
-            float dd = 0.f;
-            if (src >= 0) {
-                const int2 bs = reinterpret_cast<const int2 *>(a.bs + (size_t)src * (K / 16))[j];
-                sm = bs.x + bs.y;
-                if ((j & 7) == 0) dd = a.d[(size_t)src * NB + j / 8];
+            if constexpr (Q8) {
+                s_d[j][c] = src >= 0 ? a.d[(size_t)src * (K / 32) + j] : 0.f;
+            } else {
+                int sm = 0;
+                float dd = 0.f;
+                if (src >= 0) {
+                    const int2 bs = reinterpret_cast<const int2 *>(a.bs + (size_t)src * (K / 16))[j];
+                    sm = bs.x + bs.y;
+                    if ((j & 7) == 0) dd = a.d[(size_t)src * (K / 32) + j / 8];
+                }
+                s_bsf[j][c] = (float)sm;
+                if ((j & 7) == 0) s_d[j / 8][c] = dd;
             }
-            s_bsf[j][c] = (float)sm;
-            if ((j & 7) == 0) s_d[j / 8][c] = dd;
         }
         __syncthreads();
 
@@ -302,6 +321,41 @@ __global__ void __launch_bounds__(256, (pf_occupancy<NB, GU>())) k_pf_gemm(PfArg
                 facc_m[r] = __builtin_fmaf(-dx * dmw, mins[r], facc_m[r]);
             }
         };
+        // Q8_0: the step's 8 blocks of one weight row (w = its 272 staged bytes, dword
+        // aligned).  Block j is d (fp16) at 34 j and 32 int8 values after it; lane kq's
+        // 8 values start at 34 j + 2 + 8 kq, dword aligned for odd j and 2 bytes off for
+        // even j (three dwords read and realigned).  sumi is exact (32 products of
+        // |v| <= 128); the scaling is fma(d_w d_x, sumi, acc) per block, in block order.
+        auto q80_step_dot = [&](int b, const uint8_t * w, float (&facc)[4]) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int o = 34 * j + 2 + 8 * kq;
+                uint32_t w0, w1, dbits;
+                if (j & 1) {
+                    const uint32_t * v = reinterpret_cast<const uint32_t *>(w + o);
+                    w0 = v[0];
+                    w1 = v[1];
+                    dbits = *reinterpret_cast<const uint32_t *>(w + 34 * j - 2) >> 16;
+                } else {
+                    const uint32_t * v = reinterpret_cast<const uint32_t *>(w + o - 2);
+                    const uint32_t d0 = v[0], d1 = v[1], d2 = v[2];
+                    w0 = __builtin_amdgcn_alignbit(d1, d0, 16);
+                    w1 = __builtin_amdgcn_alignbit(d2, d1, 16);
+                    dbits = *reinterpret_cast<const uint32_t *>(w + 34 * j) & 0xffff;
+                }
+                const long bw = (long)(((uint64_t)w1 << 32) | w0);
+                const uint2 xv = *reinterpret_cast<const uint2 *>(&s_q[rl][b * QK_K + 32 * j + 8 * kq]);
+                const long ax = (long)(((uint64_t)xv.y << 32) | xv.x);
+                const v4i z = {0, 0, 0, 0};
+                const v4i dj = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, bw, z, 0, 0, 0);
+                const float dw = fp16_to_f32((uint16_t)dbits);
+                const float4 dx = *reinterpret_cast<const float4 *>(&s_d[b * 8 + j][4 * kq]);
+                facc[0] = __builtin_fmaf(dw * dx.x, (float)dj[0], facc[0]);
+                facc[1] = __builtin_fmaf(dw * dx.y, (float)dj[1], facc[1]);
+                facc[2] = __builtin_fmaf(dw * dx.z, (float)dj[2], facc[2]);
+                facc[3] = __builtin_fmaf(dw * dx.w, (float)dj[3], facc[3]);
+            }
+        };
         float facc[NS][4], facc_m[NS][4];
 #pragma unroll
         for (int q = 0; q < NS; ++q)
@@ -323,17 +377,22 @@ __global__ void __launch_bounds__(256, (pf_occupancy<NB, GU>())) k_pf_gemm(PfArg
                 // A wave's LDS operations run in order, so the buffer needs no barrier between
                 // steps or between the gate and up streams.
                 u32x4 * wb4 = reinterpret_cast<u32x4 *>(wbuf);
-                wb4[lane] = wr0[q][pslot];
-                wb4[lane + 64] = wr1[q][pslot];
-                if (lane < 16) wb4[lane + 128] = wr2[q][pslot];
-                load_s(wbase[q], min(st + PF, nsteps - 1), wr0[q][pslot], wr1[q][pslot], wr2[q][pslot]);
-                __builtin_amdgcn_wave_barrier();
-                const uint4 hd = *reinterpret_cast<const uint4 *>(wbuf + rl * 144);
-                uint2 qq[4];
 #pragma unroll
-                for (int jp = 0; jp < 4; ++jp) qq[jp] = *reinterpret_cast<const uint2 *>(wbuf + rl * 144 + 16 + 32 * jp + 8 * kq);
+                for (int i = 0; i < NL; ++i)
+                    if (64 * (i + 1) <= SP || lane < SP - 64 * i) wb4[lane + 64 * i] = wr[i][q][pslot];
+                load_s(q, pslot, min(st + PF, nsteps - 1));
                 __builtin_amdgcn_wave_barrier();
-                block_dot(b, hd, qq, facc[q], facc_m[q]);
+                if constexpr (Q8) {
+                    q80_step_dot(b, wbuf + rl * SROW, facc[q]);
+                } else {
+                    const uint4 hd = *reinterpret_cast<const uint4 *>(wbuf + rl * SROW);
+                    uint2 qq[4];
+#pragma unroll
+                    for (int jp = 0; jp < 4; ++jp)
+                        qq[jp] = *reinterpret_cast<const uint2 *>(wbuf + rl * SROW + 16 + 32 * jp + 8 * kq);
+                    __builtin_amdgcn_wave_barrier();
+                    block_dot(b, hd, qq, facc[q], facc_m[q]);
+                }
             }
             if (b == NB - 1) {                          // the row tile is done: its outputs, then the next tile
 #pragma unroll
@@ -364,7 +423,7 @@ size_t prefill_workspace(int64_t K, int64_t N, int64_t n_as, int64_t T, int64_t 
     size_t o = 0;
     auto take = [&](size_t bytes) { o = align_up(o + bytes, 256); };
     take((size_t)rows * K);
-    take(sizeof(float) * rows * (K / QK_K));
+    take(sizeof(float) * rows * (K / 32));                           // scales: per 32 (Q8_0) or per 256 (Q8_K)
     take(sizeof(int32_t) * rows * (K / 16));
     for (int i = 0; i < 4; ++i) take(sizeof(int32_t) * (n_as + 1));   // cnt_copy, off, fill, item_off
     take(sizeof(int4) * max_tiles);
@@ -374,17 +433,25 @@ size_t prefill_workspace(int64_t K, int64_t N, int64_t n_as, int64_t T, int64_t 
     return o;
 }
 
-bool prefill_supported(int64_t K, int64_t N, int64_t n_as, std::string & why) {
+// bytes per 256 weights of a row: a Q4_K block, or eight Q8_0 blocks
+static int64_t pf_bytes_per_256(int32_t wtype) { return wtype == T_Q8_0 ? 272 : 144; }
+
+bool prefill_supported(int32_t wtype, int64_t K, int64_t N, int64_t n_as, const void * as, std::string & why) {
+    if (wtype != T_Q4_K && wtype != T_Q8_0) { why = "prefill mul_mat_id: Q4_K or Q8_0 weights only"; return false; }
     if (K % QK_K || K > PF_MAXK) { why = "prefill mul_mat_id: K must be a multiple of 256, <= 2048"; return false; }
     if (N % PF_ROWS) { why = "prefill mul_mat_id: N must be a multiple of 64"; return false; }
     if (n_as > PF_MAX_AS) { why = "prefill mul_mat_id: more than 4096 experts"; return false; }
-    if ((uint64_t)N * (uint64_t)(K / QK_K) * 144u >= (1ull << 31)) { why = "prefill mul_mat_id: expert slab of 2 GiB or more"; return false; }
+    if ((uint64_t)N * (uint64_t)(K / QK_K) * (uint64_t)pf_bytes_per_256(wtype) >= (1ull << 31)) {
+        why = "prefill mul_mat_id: expert slab of 2 GiB or more";
+        return false;
+    }
+    if ((uintptr_t)as % 16) { why = "prefill mul_mat_id: weights must be 16-byte aligned"; return false; }
     return true;
 }
 
 // The persistent GEMM's grid: the workgroups one launch keeps resident (the
 // occupancy query per kernel and device, done once).
-template <int NB, bool GU>
+template <int NB, bool GU, bool Q8>
 static int launch_gemm(const PfArgs & a, hipStream_t s) {
     static int grid[64] = {};
     int dev = 0;
@@ -392,29 +459,30 @@ static int launch_gemm(const PfArgs & a, hipStream_t s) {
     if (dev < 0 || dev >= 64) return fail(QWM_ERR_UNSUPPORTED, "prefill mul_mat_id: device index past 63");
     if (!grid[dev]) {
         int per_cu = 0, cus = 0;
-        QWM_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_pf_gemm<NB, GU>, 256, 0));
+        QWM_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_pf_gemm<NB, GU, Q8>, 256, 0));
         QWM_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
         grid[dev] = std::max(1, per_cu) * std::max(1, cus);
     }
-    k_pf_gemm<NB, GU><<<dim3((unsigned)grid[dev]), 256, 0, s>>>(a);
+    k_pf_gemm<NB, GU, Q8><<<dim3((unsigned)grid[dev]), 256, 0, s>>>(a);
     return QWM_OK;
 }
 
 int launch_prefill(const MmidArgs & m, uint8_t * ws, hipStream_t s, const uint8_t * up) {
-    if (m.wtype != T_Q4_K) return fail(QWM_ERR_UNSUPPORTED, "prefill mul_mat_id: Q4_K weights only");
     std::string why;
-    if (!prefill_supported(m.K, m.N, m.n_as, why)) return fail(QWM_ERR_UNSUPPORTED, why);
+    if (!prefill_supported(m.wtype, m.K, m.N, m.n_as, m.as, why) || (up && !prefill_supported(m.wtype, m.K, m.N, m.n_as, up, why)))
+        return fail(QWM_ERR_UNSUPPORTED, why);
     const int64_t rows = m.T * m.ne11, P = m.T * m.n_ids;
     const int64_t max_tiles = P / PF_TOK + m.n_as;
     size_t o = 0;
     auto take = [&](size_t bytes) { size_t at = o; o = align_up(o + bytes, 256); return at; };
     PfArgs a;
     a.b = m.b; a.b_nb1 = m.b_nb1; a.b_nb2 = m.b_nb2; a.ids = m.ids; a.ids_nb1 = m.ids_nb1;
-    a.as = m.as; a.slab = m.slab; a.row_bytes = (size_t)(m.K / QK_K) * 144;
+    a.as = m.as; a.slab = m.slab; a.row_bytes = (size_t)((m.K / QK_K) * pf_bytes_per_256(m.wtype));
     a.as2 = up;
+    a.q8 = m.wtype == T_Q8_0;
     a.K = (int)m.K; a.N = (int)m.N; a.ne11 = (int)m.ne11; a.T = (int)m.T; a.n_ids = (int)m.n_ids; a.n_as = (int)m.n_as;
     a.qs = reinterpret_cast<int8_t *>(ws + take((size_t)rows * m.K));
-    a.d = reinterpret_cast<float *>(ws + take(sizeof(float) * rows * (m.K / QK_K)));
+    a.d = reinterpret_cast<float *>(ws + take(sizeof(float) * rows * (m.K / 32)));
     a.bs = reinterpret_cast<int32_t *>(ws + take(sizeof(int32_t) * rows * (m.K / 16)));
     a.cnt_copy = reinterpret_cast<int32_t *>(ws + take(sizeof(int32_t) * (m.n_as + 1)));
     a.off = reinterpret_cast<int32_t *>(ws + take(sizeof(int32_t) * (m.n_as + 1)));
@@ -434,16 +502,17 @@ int launch_prefill(const MmidArgs & m, uint8_t * ws, hipStream_t s, const uint8_
     const char * label = up ? "prefill_gemm_gu" : "prefill_gemm";
     prof_begin(label, s);
     int rc = QWM_OK;
+    const bool q8 = a.q8 != 0;
+#define QWM_PF_CASE(NBV)                                                                                            \
+    case NBV:                                                                                                       \
+        rc = q8 ? (up ? launch_gemm<NBV, true, true>(a, s) : launch_gemm<NBV, false, true>(a, s))                   \
+                : (up ? launch_gemm<NBV, true, false>(a, s) : launch_gemm<NBV, false, false>(a, s));                \
+        break;
     switch (m.K / QK_K) {
-        case 1: rc = up ? launch_gemm<1, true>(a, s) : launch_gemm<1, false>(a, s); break;
-        case 2: rc = up ? launch_gemm<2, true>(a, s) : launch_gemm<2, false>(a, s); break;
-        case 3: rc = up ? launch_gemm<3, true>(a, s) : launch_gemm<3, false>(a, s); break;
-        case 4: rc = up ? launch_gemm<4, true>(a, s) : launch_gemm<4, false>(a, s); break;
-        case 5: rc = up ? launch_gemm<5, true>(a, s) : launch_gemm<5, false>(a, s); break;
-        case 6: rc = up ? launch_gemm<6, true>(a, s) : launch_gemm<6, false>(a, s); break;
-        case 7: rc = up ? launch_gemm<7, true>(a, s) : launch_gemm<7, false>(a, s); break;
-        default: rc = up ? launch_gemm<8, true>(a, s) : launch_gemm<8, false>(a, s); break;
+        QWM_PF_CASE(1) QWM_PF_CASE(2) QWM_PF_CASE(3) QWM_PF_CASE(4) QWM_PF_CASE(5) QWM_PF_CASE(6) QWM_PF_CASE(7)
+        default: QWM_PF_CASE(8)
     }
+#undef QWM_PF_CASE
     if (rc != QWM_OK) return rc;
     prof_end(label, s);
     QWM_HIP_CHECK(hipGetLastError());

@@ -47,21 +47,28 @@ def test_argument_validation_without_gpu():
     ids_bad = qa.tensor(qa.TYPE_I32, 3, 2, 1)   # ids->ne[1] != b->ne[2]
     assert L.qwm_mul_mat_id(a, b, ids_bad, None, None, 0, None) == qa.ERR_ARG
     assert L.qwm_mul_mat_id(a, b, ids, qa.tensor(qa.TYPE_F32, 4, 2, 1), None, 0, None) == qa.ERR_WORKSPACE
-    wide = qa.tensor(qa.TYPE_F32, 256, 1, 9)    # 9 columns: the prefill GEMM, which needs N % 64 == 0
-    assert L.qwm_mul_mat_id(a, wide, qa.tensor(qa.TYPE_I32, 2, 9, 1), None, None, 0, None) == qa.ERR_UNSUPPORTED
+    wide = qa.tensor(qa.TYPE_F32, 256, 1, 9)    # 9 columns, N 4: not the grouped GEMM's shape (N % 64), so GEMV chunks
+    i9 = qa.tensor(qa.TYPE_I32, 2, 9, 1)
+    assert L.qwm_mul_mat_id_workspace_size(a, wide, i9) > 0
+    assert L.qwm_mul_mat_id(a, wide, i9, None, None, 0, None) == qa.ERR_ARG          # dst NULL
     a64 = qa.tensor(qa.TYPE_Q4_K, 2048, 512, 8)
     b64 = qa.tensor(qa.TYPE_F32, 2048, 1, 64)
     i64 = qa.tensor(qa.TYPE_I32, 4, 64, 1)
     assert L.qwm_mul_mat_id_workspace_size(a64, b64, i64) > 0
     assert L.qwm_mul_mat_id(a64, b64, i64, qa.tensor(qa.TYPE_F32, 512, 4, 64), None, 0, None) == qa.ERR_WORKSPACE
     # other types: GEMV launches over column chunks, whose workspace holds one chunk
-    assert 0 < L.qwm_mul_mat_id_workspace_size(qa.tensor(qa.TYPE_Q8_0, 2048, 512, 8), b64, i64) < \
+    assert 0 < L.qwm_mul_mat_id_workspace_size(qa.tensor(qa.TYPE_Q6_K, 2048, 512, 8), b64, i64) < \
         L.qwm_mul_mat_id_workspace_size(a64, b64, i64)
+    # sizes cover either path: the grouped GEMM, or the GEMV chunks that unaligned weights fall back to
+    q80 = qa.tensor(qa.TYPE_Q8_0, 2048, 512, 8)
+    assert L.qwm_mul_mat_id_workspace_size(q80, b64, i64) >= L.qwm_mul_mat_id_workspace_size(a64, b64, i64) > 0
     i200 = qa.tensor(qa.TYPE_I32, 200, 64, 1)     # more ids per column than the pair table holds
-    assert L.qwm_mul_mat_id_workspace_size(qa.tensor(qa.TYPE_Q8_0, 2048, 512, 256), b64, i200) == 0
+    assert L.qwm_mul_mat_id_workspace_size(qa.tensor(qa.TYPE_Q6_K, 2048, 512, 256), b64, i200) == 0
     # the gate/up/SwiGLU call: up must match gate in type and shape; act is [N, n_ids, T]
     act64 = qa.tensor(qa.TYPE_F32, 512, 4, 64)
-    assert L.qwm_mul_mat_id_swiglu_workspace_size(a64, a64, b64, i64) == L.qwm_mul_mat_id_workspace_size(a64, b64, i64)
+    # covers the grouped pass and the split path (gate and up in the workspace) that unaligned weights take
+    assert L.qwm_mul_mat_id_swiglu_workspace_size(a64, a64, b64, i64) == \
+        2 * 512 * 4 * 64 * 4 + L.qwm_mul_mat_id_workspace_size(a64, b64, i64)
     for up in (qa.tensor(qa.TYPE_Q4_K, 2048, 512, 4), qa.tensor(qa.TYPE_Q8_0, 2048, 512, 8)):
         assert L.qwm_mul_mat_id_swiglu_workspace_size(a64, up, b64, i64) == 0
         assert L.qwm_mul_mat_id_swiglu(a64, up, b64, i64, act64, None, 0, None) == qa.ERR_ARG

@@ -240,9 +240,11 @@ def test_mul_mat_id_rejects_bad_shapes(dev):
 
 @pytest.mark.parametrize("wt", ["q8_0", "q6_K", "q5_K"])
 def test_mul_mat_id_wide_batch(dev, wt):
-    """A batch of 40 columns x 10 ids (prefill-sized) with weights that have
-    no grouped GEMM runs as GEMV launches over column chunks: bit-exact
-    against the oracle, with ne11 = 1 broadcast and with per-id rows."""
+    """A batch of 40 columns x 10 ids (prefill-sized), with ne11 = 1 broadcast
+    and with per-id rows.  Q6_K and Q5_K have no grouped GEMM and run as GEMV
+    launches over column chunks: bit-exact against the oracle.  Q8_0 takes the
+    grouped GEMM (each block's sum from one MFMA, not ggml's eight 4-element
+    partial sums): within 1e-3."""
     rng = np.random.default_rng(40)
     K, N, n_as, n_ids, T = 512, 256, 16, 10, 40
     w = (rng.standard_normal((n_as, N, K)) * 0.02).astype(np.float32)
@@ -265,4 +267,8 @@ def test_mul_mat_id_wide_batch(dev, wt):
         qa.check(qa.lib().qwm_mul_mat_id(tas, tb, tids, qa.tensor(qa.TYPE_F32, N, n_ids, T, dst), ws.data_ptr(),
                                          ws.numel(), None))
         torch.cuda.synchronize()
-        assert np.array_equal(bits(dst.cpu().numpy()), bits(exp)), f"{wt} ne11={ne11}"
+        got = dst.cpu().numpy()
+        if wt == "q8_0":
+            assert np.isfinite(got).all() and rel_err(got, exp) < 1e-3, f"{wt} ne11={ne11}"
+        else:
+            assert np.array_equal(bits(got), bits(exp)), f"{wt} ne11={ne11}"

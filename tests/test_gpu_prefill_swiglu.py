@@ -7,7 +7,7 @@ the GPU's own separate path (two qwm_mul_mat_id calls, then SwiGLU of those
 outputs) bit for bit: the fused pass runs the same dots in the same order and
 the same SwiGLU expressions.  Shapes: Qwen3-Next's gate/up (K 2048, N 512,
 512 experts, top-10, 512 tokens) at full size, skewed and ragged groups on
-smaller pools, the T <= 8 and non-Q4_K paths (separate calls inside), and two
+smaller pools, Q8_0 weights, the T <= 8 path (separate calls inside), and two
 calls in a row on one workspace."""
 import numpy as np
 import pytest
@@ -92,7 +92,8 @@ def oracle_act(gtype, qg, qu, b, ids, K, N, n_as):
     (GGML_Q4_K, 768, 128, 32, 4, 24, 0.0),      # K = 3 blocks, ragged 16-column tiles
     (GGML_Q4_K, 256, 64, 16, 2, 9, 0.0),        # smallest prefill: one block, one row tile
     (GGML_Q4_K, 2048, 512, 64, 10, 5, 0.0),     # T <= 8: the GEMV path, separate calls
-    (GGML_Q8_0, 512, 256, 16, 4, 20, 0.0),      # Q8_0 past 8 columns: GEMV chunks, separate calls
+    (GGML_Q8_0, 512, 256, 16, 4, 20, 0.0),      # Q8_0 past 8 columns: the grouped pass
+    (GGML_Q8_0, 2048, 512, 64, 10, 64, 1.1),    # Q8_0 at the gate/up shape, Zipf(1.1)
 ])
 def test_swiglu_matches_oracle_and_separate_calls(dev, gtype, K, N, n_as, n_ids, T, skew):
     rng = np.random.default_rng(K + N + T + gtype)

@@ -39,19 +39,103 @@ struct PfArgs {
     int q8;                                   // weights Q8_0 (b quantized to Q8_0), else Q4_K (b to Q8_K)
     int8_t * qs; float * d; int32_t * bs;     // quantized rows of b [T * ne11]: values, scales (K/32 per
                                               // row), Q8_K sums of 16 (Q4_K only)
-    int32_t * cnt_copy; int32_t * off; int32_t * fill; int32_t * item_off;
-    int4 * items;                             // per work item: expert, first column, columns, first row tile
-    int32_t * perm; int32_t * eid; int32_t * total; int32_t * err;
+    int4 * items;                             // per column tile: expert, first column, columns, 0
+    int32_t * perm; int32_t * total; int32_t * err;
     float * dst; size_t dst_nb1, dst_nb2;
 };
 
-// b's columns quantized (one 256-block per wave): Q8_K for Q4_K weights
-// (quantize_row_q8_K), ggml's x86 Q8_0 quantizer for Q8_0 weights; and each
-// pair's expert.
-__global__ void __launch_bounds__(256) k_pf_prep(PfArgs a) {
+constexpr int PF_PREP_THREADS = 1024;
+
+// The expert of pair p (column t = p / n_ids, id slot p % n_ids), or -1 past
+// the last pair; an id outside [0, n_as) sets `bad` and reads expert 0.
+__device__ inline int pf_pair_expert(const PfArgs & a, int p, int P, bool & bad) {
+    if (p >= P) return -1;
+    const int t = p / a.n_ids, e = p % a.n_ids;
+    const int v = *reinterpret_cast<const int32_t *>(reinterpret_cast<const uint8_t *>(a.ids) + t * a.ids_nb1 + e * 4);
+    if (v < 0 || v >= a.n_as) { bad = true; return 0; }
+    return v;
+}
+
+// The grouping, in one workgroup: the expert histogram of this call's pairs
+// (in LDS), its exclusive scan, the column-tile table (the tiles of expert e
+// are consecutive: first column, columns) and the pairs placed in their
+// expert's group through per-expert cursors in LDS.  Inside a group the order
+// is whatever the LDS atomics give: a column's result does not depend on its
+// position.  Each pass requests a batch of ids before it touches LDS, so the
+// loads overlap.  Nothing carries over between calls, so calls of any shape
+// may share a workspace.
+__device__ void pf_group(const PfArgs & a) {
+    constexpr int G = PF_PREP_THREADS, NW = G / 64, PER = PF_MAX_AS / G, UN = 4;
+    __shared__ int32_t s_c[PF_MAX_AS];
+    __shared__ int32_t s_wsum[2][NW];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int P = a.T * a.n_ids;
+    bool bad = false;
+    for (int e = tid; e < a.n_as; e += G) s_c[e] = 0;
+    __syncthreads();
+    for (int p0 = 0; p0 < P; p0 += G * UN) {
+        int v[UN];
+#pragma unroll
+        for (int j = 0; j < UN; ++j) v[j] = pf_pair_expert(a, p0 + j * G + tid, P, bad);
+#pragma unroll
+        for (int j = 0; j < UN; ++j)
+            if (v[j] >= 0) atomicAdd(&s_c[v[j]], 1);
+    }
+    if (bad) st_agent(a.err, 1);
+    __syncthreads();
+    int c[PER], cs = 0, is = 0;
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+        const int e = PER * tid + q;
+        c[q] = e < a.n_as ? s_c[e] : 0;
+        cs += c[q];
+        is += (c[q] + PF_TOK - 1) / PF_TOK;
+    }
+    int cx = cs, ix = is;    // inclusive scans over the wave
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int cy = __shfl_up(cx, o, 64), iy = __shfl_up(ix, o, 64);
+        if (lane >= o) { cx += cy; ix += iy; }
+    }
+    if (lane == 63) { s_wsum[0][wave] = cx; s_wsum[1][wave] = ix; }
+    __syncthreads();
+    int cb = cx - cs, ib = ix - is;
+    for (int w = 0; w < wave; ++w) { cb += s_wsum[0][w]; ib += s_wsum[1][w]; }
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+        const int e = PER * tid + q;
+        if (e < a.n_as) {
+            for (int ct = 0; ct * PF_TOK < c[q]; ++ct)
+                a.items[ib + ct] = make_int4(e, cb + ct * PF_TOK, min(PF_TOK, c[q] - ct * PF_TOK), 0);
+            s_c[e] = cb;     // this thread's own entries: the cursor starts at the group's first column
+        }
+        cb += c[q];
+        ib += (c[q] + PF_TOK - 1) / PF_TOK;
+    }
+    if (tid == G - 1) *a.total = ib;
+    __syncthreads();
+    for (int p0 = 0; p0 < P; p0 += G * UN) {
+        int v[UN];
+#pragma unroll
+        for (int j = 0; j < UN; ++j) v[j] = pf_pair_expert(a, p0 + j * G + tid, P, bad);
+#pragma unroll
+        for (int j = 0; j < UN; ++j)
+            if (v[j] >= 0) a.perm[atomicAdd(&s_c[v[j]], 1)] = p0 + j * G + tid;
+    }
+}
+
+// One launch before the GEMM: workgroup 0 groups the pairs by expert while the
+// others quantize b's columns (one 256-block per wave): Q8_K for Q4_K weights
+// (quantize_row_q8_K), ggml's x86 Q8_0 quantizer for Q8_0 weights.
+__global__ void __launch_bounds__(PF_PREP_THREADS) k_pf_prep(PfArgs a) {
+    if (blockIdx.x == 0) {
+        pf_group(a);
+        return;
+    }
+    constexpr int NW = PF_PREP_THREADS / 64;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int rows = a.T * a.ne11, nb = a.K / QK_K;
-    for (int jb = blockIdx.x * 4 + wave; jb < rows * nb; jb += gridDim.x * 4) {
+    for (int jb = (blockIdx.x - 1) * NW + wave; jb < rows * nb; jb += (gridDim.x - 1) * NW) {
         const int row = jb / nb, b = jb % nb;
         const int t = row / a.ne11, i = row % a.ne11;
         const float * src = reinterpret_cast<const float *>(reinterpret_cast<const uint8_t *>(a.b) + t * a.b_nb2 + i * a.b_nb1);
@@ -61,82 +145,6 @@ __global__ void __launch_bounds__(256) k_pf_prep(PfArgs a) {
         else
             quantize_block_q8K(src + b * QK_K, a.qs + (size_t)row * a.K + b * QK_K, a.d + (size_t)row * (a.K / 32) + b,
                                a.bs + (size_t)row * (a.K / 16) + b * 16, lane);
-    }
-    const int P = a.T * a.n_ids;
-    for (int p = blockIdx.x * blockDim.x + threadIdx.x; p < P; p += gridDim.x * blockDim.x) {
-        const int t = p / a.n_ids, e = p % a.n_ids;
-        int v = *reinterpret_cast<const int32_t *>(reinterpret_cast<const uint8_t *>(a.ids) + t * a.ids_nb1 + e * 4);
-        if (v < 0 || v >= a.n_as) { st_agent(a.err, 1); v = 0; }
-        a.eid[p] = v;
-    }
-}
-
-// One workgroup: the expert histogram (in LDS, from this call's pairs), group
-// offsets (its exclusive scan) and the column-tile table (the 16-column tiles of expert e are
-// item_off[e] .. item_off[e + 1] - 1).  Nothing carries over between calls,
-// so calls of any shape may share a workspace.
-__global__ void __launch_bounds__(1024) k_pf_scan(PfArgs a) {
-    __shared__ int32_t s_c[PF_MAX_AS], s_i[PF_MAX_AS];
-    __shared__ int32_t s_wsum[2][16];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    for (int e = tid; e < a.n_as; e += 1024) s_c[e] = 0;
-    __syncthreads();
-    const int P = a.T * a.n_ids;
-    for (int p = tid; p < P; p += 1024) atomicAdd(&s_c[a.eid[p]], 1);
-    __syncthreads();
-    for (int e = tid; e < a.n_as; e += 1024) {
-        const int c = s_c[e];
-        s_i[e] = (c + PF_TOK - 1) / PF_TOK;
-        a.cnt_copy[e] = c;
-        a.fill[e] = 0;
-    }
-    __syncthreads();
-    // exclusive scans of s_c and s_i over n_as <= 4096 entries, 4 per thread
-    int c4[4], i4[4], cs = 0, is = 0;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int e = 4 * tid + q;
-        c4[q] = e < a.n_as ? s_c[e] : 0;
-        i4[q] = e < a.n_as ? s_i[e] : 0;
-        cs += c4[q];
-        is += i4[q];
-    }
-    int cx = cs, ix = is;    // inclusive scan over the wave
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int cy = __shfl_up(cx, o, 64), iy = __shfl_up(ix, o, 64);
-        if (lane >= o) { cx += cy; ix += iy; }
-    }
-    if (lane == 63) { s_wsum[0][wave] = cx; s_wsum[1][wave] = ix; }
-    __syncthreads();
-    int cb = 0, ib = 0;
-    for (int w = 0; w < wave; ++w) { cb += s_wsum[0][w]; ib += s_wsum[1][w]; }
-    cb += cx - cs;
-    ib += ix - is;
-    __syncthreads();
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int e = 4 * tid + q;
-        if (e < a.n_as) {
-            a.off[e] = cb;
-            a.item_off[e] = ib;
-            for (int ct = 0; ct < i4[q]; ++ct)
-                a.items[ib + ct] = make_int4(e, cb + ct * PF_TOK, min(PF_TOK, c4[q] - ct * PF_TOK), 0);
-        }
-        cb += c4[q];
-        ib += i4[q];
-    }
-    if (tid == 1023) { a.off[a.n_as] = cb; a.item_off[a.n_as] = ib; *a.total = ib; }
-}
-
-// Pairs into their expert's group (any order inside a group: each column's
-// result does not depend on its position).
-__global__ void __launch_bounds__(256) k_pf_scatter(PfArgs a) {
-    const int P = a.T * a.n_ids;
-    for (int p = blockIdx.x * blockDim.x + threadIdx.x; p < P; p += gridDim.x * blockDim.x) {
-        const int e = a.eid[p];
-        const int pos = a.off[e] + __hip_atomic_fetch_add(a.fill + e, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        a.perm[pos] = p;
     }
 }
 
@@ -274,7 +282,11 @@ __global__ void __launch_bounds__(256, (pf_occupancy<NB, GU, Q8>())) k_pf_gemm(P
         // one block of one weight row against the tile's 16 columns.  The sub-block
         // dots are exact int32 (one int8 MFMA each, issued back to back into their
         // own accumulators) and the 6-bit scales multiply them in 24-bit integer
-        // multiplies (|dot| <= 32 * 15 * 128 < 2^23).  The mins term
+        // multiply-adds (|dot| <= 32 * 15 * 128 < 2^17, the block's sum below 2^23):
+        // each step of that sum goes through an empty asm, so the compiler keeps it
+        // a chain of v_mad_i32_i24 instead of regrouping it into multiplies and
+        // three-way adds.  The scales are unpacked four to a register (scales 4..7:
+        // the low nibbles of bytes 8..11 and bits 6..7 of bytes 0..3).  The mins term
         // sum_j min_j * bsum_j (|product| < 2^18, every partial sum < 2^24) runs as
         // two f32 MFMAs (16x16x4): each value and partial sum is an integer that
         // fp32 holds exactly, so the result is the integer sum in any order.
@@ -287,6 +299,7 @@ __global__ void __launch_bounds__(256, (pf_occupancy<NB, GU, Q8>())) k_pf_gemm(P
             v4f mins = {0.f, 0.f, 0.f, 0.f};
             mins = __builtin_amdgcn_mfma_f32_16x16x4f32(s_bsf[b * 8 + kq][rl], mn_lo, mins, 0, 0, 0);
             mins = __builtin_amdgcn_mfma_f32_16x16x4f32(s_bsf[b * 8 + 4 + kq][rl], mn_hi, mins, 0, 0, 0);
+            const uint32_t sc_hi = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);   // scales 4..7, one a byte
             int acc[4] = {0, 0, 0, 0};
 #pragma unroll
             for (int h = 0; h < 2; ++h) {                 // two groups of 4 sub-blocks
@@ -307,10 +320,12 @@ __global__ void __launch_bounds__(256, (pf_occupancy<NB, GU, Q8>())) k_pf_gemm(P
                 }
 #pragma unroll
                 for (int jj = 0; jj < 4; ++jj) {
-                    int scj, mnj;
-                    q4k_scale_min_reg(4 * h + jj, hd.y, hd.z, hd.w, scj, mnj);
+                    const int scj = h == 0 ? (int)((hd.y >> (8 * jj)) & 63) : (int)((sc_hi >> (8 * jj)) & 0xff);
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) acc[r] = __mul24(scj, dj[jj][r]) + acc[r];
+                    for (int r = 0; r < 4; ++r) {
+                        acc[r] = __mul24(scj, dj[jj][r]) + acc[r];
+                        if (4 * h + jj < 7) asm("" : "+v"(acc[r]));
+                    }
                 }
             }
             const float dw = fp16_to_f32((uint16_t)(hd.x & 0xffff)), dmw = fp16_to_f32((uint16_t)(hd.x >> 16));
@@ -425,10 +440,8 @@ size_t prefill_workspace(int64_t K, int64_t N, int64_t n_as, int64_t T, int64_t 
     take((size_t)rows * K);
     take(sizeof(float) * rows * (K / 32));                           // scales: per 32 (Q8_0) or per 256 (Q8_K)
     take(sizeof(int32_t) * rows * (K / 16));
-    for (int i = 0; i < 4; ++i) take(sizeof(int32_t) * (n_as + 1));   // cnt_copy, off, fill, item_off
     take(sizeof(int4) * max_tiles);
     take(sizeof(int32_t) * P);                                        // perm
-    take(sizeof(int32_t) * P);                                        // eid
     take(256);                                                        // total, err
     return o;
 }
@@ -484,21 +497,15 @@ int launch_prefill(const MmidArgs & m, uint8_t * ws, hipStream_t s, const uint8_
     a.qs = reinterpret_cast<int8_t *>(ws + take((size_t)rows * m.K));
     a.d = reinterpret_cast<float *>(ws + take(sizeof(float) * rows * (m.K / 32)));
     a.bs = reinterpret_cast<int32_t *>(ws + take(sizeof(int32_t) * rows * (m.K / 16)));
-    a.cnt_copy = reinterpret_cast<int32_t *>(ws + take(sizeof(int32_t) * (m.n_as + 1)));
-    a.off = reinterpret_cast<int32_t *>(ws + take(sizeof(int32_t) * (m.n_as + 1)));
-    a.fill = reinterpret_cast<int32_t *>(ws + take(sizeof(int32_t) * (m.n_as + 1)));
-    a.item_off = reinterpret_cast<int32_t *>(ws + take(sizeof(int32_t) * (m.n_as + 1)));
     a.items = reinterpret_cast<int4 *>(ws + take(sizeof(int4) * max_tiles));
     a.perm = reinterpret_cast<int32_t *>(ws + take(sizeof(int32_t) * P));
-    a.eid = reinterpret_cast<int32_t *>(ws + take(sizeof(int32_t) * P));
     a.total = reinterpret_cast<int32_t *>(ws + take(256));
     a.err = a.total + 1;
     a.dst = m.dst; a.dst_nb1 = m.dst_nb1; a.dst_nb2 = m.dst_nb2;
     const int64_t nblk = rows * (m.K / QK_K);
-    const unsigned prep_grid = (unsigned)std::max<int64_t>(1, std::min<int64_t>(1024, std::max((nblk + 3) / 4, (P + 255) / 256)));
-    QWM_TIMED("prefill_prep", s, k_pf_prep<<<prep_grid, 256, 0, s>>>(a));
-    k_pf_scan<<<1, 1024, 0, s>>>(a);
-    k_pf_scatter<<<(unsigned)std::max<int64_t>(1, std::min<int64_t>(1024, (P + 255) / 256)), 256, 0, s>>>(a);
+    const int64_t nw = PF_PREP_THREADS / 64;
+    const unsigned prep_grid = 1 + (unsigned)std::max<int64_t>(1, std::min<int64_t>(512, (nblk + nw - 1) / nw));
+    QWM_TIMED("prefill_prep", s, k_pf_prep<<<prep_grid, PF_PREP_THREADS, 0, s>>>(a));
     const char * label = up ? "prefill_gemm_gu" : "prefill_gemm";
     prof_begin(label, s);
     int rc = QWM_OK;

@@ -82,8 +82,9 @@ int qwm_workspace_init(void * workspace, size_t bytes, void * stream);
 /* GGML_OP_MUL_MAT_ID (ggml.c:3398-3440; CPU: ggml-cpu.c:1554-1734):
  *   dst[:, e, t] = as[:, :, ids[e, t]] . b[:, e % ne11(b), t]
  * as: Q4_K, Q5_K, Q6_K or Q8_0 [K, N, n_as]; b: f32 [K, ne11, T]; ids: i32
- * [n_ids, T]; dst: f32 [N, n_ids, T].  Supported: K % 256 == 0 and
- * K <= 2048; Q5_K data 16-byte aligned, Q6_K and Q8_0 4-byte aligned.
+ * [n_ids, T]; dst: f32 [N, n_ids, T].  Supported: K a multiple of 256 up
+ * to 2048, or 3072 or 4096; Q5_K data 16-byte aligned, Q6_K and Q8_0 4-byte
+ * aligned.
  *   T <= 8: one GEMV launch, n_ids * T <= 128.
  *   T > 8, Q4_K or Q8_0 with N % 64 == 0 and 16-byte aligned data: the
  *   grouped int8-MFMA GEMM (prefill), n_ids * T <= 2^22.
@@ -123,8 +124,9 @@ int qwm_mul_mat_id_swiglu(const qwm_tensor * gate, const qwm_tensor * up, const 
  * (data == NULL when absent): gate/up [H, N_sh], down [N_sh, H], and the
  * optional f32 shared gate row [H, 1].  gate/up are Q4_K, Q5_K or Q8_0 and
  * down the same type (or Q6_K beside Q4_K/Q5_K, as K-quant "_M" files have
- * it); the shared expert's types match the pools'.  H and N are multiples of
- * 256 up to 2048. */
+ * it); the shared expert's types match the pools'.  N is a multiple of 256
+ * up to 2048; H too, or 3072 or 4096 (the fused verify step and the
+ * persistent decode take 2048 only). */
 typedef struct qwm_moe_layer {
     qwm_tensor gate_pool, up_pool, down_pool;
     qwm_tensor router;
@@ -216,7 +218,8 @@ int qwm_moe_decode_sel(const qwm_moe_layer * layers, int32_t n_layers, const int
  *   a = longest prefix with vA[j] == drafts[j], j < n_draft;  x_new = vA[a]
  * x: f32 [H, T]; norm_w: optional f32 [H]; drafts: device i32 [n_draft]
  * (n_draft = T - 1); result: device i32 [T + 2] = vA[0..T-1], a, x_new.
- * Supported: H in {512, 1024, 1536, 2048}, 1 <= T <= 8; x and norm_w 16-byte
+ * Supported: H in {512, 1024, 1536, 2048} with 1 <= T <= 8, H in {3072, 4096}
+ * with 1 <= T <= 4; x and norm_w 16-byte
  * aligned, lm_head 4-byte aligned with contiguous rows. */
 size_t qwm_verify_workspace_size(const qwm_tensor * lm_head, int64_t T);
 int qwm_verify_accept(const qwm_tensor * lm_head, const qwm_tensor * x, const float * norm_w, float eps,

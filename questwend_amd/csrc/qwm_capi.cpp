@@ -188,7 +188,7 @@ static int check_mmid(const qwm_tensor * as, const qwm_tensor * b, const qwm_ten
     } else if (ids->ne[0] * ids->ne[1] > MAX_PAIRS) {
         return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: too many (expert, column) pairs");
     }
-    if (as->ne[0] > 2048) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: K > 2048");
+    if (!hidden_supported(as->ne[0])) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: K must be 256 .. 2048, 3072 or 4096");
     if (as->type == T_Q8_0 && as->ne[0] % 256) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: Q8_0 needs K a multiple of 256");
     if (dst) {
         if (dst->type != T_F32 || dst->ne[0] != as->ne[1] || dst->ne[1] != ids->ne[0] || dst->ne[2] != b->ne[2])

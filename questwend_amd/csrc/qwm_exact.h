@@ -109,24 +109,15 @@ QWM_DEV void load_xblk(XBlk & B, const uint8_t * blk, int m) {
 // |dot4| <= 4 * 63 * 128 (Q6_K), scales and mins <= 63 (Q4_K/Q5_K) or 128
 // (Q6_K), |q8s| <= 32 * 128, so the products and sums are the exact integers.
 
-// Row dots of one weight row (NB blocks in W) with n <= MAXP activation rows
-// at sx + off[i] in LDS (NB consecutive blocks of XS dwords each).  out[i] is
-// valid in lane m == 0 of the group.
-// FIXN > 0: exactly FIXN tokens (a compile-time count, so that no branch
-// splits the unrolled block loop and the scheduler can request later blocks'
-// activations early); 0: n at run time.
+// The block loop of a Q4_K row dot: the NB blocks in W against n <= MAXP
+// activation rows at xt[i] (NB consecutive blocks of XS dwords each in LDS),
+// added to each lane's 8-lane accumulators acc (scales) and accm (mins) in
+// block order.  A row of more blocks than a lane's registers hold runs as
+// several calls on consecutive chunks, the accumulators carried between them:
+// the same sums in the same order.  FIXN as in q4k_dot8_off.
 template <int NB, int MAXP, int FIXN = 0>
-QWM_DEV void q4k_dot8_off(float (&out)[MAXP], const XBlk (&W)[NB], const uint32_t * sx, const int (&off)[MAXP], int n_,
-                          int m) {
-    // the token count and offsets are uniform: scalar loop control, and each
-    // token's activation rows at one scalar base (block offsets immediate)
-    const int n = FIXN > 0 ? FIXN : __builtin_amdgcn_readfirstlane(n_);
-    const uint32_t * xt[MAXP];
-#pragma unroll
-    for (int i = 0; i < MAXP; ++i) xt[i] = sx + __builtin_amdgcn_readfirstlane(off[i]);
-    float acc[MAXP], accm[MAXP];
-#pragma unroll
-    for (int i = 0; i < MAXP; ++i) { acc[i] = 0.f; accm[i] = 0.f; }
+QWM_DEV void q4k_acc8(float (&acc)[MAXP], float (&accm)[MAXP], const XBlk (&W)[NB], const uint32_t * const (&xt)[MAXP],
+                      int n, int m) {
     const uint32_t k1 = 0x3f3f3f3fu, k2 = 0x0f0f0f0fu, k3 = 0x03030303u, m4 = 0x0f0f0f0fu;
     const int l = m & 3;
 #pragma unroll
@@ -174,7 +165,12 @@ QWM_DEV void q4k_dot8_off(float (&out)[MAXP], const XBlk (&W)[NB], const uint32_
             }
         }
     }
-    // hsum_float_8(acc) + hsum_float_4(acc_m) (quants.c:43-49, 2181-2184)
+}
+
+// hsum_float_8(acc) + hsum_float_4(acc_m) (quants.c:43-49, 2181-2184): the
+// row's dot in lane m == 0 of each 8-lane group.
+template <int MAXP>
+QWM_DEV void q4k_fin8(float (&out)[MAXP], const float (&acc)[MAXP], const float (&accm)[MAXP], int n) {
 #pragma unroll
     for (int i = 0; i < MAXP; ++i) {
         if (i < n) {
@@ -188,6 +184,77 @@ QWM_DEV void q4k_dot8_off(float (&out)[MAXP], const XBlk (&W)[NB], const uint32_
             out[i] = 0.f;
         }
     }
+}
+
+// Row dots of one weight row (NB blocks in W) with n <= MAXP activation rows
+// at sx + off[i] in LDS (NB consecutive blocks of XS dwords each).  out[i] is
+// valid in lane m == 0 of the group.
+// FIXN > 0: exactly FIXN tokens (a compile-time count, so that no branch
+// splits the unrolled block loop and the scheduler can request later blocks'
+// activations early); 0: n at run time.
+template <int NB, int MAXP, int FIXN = 0>
+QWM_DEV void q4k_dot8_off(float (&out)[MAXP], const XBlk (&W)[NB], const uint32_t * sx, const int (&off)[MAXP], int n_,
+                          int m) {
+    // the token count and offsets are uniform: scalar loop control, and each
+    // token's activation rows at one scalar base (block offsets immediate)
+    const int n = FIXN > 0 ? FIXN : __builtin_amdgcn_readfirstlane(n_);
+    const uint32_t * xt[MAXP];
+#pragma unroll
+    for (int i = 0; i < MAXP; ++i) xt[i] = sx + __builtin_amdgcn_readfirstlane(off[i]);
+    float acc[MAXP], accm[MAXP];
+#pragma unroll
+    for (int i = 0; i < MAXP; ++i) { acc[i] = 0.f; accm[i] = 0.f; }
+    q4k_acc8<NB, MAXP, FIXN>(acc, accm, W, xt, n, m);
+    q4k_fin8<MAXP>(out, acc, accm, n);
+}
+
+// One chunk step of q4k_dot8_chunked: the loads of chunk C + 1 into the other
+// buffer, then chunk C's arithmetic, then the next step (a compile-time
+// recursion, so every buffer index is a constant and the buffers stay in
+// registers).
+template <int NB, int CB, int NR, int MAXP, int C>
+QWM_DEV void q4k_chunk_step(float (&acc)[NR][MAXP], float (&accm)[NR][MAXP], XBlk (&W)[2][NR][CB],
+                            const uint8_t * const (&row)[NR], const uint32_t * sx, int n, int m) {
+    constexpr int NC = NB / CB;
+    if constexpr (C < NC) {
+        if constexpr (C + 1 < NC) {
+#pragma unroll
+            for (int q = 0; q < NR; ++q)
+#pragma unroll
+                for (int b = 0; b < CB; ++b) load_xblk(W[(C + 1) & 1][q][b], row[q] + ((C + 1) * CB + b) * 144, m);
+        }
+        const uint32_t * xt[MAXP];
+#pragma unroll
+        for (int i = 0; i < MAXP; ++i) xt[i] = sx + i * NB * XS + C * CB * XS;
+#pragma unroll
+        for (int q = 0; q < NR; ++q) q4k_acc8<CB, MAXP>(acc[q], accm[q], W[C & 1][q], xt, n, m);
+        q4k_chunk_step<NB, CB, NR, MAXP, C + 1>(acc, accm, W, row, sx, n, m);
+    }
+}
+
+// NR rows of NB > 8 blocks (hidden sizes above 2048), each against the same
+// n <= MAXP activation rows packed at sx + i * NB * XS: the blocks are
+// requested CB at a time into two register buffers, the next chunk's loads
+// issued before the current chunk's arithmetic, and each chunk runs through
+// q4k_acc8 with the accumulators carried over.  CB divides NB.
+template <int NB, int CB, int NR, int MAXP>
+QWM_DEV void q4k_dot8_chunked(float (&out)[NR][MAXP], const uint8_t * const (&row)[NR], const uint32_t * sx, int n_,
+                              int m) {
+    static_assert(NB % CB == 0, "the chunk must divide the row");
+    const int n = __builtin_amdgcn_readfirstlane(n_);
+    float acc[NR][MAXP], accm[NR][MAXP];
+#pragma unroll
+    for (int q = 0; q < NR; ++q)
+#pragma unroll
+        for (int i = 0; i < MAXP; ++i) { acc[q][i] = 0.f; accm[q][i] = 0.f; }
+    XBlk W[2][NR][CB];
+#pragma unroll
+    for (int q = 0; q < NR; ++q)
+#pragma unroll
+        for (int b = 0; b < CB; ++b) load_xblk(W[0][q][b], row[q] + b * 144, m);
+    q4k_chunk_step<NB, CB, NR, MAXP, 0>(acc, accm, W, row, sx, n, m);
+#pragma unroll
+    for (int q = 0; q < NR; ++q) q4k_fin8<MAXP>(out[q], acc[q], accm[q], n);
 }
 
 // q4k_dot8_off with the common token counts (1 and 2, most expert units of a

@@ -65,6 +65,12 @@ constexpr int MAX_K = 16;       // experts per token
 constexpr int MAX_E = 2048;     // experts per layer
 constexpr int MAX_PAIRS = MAX_T * MAX_K;
 
+// Row lengths the expert GEMVs are built for (the hidden size as their K):
+// 256 .. 2048 in steps of 256, then 3072 and 4096.
+inline bool hidden_supported(int64_t K) {
+    return K > 0 && K % 256 == 0 && (K <= 2048 || K == 3072 || K == 4096);
+}
+
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 // One expert of the layer's batch union and the (token, slot) pairs that

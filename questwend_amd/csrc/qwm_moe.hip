@@ -48,8 +48,8 @@ struct RouteKArgs {
 constexpr int ROUTE_LDS_INTS = 3 * MAX_E + 3 * 512;
 
 // One kernel for the whole routing step, one router row per workgroup (the
-// whole row in one round trip of coalesced 16-byte loads; H <= 2048, a
-// multiple of 256).
+// whole row in one round trip of coalesced loads for H <= 2048, step by step
+// for 3072 and 4096).
 //  * Router rows in ggml_vec_dot_f32's AVX-512 order (ggml-cpu/vec.cpp:
 //    11-135), which ggml-CPU runs per (row, token) at every token count
 //    (ggml-cpu.c:1165-1244; the reference builds it without llamafile): one
@@ -85,7 +85,26 @@ __global__ void __launch_bounds__(256) k_route(RouteKArgs a) {
     }
 
     const int rows = E + (a.sgi ? 1 : 0);
-    if (g < rows) {
+    if (g < rows && H > 2048) {
+        // hidden sizes 3072 and 4096: the same lane order over more 64-wide
+        // steps, the row and x read step by step
+        const bool sh_row = g == E;
+        const float * w = sh_row ? a.sgi : a.W + (size_t)g * H;
+        const int ns = H / 64;
+        for (int t = wave; t < T; t += 4) {
+            const float * xr = a.x + (size_t)t * H;
+            float acc = 0.f;
+#pragma unroll 8
+            for (int st = 0; st < ns; ++st) acc = __builtin_fmaf(w[64 * st + lane], xr[64 * st + lane], acc);
+            acc += lane_xor32_f(acc);
+            acc += lane_xor16_f(acc);
+            acc = tree16_dpp(acc);
+            if (lane == 0) {
+                if (sh_row) st_agent(a.sh_logit + t, acc);
+                else st_agent(a.logits + (size_t)t * E + g, a.rm ? acc + a.rm[(size_t)t * E + g] : acc);
+            }
+        }
+    } else if (g < rows) {
         const bool sh_row = g == E;
         const float * w = sh_row ? a.sgi : a.W + (size_t)g * H;
         {
@@ -293,11 +312,17 @@ __global__ void __launch_bounds__(256) k_gateup_x(GateUpArgs a) {
     const uint8_t * gbase = shared ? a.sh_gate : a.gate + (size_t)U.slot[0] * a.gate_slab;
     const uint8_t * ubase = shared ? a.sh_up : a.up + (size_t)U.slot[1] * a.up_slab;
     const int rc = min(r, rows - 1);
-    XBlk G[NB], W[NB];
+    // rows of up to 8 blocks are requested whole before the activations are
+    // copied; longer rows (hidden sizes 3072 and 4096) in double-buffered
+    // chunks of 4 blocks after it (q4k_dot8_chunked)
+    constexpr int NBR = NB <= 8 ? NB : 1;
+    XBlk G[NBR], W[NBR];
+    if constexpr (NB <= 8) {
 #pragma unroll
-    for (int b = 0; b < NB; ++b) {
-        load_xblk(G[b], gbase + (size_t)rc * row_bytes + b * 144, m);
-        load_xblk(W[b], ubase + (size_t)rc * row_bytes + b * 144, m);
+        for (int b = 0; b < NB; ++b) {
+            load_xblk(G[b], gbase + (size_t)rc * row_bytes + b * 144, m);
+            load_xblk(W[b], ubase + (size_t)rc * row_bytes + b * 144, m);
+        }
     }
     // the unit's tokens' activation blocks into LDS (uint4 copies)
     constexpr int Q4 = NB * XS / 4;
@@ -311,8 +336,16 @@ __global__ void __launch_bounds__(256) k_gateup_x(GateUpArgs a) {
     }
     __syncthreads();
     float g[MAXP], up[MAXP];
-    q4k_dot8<NB, MAXP>(g, G, s_x, n, m);
-    q4k_dot8<NB, MAXP>(up, W, s_x, n, m);
+    if constexpr (NB <= 8) {
+        q4k_dot8<NB, MAXP>(g, G, s_x, n, m);
+        q4k_dot8<NB, MAXP>(up, W, s_x, n, m);
+    } else {
+        const uint8_t * const rw[2] = {gbase + (size_t)rc * row_bytes, ubase + (size_t)rc * row_bytes};
+        float gu[2][MAXP];
+        q4k_dot8_chunked<NB, 4, 2, MAXP>(gu, rw, s_x, n, m);
+#pragma unroll
+        for (int i = 0; i < MAXP; ++i) { g[i] = gu[0][i]; up[i] = gu[1][i]; }
+    }
     if (m == 0 && r < rows) {
 #pragma unroll
         for (int i = 0; i < MAXP; ++i)
@@ -671,7 +704,7 @@ bool moe_plan(const qwm_moe_layer * L, int64_t T, MoePlan & p, std::string & why
     if (T < 1 || T > MAX_T) { why = "T must be in [1, 8]"; return false; }
     if (p.k < 1 || p.k > MAX_K || p.k > p.E) { why = "n_expert_used out of range"; return false; }
     if (p.E < 1 || p.E > MAX_E) { why = "n_expert out of range"; return false; }
-    if (p.H % QK_K || p.H > 2048) { why = "hidden size must be a multiple of 256, <= 2048"; return false; }
+    if (!hidden_supported(p.H)) { why = "hidden size must be a multiple of 256 up to 2048, 3072 or 4096"; return false; }
     if (p.N % QK_K || p.N > MAX_NDOWN) { why = "expert FFN size must be a multiple of 256, <= 2048"; return false; }
     if (p.shared && p.N_sh != p.N) { why = "the shared expert's FFN width must equal the routed one"; return false; }
     const int64_t P = T * p.k;
@@ -757,6 +790,8 @@ static bool launch_gateup_x(const GateUpArgs & g, int nb, int maxp, dim3 grid, h
         case 6: launch_gateup_x_nb<6>(g, maxp, grid, s); return true;
         case 7: launch_gateup_x_nb<7>(g, maxp, grid, s); return true;
         case 8: launch_gateup_x_nb<8>(g, maxp, grid, s); return true;
+        case 12: launch_gateup_x_nb<12>(g, maxp, grid, s); return true;
+        case 16: launch_gateup_x_nb<16>(g, maxp, grid, s); return true;
         default: return false;
     }
 }
@@ -779,6 +814,8 @@ static bool launch_gateup_x5(const GateUpArgs & g, int nb, int maxp, dim3 grid, 
         case 6: launch_gateup_x5_nb<6>(g, maxp, grid, s); return true;
         case 7: launch_gateup_x5_nb<7>(g, maxp, grid, s); return true;
         case 8: launch_gateup_x5_nb<8>(g, maxp, grid, s); return true;
+        case 12: launch_gateup_x5_nb<12>(g, maxp, grid, s); return true;
+        case 16: launch_gateup_x5_nb<16>(g, maxp, grid, s); return true;
         default: return false;
     }
 }
@@ -801,6 +838,8 @@ static bool launch_gateup_x80(const GateUpArgs & g, int npair, int maxp, dim3 gr
         case 24: launch_gateup_x80_np<24>(g, maxp, grid, s); return true;
         case 28: launch_gateup_x80_np<28>(g, maxp, grid, s); return true;
         case 32: launch_gateup_x80_np<32>(g, maxp, grid, s); return true;
+        case 48: launch_gateup_x80_np<48>(g, maxp, grid, s); return true;
+        case 64: launch_gateup_x80_np<64>(g, maxp, grid, s); return true;
         default: return false;
     }
 }
@@ -869,7 +908,6 @@ int launch_experts(const ExpertArgs & a, const MoePlan & p, uint8_t * ws, hipStr
     g.act = reinterpret_cast<float *>(ws + p.act);
     g.act_sh = reinterpret_cast<float *>(ws + p.act_sh);
     g.H = (int)p.H; g.N = (int)p.N; g.N_sh = (int)p.N_sh; g.k = (int)p.k; g.T = (int)p.T;
-    if (p.H > 2048) return fail(QWM_ERR_UNSUPPORTED, "hidden size > 2048 not tiled");
     const int rows_g = (int)std::max(p.N, p.N_sh);
     prof_begin("gate_up", s);
     const dim3 grid_x((rows_g + GUX_ROWS - 1) / GUX_ROWS, grid_y);
@@ -1007,9 +1045,14 @@ __global__ void __launch_bounds__(256) k_mmid_x(MmidGemv a) {
     const uint8_t * base = a.as + (size_t)U.expert * a.slab;
     const int r = blockIdx.x * 32 + wave * 8 + rsub;
     const int rc = min(r, a.N - 1);
-    XBlk W[NB];
+    // rows of up to 8 blocks requested whole before the column copy, longer
+    // rows in double-buffered chunks of 8 (or 6) blocks after it
+    constexpr int NBR = NB <= 8 ? NB : 1;
+    XBlk W[NBR];
+    if constexpr (NB <= 8) {
 #pragma unroll
-    for (int b = 0; b < NB; ++b) load_xblk(W[b], base + (size_t)rc * a.row_bytes + b * 144, m);
+        for (int b = 0; b < NB; ++b) load_xblk(W[b], base + (size_t)rc * a.row_bytes + b * 144, m);
+    }
     constexpr int Q4 = NB * XS / 4;
     for (int q = tid; q < n * Q4; q += 256) {
         const int i = q / Q4, o = q % Q4;
@@ -1021,7 +1064,15 @@ __global__ void __launch_bounds__(256) k_mmid_x(MmidGemv a) {
     }
     __syncthreads();
     float acc[MAXP];
-    q4k_dot8<NB, MAXP>(acc, W, s_x, n, m);
+    if constexpr (NB <= 8) {
+        q4k_dot8<NB, MAXP>(acc, W, s_x, n, m);
+    } else {
+        const uint8_t * const rw[1] = {base + (size_t)rc * a.row_bytes};
+        float o1[1][MAXP];
+        q4k_dot8_chunked<NB, (NB % 8 == 0 ? 8 : 6), 1, MAXP>(o1, rw, s_x, n, m);
+#pragma unroll
+        for (int i = 0; i < MAXP; ++i) acc[i] = o1[0][i];
+    }
     if (m == 0 && r < a.N) {
 #pragma unroll
         for (int i = 0; i < MAXP; ++i)
@@ -1195,7 +1246,7 @@ int launch_mmid(const MmidArgs & a, uint8_t * ws, hipStream_t s) {
     g.units = pr.units; g.n_units = pr.n_units; g.qs = pr.qs; g.d = pr.d; g.bs = pr.bs; g.xq = pr.xq;
     g.K = (int)a.K; g.N = (int)a.N; g.ne11 = (int)a.ne11; g.n_ids = (int)a.n_ids;
     g.dst = a.dst; g.dst_nb1 = a.dst_nb1; g.dst_nb2 = a.dst_nb2;
-    if (a.K > 2048) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: K > 2048 not tiled");
+    if (!hidden_supported(a.K)) return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: K must be 256 .. 2048, 3072 or 4096");
     if (!q80) {
         const dim3 gx((unsigned)((a.N + 31) / 32), (unsigned)(a.T * a.n_ids));
 #define QWM_MMIDX(NB_)                                                              \
@@ -1225,8 +1276,8 @@ int launch_mmid(const MmidArgs & a, uint8_t * ws, hipStream_t s) {
         prof_begin("mul_mat_id", s);
         switch (a.K / QK_K) {
             QWM_MMIDX(1) QWM_MMIDX(2) QWM_MMIDX(3) QWM_MMIDX(4)
-            QWM_MMIDX(5) QWM_MMIDX(6) QWM_MMIDX(7) QWM_MMIDX(8)
-            default: return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: K > 2048 not tiled");
+            QWM_MMIDX(5) QWM_MMIDX(6) QWM_MMIDX(7) QWM_MMIDX(8) QWM_MMIDX(12) QWM_MMIDX(16)
+            default: return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: K must be 256 .. 2048, 3072 or 4096");
         }
         prof_end("mul_mat_id", s);
 #undef QWM_MMIDX
@@ -1246,8 +1297,8 @@ int launch_mmid(const MmidArgs & a, uint8_t * ws, hipStream_t s) {
     prof_begin("mul_mat_id", s);
     switch (a.K / 64) {                       // pairs of Q8_0 blocks per row
         QWM_MMIDX80(4) QWM_MMIDX80(8) QWM_MMIDX80(12) QWM_MMIDX80(16)
-        QWM_MMIDX80(20) QWM_MMIDX80(24) QWM_MMIDX80(28) QWM_MMIDX80(32)
-        default: return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: K > 2048 not tiled");
+        QWM_MMIDX80(20) QWM_MMIDX80(24) QWM_MMIDX80(28) QWM_MMIDX80(32) QWM_MMIDX80(48) QWM_MMIDX80(64)
+        default: return fail(QWM_ERR_UNSUPPORTED, "mul_mat_id: K must be 256 .. 2048, 3072 or 4096");
     }
     prof_end("mul_mat_id", s);
 #undef QWM_MMIDX80

@@ -7,8 +7,10 @@ namespace qwm {
 
 template <int NT, int NS, int PF>
 __global__ void __launch_bounds__(256) k_verify_head(VerifyArgs a) {
-    __shared__ __align__(16) uint8_t smem[VhSmem<NT>::bytes];
-    verify_body<NT, NS, PF>(a, blockIdx.x, gridDim.x, smem);
+    __shared__ __align__(16) uint8_t smem[VhSmem<NT, NS>::bytes];
+    // hidden sizes above 2048: the first tiles after the prep (their windows
+    // and the prep's inputs do not fit the registers together)
+    verify_body<NT, NS, PF, (NS > 4 ? VH_LATE : VH_EARLY)>(a, blockIdx.x, gridDim.x, smem);
 }
 
 static int device_cus() {
@@ -26,8 +28,12 @@ bool verify_plan(const qwm_tensor * lm_head, int64_t T, VerifyPlan & p, std::str
     p.V = lm_head->ne[1];
     p.T = T;
     if (lm_head->type != T_Q8_0) { why = "lm_head must be Q8_0"; return false; }
-    if (p.H % 512 || p.H > 2048) { why = "lm_head: H must be 512, 1024, 1536 or 2048"; return false; }
+    if (p.H % 512 || (p.H > 2048 && p.H != 3072 && p.H != 4096)) {
+        why = "lm_head: H must be 512, 1024, 1536, 2048, 3072 or 4096";
+        return false;
+    }
     if (T < 1 || T > VH_MAX_T) { why = "verify batch must hold 1..8 tokens"; return false; }
+    if (p.H > 2048 && T > 4) { why = "lm_head: hidden sizes 3072 and 4096 take 1..4 tokens"; return false; }
     if (p.V < 1 || p.V > (1LL << 30)) { why = "lm_head: vocabulary size out of range"; return false; }
     p.n_wg = (int)std::min<int64_t>(2 * 256, (p.V + 7) / 8);
     size_t o = 0;
@@ -40,6 +46,9 @@ bool verify_plan(const qwm_tensor * lm_head, int64_t T, VerifyPlan & p, std::str
     return true;
 }
 
+// Hidden sizes 3072 and 4096 (6 and 8 block sets per lane) run at one tile in
+// flight and up to 4 tokens: the lane's windows and activations then fill its
+// registers.
 template <int NT>
 static void launch_nt(const VerifyArgs & a, int n_wg, hipStream_t s) {
     constexpr int PF = NT <= 4 ? 2 : 1;
@@ -48,6 +57,12 @@ static void launch_nt(const VerifyArgs & a, int n_wg, hipStream_t s) {
         case 512: k_verify_head<NT, 1, PF><<<grid, 256, 0, s>>>(a); break;
         case 1024: k_verify_head<NT, 2, PF><<<grid, 256, 0, s>>>(a); break;
         case 1536: k_verify_head<NT, 3, PF><<<grid, 256, 0, s>>>(a); break;
+        case 3072:
+            if constexpr (NT <= 4) k_verify_head<NT, 6, 1><<<grid, 256, 0, s>>>(a);
+            break;
+        case 4096:
+            if constexpr (NT <= 4) k_verify_head<NT, 8, 1><<<grid, 256, 0, s>>>(a);
+            break;
         default: k_verify_head<NT, 4, PF><<<grid, 256, 0, s>>>(a); break;
     }
 }

@@ -53,14 +53,16 @@ QWM_DEV void load_tile(uint32_t (&w)[NS][VH_WIN], const uint8_t * p0) {
     }
 }
 
-// LDS bytes of the quantized activations for NT tokens (s_q, s_d, s_sq).
-template <int NT> struct VhSmem {
-    static constexpr size_t q = (size_t)NT * 64 * 32, d = (size_t)NT * 64 * 4, sq = (size_t)NT * 64 * 8;
+// LDS bytes of the quantized activations for NT tokens of 512 NS values
+// (s_q, s_d, s_sq: 16 NS Q8_0 blocks per token).
+template <int NT, int NS = 4> struct VhSmem {
+    static constexpr size_t nb = (size_t)16 * NS;
+    static constexpr size_t q = (size_t)NT * nb * 32, d = (size_t)NT * nb * 4, sq = (size_t)NT * nb * 8;
     static constexpr size_t bytes = q + d + sq;
 };
 
 // The whole verify head for one workgroup `wg` of `n_wg` (grid-stride over
-// vocabulary rows), with `smem` holding VhSmem<NT>::bytes of LDS.  Returns
+// vocabulary rows), with `smem` holding VhSmem<NT, NS>::bytes of LDS.  Returns
 // true in the workgroup that finished last (it wrote the result).
 // NS = H / 512 block sets per lane (H = 512 * NS), PF tiles in flight.
 // ISSUE: when the first weight tiles are requested.  VH_EARLY: before the
@@ -74,9 +76,10 @@ QWM_DEV bool verify_body(const VerifyArgs & a, int wg, int n_wg, uint8_t * smem,
                          int32_t ready_target = 0, int32_t * err = nullptr, uint32_t spin_limit = 0) {
     constexpr int NG = (NT + 3) / 4;                  // token groups (MFMA A rows)
     __shared__ float s_scale[NT];
-    uint4 (*s_q)[64][2] = reinterpret_cast<uint4 (*)[64][2]>(smem);
-    float (*s_d)[64] = reinterpret_cast<float (*)[64]>(smem + VhSmem<NT>::q);
-    double * s_sq = reinterpret_cast<double *>(smem + VhSmem<NT>::q + VhSmem<NT>::d);
+    using Sm = VhSmem<NT, NS>;
+    uint4 (*s_q)[16 * NS][2] = reinterpret_cast<uint4 (*)[16 * NS][2]>(smem);
+    float (*s_d)[16 * NS] = reinterpret_cast<float (*)[16 * NS]>(smem + Sm::q);
+    double * s_sq = reinterpret_cast<double *>(smem + Sm::q + Sm::d);
     __shared__ float s_bv[4][NT];
     __shared__ int32_t s_bi[4][NT];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;

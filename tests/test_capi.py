@@ -93,6 +93,38 @@ def test_argument_validation_without_gpu():
     assert L.qwm_verify_workspace_size(qa.tensor(qa.TYPE_Q8_0, 2048, 151936), 4) > 0
 
 
+def test_wide_hidden_sizes_without_gpu():
+    """Hidden sizes 3072 and 4096 (Qwen3-235B-A22B: 4096, FFN 1536) are taken by
+    the MoE layer, MUL_MAT_ID and verify-head entry points; other sizes above
+    2048 are refused (workspace size 0)."""
+    L = qa.lib()
+    for H, ok in ((4096, True), (3072, True), (2304, False), (5120, False)):
+        lay = qa.MoeLayer()
+        lay.router = qa.tensor(qa.TYPE_F32, H, 128)
+        lay.gate_pool = qa.tensor(qa.TYPE_Q4_K, H, 1536, 4)
+        lay.up_pool = qa.tensor(qa.TYPE_Q4_K, H, 1536, 4)
+        lay.down_pool = qa.tensor(qa.TYPE_Q4_K, 1536, H, 4)
+        lay.n_expert_used = 8
+        assert (L.qwm_moe_workspace_size(lay, 4) > 0) == ok, H
+        b = qa.tensor(qa.TYPE_F32, H, 1, 4)
+        ids = qa.tensor(qa.TYPE_I32, 8, 4)
+        for t in (qa.TYPE_Q4_K, qa.TYPE_Q5_K, qa.TYPE_Q6_K, qa.TYPE_Q8_0):
+            assert (L.qwm_mul_mat_id_workspace_size(qa.tensor(t, H, 1536, 16), b, ids) > 0) == ok, (H, t)
+    # the verify head takes 3072 and 4096 for up to 4 tokens
+    for H in (3072, 4096):
+        lm = qa.tensor(qa.TYPE_Q8_0, H, 151936)
+        assert L.qwm_verify_workspace_size(lm, 4) > 0 and L.qwm_verify_workspace_size(lm, 5) == 0
+    assert L.qwm_verify_workspace_size(qa.tensor(qa.TYPE_Q8_0, 2560, 1000), 1) == 0
+    # the fused verify step stays at hidden size 2048 (it returns 0, the per-op path serves 4096)
+    lay = qa.MoeLayer()
+    lay.router = qa.tensor(qa.TYPE_F32, 4096, 128)
+    lay.gate_pool = qa.tensor(qa.TYPE_Q4_K, 4096, 1536, 4)
+    lay.up_pool = qa.tensor(qa.TYPE_Q4_K, 4096, 1536, 4)
+    lay.down_pool = qa.tensor(qa.TYPE_Q4_K, 1536, 4096, 4)
+    lay.n_expert_used = 8
+    assert L.qwm_verify_step_workspace_size(lay, qa.tensor(qa.TYPE_Q8_0, 4096, 151936), 4) == 0
+
+
 def test_block_resident_rejects_short_tensors_without_gpu():
     """qwm_moe_block_resident checks out/resid columns and the ids/weights
     outputs' type, shape and stride before any device work (a tensor with

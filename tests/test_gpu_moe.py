@@ -117,11 +117,18 @@ def experts_gpu(case, x, slots, weights, resid=None):
     dict(N=768, E=128, k=8, T=1, shared=False, wtype="q5_K"),   # Q5_K slabs (Q5_K_S/M model files)
     dict(N=512, E=512, k=10, T=4, shared=True, wtype="q5_K"),
     dict(N=768, E=128, k=8, T=4, shared=False, wtype="q5_K", down="q6_K"),
+    # hidden sizes above 2048 (gate/up rows in register chunks, router rows step by step)
+    dict(H=4096, N=1536, E=128, k=8, T=1, shared=False, S=8),    # Qwen3-235B-A22B shape
+    dict(H=4096, N=1536, E=128, k=8, T=4, shared=False, S=8),
+    dict(H=4096, N=1536, E=128, k=8, T=8, shared=False, S=8, down="q6_K"),
+    dict(H=4096, N=1536, E=128, k=8, T=4, shared=False, S=8, wtype="q8_0"),
+    dict(H=4096, N=512, E=64, k=4, T=2, shared=True, S=8, wtype="q5_K"),
+    dict(H=3072, N=512, E=64, k=4, T=3, shared=True, S=8),
 ])
 def test_moe_block_parity(dev, cfg):
     T = cfg["T"]
-    case = MoeCase(seed=11 + T, N=cfg["N"], E=cfg["E"], k=cfg["k"], S=24, shared=cfg["shared"],
-                   wtype=cfg.get("wtype", "q4_K"), down=cfg.get("down", "same"))
+    case = MoeCase(seed=11 + T, H=cfg.get("H", 2048), N=cfg["N"], E=cfg["E"], k=cfg["k"], S=cfg.get("S", 24),
+                   shared=cfg["shared"], wtype=cfg.get("wtype", "q4_K"), down=cfg.get("down", "same"))
     case.upload(torch)
     x = case.rng.standard_normal((T, case.H)).astype(np.float32)
     ids, w, _, _ = case.route(x)
@@ -189,7 +196,8 @@ def test_moe_block_residual(dev):
 @pytest.mark.parametrize("wt", ["q4_K", "q8_0", "q6_K", "q5_K"])
 @pytest.mark.parametrize("K,N,n_as,n_ids,ne11,T", [(2048, 768, 8, 8, 1, 1), (2048, 768, 8, 8, 1, 4),
                                                   (768, 2048, 8, 8, 8, 4), (512, 2048, 6, 10, 10, 2),
-                                                  (256, 64, 4, 3, 3, 2)])
+                                                  (256, 64, 4, 3, 3, 2), (4096, 512, 6, 4, 1, 3),
+                                                  (3072, 256, 4, 3, 3, 2)])
 def test_mul_mat_id_op(dev, K, N, n_as, n_ids, ne11, T, wt):
     """GGML_OP_MUL_MAT_ID contract, including broadcast b (ne11 = 1) and
     repeated experts across columns, for Q4_K, Q8_0 and Q6_K slabs (Q6_K rows

@@ -64,9 +64,10 @@ def check_case(vA, a, xn, gvA, ga, gxn, mg):
     return True
 
 
-@pytest.mark.parametrize("V,T", [(32768, 4), (4096, 1), (8192, 8), (1000, 2)])
-def test_verify_accept_parity(dev, V, T):
-    H = 2048
+@pytest.mark.parametrize("H,V,T", [(2048, 32768, 4), (2048, 4096, 1), (2048, 8192, 8), (2048, 1000, 2),
+                                   (4096, 16384, 4), (4096, 3000, 1), (3072, 8192, 3)])
+def test_verify_accept_parity(dev, H, V, T):
+    """Hidden sizes 3072 and 4096 (up to 4 tokens) beside 2048."""
     rng = np.random.default_rng(V + T)
     W = (rng.standard_normal((V, H)) / np.sqrt(H)).astype(np.float32)
     Wq = quantize_q8_0_model(W)
@@ -87,7 +88,7 @@ def test_verify_accept_parity(dev, V, T):
         check_case(vA, a, xn, gvA, ga, gxn, mg)
         if T > 1:
             assert a == (rep % T if rep % T < T - 1 else T - 1)
-    print(f"verify V={V} T={T}: min top-2 margin {min(margins):.3e}")
+    print(f"verify H={H} V={V} T={T}: min top-2 margin {min(margins):.3e}")
 
 
 def test_verify_full_vocab(dev):

@@ -260,6 +260,87 @@ def test_mul_mat_id_indexing(wtype):
 
 # ------------------------------------------------------------- verify --
 
+def _silu64(v):
+    return v / (1.0 + np.exp(-v))
+
+
+def _block_fp64(case, x, slots, w, plant=None):
+    """The MoE block as an fp64 textbook composition of pinned parts: Q4_K
+    weights dequantized, Q8_K of x and of the SwiGLU activations (the
+    quantizer is pinned against the reference's own), gate and up dots,
+    silu(gate) * up, the down dot, the weighted sum over the k experts, and
+    the shared expert times sigmoid(g . x).  `plant` swaps in one plausible
+    mistake, to show the bound catches it."""
+    T, H, N, k = x.shape[0], case.H, case.N, case.k
+    gate = dequant_q4k(case.gate_q, H).reshape(case.S, N, H)
+    up = dequant_q4k(case.up_q, H).reshape(case.S, N, H)
+    down = dequant_q4k(case.down_q, N).reshape(case.S, H, N)
+    xq = dequant_q8k(x)
+    out = np.zeros((T, H))
+    gates = np.zeros((T, k, N))
+    ups = np.zeros((T, k, N))
+    for t in range(T):
+        for j in range(k):
+            e = slots[t, j]
+            if plant == "slot":
+                e = (e + 1) % case.S
+            g = gate[e] @ xq[t]
+            u = up[e] @ xq[t]
+            gates[t, j], ups[t, j] = g, u
+            act = _silu64(u) * g if plant == "swap" else _silu64(g) * u
+            aq = dequant_q8k(act.astype(np.float32)[None, :])[0]
+            wd = down[e].reshape(N, H).T if plant == "transpose" else down[e]   # the slab read as [N][H]
+            dn = wd @ aq
+            out[t] += (1.0 if plant == "weights" else w[t, j]) * dn
+        if case.shared and plant != "no_shared":
+            sg = dequant_q4k(case.shg_q, H) @ xq[t]
+            su = dequant_q4k(case.shu_q, H) @ xq[t]
+            sa = dequant_q8k((_silu64(sg) * su).astype(np.float32)[None, :])[0]
+            sh = dequant_q4k(case.shd_q, case.N_sh) @ sa
+            z = case.sh_inp.astype(np.float64) @ x[t].astype(np.float64)
+            out[t] += sh / (1.0 + np.exp(-z))
+    return out, gates, ups
+
+
+@pytest.mark.parametrize("T,shared", [(1, False), (3, True)])
+def test_moe_block_against_fp64(T, shared):
+    """The oracle's block graph (qwo_moe_block: gate/up MUL_MAT_ID, SwiGLU, down
+    MUL_MAT_ID, the k-weighted combine, the gated shared expert) against the
+    fp64 composition above, with the router's ids and weights (pinned by the
+    routing tests).  The gap is the oracle's fp32 roundings (~1e-7); a slot off
+    by one, gate and up swapped, a transposed down matrix, unweighted experts
+    or a dropped shared expert each miss by more than 1e-2."""
+    from tests.moe_case import MoeCase, QwoMoeArgs
+    case = MoeCase(seed=40 + T, H=512, N=256, E=16, k=4, S=16, shared=shared, N_sh=256)
+    x = case.rng.standard_normal((T, case.H)).astype(np.float32)
+    ids, w, _, _ = case.route(x)
+    slots = ids.astype(np.int32)
+    exp64, g64, u64 = _block_fp64(case, x, slots, w)
+    got = case.block(x, slots, w).astype(np.float64)
+    err = np.linalg.norm(got - exp64) / np.linalg.norm(exp64)
+    assert err < 1e-5, err
+    # the intermediates the oracle exposes: gate and up rows of every (token, expert)
+    gate = np.zeros((T, case.k, case.N), np.float32)
+    up = np.zeros_like(gate)
+    a = QwoMoeArgs()
+    a.H, a.N, a.k, a.T = case.H, case.N, case.k, T
+    a.weight_type = case.ggml_type
+    a.gate_pool, a.up_pool, a.down_pool = case.gate_q.ctypes.data, case.up_q.ctypes.data, case.down_q.ctypes.data
+    a.n_slots = case.S
+    a.slot_g = a.slot_u = a.slot_d = slots.ctypes.data
+    a.weights = w.ctypes.data
+    a.x = x.ctypes.data
+    out = np.zeros((T, case.H), np.float32)
+    a.out = out.ctypes.data
+    a.gate_out, a.up_out = gate.ctypes.data, up.ctypes.data
+    assert oracle().qwo_moe_block(ctypes.byref(a)) == 0
+    assert np.abs(gate - g64).max() <= 1e-5 * np.abs(g64).max()
+    assert np.abs(up - u64).max() <= 1e-5 * np.abs(u64).max()
+    for plant in ("slot", "swap", "transpose", "weights") + (("no_shared",) if shared else ()):
+        bad, _, _ = _block_fp64(case, x, slots, w, plant)
+        assert np.linalg.norm(got - bad) / np.linalg.norm(bad) > 1e-2, plant
+
+
 def test_rms_norm_and_accept():
     rng = np.random.default_rng(9)
     x = rng.standard_normal(2048).astype(np.float32) * 3

@@ -287,14 +287,14 @@ int qwm_profile_start(const char * kernel, int32_t max_launches);
 int qwm_profile_stop(float * durations_ms, int32_t capacity);
 
 /* The bound of every wait inside the persistent launches (the fused verify
- * step, the persistent decode loop), in 64-cycle sleeps of the polling wave;
- * default 2^21.  A wait that runs out lets its workgroup go on, and the call
+ * step, the persistent decode loop), in polls of the waiting wave (a read of
+ * the counter and a 64-cycle sleep each); default 2^21.  A wait that runs out lets its workgroup go on, and the call
  * reports it: the verify result's a and x_new are -1, the decode miss flag
  * gets bit 1 (value 2).  The launches re-arm their counters either way, so
  * the next call on the same workspace is unaffected.  A small bound (0 gives
- * up after one sleep) forces that path, for tests of it.  Calls launched
+ * up after one read) forces that path, for tests of it.  Calls launched
  * afterwards use the new bound. */
-int qwm_set_spin_limit(uint32_t sleeps);
+int qwm_set_spin_limit(uint32_t polls);
 
 /* ---------------------------------------------------------- slot pool --- */
 

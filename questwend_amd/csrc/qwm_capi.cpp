@@ -123,8 +123,8 @@ int qwm_profile_start(const char * kernel, int32_t max_launches) {
     });
 }
 
-int qwm_set_spin_limit(uint32_t sleeps) {
-    set_spin_limit(sleeps);
+int qwm_set_spin_limit(uint32_t polls) {
+    set_spin_limit(polls);
     return QWM_OK;
 }
 

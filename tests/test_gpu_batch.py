@@ -35,13 +35,17 @@ def workspace(nbytes):
     return ws
 
 
-@pytest.mark.parametrize("T,max_slice,shared,fetch,S", [(40, 0, True, qa.FETCH_GATHER, 20), (40, 0, False, qa.FETCH_MEMCPY, 20),
-                                                        (30, 6, True, qa.FETCH_GATHER, 20), (5, 0, True, qa.FETCH_MEMCPY, 20),
-                                                        (40, 0, True, qa.FETCH_GATHER, 64)])
-def test_cached_batch_matches_oracle(dev, T, max_slice, shared, fetch, S):
+@pytest.mark.parametrize("T,max_slice,shared,fetch,S,H,E", [(40, 0, True, qa.FETCH_GATHER, 20, 512, 64),
+                                                            (40, 0, False, qa.FETCH_MEMCPY, 20, 512, 64),
+                                                            (30, 6, True, qa.FETCH_GATHER, 20, 512, 64),
+                                                            (5, 0, True, qa.FETCH_MEMCPY, 20, 512, 64),
+                                                            (40, 0, True, qa.FETCH_GATHER, 64, 512, 64),
+                                                            (24, 0, True, qa.FETCH_GATHER, 20, 4096, 32)])
+def test_cached_batch_matches_oracle(dev, T, max_slice, shared, fetch, S, H, E):
     """S = 64 slots hold every expert: one slice of 40 tokens, whose gate and up
-    slots agree, so it runs the fused gate/up/SwiGLU pass."""
-    H, N, E, k = 512, 256, 64, 4
+    slots agree, so it runs the fused gate/up/SwiGLU pass.  H = 4096: the
+    slices' MUL_MAT_IDs run as GEMV chunks (the grouped GEMM holds K <= 2048)."""
+    N, k = 256, 4
     case = MoeCase(seed=71 + T, H=H, N=N, E=E, k=k, S=E, shared=shared, N_sh=N)
     rng = np.random.default_rng(T + max_slice)
     slab = case.gate_q.nbytes // E
@@ -90,7 +94,7 @@ def test_cached_batch_matches_oracle(dev, T, max_slice, shared, fetch, S):
             hids = np.zeros(T * k, np.int32)
             hsl = np.zeros(2 * T, np.int32)
             nsl = ctypes.c_int32()
-            print(f"cached batch T={T} max_slice={max_slice} shared={shared} S={S}: rep {rep}", flush=True)
+            print(f"cached batch T={T} max_slice={max_slice} shared={shared} S={S} H={H}: rep {rep}", flush=True)
             qa.check(L.qwm_profile_start(b"prefill_gemm_gu", 64))
             qa.check(L.qwm_moe_cached_batch(lay, h, 0, qa.tensor(qa.TYPE_F32, H, T, 1, dx),
                                             qa.tensor(qa.TYPE_F32, E, T, 1, drm), qa.tensor(qa.TYPE_F32, H, T, 1, dr),

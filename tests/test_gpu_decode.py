@@ -29,9 +29,13 @@ def workspace(nbytes):
     return ws
 
 
-@pytest.mark.parametrize("T,n_layers,wtype", [(1, 4, "q4_K"), (4, 5, "q4_K"), (2, 3, "q8_0")])
-def test_decode_layers(dev, T, n_layers, wtype):
-    H, N, E, k = 512, 256, 16, 4
+@pytest.mark.parametrize("T,n_layers,wtype,H,N", [(1, 4, "q4_K", 512, 256), (4, 5, "q4_K", 512, 256),
+                                                  (2, 3, "q8_0", 512, 256),
+                                                  (1, 2, "q4_K", 4096, 512), (3, 2, "q8_0", 3072, 256)])
+def test_decode_layers(dev, T, n_layers, wtype, H, N):
+    """Hidden sizes 3072 and 4096 take the per-layer launches (the persistent
+    decode is built for 2048)."""
+    E, k = 16, 4
     cases = [MoeCase(seed=100 + l, H=H, N=N, E=E, k=k, S=E, wtype=wtype) for l in range(n_layers)]
     rng = np.random.default_rng(7)
     perms = [rng.permutation(E).astype(np.int32) for _ in range(n_layers)]   # expert -> slot, per layer
@@ -68,7 +72,7 @@ def test_decode_layers(dev, T, n_layers, wtype):
     torch.cuda.synchronize()
     got = dx.cpu().numpy()
     err = rel_err(got, exp)
-    print(f"decode T={T} layers={n_layers} {wtype}: rel err {err:.3e}")
+    print(f"decode T={T} layers={n_layers} {wtype} H={H}: rel err {err:.3e}")
     assert err < TOL
     assert np.array_equal(got.view(np.uint32), exp.view(np.uint32)), f"{wtype} decode loop not bit-exact"
     assert np.array_equal(got.view(np.uint32), a.cpu().numpy().view(np.uint32)), "loop and per-block calls differ"

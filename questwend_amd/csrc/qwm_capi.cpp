@@ -153,7 +153,8 @@ int qwm_profile_stop(float * durations_ms, int32_t capacity) {
 // ------------------------------------------------------------ mul_mat_id --
 
 // The grouped GEMM takes more than MAX_T columns of Q4_K or Q8_0 weights in the
-// shapes it supports (N % 64, K <= 2048, 16-byte aligned data); `data` false
+// shapes it supports (N % 64, K up to 2048, 3072 or 4096, 16-byte aligned
+// data); `data` false
 // leaves the alignment out (a size query before the weights are placed).
 static bool prefill_shape(const qwm_tensor * as, const qwm_tensor * b, bool data = true) {
     std::string why;

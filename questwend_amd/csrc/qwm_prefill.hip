@@ -23,7 +23,7 @@ namespace qwm {
 
 constexpr int PF_TOK = 16;     // columns per tile
 constexpr int PF_ROWS = 64;    // weight rows per tile
-constexpr int PF_MAXK = 2048;  // longest K held in LDS
+constexpr int PF_MAXK = 4096;  // longest K held in LDS (3072 and 4096 above 2048)
 constexpr int PF_MAX_AS = 4096;
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -160,9 +160,12 @@ __global__ void __launch_bounds__(PF_PREP_THREADS) k_pf_prep(PfArgs a) {
 // Q8_0 (ggml's vec_dot_type for Q8_0).
 // Three workgroups per CU for Q4_K (LDS 47 KB each at K 2048; 168 VGPRs), two
 // where that budget spills (gate/up with 1, 6 or 7 blocks per row) and for Q8_0
-// (64 KB of LDS at K 2048).
+// (64 KB of LDS at K 2048); two at K 3072 (66-73 KB) and one at K 4096
+// (84-91 KB: the 16 activation rows alone take 66 KB).
 template <int NB, bool GU, bool Q8>
-constexpr int pf_occupancy() { return (Q8 || (GU && (NB == 1 || NB >= 6 && NB != 8))) ? 2 : 3; }
+constexpr int pf_occupancy() {
+    return NB > 12 ? 1 : NB > 8 ? 2 : (Q8 || (GU && (NB == 1 || NB >= 6 && NB != 8))) ? 2 : 3;
+}
 
 template <int NB, bool GU, bool Q8>
 __global__ void __launch_bounds__(256, (pf_occupancy<NB, GU, Q8>())) k_pf_gemm(PfArgs a) {
@@ -451,7 +454,10 @@ static int64_t pf_bytes_per_256(int32_t wtype) { return wtype == T_Q8_0 ? 272 : 
 
 bool prefill_supported(int32_t wtype, int64_t K, int64_t N, int64_t n_as, const void * as, std::string & why) {
     if (wtype != T_Q4_K && wtype != T_Q8_0) { why = "prefill mul_mat_id: Q4_K or Q8_0 weights only"; return false; }
-    if (K % QK_K || K > PF_MAXK) { why = "prefill mul_mat_id: K must be a multiple of 256, <= 2048"; return false; }
+    if (K % QK_K || (K > 2048 && K != 3072 && K != 4096)) {
+        why = "prefill mul_mat_id: K must be a multiple of 256 up to 2048, or 3072 or 4096";
+        return false;
+    }
     if (N % PF_ROWS) { why = "prefill mul_mat_id: N must be a multiple of 64"; return false; }
     if (n_as > PF_MAX_AS) { why = "prefill mul_mat_id: more than 4096 experts"; return false; }
     if ((uint64_t)N * (uint64_t)(K / QK_K) * (uint64_t)pf_bytes_per_256(wtype) >= (1ull << 31)) {
@@ -517,7 +523,8 @@ int launch_prefill(const MmidArgs & m, uint8_t * ws, hipStream_t s, const uint8_
         break;
     switch (m.K / QK_K) {
         QWM_PF_CASE(1) QWM_PF_CASE(2) QWM_PF_CASE(3) QWM_PF_CASE(4) QWM_PF_CASE(5) QWM_PF_CASE(6) QWM_PF_CASE(7)
-        default: QWM_PF_CASE(8)
+        QWM_PF_CASE(8) QWM_PF_CASE(12)
+        default: QWM_PF_CASE(16)
     }
 #undef QWM_PF_CASE
     if (rc != QWM_OK) return rc;

@@ -81,6 +81,8 @@ def run_case(rng, K, N, n_as, n_ids, ne11, T, skew, ws=None, q=None, wtype=GGML_
     (512, 2048, 64, 8, 8, 48, 0.5),      # down shape: one b row per (column, slot)
     (768, 2048, 32, 4, 4, 24, 0.0),      # K = 3 blocks
     (256, 64, 16, 2, 1, 9, 0.0),         # smallest: K one block, one row tile
+    (4096, 256, 16, 8, 1, 24, 0.0),      # hidden 4096 (Qwen3-235B-A22B gate/up): one workgroup per CU
+    (3072, 128, 16, 4, 1, 20, 0.5),      # hidden 3072: two workgroups per CU
 ])
 def test_prefill_mul_mat_id(dev, wtype, K, N, n_as, n_ids, ne11, T, skew):
     rng = np.random.default_rng(K + N + T)

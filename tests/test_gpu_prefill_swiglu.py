@@ -94,6 +94,8 @@ def oracle_act(gtype, qg, qu, b, ids, K, N, n_as):
     (GGML_Q4_K, 2048, 512, 64, 10, 5, 0.0),     # T <= 8: the GEMV path, separate calls
     (GGML_Q8_0, 512, 256, 16, 4, 20, 0.0),      # Q8_0 past 8 columns: the grouped pass
     (GGML_Q8_0, 2048, 512, 64, 10, 64, 1.1),    # Q8_0 at the gate/up shape, Zipf(1.1)
+    (GGML_Q4_K, 4096, 256, 16, 8, 24, 0.0),     # hidden 4096 (Qwen3-235B-A22B): K of 16 blocks
+    (GGML_Q8_0, 3072, 128, 16, 4, 20, 0.5),     # hidden 3072
 ])
 def test_swiglu_matches_oracle_and_separate_calls(dev, gtype, K, N, n_as, n_ids, T, skew):
     rng = np.random.default_rng(K + N + T + gtype)

@@ -37,7 +37,8 @@ LM_ROW = H // 32 * 34                # 2176 B
 QK_K_ = 256
 CAL_BYTES = 256 << 20                # calibration copy for the PMC byte counters
 TRAFFIC_SUMMARY = {"step": os.path.join(ROOT, "profiles", "verify_step_T4_traffic.json"),
-                   "ops": os.path.join(ROOT, "profiles", "verify_ops_T4_traffic.json")}
+                   "ops": os.path.join(ROOT, "profiles", "verify_ops_T4_traffic.json"),
+                   "prefill": os.path.join(ROOT, "profiles", "prefill_T512_traffic.json")}
 
 
 def measured_traffic(path, kernel):
@@ -487,6 +488,13 @@ def bench_prefill(args, torch, qa, T_pf=512, E_pf=512, k_pf=10, N_pf=512):
     ms_sep, g_sep = timed(step_separate, 3)
     down_sep = down.clone()
     ms, g_ms = timed(step, 2)
+    # the PMC byte counters' scale (as in the verify bench): torch.neg over 256 MiB
+    cal_src = torch.full((CAL_BYTES // 4,), 1.0, dtype=torch.float32, device=dev)
+    cal_dst = torch.empty_like(cal_src)
+    for _ in range(3):
+        torch.neg(cal_src, out=cal_dst)
+    torch.cuda.synchronize()
+    del cal_src, cal_dst
     act_fused = act.clone()
     torch.mul(torch.nn.functional.silu(gate), up, out=act)     # the separate path's act, same x and ids
     act_diff = float((act_fused - act).abs().max())
@@ -542,7 +550,9 @@ def bench_prefill(args, torch, qa, T_pf=512, E_pf=512, k_pf=10, N_pf=512):
                                 "gemm_ms_each": g_sep.mean(0).tolist() if g_sep is not None else None,
                                 "act_max_abs_diff_vs_torch_silu": act_diff, "down_max_abs_diff": down_diff}},
         "roofline": {"bound": "hbm", "kernel": "k_pf_gemm<8, gate/up> (1 of 2 launches per step)", "achieved": gbs,
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS, "traffic": None,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
+                     "traffic": measured_traffic("prefill", "gate_up"),
+                     "traffic_source": os.path.relpath(TRAFFIC_SUMMARY["prefill"], ROOT),
                      "bytes_per_launch": gu_bytes},
         "mfma": {"tops": flops / (gemm_ms * 1e-3) / 1e12, "peak_int8_tops": 5000.0,
                  "frac": flops / (gemm_ms * 1e-3) / 5e15},

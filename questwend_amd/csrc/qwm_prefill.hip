@@ -61,19 +61,31 @@ __device__ inline int pf_pair_expert(const PfArgs & a, int p, int P, bool & bad)
 // are consecutive: first column, columns) and the pairs placed in their
 // expert's group through per-expert cursors in LDS.  Inside a group the order
 // is whatever the LDS atomics give: a column's result does not depend on its
-// position.  Each pass requests a batch of ids before it touches LDS, so the
+// position.  The first KB * UN * G pairs' experts are read once and kept in
+// registers for both passes (all of a 512-token chunk's top-10); further pairs
+// are read in batches of UN * G, each requested before it touches LDS, so the
 // loads overlap.  Nothing carries over between calls, so calls of any shape
 // may share a workspace.
 __device__ void pf_group(const PfArgs & a) {
-    constexpr int G = PF_PREP_THREADS, NW = G / 64, PER = PF_MAX_AS / G, UN = 4;
+    constexpr int G = PF_PREP_THREADS, NW = G / 64, PER = PF_MAX_AS / G, UN = 4, KB = 2;
     __shared__ int32_t s_c[PF_MAX_AS];
     __shared__ int32_t s_wsum[2][NW];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int P = a.T * a.n_ids;
     bool bad = false;
+    int keep[KB][UN];                              // pair (kb UN + j) G + tid
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int j = 0; j < UN; ++j) keep[kb][j] = pf_pair_expert(a, (kb * UN + j) * G + tid, P, bad);
     for (int e = tid; e < a.n_as; e += G) s_c[e] = 0;
     __syncthreads();
-    for (int p0 = 0; p0 < P; p0 += G * UN) {
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int j = 0; j < UN; ++j)
+            if (keep[kb][j] >= 0) atomicAdd(&s_c[keep[kb][j]], 1);
+    for (int p0 = KB * UN * G; p0 < P; p0 += G * UN) {
         int v[UN];
 #pragma unroll
         for (int j = 0; j < UN; ++j) v[j] = pf_pair_expert(a, p0 + j * G + tid, P, bad);
@@ -114,7 +126,12 @@ __device__ void pf_group(const PfArgs & a) {
     }
     if (tid == G - 1) *a.total = ib;
     __syncthreads();
-    for (int p0 = 0; p0 < P; p0 += G * UN) {
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int j = 0; j < UN; ++j)
+            if (keep[kb][j] >= 0) a.perm[atomicAdd(&s_c[keep[kb][j]], 1)] = (kb * UN + j) * G + tid;
+    for (int p0 = KB * UN * G; p0 < P; p0 += G * UN) {
         int v[UN];
 #pragma unroll
         for (int j = 0; j < UN; ++j) v[j] = pf_pair_expert(a, p0 + j * G + tid, P, bad);

@@ -110,6 +110,12 @@ def test_wide_hidden_sizes_without_gpu():
         ids = qa.tensor(qa.TYPE_I32, 8, 4)
         for t in (qa.TYPE_Q4_K, qa.TYPE_Q5_K, qa.TYPE_Q6_K, qa.TYPE_Q8_0):
             assert (L.qwm_mul_mat_id_workspace_size(qa.tensor(t, H, 1536, 16), b, ids) > 0) == ok, (H, t)
+    # prefill-sized batches at K 4096 take the grouped GEMM (Q4_K, Q8_0) or the GEMV chunks (Q6_K): both sized
+    b64 = qa.tensor(qa.TYPE_F32, 4096, 1, 64)
+    i64 = qa.tensor(qa.TYPE_I32, 8, 64)
+    sz = {t: L.qwm_mul_mat_id_workspace_size(qa.tensor(t, 4096, 1536, 128), b64, i64)
+          for t in (qa.TYPE_Q4_K, qa.TYPE_Q8_0, qa.TYPE_Q6_K)}
+    assert all(v > 0 for v in sz.values()) and sz[qa.TYPE_Q8_0] >= sz[qa.TYPE_Q4_K] > sz[qa.TYPE_Q6_K], sz
     # the verify head takes 3072 and 4096 for up to 4 tokens
     for H in (3072, 4096):
         lm = qa.tensor(qa.TYPE_Q8_0, H, 151936)

@@ -236,7 +236,7 @@ __global__ void __launch_bounds__(256, (pf_occupancy<NB, GU, Q8>())) k_pf_gemm(P
         uint32_t poff[NL];
 #pragma unroll
         for (int i = 0; i < NL; ++i) {
-            const int pc = min(lane + 64 * i, SP - 1);        // lanes past the last piece load it again (not staged)
+            const int pc = min(lane + 64 * i, SP - 1);        // lanes past the last piece: an in-bounds address, never loaded
             poff[i] = (uint32_t)(pc / PPR) * (uint32_t)a.row_bytes + (uint32_t)(pc % PPR) * 16u;
         }
         // ring depth: steps in flight per stream, a divisor of NB (every group of PF steps is
@@ -248,7 +248,16 @@ __global__ void __launch_bounds__(256, (pf_occupancy<NB, GU, Q8>())) k_pf_gemm(P
         auto load_s = [&](int q, int p, int st) {
             const uint32_t o = (uint32_t)(st / NB) * (uint32_t)(PF_ROWS * a.row_bytes) + (uint32_t)(st % NB) * (uint32_t)SROW;
 #pragma unroll
-            for (int i = 0; i < NL; ++i) wr[i][q][p] = *reinterpret_cast<const u32x4 *>(wbase[q] + (poff[i] + o));
+            for (int i = 0; i < NL; ++i) {
+                if (SP % 64 != 0 && i == NL - 1) {
+                    // the last load's lanes past the step's pieces stay idle (their values are never staged)
+                    u32x4 t = __builtin_nondeterministic_value(wr[i][q][p]);
+                    if (lane < SP - 64 * (NL - 1)) t = *reinterpret_cast<const u32x4 *>(wbase[q] + (poff[i] + o));
+                    wr[i][q][p] = t;
+                } else {
+                    wr[i][q][p] = *reinterpret_cast<const u32x4 *>(wbase[q] + (poff[i] + o));
+                }
+            }
         };
 #pragma unroll
         for (int p = 0; p < PF; ++p)
